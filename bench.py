@@ -1,0 +1,159 @@
+#!/usr/bin/env python3
+"""BeamAttention decode benchmark on one MI355X.
+
+Workload: one decode step of 8 requests x 128 beams over a 2048-token shared
+prefix (per-request suffix length uniform in [1, 8]), 32 query / 8 KV heads,
+head_dim 128, block 16, bf16 -- synthetic seeded inputs already resident in
+HBM.  A "step" is one gr_beam_attn_decode launch over the whole batch.
+
+Prints one JSON line: value = algorithmic GB/s (each request's prefix K/V
+counted once + suffix K/V + Q + O + tables) over the average step time;
+roofline for the decode kernel against 8 TB/s; cpu_baseline = the torch
+float32 cascade restatement of the reference (oracle/cpu_baseline.py) on the
+host cores for the same step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "vllm-gr-ehaleva_amd")]
+
+METRIC = "BeamAttention decode µs/step + HBM GB/s (% peak) at 128 beams, 2K prefix"
+HBM_PEAK_GBPS = 8000.0
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_beam128_hbm_traffic.txt")
+
+
+def _log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _traffic_from_profile():
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    calibrated against a copy kernel), when that summary has been committed."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read())
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def cpu_baseline(wl, budget_s: float = 20.0):
+    import torch
+    from oracle.cpu_baseline import cascade_decode_fp32
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    args = (wl.q, wl.k_cache, wl.v_cache, wl.prefix_bt, wl.prefix_len, wl.beam_start, wl.suffix_bt,
+            wl.suffix_len)
+    kw = dict(scale=wl.scale, block_size=wl.block_size)
+    R = len(wl.prefix_len)
+    # bounded sample: whole requests, as many as fit the budget after one timed probe
+    t0 = time.perf_counter()
+    cascade_decode_fp32(*args, **kw, requests=[0])
+    per_req = time.perf_counter() - t0
+    reqs = list(range(min(R, max(1, int(budget_s / 12 / max(per_req, 1e-6))))))
+    times = []
+    for i in range(12):  # 2 warm-ups + 10 timed
+        t0 = time.perf_counter()
+        cascade_decode_fp32(*args, **kw, requests=reqs)
+        if i >= 2:
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    us_step = med / len(reqs) * R * 1e6
+    gbps = wl.algorithmic_bytes() / (us_step * 1e-6) / 1e9
+    return {"value": round(gbps, 3), "unit": "GB/s", "cores": n, "kind": "port",
+            "us_per_step": round(us_step, 1),
+            "sample": f"{len(reqs)} of {R} requests (x128 beams, prefix 2048) per run, median of 10 "
+                      f"after 2 warm-ups, scaled to the full step; torch float32 cascade "
+                      f"(prefix pass + suffix pass + LSE merge)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel", choices=["auto", "generic"], default="auto")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (requests are "
+              "independent, so N GPUs shard requests data-parallel with no exchange).", file=sys.stderr)
+        return 2
+
+    import torch
+    from vllm_gr_amd import ops, workloads
+
+    dev = torch.device("cuda:0")
+    _log("bench: building decode_beam128 inputs (seed 0)")
+    host_wl = workloads.decode_beam128(seed=0)
+    wl = host_wl.to(dev)
+    out = torch.empty_like(wl.q)
+    ops.set_decode_kernel(args.kernel)
+
+    def step():
+        ops.beam_attn_decode(wl.q, wl.k_cache, wl.v_cache, wl.prefix_bt, wl.prefix_len, wl.beam_start,
+                             wl.suffix_bt, wl.suffix_len, scale=wl.scale, max_beams_per_req=wl.max_beams,
+                             out=out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(end)
+    us_step = ms_total * 1000.0 / args.steps
+    nbytes = host_wl.algorithmic_bytes()
+    gbps = nbytes / (us_step * 1e-6) / 1e9
+    _log(f"bench: {us_step:.2f} us/step, {gbps:.1f} GB/s algorithmic ({nbytes} B/step)")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log("bench: timing the CPU baseline")
+        cpu = cpu_baseline(host_wl)
+        _log(f"bench: cpu {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1000.0, 5),
+        "us_per_step": round(us_step, 3),
+        "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)/sqrt(128) Q/K/V, random block tables)",
+        "config": {"workload": "beam decode: 8 requests x 128 beams, shared prefix 2048, suffix U[1,8], "
+                               "32 q / 8 kv heads, head_dim 128, block 16",
+                   "requests": 8, "beams": 128, "prefix": 2048, "kernel": args.kernel,
+                   "algorithmic_bytes_per_step": nbytes, "flops_per_step": host_wl.flops()},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": _traffic_from_profile()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,188 @@
+/*
+ * gr_beam.h -- C ABI of the MI355X (gfx950) beam-aware KV-cache hot path.
+ *
+ * One shared library (libgr_beam.so) exports these entry points.  Every call
+ * is stream-ordered on the HIP stream it is given, allocates nothing, does
+ * no host synchronisation, and returns a gr_status_t.  Pointers are device
+ * pointers unless stated otherwise.  Element strides are in elements, not
+ * bytes.  The paged KV cache keeps the reference's per-K/V layout
+ * [num_blocks, block_size, num_kv_heads, head_dim] with head_dim contiguous
+ * (vllm_gr/v1/attention/backends/beam_attn.py:784-785); other block layouts
+ * (the HND stride order, :787-798) are expressed through the three strides.
+ *
+ * Table contents (block ids, lengths, parents) live on the device, so the
+ * library cannot reject them before launch; kernels skip any access they
+ * would make out of bounds and OR a GR_DEV_* bit into *dev_status (when not
+ * NULL), which the caller may read back after the stream completes.
+ */
+#ifndef GR_BEAM_H_
+#define GR_BEAM_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int gr_status_t;
+enum {
+  GR_OK = 0,
+  GR_ERR_INVALID_ARG = 1, /* bad size, stride, pointer or combination */
+  GR_ERR_UNSUPPORTED = 2, /* valid but not implemented (dtype, head size) */
+  GR_ERR_LAUNCH = 3,      /* the HIP runtime refused the launch */
+  GR_ERR_WORKSPACE = 4    /* workspace missing or too small */
+};
+
+/* bits OR-ed into *dev_status by kernels */
+enum {
+  GR_DEV_BAD_BLOCK = 1,   /* block id outside [0, num_blocks) */
+  GR_DEV_BAD_LENGTH = 2,  /* length beyond the block-table row capacity */
+  GR_DEV_BAD_PARENT = 4,  /* parent index outside [0, beam width) */
+  GR_DEV_SUFFIX_FULL = 8  /* append past the row capacity (token dropped) */
+};
+
+enum { GR_DTYPE_F32 = 0, GR_DTYPE_F16 = 1, GR_DTYPE_BF16 = 2 };
+
+/* Human-readable name of a status code (static storage). */
+const char* gr_status_string(gr_status_t status);
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int gr_version(void);
+/* Decode kernel selection for tests and measurement (no reference
+ * counterpart): 0 = automatic (matrix-core kernel where supported),
+ * 1 = always the generic kernel.  Process-wide. */
+gr_status_t gr_set_decode_kernel(int which);
+
+/*
+ * BeamAttention decode step.
+ *
+ * Replaces BeamAttentionImpl.cascade_attention
+ * (vllm_gr/v1/attention/backends/beam_attn.py:629-701): the flash-attention
+ * prefix pass (:656-678), the Triton suffix gather (:679-684, :62-117), the
+ * suffix pass (:686-695) and merge_attn_states (:697-699), as one launch.
+ *
+ * Request r owns prefix tokens [0, prefix_len[r]) of block-table row
+ * prefix_bt[r * prefix_bt_stride ...] and beams [beam_start[r],
+ * beam_start[r+1]).  Beam n owns suffix_len[n] suffix tokens; token j sits at
+ * logical position (suffix_start ? suffix_start[n] : 0) + j of row
+ * suffix_bt[n * suffix_bt_stride ...] (capacity suffix_bt_stride blocks).
+ * Each beam has q_per_beam query tokens: rows n*q_per_beam + i of q/out.
+ * Query i sees the whole prefix and suffix tokens j <= L - q_per_beam + i
+ * (bottom-right causal, the suffix pass's causal=True at :693).
+ * GQA: query head h reads KV head h / (num_q_heads / num_kv_heads) (:612).
+ * score = scale * q.k, soft-capped as softcap*tanh(score/softcap) when
+ * softcap > 0 (:607-609).  Rows with no visible key get output 0 and LSE
+ * -inf.  lse_out (nullable) receives the natural-log LSE as
+ * [num_beams*q_per_beam, num_q_heads] float32.
+ * q and out are [num_beams*q_per_beam, num_q_heads, head_dim] with token
+ * strides q_tok_stride / out_tok_stride; head_dim % 8 == 0, head_dim <= 256
+ * (BeamAttentionBackend.supports_head_size, :807-808).
+ */
+gr_status_t gr_beam_attn_decode(
+    void* out, int64_t out_tok_stride,
+    const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* prefix_bt, int prefix_bt_stride, const int32_t* prefix_len,
+    const int32_t* beam_start,
+    const int32_t* suffix_bt, int suffix_bt_stride, const int32_t* suffix_len,
+    const int32_t* suffix_start,
+    int num_reqs, int max_beams_per_req, int num_beams, int q_per_beam,
+    int num_q_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
+    float scale, float softcap, float* lse_out, int32_t* dev_status, hipStream_t stream);
+
+/*
+ * Scatter new K/V tokens into the paged cache by flat slot
+ * (slot = block * block_size + offset; slot < 0 is skipped).
+ *
+ * Replaces reshape_and_cache_flash as called by BeamAttentionImpl.forward
+ * (vllm_gr/v1/attention/backends/beam_attn.py:727-732).
+ * key/value: [num_tokens, num_kv_heads, head_dim], token stride in elements.
+ */
+gr_status_t gr_reshape_and_cache(
+    const void* key, int64_t key_tok_stride, const void* value, int64_t value_tok_stride,
+    void* k_cache, void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int64_t* slot_mapping, int num_tokens, int num_kv_heads, int head_dim,
+    int block_size, int dtype, int32_t* dev_status, hipStream_t stream);
+
+/*
+ * Beam KV fork, optionally fused with the append of one new token per beam.
+ *
+ * Replaces the reference's per-step suffix rebuild: _mega_request_step
+ * (vllm_gr/entrypoints/openai/serving_engine.py:107-120: child suffix =
+ * parent's tokens ++ chosen token), _handle_mega_request_step_update
+ * (vllm_gr/v1/engine/core.py:108-112) and the whole-prefix-block cache cap
+ * that forces the suffix to be recomputed
+ * (vllm_gr/v1/engine/engine_core_patch.py:245-252).
+ *
+ * parent [num_reqs, beam_width]: parent beam (within the request) of each
+ * child.  A parent's lowest-index child inherits its row in place; every
+ * other child takes, in ascending order, the row of the next childless
+ * parent of the same request (ascending), and receives a copy of the
+ * parent's suffix_len valid tokens.  Tables are written out of place:
+ * bt_out/len_out must not alias bt_in/len_in.  When k_new/v_new
+ * ([num_reqs*beam_width, num_kv_heads, head_dim]) are given, each child's
+ * token is appended at position len_out[c] and len_out[c] is incremented.
+ */
+gr_status_t gr_beam_kv_fork(
+    const int32_t* parent, int num_reqs, int beam_width,
+    const int32_t* bt_in, const int32_t* len_in, int32_t* bt_out, int32_t* len_out,
+    int bt_stride,
+    void* k_cache, void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const void* k_new, const void* v_new, int64_t new_tok_stride,
+    int num_kv_heads, int head_dim, int block_size, int dtype,
+    int32_t* dev_status, hipStream_t stream);
+
+/*
+ * Append one K/V token per beam at position suffix_len[n] of its row and
+ * increment suffix_len[n] (in place).  The reshape_and_cache_flash role
+ * (beam_attn.py:727-732) in block-table form.
+ */
+gr_status_t gr_beam_kv_append(
+    const void* k_new, const void* v_new, int64_t new_tok_stride,
+    void* k_cache, void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* suffix_bt, int bt_stride, int32_t* suffix_len, int num_beams,
+    int num_kv_heads, int head_dim, int block_size, int dtype,
+    int32_t* dev_status, hipStream_t stream);
+
+/*
+ * Fused beam pruning: log_softmax + cumulative logprob + top-k over
+ * beams x vocab, per request.
+ *
+ * Replaces the sampler's logprobs=W top-K (serving_engine.py:300-308) and the
+ * host pruning body (vllm_gr/entrypoints/openai/serving_engine.py:457-592;
+ * offline twin vllm_gr/entrypoints/llm.py:201-280).
+ *
+ * logits [num_reqs*beam_width, vocab] float32 (row stride logits_row_stride,
+ * vocab % 4 == 0, 16-byte aligned rows), cum [num_reqs*beam_width] float32.
+ * score(b, v) = (double)x + ((double)cum[b] - lse[b]), lse[b] = (double)m +
+ * log(S) with m the row max and S the float32 sum of exp(x - m), each term
+ * computed as exp2 of (x - m) * log2(e) by a degree-7 Taylor polynomial and
+ * summed in a fixed order (256 threads x float4 groups, then a xor
+ * butterfly per 64-lane wave, then (w0 + w1) + (w2 + w3)); the log is an
+ * atanh-series float64 evaluation.  All steps are single IEEE operations, so
+ * a CPU restatement reproduces every score bit for bit.
+ * Stage 1: each beam's top-k by (logit desc, token
+ * asc); a candidate equal to eos_token_id (>= 0) leaves the pool and its
+ * score goes to eos_score[b] (nullable; -inf when absent) -- the EOS split
+ * of :541-562.  Stage 2: top-k of the union by (score desc, flat index asc),
+ * flat = b * vocab + v.  Outputs [num_reqs, k]: parent beam, token, score
+ * (float32 of the float64 score); unfilled slots get -1, -1, -inf.
+ * Requires 1 <= k <= 1024 and k <= vocab.  workspace: device memory of
+ * gr_beam_prune_workspace_size() bytes, 256-byte aligned.
+ */
+size_t gr_beam_prune_workspace_size(int num_reqs, int beam_width, int vocab, int k);
+
+gr_status_t gr_beam_prune_topk(
+    const float* logits, int64_t logits_row_stride, const float* cum,
+    int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
+    int32_t* parent, int32_t* token, float* score, float* eos_score,
+    void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GR_BEAM_H_ */

@@ -1,0 +1,176 @@
+"""BeamAttention decode on the GPU vs the float64 oracle.
+
+Tolerances: float32 path <= 1e-5 max abs error vs the
+float64 oracle; bf16/fp16 <= 2e-2 max abs error.  Because N(0,1)/sqrt(128)
+inputs make every output tiny (|o| ~ 1e-2), bf16 cases are also checked
+relative to the output scale (<= 2e-2 * max|ref|) and on unscaled N(0,1)
+inputs where |o| ~ 0.1-1 and 2e-2 is a real bound.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from vllm_gr_amd import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _host(t):
+    return t.detach().cpu().to(torch.float64).numpy()
+
+
+def run_gpu(wl, device, kernel="auto"):
+    d = wl.to(device)
+    out = torch.empty_like(d.q)
+    lse = torch.empty((d.q.shape[0], d.q.shape[1]), dtype=torch.float32, device=device)
+    status = ops.new_status(device)
+    ops.set_decode_kernel(kernel)
+    try:
+        ops.beam_attn_decode(d.q, d.k_cache, d.v_cache, d.prefix_bt, d.prefix_len, d.beam_start,
+                             d.suffix_bt, d.suffix_len, q_per_beam=d.q_per_beam, scale=d.scale,
+                             softcap=d.softcap, max_beams_per_req=d.max_beams, out=out, lse=lse,
+                             status=status)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_decode_kernel("auto")
+    ops.check_status(status)
+    return _host(out), lse.cpu().numpy().astype(np.float64)
+
+
+def run_oracle(wl):
+    kv = wl.kv_cache.to(torch.float64).numpy()
+    return oa.beam_attention_cascade(
+        _host(wl.q), kv[0], kv[1], wl.prefix_bt.numpy(), wl.prefix_len.numpy(), wl.beam_start.numpy(),
+        wl.suffix_bt.numpy(), wl.suffix_len.numpy(), q_per_beam=wl.q_per_beam, scale=wl.scale,
+        softcap=wl.softcap, block_size=wl.block_size)
+
+
+def _check(out, lse, ref, ref_lse, atol, rel=None):
+    err = np.abs(out - ref).max()
+    assert err <= atol, f"max abs err {err:.3e} > {atol}"
+    if rel is not None:
+        scale = np.abs(ref).max()
+        assert err <= rel * scale, f"max abs err {err:.3e} > {rel} * max|ref| ({scale:.3e})"
+    fin = np.isfinite(ref_lse)
+    assert (np.isfinite(lse) == fin).all(), "LSE finiteness differs"
+    lerr = np.abs(lse[fin] - ref_lse[fin]).max() if fin.any() else 0.0
+    assert lerr <= max(atol, 1e-4), f"LSE err {lerr:.3e}"
+
+
+def test_decode_small_fp32(device):
+    """1 req x 32 beams, P=512, L=4, 16/4 heads, fp32: <= 1e-5 vs float64."""
+    wl = workloads.decode_small_fp32(seed=0)
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("kernel", ["auto", "generic"])
+def test_decode_unscaled_tail_tile(device, dtype, kernel):
+    """Prefix not a multiple of the 64-key tile, ragged suffixes, N(0,1) inputs."""
+    wl = workloads.make_decode(R=2, W=16, P=300, L=(1, 8), Hq=32, Hkv=8, D=128, dtype=dtype,
+                               input_scale=1.0, seed=1)
+    out, lse = run_gpu(wl, device, kernel)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2)
+
+
+@pytest.mark.parametrize("heads", [(4, 4), (8, 2), (16, 2), (32, 8)])
+@pytest.mark.parametrize("T", [1, 3])
+def test_decode_gqa_and_multi_query(device, heads, T):
+    """Reference grid heads (test_cascade_beam_flash_attn.py:33) and q_per_beam > 1
+    (bottom-right causal suffix)."""
+    Hq, Hkv = heads
+    wl = workloads.make_decode(R=3, W=8, P=200, L=(T, T + 5), Hq=Hq, Hkv=Hkv, D=128,
+                               dtype=torch.bfloat16, input_scale=1.0, seed=2 + T, q_per_beam=T)
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_decode_other_head_dims_generic(device, D):
+    """head_size 64 and 256 (reference HEAD_SIZES include 256) run the generic kernel."""
+    wl = workloads.make_decode(R=2, W=4, P=100, L=(1, 6), Hq=8, Hkv=2, D=D, dtype=torch.bfloat16,
+                               input_scale=1.0, seed=7)
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2)
+
+
+def test_decode_softcap(device):
+    wl = workloads.make_decode(R=2, W=8, P=130, L=(2, 6), Hq=16, Hkv=4, D=128, dtype=torch.bfloat16,
+                               input_scale=1.0, seed=9, softcap=50.0)
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2)
+
+
+def test_decode_block32(device):
+    wl = workloads.make_decode(R=2, W=8, P=100, L=(1, 20), Hq=16, Hkv=4, D=128, block_size=32,
+                               dtype=torch.bfloat16, input_scale=1.0, seed=11)
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2)
+
+
+@pytest.mark.parametrize("P,L", [(0, 5), (64, 0), (0, 0)])
+def test_decode_empty_sides(device, P, L):
+    """No shared prefix (reference case (8, 8, 8)), no suffix, and nothing at all."""
+    wl = workloads.make_decode(R=2, W=8, P=P, L=L, Hq=16, Hkv=4, D=128, dtype=torch.bfloat16,
+                               input_scale=1.0, seed=13)
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2)
+    if P == 0 and L == 0:
+        assert (out == 0).all() and np.isneginf(lse).all()
+
+
+def test_decode_beam128_full(device):
+    """8 requests x 128 beams x 2048 prefix, bf16, Q/K/V ~ N(0,1)/sqrt(128)."""
+    wl = workloads.decode_beam128(seed=0)
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2, rel=2e-2)
+
+
+def test_decode_mfma_matches_generic(device):
+    wl = workloads.make_decode(R=4, W=64, P=1000, L=(1, 8), Hq=32, Hkv=8, D=128,
+                               dtype=torch.bfloat16, input_scale=1.0, seed=21)
+    a, la = run_gpu(wl, device, "auto")
+    b, lb = run_gpu(wl, device, "generic")
+    assert np.abs(a - b).max() <= 2e-2
+    assert np.abs(la - lb).max() <= 1e-3
+
+
+def test_decode_uneven_beams_per_request(device):
+    """Requests with different beam counts in one launch (beam_start ragged)."""
+    wl = workloads.make_decode(R=3, W=40, P=150, L=(1, 4), Hq=16, Hkv=4, D=128,
+                               dtype=torch.bfloat16, input_scale=1.0, seed=23)
+    wl.beam_start = torch.tensor([0, 40, 47, 120], dtype=torch.int32)
+    wl.max_beams = 73
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2)
+
+
+def test_decode_deterministic(device):
+    wl = workloads.make_decode(R=2, W=32, P=500, L=(1, 8), Hq=32, Hkv=8, D=128,
+                               dtype=torch.bfloat16, seed=5)
+    a, _ = run_gpu(wl, device)
+    b, _ = run_gpu(wl, device)
+    assert np.array_equal(a, b)
+
+
+def test_decode_bad_block_flagged(device):
+    """An out-of-range block id is skipped and reported, never dereferenced."""
+    wl = workloads.make_decode(R=1, W=4, P=64, L=2, Hq=8, Hkv=2, D=128, dtype=torch.bfloat16, seed=3)
+    nb = wl.kv_cache.shape[1]
+    wl.prefix_bt[0, 1] = nb + 7
+    with pytest.raises(ValueError, match="block id out of range"):
+        run_gpu(wl, device)

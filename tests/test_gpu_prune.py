@@ -1,0 +1,70 @@
+"""Fused beam pruning on the GPU vs the bit-exact CPU oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import prune as op
+from vllm_gr_amd import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(wl, device, eos=-1):
+    d = wl.to(device)
+    parent, token, score, eos_score = ops.beam_prune_topk(d.logits, d.cum, wl.k, eos)
+    torch.cuda.synchronize()
+    return parent.cpu().numpy(), token.cpu().numpy(), score.cpu().numpy(), eos_score.cpu().numpy()
+
+
+def _assert_exact(got, want):
+    p, t, s, e = got
+    assert np.array_equal(p, want["parent"]), "parent beams differ"
+    assert np.array_equal(t, want["token"]), "tokens differ"
+    assert np.array_equal(s.view(np.int32), want["score"].view(np.int32)), "scores differ (bits)"
+    assert np.array_equal(e.view(np.int32), want["eos_score"].view(np.int32)), "eos scores differ"
+
+
+def test_prune_beam128_full(device):
+    """logits [64, 128, 8192] ~ N(0, 3^2), cum ~ U(-20, 0), top-128: bit-exact."""
+    wl = workloads.prune_beam128(seed=0)
+    _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), wl.k))
+
+
+@pytest.mark.parametrize("R,W,V,k", [(3, 16, 512, 16), (2, 4, 12288, 32), (1, 1, 64, 8), (2, 300, 256, 100)])
+def test_prune_shapes(device, R, W, V, k):
+    wl = workloads.make_prune(R=R, W=W, V=V, k=k, seed=R + W + V)
+    _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), k))
+
+
+def test_prune_all_equal_logits(device):
+    """Every score ties: the lowest flat indices (beam 0, tokens 0..k-1) win."""
+    wl = workloads.make_prune(R=2, W=8, V=1024, k=8, seed=1)
+    wl.logits.zero_()
+    wl.cum.zero_()
+    got = run_gpu(wl, device)
+    _assert_exact(got, op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), 8))
+    assert (got[0] == 0).all() and (got[1] == np.arange(8)).all()
+
+
+def test_prune_quantised_ties(device):
+    """Logits on a coarse grid: many exact ties inside and across rows."""
+    wl = workloads.make_prune(R=3, W=32, V=2048, k=32, seed=2)
+    wl.logits.copy_(torch.round(wl.logits))
+    wl.cum.copy_(torch.round(wl.cum))
+    _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), 32))
+
+
+def test_prune_with_eos(device):
+    wl = workloads.make_prune(R=4, W=16, V=1024, k=16, seed=3)
+    eos = 17
+    wl.logits[:, :, eos] += 8.0  # EOS lands in many rows' top-k
+    _assert_exact(run_gpu(wl, device, eos), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), 16, eos))
+
+
+def test_prune_masked_logits(device):
+    """-inf logits (masked tokens) and a fully masked beam."""
+    wl = workloads.make_prune(R=2, W=8, V=512, k=8, seed=4)
+    wl.logits[0, :, 100:] = float("-inf")
+    wl.logits[1, 3, :] = float("-inf")
+    _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), 8))

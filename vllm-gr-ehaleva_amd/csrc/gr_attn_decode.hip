@@ -1,0 +1,283 @@
+// BeamAttention decode for gfx950.
+//
+// One launch computes, for every beam's query rows, softmax attention over
+// [shared prefix ; own suffix] -- the work the reference spreads over a
+// flash-attention prefix pass, a Triton suffix gather, a suffix pass and an
+// LSE merge (vllm_gr/v1/attention/backends/beam_attn.py:629-701).
+//
+// Two kernels sit behind gr_beam_attn_decode:
+//  * decode_generic: any dtype (fp32/fp16/bf16), head_dim % 8 == 0 <= 256.
+//    One workgroup per (beam, KV head, 32-row chunk); fp32 VALU math.
+//  * the MFMA kernel in gr_attn_mfma.hip for bf16/fp16 at head_dim 128,
+//    which stages each request's prefix tile once in LDS for all its beams.
+#include "gr_common.h"
+#include "gr_attn_decode.h"
+
+namespace gr {
+
+constexpr int GEN_ROWS = 32;     // query rows per workgroup
+constexpr int GEN_TK = 32;       // keys per tile
+constexpr int GEN_THREADS = 256;
+constexpr int GEN_ACC = GEN_ROWS * 256 / GEN_THREADS;  // acc slots per thread at D=256
+
+__device__ inline int find_request(const int32_t* beam_start, int num_reqs, int n) {
+  // largest r with beam_start[r] <= n  (beam_start is non-decreasing)
+  int lo = 0, hi = num_reqs - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (beam_start[mid] <= n) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <int DT>
+__global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
+  using E = Elem<DT>;
+  using S = typename E::storage;
+  extern __shared__ float smem[];
+  const int D = a.D;
+  float* q_s = smem;                              // [ROWS][D]
+  float* k_s = q_s + GEN_ROWS * D;                // [TK][D+1]
+  float* v_s = k_s + GEN_TK * (D + 1);            // [TK][D]
+  float* p_s = v_s + GEN_TK * D;                  // [ROWS][TK+1]
+  float* m_s = p_s + GEN_ROWS * (GEN_TK + 1);     // [ROWS]
+  float* l_s = m_s + GEN_ROWS;                    // [ROWS]
+  float* a_s = l_s + GEN_ROWS;                    // [ROWS]
+  int* kv_ok = reinterpret_cast<int*>(a_s + GEN_ROWS);  // [TK]
+
+  const int G = a.Hq / a.Hkv;
+  const int rows_total = G * a.T;
+  const int chunks = (rows_total + GEN_ROWS - 1) / GEN_ROWS;
+  const int n = blockIdx.x / chunks;
+  const int chunk = blockIdx.x % chunks;
+  const int hk = blockIdx.y;
+  const int t = threadIdx.x;
+  if (n >= a.num_beams) return;
+  const int r = find_request(a.beam_start, a.num_reqs, n);
+  const int P = a.prefix_len[r];
+  const int L = a.suffix_len[n];
+  const int s0 = a.suffix_start ? a.suffix_start[n] : 0;
+  const int row0 = chunk * GEN_ROWS;
+  const int nrows = min(GEN_ROWS, rows_total - row0);
+  const int pre_cap = a.prefix_bt_stride * a.bs;
+  const int suf_cap = a.suffix_bt_stride * a.bs;
+  const int Pc = min(max(P, 0), pre_cap);
+  const int Lc = (L < 0 || s0 < 0 || s0 + L > suf_cap) ? 0 : L;
+  if (t == 0 && (Pc != P || Lc != L)) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+
+  const S* q = static_cast<const S*>(a.q);
+  const S* kc = static_cast<const S*>(a.k_cache);
+  const S* vc = static_cast<const S*>(a.v_cache);
+
+  for (int e = t; e < GEN_ROWS * D; e += GEN_THREADS) {
+    int row = e / D, d = e % D;
+    float v = 0.f;
+    if (row < nrows) {
+      int rho = row0 + row;
+      int qi = rho / G, g = rho % G;
+      v = E::to_float(q[(int64_t)(n * a.T + qi) * a.q_tok_stride + (int64_t)(hk * G + g) * D + d]);
+    }
+    q_s[e] = v;
+  }
+  if (t < GEN_ROWS) {
+    m_s[t] = -INFINITY;
+    l_s[t] = 0.f;
+  }
+  float acc[GEN_ACC];
+#pragma unroll
+  for (int i = 0; i < GEN_ACC; ++i) acc[i] = 0.f;
+
+  const int total = Pc + Lc;
+  for (int k0 = 0; k0 < total; k0 += GEN_TK) {
+    __syncthreads();
+    if (t < GEN_TK) {
+      int kk = k0 + t;
+      int ok = 0;
+      if (kk < total) {
+        int blk = kk < Pc ? a.prefix_bt[(int64_t)r * a.prefix_bt_stride + kk / a.bs]
+                          : a.suffix_bt[(int64_t)n * a.suffix_bt_stride + (s0 + kk - Pc) / a.bs];
+        ok = (blk >= 0 && blk < a.num_blocks);
+        if (!ok) flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
+      }
+      kv_ok[t] = ok;
+    }
+    __syncthreads();
+    for (int e = t; e < GEN_TK * D; e += GEN_THREADS) {
+      int key = e / D, d = e % D;
+      int kk = k0 + key;
+      float kv = 0.f, vv = 0.f;
+      if (kv_ok[key]) {
+        int blk, off;
+        if (kk < Pc) {
+          blk = a.prefix_bt[(int64_t)r * a.prefix_bt_stride + kk / a.bs];
+          off = kk % a.bs;
+        } else {
+          int pos = s0 + kk - Pc;
+          blk = a.suffix_bt[(int64_t)n * a.suffix_bt_stride + pos / a.bs];
+          off = pos % a.bs;
+        }
+        int64_t o = (int64_t)blk * a.kv_block_stride + (int64_t)off * a.kv_tok_stride +
+                    (int64_t)hk * a.kv_head_stride + d;
+        kv = E::to_float(kc[o]);
+        vv = E::to_float(vc[o]);
+      }
+      k_s[key * (D + 1) + d] = kv;
+      v_s[key * D + d] = vv;
+    }
+    __syncthreads();
+    {
+      const int key = t % GEN_TK;
+      const int kk = k0 + key;
+      for (int row = t / GEN_TK; row < GEN_ROWS; row += GEN_THREADS / GEN_TK) {
+        float s = 0.f;
+        for (int d = 0; d < D; ++d) s += q_s[row * D + d] * k_s[key * (D + 1) + d];
+        s *= a.scale;
+        if (a.softcap > 0.f) s = a.softcap * tanhf(s / a.softcap);
+        bool vis = row < nrows && kk < total && kv_ok[key];
+        if (vis && kk >= Pc) {
+          int qi = (row0 + row) / G;
+          vis = (kk - Pc) <= Lc - a.T + qi;
+        }
+        p_s[row * (GEN_TK + 1) + key] = vis ? s : -INFINITY;
+      }
+    }
+    __syncthreads();
+    if (t < GEN_ROWS) {
+      float mt = -INFINITY;
+      for (int key = 0; key < GEN_TK; ++key) mt = fmaxf(mt, p_s[t * (GEN_TK + 1) + key]);
+      float m_old = m_s[t];
+      float m_new = fmaxf(m_old, mt);
+      float alpha = 1.f, lsum = 0.f;
+      if (m_new != -INFINITY) {
+        alpha = expf(m_old - m_new);
+        for (int key = 0; key < GEN_TK; ++key) {
+          float s = p_s[t * (GEN_TK + 1) + key];
+          float p = (s == -INFINITY) ? 0.f : expf(s - m_new);
+          p_s[t * (GEN_TK + 1) + key] = p;
+          lsum += p;
+        }
+      } else {
+        for (int key = 0; key < GEN_TK; ++key) p_s[t * (GEN_TK + 1) + key] = 0.f;
+      }
+      m_s[t] = m_new;
+      l_s[t] = l_s[t] * alpha + lsum;
+      a_s[t] = alpha;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < GEN_ACC; ++i) {
+      int e = t + i * GEN_THREADS;
+      if (e < GEN_ROWS * D) {
+        int row = e / D, d = e % D;
+        float o = acc[i] * a_s[row];
+        for (int key = 0; key < GEN_TK; ++key) o += p_s[row * (GEN_TK + 1) + key] * v_s[key * D + d];
+        acc[i] = o;
+      }
+    }
+  }
+  __syncthreads();
+  S* out = static_cast<S*>(a.out);
+#pragma unroll
+  for (int i = 0; i < GEN_ACC; ++i) {
+    int e = t + i * GEN_THREADS;
+    if (e < GEN_ROWS * D) {
+      int row = e / D, d = e % D;
+      if (row < nrows) {
+        int rho = row0 + row;
+        int qi = rho / G, g = rho % G;
+        float l = l_s[row];
+        float o = l > 0.f ? acc[i] / l : 0.f;
+        out[(int64_t)(n * a.T + qi) * a.out_tok_stride + (int64_t)(hk * G + g) * D + d] = E::from_float(o);
+      }
+    }
+  }
+  if (a.lse_out && t < nrows) {
+    int rho = row0 + t;
+    int qi = rho / G, g = rho % G;
+    float l = l_s[t];
+    a.lse_out[(int64_t)(n * a.T + qi) * a.Hq + hk * G + g] = l > 0.f ? m_s[t] + logf(l) : -INFINITY;
+  }
+}
+
+static size_t generic_smem_bytes(int D) {
+  return sizeof(float) * ((size_t)GEN_ROWS * D + GEN_TK * (D + 1) + GEN_TK * D +
+                          GEN_ROWS * (GEN_TK + 1) + 3 * GEN_ROWS) + sizeof(int) * GEN_TK;
+}
+
+int g_decode_kernel_override = 0;
+
+static gr_status_t launch_generic(const DecodeArgs& a, hipStream_t stream) {
+  const int G = a.Hq / a.Hkv;
+  const int chunks = (G * a.T + GEN_ROWS - 1) / GEN_ROWS;
+  dim3 grid((unsigned)((int64_t)a.num_beams * chunks), (unsigned)a.Hkv);
+  size_t smem = generic_smem_bytes(a.D);
+  static bool attr_done[3] = {false, false, false};
+  if (!attr_done[a.dtype]) {  // head_dim 256 needs more than the default 64 KB
+    const void* fn = a.dtype == GR_DTYPE_F32 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F32>)
+                     : a.dtype == GR_DTYPE_F16 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F16>)
+                                               : reinterpret_cast<const void*>(decode_generic<GR_DTYPE_BF16>);
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)generic_smem_bytes(256));
+    attr_done[a.dtype] = true;
+  }
+  switch (a.dtype) {
+    case GR_DTYPE_F32:
+      hipLaunchKernelGGL(decode_generic<GR_DTYPE_F32>, grid, dim3(GEN_THREADS), smem, stream, a);
+      break;
+    case GR_DTYPE_F16:
+      hipLaunchKernelGGL(decode_generic<GR_DTYPE_F16>, grid, dim3(GEN_THREADS), smem, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL(decode_generic<GR_DTYPE_BF16>, grid, dim3(GEN_THREADS), smem, stream, a);
+      break;
+  }
+  return launch_status();
+}
+
+}  // namespace gr
+
+using namespace gr;
+
+extern "C" gr_status_t gr_beam_attn_decode(
+    void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* prefix_bt, int prefix_bt_stride, const int32_t* prefix_len,
+    const int32_t* beam_start, const int32_t* suffix_bt, int suffix_bt_stride,
+    const int32_t* suffix_len, const int32_t* suffix_start, int num_reqs, int max_beams_per_req,
+    int num_beams, int q_per_beam, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
+    hipStream_t stream) {
+  if (num_beams < 0 || num_reqs < 0 || q_per_beam < 1 || num_q_heads < 1 || num_kv_heads < 1 ||
+      num_q_heads % num_kv_heads != 0 || block_size < 1 || head_dim < 8 || head_dim % 8 != 0 ||
+      num_blocks < 0 || prefix_bt_stride < 0 || suffix_bt_stride < 0 || max_beams_per_req < 0 ||
+      !dtype_valid(dtype) || !(softcap >= 0.f))
+    return GR_ERR_INVALID_ARG;
+  if (head_dim > 256) return GR_ERR_UNSUPPORTED;
+  if (num_beams == 0) return GR_OK;
+  if (num_reqs == 0 || !out || !q || !k_cache || !v_cache || !prefix_bt || !prefix_len ||
+      !beam_start || !suffix_bt || !suffix_len)
+    return GR_ERR_INVALID_ARG;
+  if (q_tok_stride < (int64_t)num_q_heads * head_dim || out_tok_stride < (int64_t)num_q_heads * head_dim ||
+      kv_block_stride < 1 || kv_tok_stride < 1 || kv_head_stride < 1)
+    return GR_ERR_INVALID_ARG;
+  DecodeArgs a;
+  a.out = out; a.out_tok_stride = out_tok_stride;
+  a.q = q; a.q_tok_stride = q_tok_stride;
+  a.k_cache = k_cache; a.v_cache = v_cache; a.num_blocks = num_blocks;
+  a.kv_block_stride = kv_block_stride; a.kv_tok_stride = kv_tok_stride; a.kv_head_stride = kv_head_stride;
+  a.prefix_bt = prefix_bt; a.prefix_bt_stride = prefix_bt_stride; a.prefix_len = prefix_len;
+  a.beam_start = beam_start;
+  a.suffix_bt = suffix_bt; a.suffix_bt_stride = suffix_bt_stride; a.suffix_len = suffix_len;
+  a.suffix_start = suffix_start;
+  a.num_reqs = num_reqs; a.max_beams = max_beams_per_req; a.num_beams = num_beams; a.T = q_per_beam;
+  a.Hq = num_q_heads; a.Hkv = num_kv_heads; a.D = head_dim; a.bs = block_size; a.dtype = dtype;
+  a.scale = scale; a.softcap = softcap; a.lse_out = lse_out; a.dev_status = dev_status;
+  if (g_decode_kernel_override == 0 && mfma_decode_supported(a)) return launch_mfma_decode(a, stream);
+  return launch_generic(a, stream);
+}
+
+extern "C" int gr_set_decode_kernel(int which) {
+  if (which < 0 || which > 1) return GR_ERR_INVALID_ARG;
+  g_decode_kernel_override = which;
+  return GR_OK;
+}

@@ -1,0 +1,525 @@
+// BeamAttention decode on gfx950 matrix cores (bf16/fp16, head_dim 128).
+//
+// Work decomposition.  For request r and KV head h the query rows of all its
+// beams form one dense M x 128 matrix (M = beams * q_per_beam * GQA group):
+// the shared prefix contraction is a plain GEMM-shaped problem, which is why
+// it runs on MFMA.  A workgroup owns 128 of those rows (4 waves: 2 row groups
+// of 64 rows x 2 key halves) and streams the request's prefix K/V through
+// LDS in 64-key super-tiles, each loaded once from HBM for all 128 rows.
+// Workgroups that share (r, h) are placed on the same XCD (blockIdx % 8 is
+// the XCD under round-robin dispatch) so their prefix re-reads hit that
+// XCD's L2.  Each beam's short suffix is read from its own paged blocks into
+// masked 32-key tiles after the prefix, with the same online softmax; the two
+// key halves are merged in LDS at the end.  One launch, no gather/merge
+// passes over HBM (contrast beam_attn.py:656-699).
+//
+// MFMA formulation (v_mfma_f32_32x32x16_{bf16,f16}, wave64):
+//   S^T[key][row]  = K[key][:] . Q[row][:]    A = K tile, B = Q^T (registers)
+//   O^T[d][row]   += V^T[d][key] . P^T[key][row]
+// so every lane owns one query row (lane % 32) in both accumulators and the
+// online softmax needs no cross-lane traffic except the lane-pair (l, l^32)
+// max/sum.  K rows are fed to the A operand through the permutation PI that
+// swaps bits 2 and 3 of the row index; with it the S^T accumulator registers
+// of each lane hold keys in exactly the order the PV B operand needs, and
+// V^T is read from LDS as plain 16-byte rows.
+#include "gr_attn_decode.h"
+
+namespace gr {
+namespace {
+
+constexpr int MF_THREADS = 256;
+constexpr int MF_ROWS = 128;   // query rows per workgroup
+constexpr int ST_KEYS = 64;    // keys per super-tile (two 32-key halves)
+constexpr int HD = 128;        // head dim
+constexpr int KS_PITCH = 136;  // K tile row pitch in elements (272 B)
+constexpr int VT_PITCH = 72;   // V^T tile row pitch in elements (144 B)
+constexpr int K_TILE = ST_KEYS * KS_PITCH;
+constexpr int VT_TILE = HD * VT_PITCH;
+constexpr int BUF = K_TILE + VT_TILE;  // elements per buffer
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float RESCALE_THRESH = 8.0f;  // log2 units: rescale O only when the max grows by > 2^8
+
+typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
+typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
+typedef uint32_t u32x4_t __attribute__((__vector_size__(4 * sizeof(uint32_t))));
+typedef uint32_t u32x2_t __attribute__((__vector_size__(2 * sizeof(uint32_t))));
+
+template <int DT> struct Mma;
+template <> struct Mma<GR_DTYPE_BF16> {
+  using vec = bf16x8_t;
+  __device__ static inline f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(vec, a),
+                                                   __builtin_bit_cast(vec, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+  }
+};
+template <> struct Mma<GR_DTYPE_F16> {
+  using vec = f16x8_t;
+  __device__ static inline f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(vec, a),
+                                                  __builtin_bit_cast(vec, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+  }
+};
+
+// S^T row slot i holds tile key PI(i): bits 2 and 3 swapped.
+__device__ inline int key_perm(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+// max / sum over the lane pair (l, l ^ 32) that shares a query row
+__device__ inline float pair_max(float x) {
+  auto v = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                            __builtin_bit_cast(uint32_t, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, v[0]), __builtin_bit_cast(float, v[1]));
+}
+__device__ inline float pair_sum(float x) {
+  auto v = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                            __builtin_bit_cast(uint32_t, x), false, false);
+  return __builtin_bit_cast(float, v[0]) + __builtin_bit_cast(float, v[1]);
+}
+
+__device__ inline u32x4_t lds_read16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+
+// Per-lane online-softmax state for one 32-row block.
+struct RowState {
+  float m;     // running max in scaled log2 units (-inf before any visible key)
+  float lsum;  // this lane's partial sum of exp2(x - m)
+};
+
+// Softmax of one 32-key x 32-row S^T tile held by this lane (16 keys of its
+// row).  vis: bit r set when register r is a visible key.  Returns the
+// rescale factor for O (1 when unchanged) and writes the packed P operand.
+template <int DT, bool SOFTCAP>
+__device__ inline float softmax_tile(f32x16_t& s, uint32_t vis, RowState& st, float c,
+                                     float cap, u32x4_t& p0, u32x4_t& p1) {
+  float x[16];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float v = s[r];
+    if (SOFTCAP) v = cap * tanhf(v * c);  // c = scale / softcap here; x in log2 units below
+    v = (vis >> r) & 1 ? v : -INFINITY;
+    x[r] = v;
+    mx = fmaxf(mx, v);
+  }
+  mx = pair_max(mx);
+  // scaled log2-domain maximum of this tile
+  const float cs = SOFTCAP ? LOG2E : c;
+  const float tmax = mx * cs;  // -inf stays -inf (cs > 0)
+  float alpha = 1.f;
+  if (tmax > st.m + RESCALE_THRESH || (st.m == -INFINITY && tmax != -INFINITY)) {
+    alpha = (st.m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(st.m - tmax);
+    st.m = tmax;
+    st.lsum *= alpha;
+  }
+  const float mref = st.m == -INFINITY ? 0.f : st.m;
+  float p[16];
+  float acc = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    p[r] = __builtin_amdgcn_exp2f(fmaf(x[r], cs, -mref));
+    acc += p[r];
+  }
+  st.lsum += acc;
+  using M = Mma<DT>;
+  p0 = u32x4_t{M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]), M::pack2(p[6], p[7])};
+  p1 = u32x4_t{M::pack2(p[8], p[9]), M::pack2(p[10], p[11]), M::pack2(p[12], p[13]),
+               M::pack2(p[14], p[15])};
+  return alpha;
+}
+
+// One wave: 2 row blocks (64 rows) against one 32-key half-tile in LDS.
+// kbase: first K_s row of the half; vt_col: first V^T column of the half.
+template <int DT, bool SOFTCAP>
+__device__ inline void tile_step(const uint16_t* buf, int kbase, int lane, const u32x4_t (&qf)[2][8],
+                                 f32x16_t (&o)[2][4], RowState (&st)[2], const uint32_t (&vis)[2],
+                                 float c, float cap) {
+  using M = Mma<DT>;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const uint16_t* krow = buf + (kbase + key_perm(lrow)) * KS_PITCH + lhalf * 8;
+  f32x16_t s0 = {}, s1 = {};
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    u32x4_t kf = lds_read16(krow + kk * 16);
+    s0 = M::mma(kf, qf[0][kk], s0);
+    s1 = M::mma(kf, qf[1][kk], s1);
+  }
+  u32x4_t p[2][2];
+  float al0 = softmax_tile<DT, SOFTCAP>(s0, vis[0], st[0], c, cap, p[0][0], p[0][1]);
+  float al1 = softmax_tile<DT, SOFTCAP>(s1, vis[1], st[1], c, cap, p[1][0], p[1][1]);
+  if (__ballot(al0 != 1.f || al1 != 1.f) != 0) {  // wave-uniform: rare after the first tiles
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      o[0][mb] *= al0;
+      o[1][mb] *= al1;
+    }
+  }
+  const uint16_t* vt = buf + K_TILE + lrow * VT_PITCH + kbase + lhalf * 8;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      u32x4_t vf = lds_read16(vt + mb * 32 * VT_PITCH + kk * 16);
+      o[0][mb] = M::mma(vf, p[0][kk], o[0][mb]);
+      o[1][mb] = M::mma(vf, p[1][kk], o[1][mb]);
+    }
+  }
+}
+
+// Visibility bits of the 16 registers of a lane from a 32-bit key mask of
+// the half-tile (bit k = tile key k visible): register r holds key
+// 16*(r>>3) + 8*lhalf + (r&7).
+__device__ inline uint32_t regs_from_keymask(uint32_t km, int lhalf) {
+  return ((km >> (8 * lhalf)) & 0xFFu) | (((km >> (16 + 8 * lhalf)) & 0xFFu) << 8);
+}
+
+struct Geo {
+  int r, hk, nb0, W, G, TG, rows_r, row_base;
+};
+
+template <int DT, bool SOFTCAP>
+__global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF];
+  __shared__ uint32_t tile_mask[2][2];   // [buffer][half]: visible keys of the prefix super-tile
+  __shared__ int suf_cum[2][66];         // per row group: cumulative suffix lengths of its beams
+  __shared__ int suf_info[2][ST_KEYS];   // per row group slot: (beam << 16) | j, or -1
+
+  // ---- XCD-aware tile placement --------------------------------------------
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, local = bid >> 3;
+  const int unit = (local / mtiles) * 8 + xcd;
+  const int mt = local % mtiles;
+  if (unit >= units) return;
+  Geo g;
+  g.r = unit / a.Hkv;
+  g.hk = unit % a.Hkv;
+  g.nb0 = a.beam_start[g.r];
+  g.W = a.beam_start[g.r + 1] - g.nb0;
+  g.G = a.Hq / a.Hkv;
+  g.TG = a.T * g.G;
+  g.rows_r = g.W * g.TG;
+  g.row_base = mt * MF_ROWS;
+  if (g.row_base >= g.rows_r) return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int rg = wave >> 1, ks = wave & 1;  // row group, key half
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  using S = uint16_t;
+  const S* qp = static_cast<const S*>(a.q);
+  const S* kc = static_cast<const S*>(a.k_cache);
+  const S* vc = static_cast<const S*>(a.v_cache);
+  const int64_t head_off = (int64_t)g.hk * a.kv_head_stride;
+
+  // ---- Q fragments (B operand of S^T): row = lane % 32 of each block ----
+  u32x4_t qf[2][8];
+  int my_rho[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int rho = g.row_base + rg * 64 + rb * 32 + lrow;
+    my_rho[rb] = rho;
+    if (rho < g.rows_r) {
+      const int b = rho / g.TG, qi = (rho / g.G) % a.T, gq = rho % g.G;
+      const S* src = qp + (int64_t)((g.nb0 + b) * a.T + qi) * a.q_tok_stride +
+                     (int64_t)(g.hk * g.G + gq) * HD + lhalf * 8;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) qf[rb][kk] = *reinterpret_cast<const u32x4_t*>(src + kk * 16);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) qf[rb][kk] = u32x4_t{0, 0, 0, 0};
+    }
+  }
+  const float c = SOFTCAP ? a.scale / a.softcap : a.scale * LOG2E;
+  const float cap = a.softcap;
+
+  f32x16_t o[2][4];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) o[rb][mb] = f32x16_t{};
+  RowState st[2] = {{-INFINITY, 0.f}, {-INFINITY, 0.f}};
+
+  // ---- prefix: 64-key super-tiles, double-buffered through LDS ------------
+  const int pre_cap = a.prefix_bt_stride * a.bs;
+  int P = a.prefix_len[g.r];
+  if (P < 0 || P > pre_cap) {
+    if (tid == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+    P = P < 0 ? 0 : pre_cap;
+  }
+  const int32_t* pbt = a.prefix_bt + (int64_t)g.r * a.prefix_bt_stride;
+  const int n_st = (P + ST_KEYS - 1) / ST_KEYS;
+
+  // loader roles: K rows key = (tid>>4) + 16j, 16-byte chunk tid&15;
+  //               V rows 4*(tid>>4) .. +3 for chunk tid&15 (written transposed)
+  const int lk = tid >> 4, lc = tid & 15;
+  u32x4_t kreg[4], vreg[4];
+  auto block_of = [&](int key, bool& ok) -> int64_t {
+    int blk = pbt[key / a.bs];
+    ok = blk >= 0 && blk < a.num_blocks;
+    if (!ok) flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
+    return (int64_t)blk * a.kv_block_stride + (int64_t)(key % a.bs) * a.kv_tok_stride;
+  };
+  auto load_prefix = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = k0 + lk + 16 * j;
+      bool ok = false;
+      int64_t base = key < P ? block_of(key, ok) : 0;
+      kreg[j] = ok ? *reinterpret_cast<const u32x4_t*>(kc + base + head_off + lc * 8) : u32x4_t{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = k0 + 4 * lk + j;
+      bool ok = false;
+      int64_t base = key < P ? block_of(key, ok) : 0;
+      vreg[j] = ok ? *reinterpret_cast<const u32x4_t*>(vc + base + head_off + lc * 8) : u32x4_t{0, 0, 0, 0};
+    }
+  };
+  auto store_tile = [&](uint16_t* buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4_t*>(buf + (lk + 16 * j) * KS_PITCH + lc * 8) = kreg[j];
+    // transpose 4 keys x 8 dims -> 8 dims x 4 keys (8-byte writes)
+    uint16_t* vt = buf + K_TILE + (lc * 8) * VT_PITCH + 4 * lk;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t a0 = vreg[0][w], a1 = vreg[1][w], a2 = vreg[2][w], a3 = vreg[3][w];
+      // dim 2w of keys (0,1),(2,3) and dim 2w+1 of the same keys
+      const u32x2_t lo = {(a0 & 0xFFFFu) | (a1 << 16), (a2 & 0xFFFFu) | (a3 << 16)};
+      const u32x2_t hi = {(a0 >> 16) | (a1 & 0xFFFF0000u), (a2 >> 16) | (a3 & 0xFFFF0000u)};
+      *reinterpret_cast<u32x2_t*>(vt + (2 * w) * VT_PITCH) = lo;
+      *reinterpret_cast<u32x2_t*>(vt + (2 * w + 1) * VT_PITCH) = hi;
+    }
+  };
+  auto store_mask = [&](int bsel, int k0) {
+    if (wave == 0) {
+      const int key = k0 + lane;
+      bool ok = false;
+      if (key < P) {
+        int blk = pbt[key / a.bs];
+        ok = blk >= 0 && blk < a.num_blocks;
+      }
+      uint64_t m = __ballot(ok);
+      if (lane == 0) {
+        tile_mask[bsel][0] = (uint32_t)m;
+        tile_mask[bsel][1] = (uint32_t)(m >> 32);
+      }
+    }
+  };
+
+  if (n_st > 0) {
+    load_prefix(0);
+    store_tile(lds);
+    store_mask(0, 0);
+  }
+  __syncthreads();
+  for (int it = 0; it < n_st; ++it) {
+    const int cur = it & 1;
+    const bool more = it + 1 < n_st;
+    if (more) load_prefix((it + 1) * ST_KEYS);
+    const uint16_t* buf = lds + cur * BUF;
+    const uint32_t km = tile_mask[cur][ks];
+    const uint32_t vreg_bits = regs_from_keymask(km, lhalf);
+    const uint32_t vis[2] = {vreg_bits, vreg_bits};
+    tile_step<DT, SOFTCAP>(buf, ks * 32, lane, qf, o, st, vis, c, cap);
+    if (more) {
+      store_tile(lds + (cur ^ 1) * BUF);
+      store_mask(cur ^ 1, (it + 1) * ST_KEYS);
+    }
+    __syncthreads();
+  }
+
+  // ---- suffix: each row group's beams' own tokens, masked 32-key tiles ----
+  // beams touching row group rg: [b_lo, b_hi]
+  const int suf_cap = a.suffix_bt_stride * a.bs;
+  if (ks == 0) {
+    const int rlo = g.row_base + rg * 64;
+    const int b_lo = rlo / g.TG;
+    const int b_hi = min((rlo + 63) / g.TG, g.W - 1);
+    const int nbeams = rlo < g.rows_r ? b_hi - b_lo + 1 : 0;
+    int len = 0;
+    if (lane < nbeams) {
+      const int n = g.nb0 + b_lo + lane;
+      const int L = a.suffix_len[n];
+      const int s0 = a.suffix_start ? a.suffix_start[n] : 0;
+      len = (L < 0 || s0 < 0 || s0 + L > suf_cap) ? 0 : L;
+      if (len != L) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+    }
+    // inclusive wave scan
+    int incl = len;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    suf_cum[rg][lane + 1] = incl;
+    if (lane == 0) {
+      suf_cum[rg][0] = 0;
+      suf_cum[rg][65] = b_lo;  // stash: first beam of the group
+    }
+  }
+  __syncthreads();
+  const int tot0 = suf_cum[0][64], tot1 = suf_cum[1][64];
+  const int n_sit = (max(tot0, tot1) + ST_KEYS - 1) / ST_KEYS;
+  for (int it = 0; it < n_sit; ++it) {
+    // loader: 2 row groups x 64 slots x 16 chunks for K and for V
+    for (int e = tid; e < 2 * ST_KEYS * 16; e += MF_THREADS) {
+      const int grp = e / (ST_KEYS * 16);
+      const int slot = (e / 16) % ST_KEYS;
+      const int ch = e % 16;
+      const int gs = it * ST_KEYS + slot;
+      const int tot = suf_cum[grp][64];
+      u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+      int info = -1;
+      if (gs < tot) {
+        int lo = 0, hi = 63;  // largest beam index i with cum[i] <= gs
+        while (lo < hi) {
+          int mid = (lo + hi + 1) >> 1;
+          if (suf_cum[grp][mid] <= gs) lo = mid; else hi = mid - 1;
+        }
+        const int b = suf_cum[grp][65] + lo;
+        const int j = gs - suf_cum[grp][lo];
+        const int n = g.nb0 + b;
+        const int pos = (a.suffix_start ? a.suffix_start[n] : 0) + j;
+        const int blk = a.suffix_bt[(int64_t)n * a.suffix_bt_stride + pos / a.bs];
+        if (blk >= 0 && blk < a.num_blocks) {
+          const int64_t base = (int64_t)blk * a.kv_block_stride + (int64_t)(pos % a.bs) * a.kv_tok_stride +
+                               head_off + ch * 8;
+          kv = *reinterpret_cast<const u32x4_t*>(kc + base);
+          vv = *reinterpret_cast<const u32x4_t*>(vc + base);
+          info = (b << 16) | j;
+        } else {
+          flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
+        }
+      }
+      uint16_t* buf = lds + grp * BUF;
+      *reinterpret_cast<u32x4_t*>(buf + slot * KS_PITCH + ch * 8) = kv;
+      uint16_t* vt = buf + K_TILE + (ch * 8) * VT_PITCH + slot;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        vt[(2 * w) * VT_PITCH] = (uint16_t)(vv[w] & 0xFFFFu);
+        vt[(2 * w + 1) * VT_PITCH] = (uint16_t)(vv[w] >> 16);
+      }
+      if (ch == 0) suf_info[grp][slot] = info;
+    }
+    __syncthreads();
+    // visibility: register r of this lane is key 16*(r>>3) + 8*lhalf + (r&7) of half ks
+    uint32_t vis[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int rho = my_rho[rb];
+      const int b = rho / g.TG, qi = (rho / g.G) % a.T;
+      int lim = -1;
+      if (rho < g.rows_r) {
+        const int n = g.nb0 + b;
+        lim = a.suffix_len[n] - a.T + qi;
+      }
+      uint32_t bits = 0;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = ks * 32 + 16 * (r >> 3) + 8 * lhalf + (r & 7);
+        const int info = suf_info[rg][key];
+        const bool ok = info >= 0 && (info >> 16) == b && (info & 0xFFFF) <= lim;
+        bits |= (ok ? 1u : 0u) << r;
+      }
+      vis[rb] = bits;
+    }
+    tile_step<DT, SOFTCAP>(lds + rg * BUF, ks * 32, lane, qf, o, st, vis, c, cap);
+    __syncthreads();
+  }
+
+  // ---- merge the two key halves and write O, LSE --------------------------
+  float* xch = reinterpret_cast<float*>(lds);  // [rg][rb*4+mb][16][64] + m/l
+  float* xo = xch + rg * (2 * 4 * 16 * 64);
+  float* xm = reinterpret_cast<float*>(lds) + 2 * (2 * 4 * 16 * 64) + rg * (4 * 64);
+  if (ks == 1) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xo[((rb * 4 + mb) * 16 + r) * 64 + lane] = o[rb][mb][r];
+      xm[rb * 64 + lane] = st[rb].m;
+      xm[(2 + rb) * 64 + lane] = st[rb].lsum;
+    }
+  }
+  __syncthreads();
+  if (ks == 0) {
+    S* outp = static_cast<S*>(a.out);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const float m1 = xm[rb * 64 + lane], l1 = xm[(2 + rb) * 64 + lane];
+      const float m0 = st[rb].m, l0 = st[rb].lsum;
+      const float m = fmaxf(m0, m1);
+      const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
+      const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+      const float lrow_sum = pair_sum(l0 * a0 + l1 * a1);
+      const float inv = lrow_sum > 0.f ? 1.f / lrow_sum : 0.f;
+      const int rho = my_rho[rb];
+      if (rho < g.rows_r) {
+        const int b = rho / g.TG, qi = (rho / g.G) % a.T, gq = rho % g.G;
+        const int64_t tok = (int64_t)(g.nb0 + b) * a.T + qi;
+        S* dst = outp + tok * a.out_tok_stride + (int64_t)(g.hk * g.G + gq) * HD + 4 * lhalf;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int r = qd * 4 + u;
+              v[u] = (o[rb][mb][r] * a0 + xo[((rb * 4 + mb) * 16 + r) * 64 + lane] * a1) * inv;
+            }
+            const u32x2_t w = {Mma<DT>::pack2(v[0], v[1]), Mma<DT>::pack2(v[2], v[3])};
+            *reinterpret_cast<u32x2_t*>(dst + mb * 32 + qd * 8) = w;
+          }
+        }
+        if (a.lse_out && lhalf == 0) {
+          a.lse_out[tok * a.Hq + g.hk * g.G + gq] =
+              lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+bool mfma_decode_supported(const DecodeArgs& a) {
+  if (a.D != HD || (a.dtype != GR_DTYPE_BF16 && a.dtype != GR_DTYPE_F16)) return false;
+  // 16-byte vector access: base pointers and element strides multiples of 8 elements
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (!al(a.q) || !al(a.out) || !al(a.k_cache) || !al(a.v_cache)) return false;
+  if (a.q_tok_stride % 8 || a.out_tok_stride % 8 || a.kv_block_stride % 8 || a.kv_tok_stride % 8 ||
+      a.kv_head_stride % 8)
+    return false;
+  return true;
+}
+
+gr_status_t launch_mfma_decode(const DecodeArgs& a, hipStream_t stream) {
+  const int G = a.Hq / a.Hkv;
+  const int64_t rows = (int64_t)a.max_beams * a.T * G;
+  const int mtiles = (int)((rows + MF_ROWS - 1) / MF_ROWS);
+  const int units = a.num_reqs * a.Hkv;
+  if (mtiles == 0 || units == 0) return GR_OK;
+  const int64_t nwg = (int64_t)((units + 7) / 8) * 8 * mtiles;
+  if (nwg > 0x7fffffff) return GR_ERR_INVALID_ARG;
+  dim3 grid((unsigned)nwg);
+  const bool cap = a.softcap > 0.f;
+  if (a.dtype == GR_DTYPE_BF16) {
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+  } else {
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+  }
+  return launch_status();
+}
+
+}  // namespace gr

@@ -1,0 +1,352 @@
+// Beam KV fork / append and slot scatter for gfx950.
+//
+// All three kernels move K/V rows of head_dim elements in 16-byte vectors;
+// they are pure HBM copy work (no arithmetic), so the design goal is wide
+// coalesced accesses and no serialisation:
+//  * beam_fork: one workgroup per (request, group of children).  Every
+//    workgroup recomputes its request's row assignment from the read-only
+//    input tables (a few hundred integer ops), so there is no inter-workgroup
+//    dependency and no atomics on the tables; the new tables are written out
+//    of place.  Copy-on-write destinations are rows of childless parents,
+//    which nobody reads, and in-place appends write positions past every
+//    copied range, so the single launch is race-free.
+//  * beam_append / reshape_and_cache: one wave per beam / token.
+#include "gr_common.h"
+
+namespace gr {
+namespace {
+
+typedef uint32_t u32x4_t __attribute__((__vector_size__(4 * sizeof(uint32_t))));
+
+constexpr int FORK_THREADS = 256;
+constexpr int FORK_CHILDREN_PER_WG = 4;
+constexpr int FORK_MAX_W = 1024;
+
+struct KvGeom {
+  void* k_cache;
+  void* v_cache;
+  int64_t num_blocks, block_stride, tok_stride, head_stride;
+  int Hkv, D, bs, esize;
+};
+
+// byte offset of (block, offset, head) in the cache
+__device__ inline int64_t kv_byte_off(const KvGeom& g, int64_t blk, int off, int h) {
+  return (blk * g.block_stride + (int64_t)off * g.tok_stride + (int64_t)h * g.head_stride) * g.esize;
+}
+
+// Exclusive scan of flags[0..n) (n <= FORK_MAX_W) into out[]; returns total.
+__device__ int block_exclusive_scan(const int* flags, int* out, int n, int* tmp) {
+  const int tid = threadIdx.x;
+  // each thread scans 4 consecutive entries
+  const int base = tid * 4;
+  int loc[4], s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    loc[j] = s;
+    s += (base + j < n) ? flags[base + j] : 0;
+  }
+  tmp[tid] = s;
+  __syncthreads();
+  for (int off = 1; off < FORK_THREADS; off <<= 1) {
+    int v = tid >= off ? tmp[tid - off] : 0;
+    __syncthreads();
+    tmp[tid] += v;
+    __syncthreads();
+  }
+  const int excl = tmp[tid] - s;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (base + j < n) out[base + j] = excl + loc[j];
+  const int total = tmp[FORK_THREADS - 1];
+  __syncthreads();
+  return total;
+}
+
+__global__ __launch_bounds__(FORK_THREADS) void beam_fork(
+    const int32_t* __restrict__ parent, int R, int W, const int32_t* __restrict__ bt_in,
+    const int32_t* __restrict__ len_in, int32_t* __restrict__ bt_out, int32_t* __restrict__ len_out,
+    int S, KvGeom g, const uint8_t* k_new, const uint8_t* v_new, int64_t new_tok_stride,
+    int32_t* dev_status) {
+  __shared__ int par[FORK_MAX_W], first[FORK_MAX_W], cnt[FORK_MAX_W];
+  __shared__ int cow_flag[FORK_MAX_W], cow_rank[FORK_MAX_W];
+  __shared__ int free_flag[FORK_MAX_W], free_rank[FORK_MAX_W], free_list[FORK_MAX_W];
+  __shared__ int scan_tmp[FORK_THREADS];
+  __shared__ int bad;
+  const int chunks = (W + FORK_CHILDREN_PER_WG - 1) / FORK_CHILDREN_PER_WG;
+  const int r = blockIdx.x / chunks;
+  const int chunk = blockIdx.x % chunks;
+  const int tid = threadIdx.x;
+  if (r >= R) return;
+  if (tid == 0) bad = 0;
+  for (int c = tid; c < W; c += FORK_THREADS) {
+    first[c] = W;
+    cnt[c] = 0;
+  }
+  __syncthreads();
+  for (int c = tid; c < W; c += FORK_THREADS) {
+    int p = parent[(int64_t)r * W + c];
+    if (p < 0 || p >= W) {
+      bad = 1;
+      p = c;
+    }
+    par[c] = p;
+    atomicMin(&first[p], c);
+    atomicAdd(&cnt[p], 1);
+  }
+  __syncthreads();
+  const bool req_bad = bad != 0;
+  if (req_bad && chunk == 0 && tid == 0) flag_status(dev_status, GR_DEV_BAD_PARENT);
+  for (int c = tid; c < W; c += FORK_THREADS) {
+    cow_flag[c] = (!req_bad && first[par[c]] != c) ? 1 : 0;
+    free_flag[c] = (!req_bad && cnt[c] == 0) ? 1 : 0;
+  }
+  __syncthreads();
+  block_exclusive_scan(cow_flag, cow_rank, W, scan_tmp);
+  block_exclusive_scan(free_flag, free_rank, W, scan_tmp);
+  for (int p = tid; p < W; p += FORK_THREADS)
+    if (free_flag[p]) free_list[free_rank[p]] = p;
+  __syncthreads();
+
+  const int cap = S * g.bs;
+  const int row_vecs = g.D * g.esize / 16;  // 16-byte vectors per (token, head) row
+  uint8_t* kc = static_cast<uint8_t*>(g.k_cache);
+  uint8_t* vc = static_cast<uint8_t*>(g.v_cache);
+  const int c_end = min(W, (chunk + 1) * FORK_CHILDREN_PER_WG);
+  for (int c = chunk * FORK_CHILDREN_PER_WG; c < c_end; ++c) {
+    const int p = par[c];
+    const bool cow = cow_flag[c] != 0;
+    // beam whose old row c receives; a request with a bad parent keeps its tables
+    const int owner = req_bad ? c : (cow ? free_list[cow_rank[c]] : p);
+    const int64_t n_c = (int64_t)r * W + c;
+    const int64_t n_p = (int64_t)r * W + p;
+    const int64_t n_o = (int64_t)r * W + owner;
+    int len = len_in[n_p];
+    if (len < 0 || len > cap) {
+      if (tid == 0) flag_status(dev_status, GR_DEV_BAD_LENGTH);
+      len = len < 0 ? 0 : cap;
+    }
+    for (int j = tid; j < S; j += FORK_THREADS) bt_out[n_c * S + j] = bt_in[n_o * S + j];
+    if (req_bad) {
+      if (tid == 0) len_out[n_c] = len_in[n_c];
+      continue;
+    }
+    if (cow) {
+      // copy tokens [0, len) of the parent's row into the owner's row
+      const int work = len * g.Hkv * row_vecs;
+      for (int e = tid; e < work; e += FORK_THREADS) {
+        const int vec = e % row_vecs;
+        const int h = (e / row_vecs) % g.Hkv;
+        const int pos = e / (row_vecs * g.Hkv);
+        const int bsrc = bt_in[n_p * S + pos / g.bs];
+        const int bdst = bt_in[n_o * S + pos / g.bs];
+        if (bsrc < 0 || bsrc >= g.num_blocks || bdst < 0 || bdst >= g.num_blocks) {
+          flag_status(dev_status, GR_DEV_BAD_BLOCK);
+          continue;
+        }
+        const int64_t so = kv_byte_off(g, bsrc, pos % g.bs, h) + vec * 16;
+        const int64_t dof = kv_byte_off(g, bdst, pos % g.bs, h) + vec * 16;
+        *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(kc + so);
+        *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(vc + so);
+      }
+    }
+    int new_len = len;
+    if (k_new) {
+      if (len < cap) {
+        const int bdst = bt_in[n_o * S + len / g.bs];
+        if (bdst >= 0 && bdst < g.num_blocks) {
+          for (int e = tid; e < g.Hkv * row_vecs; e += FORK_THREADS) {
+            const int vec = e % row_vecs, h = e / row_vecs;
+            const int64_t src = (n_c * new_tok_stride + (int64_t)h * g.D) * g.esize + vec * 16;
+            const int64_t dof = kv_byte_off(g, bdst, len % g.bs, h) + vec * 16;
+            *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(k_new + src);
+            *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(v_new + src);
+          }
+          new_len = len + 1;
+        } else if (tid == 0) {
+          flag_status(dev_status, GR_DEV_BAD_BLOCK);
+        }
+      } else if (tid == 0) {
+        flag_status(dev_status, GR_DEV_SUFFIX_FULL);
+      }
+    }
+    if (tid == 0) len_out[n_c] = new_len;
+  }
+}
+
+// One 64-lane wave per beam: append its token at suffix_len[n], then bump it.
+__global__ __launch_bounds__(64) void beam_append(const uint8_t* k_new, const uint8_t* v_new,
+                                                  int64_t new_tok_stride, KvGeom g,
+                                                  const int32_t* __restrict__ bt, int S,
+                                                  int32_t* __restrict__ len, int N, int32_t* dev_status) {
+  const int n = blockIdx.x;
+  if (n >= N) return;
+  const int cur = len[n];
+  const int cap = S * g.bs;
+  const int row_vecs = g.D * g.esize / 16;
+  bool ok = cur >= 0 && cur < cap;
+  int blk = ok ? bt[(int64_t)n * S + cur / g.bs] : -1;
+  ok = ok && blk >= 0 && blk < g.num_blocks;
+  if (ok) {
+    uint8_t* kc = static_cast<uint8_t*>(g.k_cache);
+    uint8_t* vc = static_cast<uint8_t*>(g.v_cache);
+    for (int e = threadIdx.x; e < g.Hkv * row_vecs; e += 64) {
+      const int vec = e % row_vecs, h = e / row_vecs;
+      const int64_t src = ((int64_t)n * new_tok_stride + (int64_t)h * g.D) * g.esize + vec * 16;
+      const int64_t dof = kv_byte_off(g, blk, cur % g.bs, h) + vec * 16;
+      *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(k_new + src);
+      *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(v_new + src);
+    }
+  }
+  __syncthreads();  // every lane has read len[n] before it changes
+  if (threadIdx.x == 0) {
+    if (ok) len[n] = cur + 1;
+    else flag_status(dev_status, (cur >= cap) ? GR_DEV_SUFFIX_FULL : (cur < 0 ? GR_DEV_BAD_LENGTH : GR_DEV_BAD_BLOCK));
+  }
+}
+
+__global__ __launch_bounds__(64) void reshape_and_cache_k(const uint8_t* key, int64_t key_stride,
+                                                          const uint8_t* value, int64_t value_stride,
+                                                          KvGeom g, const int64_t* __restrict__ slots,
+                                                          int T, int32_t* dev_status) {
+  const int t = blockIdx.x;
+  if (t >= T) return;
+  const int64_t slot = slots[t];
+  if (slot < 0) return;
+  const int64_t blk = slot / g.bs;
+  const int off = (int)(slot % g.bs);
+  if (blk >= g.num_blocks) {
+    if (threadIdx.x == 0) flag_status(dev_status, GR_DEV_BAD_BLOCK);
+    return;
+  }
+  const int row_vecs = g.D * g.esize / 16;
+  uint8_t* kc = static_cast<uint8_t*>(g.k_cache);
+  uint8_t* vc = static_cast<uint8_t*>(g.v_cache);
+  for (int e = threadIdx.x; e < g.Hkv * row_vecs; e += 64) {
+    const int vec = e % row_vecs, h = e / row_vecs;
+    const int64_t dof = kv_byte_off(g, blk, off, h) + vec * 16;
+    *reinterpret_cast<u32x4_t*>(kc + dof) =
+        *reinterpret_cast<const u32x4_t*>(key + ((int64_t)t * key_stride + (int64_t)h * g.D) * g.esize + vec * 16);
+    *reinterpret_cast<u32x4_t*>(vc + dof) =
+        *reinterpret_cast<const u32x4_t*>(value + ((int64_t)t * value_stride + (int64_t)h * g.D) * g.esize + vec * 16);
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// 16-byte vector moves need every row start 16-byte aligned.
+gr_status_t check_geom(const KvGeom& g) {
+  if (!g.k_cache || !g.v_cache || g.num_blocks < 0 || g.Hkv < 1 || g.bs < 1 || g.D < 8)
+    return GR_ERR_INVALID_ARG;
+  if ((g.D * g.esize) % 16 || !aligned16(g.k_cache) || !aligned16(g.v_cache)) return GR_ERR_INVALID_ARG;
+  if ((g.block_stride * g.esize) % 16 || (g.tok_stride * g.esize) % 16 || (g.head_stride * g.esize) % 16)
+    return GR_ERR_INVALID_ARG;
+  if (g.block_stride < 1 || g.tok_stride < 1 || g.head_stride < 1) return GR_ERR_INVALID_ARG;
+  return GR_OK;
+}
+
+KvGeom make_geom(void* k_cache, void* v_cache, int64_t num_blocks, int64_t bstr, int64_t tstr,
+                 int64_t hstr, int Hkv, int D, int bs, int dtype) {
+  KvGeom g;
+  g.k_cache = k_cache;
+  g.v_cache = v_cache;
+  g.num_blocks = num_blocks;
+  g.block_stride = bstr;
+  g.tok_stride = tstr;
+  g.head_stride = hstr;
+  g.Hkv = Hkv;
+  g.D = D;
+  g.bs = bs;
+  g.esize = dtype_size(dtype);
+  return g;
+}
+
+}  // namespace
+}  // namespace gr
+
+using namespace gr;
+
+extern "C" gr_status_t gr_beam_kv_fork(const int32_t* parent, int num_reqs, int beam_width,
+                                       const int32_t* bt_in, const int32_t* len_in, int32_t* bt_out,
+                                       int32_t* len_out, int bt_stride, void* k_cache, void* v_cache,
+                                       int64_t num_blocks, int64_t kv_block_stride, int64_t kv_tok_stride,
+                                       int64_t kv_head_stride, const void* k_new, const void* v_new,
+                                       int64_t new_tok_stride, int num_kv_heads, int head_dim,
+                                       int block_size, int dtype, int32_t* dev_status, hipStream_t stream) {
+  if (!dtype_valid(dtype) || num_reqs < 0 || beam_width < 1 || bt_stride < 1) return GR_ERR_INVALID_ARG;
+  if (beam_width > FORK_MAX_W) return GR_ERR_UNSUPPORTED;
+  if (num_reqs == 0) return GR_OK;
+  if (!parent || !bt_in || !len_in || !bt_out || !len_out) return GR_ERR_INVALID_ARG;
+  if (bt_in == bt_out || len_in == len_out) return GR_ERR_INVALID_ARG;  // tables are written out of place
+  if ((k_new == nullptr) != (v_new == nullptr)) return GR_ERR_INVALID_ARG;
+  KvGeom g = make_geom(k_cache, v_cache, num_blocks, kv_block_stride, kv_tok_stride, kv_head_stride,
+                       num_kv_heads, head_dim, block_size, dtype);
+  gr_status_t st = check_geom(g);
+  if (st != GR_OK) return st;
+  if (k_new && (!aligned16(k_new) || !aligned16(v_new) || (new_tok_stride * g.esize) % 16 ||
+                new_tok_stride < (int64_t)num_kv_heads * head_dim))
+    return GR_ERR_INVALID_ARG;
+  const int chunks = (beam_width + FORK_CHILDREN_PER_WG - 1) / FORK_CHILDREN_PER_WG;
+  hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * chunks)), dim3(FORK_THREADS), 0, stream, parent,
+                     num_reqs, beam_width, bt_in, len_in, bt_out, len_out, bt_stride, g,
+                     static_cast<const uint8_t*>(k_new), static_cast<const uint8_t*>(v_new), new_tok_stride,
+                     dev_status);
+  return launch_status();
+}
+
+extern "C" gr_status_t gr_beam_kv_append(const void* k_new, const void* v_new, int64_t new_tok_stride,
+                                         void* k_cache, void* v_cache, int64_t num_blocks,
+                                         int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+                                         const int32_t* suffix_bt, int bt_stride, int32_t* suffix_len,
+                                         int num_beams, int num_kv_heads, int head_dim, int block_size, int dtype,
+                                         int32_t* dev_status, hipStream_t stream) {
+  if (!dtype_valid(dtype) || num_beams < 0 || bt_stride < 1) return GR_ERR_INVALID_ARG;
+  if (num_beams == 0) return GR_OK;
+  if (!k_new || !v_new || !suffix_bt || !suffix_len) return GR_ERR_INVALID_ARG;
+  KvGeom g = make_geom(k_cache, v_cache, num_blocks, kv_block_stride, kv_tok_stride, kv_head_stride,
+                       num_kv_heads, head_dim, block_size, dtype);
+  gr_status_t st = check_geom(g);
+  if (st != GR_OK) return st;
+  if (!aligned16(k_new) || !aligned16(v_new) || (new_tok_stride * g.esize) % 16 ||
+      new_tok_stride < (int64_t)num_kv_heads * head_dim)
+    return GR_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(beam_append, dim3((unsigned)num_beams), dim3(64), 0, stream,
+                     static_cast<const uint8_t*>(k_new), static_cast<const uint8_t*>(v_new), new_tok_stride, g,
+                     suffix_bt, bt_stride, suffix_len, num_beams, dev_status);
+  return launch_status();
+}
+
+extern "C" gr_status_t gr_reshape_and_cache(const void* key, int64_t key_tok_stride, const void* value,
+                                            int64_t value_tok_stride, void* k_cache, void* v_cache,
+                                            int64_t num_blocks, int64_t kv_block_stride, int64_t kv_tok_stride,
+                                            int64_t kv_head_stride, const int64_t* slot_mapping, int num_tokens,
+                                            int num_kv_heads, int head_dim, int block_size, int dtype,
+                                            int32_t* dev_status, hipStream_t stream) {
+  if (!dtype_valid(dtype) || num_tokens < 0) return GR_ERR_INVALID_ARG;
+  if (num_tokens == 0) return GR_OK;
+  if (!key || !value || !slot_mapping) return GR_ERR_INVALID_ARG;
+  KvGeom g = make_geom(k_cache, v_cache, num_blocks, kv_block_stride, kv_tok_stride, kv_head_stride,
+                       num_kv_heads, head_dim, block_size, dtype);
+  gr_status_t st = check_geom(g);
+  if (st != GR_OK) return st;
+  if (!aligned16(key) || !aligned16(value) || (key_tok_stride * g.esize) % 16 ||
+      (value_tok_stride * g.esize) % 16 || key_tok_stride < (int64_t)num_kv_heads * head_dim ||
+      value_tok_stride < (int64_t)num_kv_heads * head_dim)
+    return GR_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(reshape_and_cache_k, dim3((unsigned)num_tokens), dim3(64), 0, stream,
+                     static_cast<const uint8_t*>(key), key_tok_stride, static_cast<const uint8_t*>(value),
+                     value_tok_stride, g, slot_mapping, num_tokens, dev_status);
+  return launch_status();
+}
+
+extern "C" const char* gr_status_string(gr_status_t s) {
+  switch (s) {
+    case GR_OK: return "ok";
+    case GR_ERR_INVALID_ARG: return "invalid argument";
+    case GR_ERR_UNSUPPORTED: return "unsupported configuration";
+    case GR_ERR_LAUNCH: return "kernel launch failed";
+    case GR_ERR_WORKSPACE: return "workspace missing or too small";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int gr_version(void) { return GR_VERSION_CODE; }

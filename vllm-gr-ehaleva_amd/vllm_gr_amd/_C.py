@@ -1,0 +1,107 @@
+"""ctypes binding of libgr_beam.so (declared in include/gr_beam.h).
+
+The library is the product: there is no Python or CPU fallback.  Loading
+fails loudly with an ImportError-like RuntimeError when the shared object is
+missing, and every entry point's status code is turned into an exception.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_lib", "libgr_beam.so")
+
+GR_OK = 0
+GR_ERR_INVALID_ARG = 1
+GR_ERR_UNSUPPORTED = 2
+GR_ERR_LAUNCH = 3
+GR_ERR_WORKSPACE = 4
+
+GR_DEV_BAD_BLOCK = 1
+GR_DEV_BAD_LENGTH = 2
+GR_DEV_BAD_PARENT = 4
+GR_DEV_SUFFIX_FULL = 8
+
+GR_DTYPE_F32 = 0
+GR_DTYPE_F16 = 1
+GR_DTYPE_BF16 = 2
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/gr_beam.h one to one
+SIGNATURES = {
+    "gr_status_string": (ctypes.c_char_p, [_I]),
+    "gr_version": (_I, []),
+    "gr_set_decode_kernel": (_I, [_I]),
+    "gr_beam_attn_decode": (_I, [
+        _P, _L, _P, _L,                 # out, out_tok_stride, q, q_tok_stride
+        _P, _P, _L,                     # k_cache, v_cache, num_blocks
+        _L, _L, _L,                     # kv block/tok/head strides
+        _P, _I, _P,                     # prefix_bt, prefix_bt_stride, prefix_len
+        _P,                             # beam_start
+        _P, _I, _P, _P,                 # suffix_bt, stride, suffix_len, suffix_start
+        _I, _I, _I, _I,                 # num_reqs, max_beams_per_req, num_beams, q_per_beam
+        _I, _I, _I, _I, _I,             # Hq, Hkv, head_dim, block_size, dtype
+        _F, _F, _P, _P, _P,             # scale, softcap, lse_out, dev_status, stream
+    ]),
+    "gr_reshape_and_cache": (_I, [
+        _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _I, _I, _I, _I, _P, _P,
+    ]),
+    "gr_beam_kv_fork": (_I, [
+        _P, _I, _I, _P, _P, _P, _P, _I,
+        _P, _P, _L, _L, _L, _L,
+        _P, _P, _L, _I, _I, _I, _I, _P, _P,
+    ]),
+    "gr_beam_kv_append": (_I, [
+        _P, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P,
+    ]),
+    "gr_beam_prune_workspace_size": (_SZ, [_I, _I, _I, _I]),
+    "gr_beam_prune_topk": (_I, [
+        _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _SZ, _P,
+    ]),
+}
+
+_lib = None
+
+
+class GrError(RuntimeError):
+    """A library call returned a non-OK status."""
+
+    def __init__(self, fn: str, code: int):
+        self.code = code
+        super().__init__(f"{fn}: {status_string(code)} (status {code})")
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"libgr_beam.so not found at {LIB_PATH}; build it with "
+                "`python vllm-gr-ehaleva_amd/build.py` (there is no CPU fallback)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def status_string(code: int) -> str:
+    return lib().gr_status_string(code).decode()
+
+
+def check(fn: str, code: int) -> None:
+    if code == GR_ERR_INVALID_ARG:
+        raise ValueError(f"{fn}: {status_string(code)}")
+    if code == GR_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{fn}: {status_string(code)}")
+    if code != GR_OK:
+        raise GrError(fn, code)

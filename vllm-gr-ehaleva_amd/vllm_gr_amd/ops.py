@@ -1,0 +1,270 @@
+"""torch-tensor entry points over the C ABI (include/gr_beam.h).
+
+Each function validates shapes/devices on the host, allocates outputs with
+the torch caching allocator when the caller passes none, and launches on
+``torch.cuda.current_stream()``.  Nothing here computes on the CPU: without
+the HIP library every call raises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _C
+
+_DTYPES = {torch.float32: _C.GR_DTYPE_F32, torch.float16: _C.GR_DTYPE_F16,
+           torch.bfloat16: _C.GR_DTYPE_BF16}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise NotImplementedError(f"unsupported dtype {t.dtype}") from None
+
+
+def _need_cuda(*ts: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("all tensors must be on a HIP device (torch 'cuda')")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    return dev
+
+
+def _need_i32(name: str, t: torch.Tensor) -> None:
+    if t.dtype != torch.int32 or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous int32 tensor")
+
+
+def _cache_strides(k_cache: torch.Tensor, v_cache: torch.Tensor):
+    """(num_blocks, block_size, Hkv, D) views -> element strides."""
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache / v_cache must be matching [num_blocks, block_size, Hkv, D] views")
+    if k_cache.stride(3) != 1:
+        raise ValueError("head_dim must be contiguous in the KV cache")
+    if k_cache.dtype != v_cache.dtype:
+        raise ValueError("k_cache / v_cache dtype mismatch")
+    return k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+
+
+def split_kv_cache(kv_cache: torch.Tensor):
+    """``kv_cache [2, num_blocks, block_size, Hkv, D]`` -> (k_cache, v_cache),
+    the ``kv_cache.unbind(0)`` of ``beam_attn.py:725``."""
+    if kv_cache.dim() != 5 or kv_cache.shape[0] != 2:
+        raise ValueError("kv_cache must be [2, num_blocks, block_size, num_kv_heads, head_dim]")
+    return kv_cache[0], kv_cache[1]
+
+
+def new_status(device) -> torch.Tensor:
+    """Device status word the kernels OR error bits into."""
+    return torch.zeros(1, dtype=torch.int32, device=device)
+
+
+def check_status(status: torch.Tensor) -> None:
+    """Raise if a kernel flagged an out-of-range table entry (synchronises)."""
+    bits = int(status.item())
+    if bits:
+        names = [n for b, n in ((_C.GR_DEV_BAD_BLOCK, "block id out of range"),
+                                (_C.GR_DEV_BAD_LENGTH, "length beyond table capacity"),
+                                (_C.GR_DEV_BAD_PARENT, "parent index out of range"),
+                                (_C.GR_DEV_SUFFIX_FULL, "suffix full")) if bits & b]
+        raise ValueError("device tables rejected: " + ", ".join(names))
+
+
+def set_decode_kernel(which: str) -> None:
+    """'auto' (matrix-core kernel where supported) or 'generic'."""
+    code = {"auto": 0, "generic": 1}[which]
+    _C.check("gr_set_decode_kernel", _C.lib().gr_set_decode_kernel(code))
+
+
+def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     prefix_bt: torch.Tensor, prefix_len: torch.Tensor, beam_start: torch.Tensor,
+                     suffix_bt: torch.Tensor, suffix_len: torch.Tensor,
+                     suffix_start: torch.Tensor | None = None, *, q_per_beam: int = 1,
+                     scale: float, softcap: float = 0.0, max_beams_per_req: int | None = None,
+                     out: torch.Tensor | None = None, lse: torch.Tensor | None = None,
+                     status: torch.Tensor | None = None) -> torch.Tensor:
+    """BeamAttention decode step; see ``gr_beam_attn_decode`` in gr_beam.h.
+
+    ``q``: ``[num_beams*q_per_beam, Hq, D]`` (token stride free, heads and dims
+    contiguous).  Returns ``out`` (same shape/dtype as ``q``)."""
+    dev = _need_cuda(q, k_cache, v_cache, prefix_bt, prefix_len, beam_start, suffix_bt, suffix_len,
+                     suffix_start, out, lse, status)
+    if q.dim() != 3 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
+        raise ValueError("q must be [tokens, Hq, D] with heads and dims contiguous")
+    for name, t in (("prefix_bt", prefix_bt), ("prefix_len", prefix_len), ("beam_start", beam_start),
+                    ("suffix_bt", suffix_bt), ("suffix_len", suffix_len)):
+        _need_i32(name, t)
+    if suffix_start is not None:
+        _need_i32("suffix_start", suffix_start)
+    if q.dtype != k_cache.dtype:
+        raise ValueError("q and KV cache dtype must match")
+    NT, Hq, D = q.shape
+    NB, bs, Hkv, Dk = k_cache.shape
+    if Dk != D:
+        raise ValueError("head_dim mismatch between q and KV cache")
+    R = prefix_len.numel()
+    if prefix_bt.dim() != 2 or prefix_bt.shape[0] != R or beam_start.numel() != R + 1:
+        raise ValueError("prefix_bt must be [R, blocks], beam_start [R+1]")
+    N = suffix_len.numel()
+    if suffix_bt.dim() != 2 or suffix_bt.shape[0] != N or NT != N * q_per_beam:
+        raise ValueError("suffix_bt must be [N, blocks] and q must hold N*q_per_beam rows")
+    if suffix_start is not None and suffix_start.numel() != N:
+        raise ValueError("suffix_start must have one entry per beam")
+    if max_beams_per_req is None:
+        max_beams_per_req = int((beam_start[1:] - beam_start[:-1]).max().item()) if R else 0
+    bstr, tstr, hstr = _cache_strides(k_cache, v_cache)
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 or out.stride(1) != D:
+        raise ValueError("out must match q's shape/dtype with heads and dims contiguous")
+    if lse is not None and (lse.shape != (NT, Hq) or lse.dtype != torch.float32 or not lse.is_contiguous()):
+        raise ValueError("lse must be a contiguous float32 [tokens, Hq] tensor")
+    code = _C.lib().gr_beam_attn_decode(
+        out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), NB, bstr, tstr, hstr,
+        prefix_bt.data_ptr(), prefix_bt.shape[1], prefix_len.data_ptr(), beam_start.data_ptr(),
+        suffix_bt.data_ptr(), suffix_bt.shape[1], suffix_len.data_ptr(), _ptr(suffix_start),
+        R, max_beams_per_req, N, q_per_beam, Hq, Hkv, D, bs, _dtype_code(q),
+        float(scale), float(softcap or 0.0), _ptr(lse), _ptr(status), _stream(dev))
+    _C.check("gr_beam_attn_decode", code)
+    return out
+
+
+def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                      v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                      status: torch.Tensor | None = None) -> None:
+    """Scatter ``key/value [T, Hkv, D]`` into the paged cache by slot (the
+    ``reshape_and_cache_flash`` role, ``beam_attn.py:727-732``)."""
+    dev = _need_cuda(key, value, k_cache, v_cache, slot_mapping, status)
+    if slot_mapping.dtype != torch.int64 or not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be a contiguous int64 tensor")
+    T, Hkv, D = key.shape
+    if value.shape != key.shape or key.stride(2) != 1 or key.stride(1) != D or value.stride(2) != 1 \
+            or value.stride(1) != D:
+        raise ValueError("key/value must be [T, Hkv, D] with heads and dims contiguous")
+    if slot_mapping.numel() < T:
+        raise ValueError("slot_mapping shorter than the number of tokens")
+    NB, bs, Hk, Dk = k_cache.shape
+    if (Hk, Dk) != (Hkv, D) or key.dtype != k_cache.dtype or value.dtype != k_cache.dtype:
+        raise ValueError("key/value do not match the KV cache")
+    bstr, tstr, hstr = _cache_strides(k_cache, v_cache)
+    code = _C.lib().gr_reshape_and_cache(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0), k_cache.data_ptr(),
+        v_cache.data_ptr(), NB, bstr, tstr, hstr, slot_mapping.data_ptr(), T, Hkv, D, bs,
+        _dtype_code(key), _ptr(status), _stream(dev))
+    _C.check("gr_reshape_and_cache", code)
+
+
+def beam_kv_fork(parent: torch.Tensor, bt_in: torch.Tensor, len_in: torch.Tensor,
+                 k_cache: torch.Tensor, v_cache: torch.Tensor, k_new: torch.Tensor | None = None,
+                 v_new: torch.Tensor | None = None, *, bt_out: torch.Tensor | None = None,
+                 len_out: torch.Tensor | None = None, status: torch.Tensor | None = None):
+    """Fork each request's beams by ``parent [R, W]`` (copy-on-write suffix
+    rows) and optionally append one token per child.  Returns (bt_out, len_out)."""
+    dev = _need_cuda(parent, bt_in, len_in, k_cache, v_cache, k_new, v_new, bt_out, len_out, status)
+    _need_i32("parent", parent)
+    _need_i32("bt_in", bt_in)
+    _need_i32("len_in", len_in)
+    if parent.dim() != 2:
+        raise ValueError("parent must be [R, W]")
+    R, W = parent.shape
+    if bt_in.dim() != 2 or bt_in.shape[0] != R * W or len_in.numel() != R * W:
+        raise ValueError("bt_in must be [R*W, blocks] and len_in [R*W]")
+    NB, bs, Hkv, D = k_cache.shape
+    bstr, tstr, hstr = _cache_strides(k_cache, v_cache)
+    if bt_out is None:
+        bt_out = torch.empty_like(bt_in)
+    if len_out is None:
+        len_out = torch.empty_like(len_in)
+    _need_i32("bt_out", bt_out)
+    _need_i32("len_out", len_out)
+    if bt_out.shape != bt_in.shape or len_out.shape != len_in.shape:
+        raise ValueError("output tables must match the input tables' shapes")
+    new_stride = 0
+    if k_new is not None or v_new is not None:
+        if k_new is None or v_new is None or k_new.shape != (R * W, Hkv, D) or v_new.shape != k_new.shape:
+            raise ValueError("k_new/v_new must both be [R*W, Hkv, D]")
+        if k_new.dtype != k_cache.dtype or v_new.dtype != k_cache.dtype:
+            raise ValueError("k_new/v_new dtype must match the cache")
+        if k_new.stride(2) != 1 or k_new.stride(1) != D or v_new.stride() != k_new.stride():
+            raise ValueError("k_new/v_new must have heads and dims contiguous and equal strides")
+        new_stride = k_new.stride(0)
+    code = _C.lib().gr_beam_kv_fork(
+        parent.data_ptr(), R, W, bt_in.data_ptr(), len_in.data_ptr(), bt_out.data_ptr(),
+        len_out.data_ptr(), bt_in.shape[1], k_cache.data_ptr(), v_cache.data_ptr(), NB, bstr, tstr,
+        hstr, _ptr(k_new), _ptr(v_new), new_stride, Hkv, D, bs, _dtype_code(k_cache), _ptr(status),
+        _stream(dev))
+    _C.check("gr_beam_kv_fork", code)
+    return bt_out, len_out
+
+
+def beam_kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                   v_cache: torch.Tensor, suffix_bt: torch.Tensor, suffix_len: torch.Tensor,
+                   status: torch.Tensor | None = None) -> None:
+    """Append one token per beam at ``suffix_len[n]``; ``suffix_len`` += 1 in place."""
+    dev = _need_cuda(k_new, v_new, k_cache, v_cache, suffix_bt, suffix_len, status)
+    _need_i32("suffix_bt", suffix_bt)
+    _need_i32("suffix_len", suffix_len)
+    N = suffix_len.numel()
+    NB, bs, Hkv, D = k_cache.shape
+    if k_new.shape != (N, Hkv, D) or v_new.shape != k_new.shape or suffix_bt.shape[0] != N:
+        raise ValueError("k_new/v_new must be [N, Hkv, D] with N = len(suffix_len) = suffix_bt rows")
+    if k_new.stride(2) != 1 or k_new.stride(1) != D or v_new.stride() != k_new.stride():
+        raise ValueError("k_new/v_new must have heads and dims contiguous and equal strides")
+    bstr, tstr, hstr = _cache_strides(k_cache, v_cache)
+    code = _C.lib().gr_beam_kv_append(
+        k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+        NB, bstr, tstr, hstr, suffix_bt.data_ptr(), suffix_bt.shape[1], suffix_len.data_ptr(), N,
+        Hkv, D, bs, _dtype_code(k_cache), _ptr(status), _stream(dev))
+    _C.check("gr_beam_kv_append", code)
+
+
+def prune_workspace_bytes(num_reqs: int, beam_width: int, vocab: int, k: int) -> int:
+    return int(_C.lib().gr_beam_prune_workspace_size(num_reqs, beam_width, vocab, k))
+
+
+def beam_prune_topk(logits: torch.Tensor, cum: torch.Tensor, k: int, eos_token_id: int = -1, *,
+                    workspace: torch.Tensor | None = None, out=None):
+    """Fused log_softmax + cum + top-k over beams x vocab per request.
+
+    ``logits``: ``[R, W, V]`` float32 (vocab contiguous), ``cum``: ``[R, W]``.
+    Returns ``(parent [R,k] int32, token [R,k] int32, score [R,k] float32,
+    eos_score [R,W] float32)``."""
+    dev = _need_cuda(logits, cum, workspace)
+    if logits.dim() != 3 or logits.dtype != torch.float32 or logits.stride(2) != 1 \
+            or logits.stride(0) != logits.shape[1] * logits.stride(1):
+        raise ValueError("logits must be float32 [R, W, V] with rows at a uniform stride")
+    R, W, V = logits.shape
+    if cum.shape != (R, W) or cum.dtype != torch.float32 or not cum.is_contiguous():
+        raise ValueError("cum must be a contiguous float32 [R, W] tensor")
+    need = prune_workspace_bytes(R, W, V, k)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    if out is None:
+        parent = torch.empty((R, k), dtype=torch.int32, device=dev)
+        token = torch.empty((R, k), dtype=torch.int32, device=dev)
+        score = torch.empty((R, k), dtype=torch.float32, device=dev)
+        eos_score = torch.empty((R, W), dtype=torch.float32, device=dev)
+    else:
+        parent, token, score, eos_score = out
+    code = _C.lib().gr_beam_prune_topk(
+        logits.data_ptr(), logits.stride(1), cum.data_ptr(), R, W, V, int(k), int(eos_token_id),
+        parent.data_ptr(), token.data_ptr(), score.data_ptr(), eos_score.data_ptr(),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(dev))
+    _C.check("gr_beam_prune_topk", code)
+    return parent, token, score, eos_score
