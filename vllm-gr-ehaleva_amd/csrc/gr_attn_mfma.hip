@@ -205,6 +205,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   g.TG = a.T * g.G;
   g.rows_r = g.W * g.TG;
   g.row_base = mt * MF_ROWS;
+  if (g.nb0 < 0 || g.W < 0 || g.nb0 + g.W > a.num_beams) {  // beam_start is device data: never trust it
+    if (threadIdx.x == 0 && mt == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+    return;
+  }
   if (g.row_base >= g.rows_r) return;
 
   const int tid = threadIdx.x;
