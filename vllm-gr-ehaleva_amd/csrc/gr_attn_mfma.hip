@@ -72,17 +72,20 @@ template <> struct Mma<GR_DTYPE_F16> {
 // S^T row slot i holds tile key PI(i): bits 2 and 3 swapped.
 __device__ inline int key_perm(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
-// max / sum over the lane pair (l, l ^ 32) that shares a query row
-__device__ inline float pair_max(float x) {
+// Value of x held by lane l ^ 32 (the other lane of the same query row).
+// v_permlane32_swap exchanges the upper 32 lanes of its first operand with the
+// lower 32 lanes of its second: with both operands = x, lanes 0..31 find the
+// partner in the second result and lanes 32..63 in the first.  The half is
+// selected explicitly: the compiler folds fmaxf(v[0], v[1]) to v[0] when both
+// operands are the same value, which drops the partner on lanes 0..31.
+__device__ inline float lane_partner(float x) {
   auto v = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
                                             __builtin_bit_cast(uint32_t, x), false, false);
-  return fmaxf(__builtin_bit_cast(float, v[0]), __builtin_bit_cast(float, v[1]));
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? v[0] : v[1]);
 }
-__device__ inline float pair_sum(float x) {
-  auto v = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
-                                            __builtin_bit_cast(uint32_t, x), false, false);
-  return __builtin_bit_cast(float, v[0]) + __builtin_bit_cast(float, v[1]);
-}
+// max / sum over the lane pair (l, l ^ 32); both lanes get the same result
+__device__ inline float pair_max(float x) { return fmaxf(x, lane_partner(x)); }
+__device__ inline float pair_sum(float x) { return x + lane_partner(x); }
 
 __device__ inline u32x4_t lds_read16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 
