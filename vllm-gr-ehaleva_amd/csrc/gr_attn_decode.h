@@ -23,6 +23,7 @@ struct DecodeArgs {
   const int32_t* suffix_len;
   const int32_t* suffix_start;
   int num_reqs, max_beams, num_beams, T, Hq, Hkv, D, bs, dtype;
+  int bs_shift;  // log2(bs) when bs is a power of two, else -1
   float scale, softcap;
   float* lse_out;
   int32_t* dev_status;

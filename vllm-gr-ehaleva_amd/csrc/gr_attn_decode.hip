@@ -272,6 +272,7 @@ extern "C" gr_status_t gr_beam_attn_decode(
   a.num_reqs = num_reqs; a.max_beams = max_beams_per_req; a.num_beams = num_beams; a.T = q_per_beam;
   a.Hq = num_q_heads; a.Hkv = num_kv_heads; a.D = head_dim; a.bs = block_size; a.dtype = dtype;
   a.scale = scale; a.softcap = softcap; a.lse_out = lse_out; a.dev_status = dev_status;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   if (g_decode_kernel_override == 0 && mfma_decode_supported(a)) return launch_mfma_decode(a, stream);
   return launch_generic(a, stream);
 }

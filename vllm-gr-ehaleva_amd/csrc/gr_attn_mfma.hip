@@ -3,9 +3,10 @@
 // Work decomposition.  For request r and KV head h the query rows of all its
 // beams form one dense M x 128 matrix (M = beams * q_per_beam * GQA group):
 // the shared prefix contraction is a plain GEMM-shaped problem, which is why
-// it runs on MFMA.  A workgroup owns 128 of those rows (4 waves: 2 row groups
-// of 64 rows x 2 key halves) and streams the request's prefix K/V through
-// LDS in 64-key super-tiles, each loaded once from HBM for all 128 rows.
+// it runs on MFMA.  A workgroup owns 128 of those rows (8 waves: 4 row groups
+// of 32 rows x 2 key halves, two waves per SIMD so one wave's matrix work
+// overlaps the other's softmax and loads) and streams the request's prefix
+// K/V through LDS in 64-key super-tiles, each loaded once for all 128 rows.
 // Workgroups that share (r, h) are placed on the same XCD (blockIdx % 8 is
 // the XCD under round-robin dispatch) so their prefix re-reads hit that
 // XCD's L2.  Each beam's short suffix is read from its own paged blocks into
@@ -27,7 +28,7 @@
 namespace gr {
 namespace {
 
-constexpr int MF_THREADS = 256;
+constexpr int MF_THREADS = 512;
 constexpr int MF_ROWS = 128;   // query rows per workgroup
 constexpr int ST_KEYS = 64;    // keys per super-tile (two 32-key halves)
 constexpr int HD = 128;        // head dim
@@ -37,7 +38,8 @@ constexpr int K_TILE = ST_KEYS * KS_PITCH;
 constexpr int VT_TILE = HD * VT_PITCH;
 constexpr int BUF = K_TILE + VT_TILE;  // elements per buffer
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr float RESCALE_THRESH = 8.0f;  // log2 units: rescale O only when the max grows by > 2^8
+constexpr float RESCALE_THRESH = 8.0f;
+constexpr int PBT_WIN = 4096;  // prefix block-table entries staged in LDS  // log2 units: rescale O only when the max grows by > 2^8
 
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
@@ -89,7 +91,7 @@ __device__ inline float pair_sum(float x) { return x + lane_partner(x); }
 
 __device__ inline u32x4_t lds_read16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 
-// Per-lane online-softmax state for one 32-row block.
+// Per-lane online-softmax state of the lane's query row.
 struct RowState {
   float m;     // running max in scaled log2 units (-inf before any visible key)
   float lsum;  // this lane's partial sum of exp2(x - m)
@@ -98,19 +100,20 @@ struct RowState {
 // Softmax of one 32-key x 32-row S^T tile held by this lane (16 keys of its
 // row).  vis: bit r set when register r is a visible key.  Returns the
 // rescale factor for O (1 when unchanged) and writes the packed P operand.
-template <int DT, bool SOFTCAP>
-__device__ inline float softmax_tile(f32x16_t& s, uint32_t vis, RowState& st, float c,
-                                     float cap, u32x4_t& p0, u32x4_t& p1) {
+template <int DT, bool SOFTCAP, bool MASKED>
+__device__ inline float softmax_tile(f32x16_t& s, uint32_t vis, RowState& st, float c, float cap,
+                                     u32x4_t& p0, u32x4_t& p1) {
   float x[16];
   float mx = -INFINITY;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     float v = s[r];
-    if (SOFTCAP) v = cap * tanhf(v * c);  // c = scale / softcap here; x in log2 units below
-    v = (vis >> r) & 1 ? v : -INFINITY;
+    if (SOFTCAP) v = cap * tanhf(v * c);  // c = scale / softcap here
+    if (MASKED) v = (vis >> r) & 1 ? v : -INFINITY;
     x[r] = v;
-    mx = fmaxf(mx, v);
   }
+#pragma unroll
+  for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(x[r], x[r + 1]));
   mx = pair_max(mx);
   // scaled log2-domain maximum of this tile
   const float cs = SOFTCAP ? LOG2E : c;
@@ -137,41 +140,28 @@ __device__ inline float softmax_tile(f32x16_t& s, uint32_t vis, RowState& st, fl
   return alpha;
 }
 
-// One wave: 2 row blocks (64 rows) against one 32-key half-tile in LDS.
-// kbase: first K_s row of the half; vt_col: first V^T column of the half.
-template <int DT, bool SOFTCAP>
-__device__ inline void tile_step(const uint16_t* buf, int kbase, int lane, const u32x4_t (&qf)[2][8],
-                                 f32x16_t (&o)[2][4], RowState (&st)[2], const uint32_t (&vis)[2],
-                                 float c, float cap) {
+// One wave: its 32 query rows against one 32-key half-tile in LDS.
+// kbase: first K_s row / V^T column of the half.
+template <int DT, bool SOFTCAP, bool MASKED>
+__device__ inline void tile_step(const uint16_t* buf, int kbase, int lane, const u32x4_t (&qf)[8],
+                                 f32x16_t (&o)[4], RowState& st, uint32_t vis, float c, float cap) {
   using M = Mma<DT>;
   const int lrow = lane & 31, lhalf = lane >> 5;
   const uint16_t* krow = buf + (kbase + key_perm(lrow)) * KS_PITCH + lhalf * 8;
-  f32x16_t s0 = {}, s1 = {};
+  f32x16_t s = {};
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) {
-    u32x4_t kf = lds_read16(krow + kk * 16);
-    s0 = M::mma(kf, qf[0][kk], s0);
-    s1 = M::mma(kf, qf[1][kk], s1);
-  }
-  u32x4_t p[2][2];
-  float al0 = softmax_tile<DT, SOFTCAP>(s0, vis[0], st[0], c, cap, p[0][0], p[0][1]);
-  float al1 = softmax_tile<DT, SOFTCAP>(s1, vis[1], st[1], c, cap, p[1][0], p[1][1]);
-  if (__ballot(al0 != 1.f || al1 != 1.f) != 0) {  // wave-uniform: rare after the first tiles
+  for (int kk = 0; kk < 8; ++kk) s = M::mma(lds_read16(krow + kk * 16), qf[kk], s);
+  u32x4_t p0, p1;
+  const float al = softmax_tile<DT, SOFTCAP, MASKED>(s, vis, st, c, cap, p0, p1);
+  if (__ballot(al != 1.f) != 0) {  // wave-uniform: rare after the first tiles
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      o[0][mb] *= al0;
-      o[1][mb] *= al1;
-    }
+    for (int mb = 0; mb < 4; ++mb) o[mb] *= al;
   }
   const uint16_t* vt = buf + K_TILE + lrow * VT_PITCH + kbase + lhalf * 8;
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      u32x4_t vf = lds_read16(vt + mb * 32 * VT_PITCH + kk * 16);
-      o[0][mb] = M::mma(vf, p[0][kk], o[0][mb]);
-      o[1][mb] = M::mma(vf, p[1][kk], o[1][mb]);
-    }
+    o[mb] = M::mma(lds_read16(vt + mb * 32 * VT_PITCH), p0, o[mb]);
+    o[mb] = M::mma(lds_read16(vt + mb * 32 * VT_PITCH + 16), p1, o[mb]);
   }
 }
 
@@ -182,137 +172,145 @@ __device__ inline uint32_t regs_from_keymask(uint32_t km, int lhalf) {
   return ((km >> (8 * lhalf)) & 0xFFu) | (((km >> (16 + 8 * lhalf)) & 0xFFu) << 8);
 }
 
-struct Geo {
-  int r, hk, nb0, W, G, TG, rows_r, row_base;
-};
-
 template <int DT, bool SOFTCAP>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF];
   __shared__ uint32_t tile_mask[2][2];   // [buffer][half]: visible keys of the prefix super-tile
-  __shared__ int suf_cum[2][66];         // per row group: cumulative suffix lengths of its beams
-  __shared__ int suf_info[2][ST_KEYS];   // per row group slot: (beam << 16) | j, or -1
+  __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
+  __shared__ int suf_info[4][32];        // per row group slot: (beam << 16) | j, or -1
+  __shared__ int pbt_s[PBT_WIN];         // staged prefix block ids (-1 = invalid)
 
-  // ---- XCD-aware tile placement --------------------------------------------
+  // ---- XCD-aware tile placement: all m-tiles of a (request, KV head) land on
+  // the same XCD (round-robin dispatch puts workgroup i on XCD i % 8)
   const int bid = blockIdx.x;
   const int xcd = bid & 7, local = bid >> 3;
   const int unit = (local / mtiles) * 8 + xcd;
   const int mt = local % mtiles;
   if (unit >= units) return;
-  Geo g;
-  g.r = unit / a.Hkv;
-  g.hk = unit % a.Hkv;
-  g.nb0 = a.beam_start[g.r];
-  g.W = a.beam_start[g.r + 1] - g.nb0;
-  g.G = a.Hq / a.Hkv;
-  g.TG = a.T * g.G;
-  g.rows_r = g.W * g.TG;
-  g.row_base = mt * MF_ROWS;
-  if (g.nb0 < 0 || g.W < 0 || g.nb0 + g.W > a.num_beams) {  // beam_start is device data: never trust it
+  const int r = unit / a.Hkv, hk = unit % a.Hkv;
+  const int nb0 = a.beam_start[r];
+  const int W = a.beam_start[r + 1] - nb0;
+  const int G = a.Hq / a.Hkv, TG = a.T * G;
+  const int rows_r = W * TG;
+  const int row_base = mt * MF_ROWS;
+  if (nb0 < 0 || W < 0 || nb0 + W > a.num_beams) {  // beam_start is device data: never trust it
     if (threadIdx.x == 0 && mt == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
     return;
   }
-  if (g.row_base >= g.rows_r) return;
+  if (row_base >= rows_r) return;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int rg = wave >> 1, ks = wave & 1;  // row group, key half
+  const int rg = wave >> 1, ks = wave & 1;  // row group (32 rows), key half
   const int lrow = lane & 31, lhalf = lane >> 5;
   using S = uint16_t;
   const S* qp = static_cast<const S*>(a.q);
   const S* kc = static_cast<const S*>(a.k_cache);
   const S* vc = static_cast<const S*>(a.v_cache);
-  const int64_t head_off = (int64_t)g.hk * a.kv_head_stride;
+  const int64_t head_off = (int64_t)hk * a.kv_head_stride;
 
-  // ---- Q fragments (B operand of S^T): row = lane % 32 of each block ----
-  u32x4_t qf[2][8];
-  int my_rho[2];
+  // ---- Q fragments (B operand of S^T): this lane's query row ----
+  const int my_rho = row_base + rg * 32 + lrow;
+  const bool row_ok = my_rho < rows_r;
+  const int my_b = my_rho / TG, my_qi = (my_rho / G) % a.T, my_g = my_rho % G;
+  u32x4_t qf[8];
+  {
+    const S* src = qp + (int64_t)((nb0 + my_b) * a.T + my_qi) * a.q_tok_stride +
+                   (int64_t)(hk * G + my_g) * HD + lhalf * 8;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int rho = g.row_base + rg * 64 + rb * 32 + lrow;
-    my_rho[rb] = rho;
-    if (rho < g.rows_r) {
-      const int b = rho / g.TG, qi = (rho / g.G) % a.T, gq = rho % g.G;
-      const S* src = qp + (int64_t)((g.nb0 + b) * a.T + qi) * a.q_tok_stride +
-                     (int64_t)(g.hk * g.G + gq) * HD + lhalf * 8;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) qf[rb][kk] = *reinterpret_cast<const u32x4_t*>(src + kk * 16);
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) qf[rb][kk] = u32x4_t{0, 0, 0, 0};
-    }
+    for (int kk = 0; kk < 8; ++kk)
+      qf[kk] = row_ok ? *reinterpret_cast<const u32x4_t*>(src + kk * 16) : u32x4_t{0, 0, 0, 0};
   }
   const float c = SOFTCAP ? a.scale / a.softcap : a.scale * LOG2E;
   const float cap = a.softcap;
 
-  f32x16_t o[2][4];
+  f32x16_t o[4];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) o[rb][mb] = f32x16_t{};
-  RowState st[2] = {{-INFINITY, 0.f}, {-INFINITY, 0.f}};
+  for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
+  RowState st = {-INFINITY, 0.f};
 
   // ---- prefix: 64-key super-tiles, double-buffered through LDS ------------
   const int pre_cap = a.prefix_bt_stride * a.bs;
-  int P = a.prefix_len[g.r];
+  int P = a.prefix_len[r];
   if (P < 0 || P > pre_cap) {
     if (tid == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
     P = P < 0 ? 0 : pre_cap;
   }
-  const int32_t* pbt = a.prefix_bt + (int64_t)g.r * a.prefix_bt_stride;
+  const int32_t* pbt = a.prefix_bt + (int64_t)r * a.prefix_bt_stride;
   const int n_st = (P + ST_KEYS - 1) / ST_KEYS;
+  const int bsh = a.bs_shift;
 
-  // loader roles: K rows key = (tid>>4) + 16j, 16-byte chunk tid&15;
-  //               V rows 4*(tid>>4) .. +3 for chunk tid&15 (written transposed)
-  const int lk = tid >> 4, lc = tid & 15;
-  u32x4_t kreg[4], vreg[4];
-  auto block_of = [&](int key, bool& ok) -> int64_t {
-    int blk = pbt[key / a.bs];
-    ok = blk >= 0 && blk < a.num_blocks;
-    if (!ok) flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
-    return (int64_t)blk * a.kv_block_stride + (int64_t)(key % a.bs) * a.kv_tok_stride;
-  };
-  auto load_prefix = [&](int k0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int key = k0 + lk + 16 * j;
-      bool ok = false;
-      int64_t base = key < P ? block_of(key, ok) : 0;
-      kreg[j] = ok ? *reinterpret_cast<const u32x4_t*>(kc + base + head_off + lc * 8) : u32x4_t{0, 0, 0, 0};
+  // The request's prefix block-table row is staged in LDS (a window of
+  // PBT_WIN entries), validated once; invalid ids become -1 and read as zeros.
+  // Tile loads then need no dependent global reads and no atomics.
+  const int nblk = (P + a.bs - 1) / a.bs;
+  int win0 = 0;
+  auto load_window = [&](int w0) {
+    for (int i = tid; i < PBT_WIN; i += MF_THREADS) {
+      const int bi = w0 + i;
+      int blk = -1;
+      if (bi < nblk) {
+        blk = pbt[bi];
+        if (blk < 0 || blk >= a.num_blocks) {
+          flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
+          blk = -1;
+        }
+      }
+      pbt_s[i] = blk;
     }
+  };
+  load_window(0);
+  __syncthreads();
+
+  // loader roles: thread (lk, lc) moves keys 2*lk and 2*lk+1 (one block: the
+  // block size is a power of two >= 4), 16-byte chunk lc of K and of V; V is
+  // written transposed as 32-bit key pairs.
+  const int lk = tid >> 4, lc = tid & 15;
+  u32x4_t kreg[2], vreg[2];
+  auto load_prefix = [&](int k0) {
+    const int key0 = k0 + 2 * lk;
+    const int blk = key0 < P ? pbt_s[(key0 >> bsh) - win0] : -1;
+    const int64_t off = (int64_t)(blk < 0 ? 0 : blk) * a.kv_block_stride +
+                        (int64_t)(key0 & (a.bs - 1)) * a.kv_tok_stride + head_off + lc * 8;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int key = k0 + 4 * lk + j;
-      bool ok = false;
-      int64_t base = key < P ? block_of(key, ok) : 0;
-      vreg[j] = ok ? *reinterpret_cast<const u32x4_t*>(vc + base + head_off + lc * 8) : u32x4_t{0, 0, 0, 0};
+    for (int j = 0; j < 2; ++j) {
+      kreg[j] = u32x4_t{0, 0, 0, 0};
+      vreg[j] = u32x4_t{0, 0, 0, 0};
+      if (blk >= 0 && key0 + j < P) {
+        kreg[j] = *reinterpret_cast<const u32x4_t*>(kc + off + j * a.kv_tok_stride);
+        vreg[j] = *reinterpret_cast<const u32x4_t*>(vc + off + j * a.kv_tok_stride);
+      }
+    }
+  };
+  // keep the window over [k0, k0 + 64); switching costs two barriers and
+  // happens once per PBT_WIN blocks
+  auto ensure_window = [&](int k0) {
+    const int last = min(k0 + ST_KEYS, P) - 1;
+    if ((k0 >> bsh) < win0 || (last >> bsh) >= win0 + PBT_WIN) {
+      __syncthreads();
+      win0 = k0 >> bsh;
+      load_window(win0);
+      __syncthreads();
     }
   };
   auto store_tile = [&](uint16_t* buf) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<u32x4_t*>(buf + (lk + 16 * j) * KS_PITCH + lc * 8) = kreg[j];
-    // transpose 4 keys x 8 dims -> 8 dims x 4 keys (8-byte writes)
-    uint16_t* vt = buf + K_TILE + (lc * 8) * VT_PITCH + 4 * lk;
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<u32x4_t*>(buf + (2 * lk + j) * KS_PITCH + lc * 8) = kreg[j];
+    // transpose 2 keys x 8 dims -> 8 dims x 2 keys (4-byte writes)
+    uint16_t* vt = buf + K_TILE + (lc * 8) * VT_PITCH + 2 * lk;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const uint32_t a0 = vreg[0][w], a1 = vreg[1][w], a2 = vreg[2][w], a3 = vreg[3][w];
-      // dim 2w of keys (0,1),(2,3) and dim 2w+1 of the same keys
-      const u32x2_t lo = {(a0 & 0xFFFFu) | (a1 << 16), (a2 & 0xFFFFu) | (a3 << 16)};
-      const u32x2_t hi = {(a0 >> 16) | (a1 & 0xFFFF0000u), (a2 >> 16) | (a3 & 0xFFFF0000u)};
-      *reinterpret_cast<u32x2_t*>(vt + (2 * w) * VT_PITCH) = lo;
-      *reinterpret_cast<u32x2_t*>(vt + (2 * w + 1) * VT_PITCH) = hi;
+      const uint32_t a0 = vreg[0][w], a1 = vreg[1][w];
+      *reinterpret_cast<uint32_t*>(vt + (2 * w) * VT_PITCH) = (a0 & 0xFFFFu) | (a1 << 16);
+      *reinterpret_cast<uint32_t*>(vt + (2 * w + 1) * VT_PITCH) = (a0 >> 16) | (a1 & 0xFFFF0000u);
     }
   };
   auto store_mask = [&](int bsel, int k0) {
     if (wave == 0) {
       const int key = k0 + lane;
-      bool ok = false;
-      if (key < P) {
-        int blk = pbt[key / a.bs];
-        ok = blk >= 0 && blk < a.num_blocks;
-      }
-      uint64_t m = __ballot(ok);
+      const bool ok = key < P && pbt_s[(key >> bsh) - win0] >= 0;
+      const uint64_t m = __ballot(ok);
       if (lane == 0) {
         tile_mask[bsel][0] = (uint32_t)m;
         tile_mask[bsel][1] = (uint32_t)(m >> 32);
@@ -321,6 +319,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   };
 
   if (n_st > 0) {
+    ensure_window(0);
     load_prefix(0);
     store_tile(lds);
     store_mask(0, 0);
@@ -329,12 +328,17 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   for (int it = 0; it < n_st; ++it) {
     const int cur = it & 1;
     const bool more = it + 1 < n_st;
-    if (more) load_prefix((it + 1) * ST_KEYS);
+    if (more) {
+      ensure_window((it + 1) * ST_KEYS);
+      load_prefix((it + 1) * ST_KEYS);
+    }
     const uint16_t* buf = lds + cur * BUF;
     const uint32_t km = tile_mask[cur][ks];
-    const uint32_t vreg_bits = regs_from_keymask(km, lhalf);
-    const uint32_t vis[2] = {vreg_bits, vreg_bits};
-    tile_step<DT, SOFTCAP>(buf, ks * 32, lane, qf, o, st, vis, c, cap);
+    if (km == 0xFFFFFFFFu) {
+      tile_step<DT, SOFTCAP, false>(buf, ks * 32, lane, qf, o, st, 0xFFFFu, c, cap);
+    } else {
+      tile_step<DT, SOFTCAP, true>(buf, ks * 32, lane, qf, o, st, regs_from_keymask(km, lhalf), c, cap);
+    }
     if (more) {
       store_tile(lds + (cur ^ 1) * BUF);
       store_mask(cur ^ 1, (it + 1) * ST_KEYS);
@@ -343,56 +347,57 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   }
 
   // ---- suffix: each row group's beams' own tokens, masked 32-key tiles ----
-  // beams touching row group rg: [b_lo, b_hi]
+  // (computed by the key-half-0 wave of each row group; all threads load)
   const int suf_cap = a.suffix_bt_stride * a.bs;
   if (ks == 0) {
-    const int rlo = g.row_base + rg * 64;
-    const int b_lo = rlo / g.TG;
-    const int b_hi = min((rlo + 63) / g.TG, g.W - 1);
-    const int nbeams = rlo < g.rows_r ? b_hi - b_lo + 1 : 0;
+    const int rlo = row_base + rg * 32;
+    const int b_lo = rlo / TG;
+    const int b_hi = min((rlo + 31) / TG, W - 1);
+    const int nbeams = rlo < rows_r ? b_hi - b_lo + 1 : 0;  // <= 32
     int len = 0;
     if (lane < nbeams) {
-      const int n = g.nb0 + b_lo + lane;
+      const int n = nb0 + b_lo + lane;
       const int L = a.suffix_len[n];
       const int s0 = a.suffix_start ? a.suffix_start[n] : 0;
       len = (L < 0 || s0 < 0 || s0 + L > suf_cap) ? 0 : L;
       if (len != L) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
     }
-    // inclusive wave scan
-    int incl = len;
+    int incl = len;  // inclusive scan over the first 32 lanes
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      int y = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += y;
+    for (int off = 1; off < 32; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if ((lane & 31) >= off) incl += y;
     }
-    suf_cum[rg][lane + 1] = incl;
+    if (lane < 32) suf_cum[rg][lane + 1] = incl;
     if (lane == 0) {
       suf_cum[rg][0] = 0;
-      suf_cum[rg][65] = b_lo;  // stash: first beam of the group
+      suf_cum[rg][33] = b_lo;  // first beam of the group
     }
   }
   __syncthreads();
-  const int tot0 = suf_cum[0][64], tot1 = suf_cum[1][64];
-  const int n_sit = (max(tot0, tot1) + ST_KEYS - 1) / ST_KEYS;
+  int max_tot = 0;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) max_tot = max(max_tot, suf_cum[g][32]);
+  const int n_sit = (max_tot + 31) / 32;
   for (int it = 0; it < n_sit; ++it) {
-    // loader: 2 row groups x 64 slots x 16 chunks for K and for V
-    for (int e = tid; e < 2 * ST_KEYS * 16; e += MF_THREADS) {
-      const int grp = e / (ST_KEYS * 16);
-      const int slot = (e / 16) % ST_KEYS;
-      const int ch = e % 16;
-      const int gs = it * ST_KEYS + slot;
-      const int tot = suf_cum[grp][64];
+    // loader: 4 row groups x 32 slots x 16 chunks; row group g's slots live in
+    // buffer g >> 1, rows / columns (g & 1) * 32 .. + 31
+    for (int e = tid; e < 4 * 32 * 16; e += MF_THREADS) {
+      const int grp = e >> 9;
+      const int slot = (e >> 4) & 31;
+      const int ch = e & 15;
+      const int gs = it * 32 + slot;
       u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
       int info = -1;
-      if (gs < tot) {
-        int lo = 0, hi = 63;  // largest beam index i with cum[i] <= gs
+      if (gs < suf_cum[grp][32]) {
+        int lo = 0, hi = 31;  // largest beam index i with cum[i] <= gs (skips empty beams)
         while (lo < hi) {
-          int mid = (lo + hi + 1) >> 1;
+          const int mid = (lo + hi + 1) >> 1;
           if (suf_cum[grp][mid] <= gs) lo = mid; else hi = mid - 1;
         }
-        const int b = suf_cum[grp][65] + lo;
+        const int b = suf_cum[grp][33] + lo;
         const int j = gs - suf_cum[grp][lo];
-        const int n = g.nb0 + b;
+        const int n = nb0 + b;
         const int pos = (a.suffix_start ? a.suffix_start[n] : 0) + j;
         const int blk = a.suffix_bt[(int64_t)n * a.suffix_bt_stride + pos / a.bs];
         if (blk >= 0 && blk < a.num_blocks) {
@@ -405,9 +410,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
           flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
         }
       }
-      uint16_t* buf = lds + grp * BUF;
-      *reinterpret_cast<u32x4_t*>(buf + slot * KS_PITCH + ch * 8) = kv;
-      uint16_t* vt = buf + K_TILE + (ch * 8) * VT_PITCH + slot;
+      uint16_t* buf = lds + (grp >> 1) * BUF;
+      const int key = (grp & 1) * 32 + slot;
+      *reinterpret_cast<u32x4_t*>(buf + key * KS_PITCH + ch * 8) = kv;
+      uint16_t* vt = buf + K_TILE + (ch * 8) * VT_PITCH + key;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         vt[(2 * w) * VT_PITCH] = (uint16_t)(vv[w] & 0xFFFFu);
@@ -416,81 +422,61 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       if (ch == 0) suf_info[grp][slot] = info;
     }
     __syncthreads();
-    // visibility: register r of this lane is key 16*(r>>3) + 8*lhalf + (r&7) of half ks
-    uint32_t vis[2];
+    if (ks == 0) {
+      // register r of this lane is slot 16*(r>>3) + 8*lhalf + (r&7) of the group's 32
+      const int lim = row_ok ? a.suffix_len[nb0 + my_b] - a.T + my_qi : -1;
+      uint32_t vis = 0;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const int rho = my_rho[rb];
-      const int b = rho / g.TG, qi = (rho / g.G) % a.T;
-      int lim = -1;
-      if (rho < g.rows_r) {
-        const int n = g.nb0 + b;
-        lim = a.suffix_len[n] - a.T + qi;
+      for (int rr = 0; rr < 16; ++rr) {
+        const int info = suf_info[rg][16 * (rr >> 3) + 8 * lhalf + (rr & 7)];
+        const bool ok = info >= 0 && (info >> 16) == my_b && (info & 0xFFFF) <= lim;
+        vis |= (ok ? 1u : 0u) << rr;
       }
-      uint32_t bits = 0;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = ks * 32 + 16 * (r >> 3) + 8 * lhalf + (r & 7);
-        const int info = suf_info[rg][key];
-        const bool ok = info >= 0 && (info >> 16) == b && (info & 0xFFFF) <= lim;
-        bits |= (ok ? 1u : 0u) << r;
-      }
-      vis[rb] = bits;
+      tile_step<DT, SOFTCAP, true>(lds + (rg >> 1) * BUF, (rg & 1) * 32, lane, qf, o, st, vis, c, cap);
     }
-    tile_step<DT, SOFTCAP>(lds + rg * BUF, ks * 32, lane, qf, o, st, vis, c, cap);
     __syncthreads();
   }
 
   // ---- merge the two key halves and write O, LSE --------------------------
-  float* xch = reinterpret_cast<float*>(lds);  // [rg][rb*4+mb][16][64] + m/l
-  float* xo = xch + rg * (2 * 4 * 16 * 64);
-  float* xm = reinterpret_cast<float*>(lds) + 2 * (2 * 4 * 16 * 64) + rg * (4 * 64);
+  float* xo = reinterpret_cast<float*>(lds) + rg * (4 * 16 * 64);           // [rg][mb][r][lane]
+  float* xm = reinterpret_cast<float*>(lds) + 4 * (4 * 16 * 64) + rg * 128;  // [rg][m | lsum][lane]
   if (ks == 1) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) xo[((rb * 4 + mb) * 16 + r) * 64 + lane] = o[rb][mb][r];
-      xm[rb * 64 + lane] = st[rb].m;
-      xm[(2 + rb) * 64 + lane] = st[rb].lsum;
-    }
+      for (int rr = 0; rr < 16; ++rr) xo[(mb * 16 + rr) * 64 + lane] = o[mb][rr];
+    xm[lane] = st.m;
+    xm[64 + lane] = st.lsum;
   }
   __syncthreads();
   if (ks == 0) {
-    S* outp = static_cast<S*>(a.out);
+    const float m1 = xm[lane], l1 = xm[64 + lane];
+    const float m0 = st.m, l0 = st.lsum;
+    const float m = fmaxf(m0, m1);
+    const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
+    const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+    const float lrow_sum = pair_sum(l0 * a0 + l1 * a1);
+    const float inv = lrow_sum > 0.f ? 1.f / lrow_sum : 0.f;
+    if (row_ok) {
+      const int64_t tok = (int64_t)(nb0 + my_b) * a.T + my_qi;
+      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + my_g) * HD + 4 * lhalf;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const float m1 = xm[rb * 64 + lane], l1 = xm[(2 + rb) * 64 + lane];
-      const float m0 = st[rb].m, l0 = st[rb].lsum;
-      const float m = fmaxf(m0, m1);
-      const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
-      const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
-      const float lrow_sum = pair_sum(l0 * a0 + l1 * a1);
-      const float inv = lrow_sum > 0.f ? 1.f / lrow_sum : 0.f;
-      const int rho = my_rho[rb];
-      if (rho < g.rows_r) {
-        const int b = rho / g.TG, qi = (rho / g.G) % a.T, gq = rho % g.G;
-        const int64_t tok = (int64_t)(g.nb0 + b) * a.T + qi;
-        S* dst = outp + tok * a.out_tok_stride + (int64_t)(g.hk * g.G + gq) * HD + 4 * lhalf;
+      for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
+        for (int qd = 0; qd < 4; ++qd) {
+          float v[4];
 #pragma unroll
-          for (int qd = 0; qd < 4; ++qd) {
-            float v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int r = qd * 4 + u;
-              v[u] = (o[rb][mb][r] * a0 + xo[((rb * 4 + mb) * 16 + r) * 64 + lane] * a1) * inv;
-            }
-            const u32x2_t w = {Mma<DT>::pack2(v[0], v[1]), Mma<DT>::pack2(v[2], v[3])};
-            *reinterpret_cast<u32x2_t*>(dst + mb * 32 + qd * 8) = w;
+          for (int u = 0; u < 4; ++u) {
+            const int rr = qd * 4 + u;
+            v[u] = (o[mb][rr] * a0 + xo[(mb * 16 + rr) * 64 + lane] * a1) * inv;
           }
+          const u32x2_t w = {Mma<DT>::pack2(v[0], v[1]), Mma<DT>::pack2(v[2], v[3])};
+          *reinterpret_cast<u32x2_t*>(dst + mb * 32 + qd * 8) = w;
         }
-        if (a.lse_out && lhalf == 0) {
-          a.lse_out[tok * a.Hq + g.hk * g.G + gq] =
-              lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
-        }
+      }
+      if (a.lse_out && lhalf == 0) {
+        a.lse_out[tok * a.Hq + hk * G + my_g] =
+            lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
       }
     }
   }
@@ -500,6 +486,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 
 bool mfma_decode_supported(const DecodeArgs& a) {
   if (a.D != HD || (a.dtype != GR_DTYPE_BF16 && a.dtype != GR_DTYPE_F16)) return false;
+  if (a.bs_shift < 2) return false;  // power-of-two block size >= 4
   // 16-byte vector access: base pointers and element strides multiples of 8 elements
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!al(a.q) || !al(a.out) || !al(a.k_cache) || !al(a.v_cache)) return false;
