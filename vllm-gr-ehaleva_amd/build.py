@@ -32,6 +32,8 @@ COMMON = [
 EXTRA = {
     # bit-exact pruning numerics: no mul+add fusion anywhere in this file
     "gr_prune.hip": ["-ffp-contract=off", "-Wno-pass-failed"],
+    # masking uses -inf, never NaN: lets fmaxf lower to v_max3_f32 without canonicalisation
+    "gr_attn_mfma.hip": ["-fno-honor-nans"],
 }
 
 

@@ -21,8 +21,11 @@
 // online softmax needs no cross-lane traffic except the lane-pair (l, l^32)
 // max/sum.  K rows are fed to the A operand through the permutation PI that
 // swaps bits 2 and 3 of the row index; with it the S^T accumulator registers
-// of each lane hold keys in exactly the order the PV B operand needs, and
-// V^T is read from LDS as plain 16-byte rows.
+// of each lane hold keys in exactly the order the PV B operand needs.  V stays
+// in its natural [key][d] layout in LDS and the V^T operand is assembled with
+// gfx950's transposing LDS read (ds_read_b64_tr_b16): in each 16-lane group,
+// source lane s addresses V[k0 + s/4][d0 + 4*(s%4) .. +3] and lane i receives
+// V[k0 .. k0+3][d0 + i].
 #include "gr_attn_decode.h"
 
 namespace gr {
@@ -32,11 +35,11 @@ constexpr int MF_THREADS = 512;
 constexpr int MF_ROWS = 128;   // query rows per workgroup
 constexpr int ST_KEYS = 64;    // keys per super-tile (two 32-key halves)
 constexpr int HD = 128;        // head dim
-constexpr int KS_PITCH = 136;  // K tile row pitch in elements (272 B)
-constexpr int VT_PITCH = 72;   // V^T tile row pitch in elements (144 B)
+constexpr int KS_PITCH = 128;  // K tile row pitch in elements (256 B); 16-byte chunks XOR-swizzled
+constexpr int VS_PITCH = 160;  // V tile row pitch in elements (320 B): rows alternate 64-byte bank halves
 constexpr int K_TILE = ST_KEYS * KS_PITCH;
-constexpr int VT_TILE = HD * VT_PITCH;
-constexpr int BUF = K_TILE + VT_TILE;  // elements per buffer
+constexpr int V_TILE = ST_KEYS * VS_PITCH;
+constexpr int BUF = K_TILE + V_TILE;  // elements per buffer
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESH = 8.0f;
 constexpr int PBT_WIN = 4096;  // prefix block-table entries staged in LDS  // log2 units: rescale O only when the max grows by > 2^8
@@ -73,6 +76,19 @@ template <> struct Mma<GR_DTYPE_F16> {
 
 // S^T row slot i holds tile key PI(i): bits 2 and 3 swapped.
 __device__ inline int key_perm(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+// Physical 16-byte chunk of logical chunk c in K tile row `row`.  The A
+// operand reads rows PI(0..7) = {0..3, 8..11} (and +4, +16) in one 8-lane
+// group; the XOR spreads those rows over 8 distinct 16-byte bank groups.
+__device__ inline int kchunk(int row, int c) { return c ^ ((row & 3) | (((row >> 3) & 1) << 2)); }
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+// 4 keys x 1 dim per lane via the transposing LDS read (see the header comment)
+__device__ inline uint2 lds_read_tr(const uint16_t* p) {
+  auto v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_t*)(reinterpret_cast<uintptr_t>(p)));
+  return __builtin_bit_cast(uint2, v);
+}
 
 // Value of x held by lane l ^ 32 (the other lane of the same query row).
 // v_permlane32_swap exchanges the upper 32 lanes of its first operand with the
@@ -147,21 +163,31 @@ __device__ inline void tile_step(const uint16_t* buf, int kbase, int lane, const
                                  f32x16_t (&o)[4], RowState& st, uint32_t vis, float c, float cap) {
   using M = Mma<DT>;
   const int lrow = lane & 31, lhalf = lane >> 5;
-  const uint16_t* krow = buf + (kbase + key_perm(lrow)) * KS_PITCH + lhalf * 8;
+  const int krow_i = kbase + key_perm(lrow);
+  const uint16_t* krow = buf + krow_i * KS_PITCH;
   f32x16_t s = {};
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) s = M::mma(lds_read16(krow + kk * 16), qf[kk], s);
+  for (int kk = 0; kk < 8; ++kk)
+    s = M::mma(lds_read16(krow + kchunk(krow_i, 2 * kk + lhalf) * 8), qf[kk], s);
   u32x4_t p0, p1;
   const float al = softmax_tile<DT, SOFTCAP, MASKED>(s, vis, st, c, cap, p0, p1);
   if (__ballot(al != 1.f) != 0) {  // wave-uniform: rare after the first tiles
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) o[mb] *= al;
   }
-  const uint16_t* vt = buf + K_TILE + lrow * VT_PITCH + kbase + lhalf * 8;
+  // V^T operand: lane group g = lane/16 covers dims 16*(g&1) .. +15 of the
+  // 32-dim block and keys 8*(g>>1) .. +7 of the 16-key step (two 4-key reads)
+  const int g = lane >> 4, sl = lane & 15;
+  const uint16_t* vsrc = buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
-    o[mb] = M::mma(lds_read16(vt + mb * 32 * VT_PITCH), p0, o[mb]);
-    o[mb] = M::mma(lds_read16(vt + mb * 32 * VT_PITCH + 16), p1, o[mb]);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint16_t* vp = vsrc + (16 * kk) * VS_PITCH + 32 * mb;
+      const uint2 lo = lds_read_tr(vp);
+      const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
+      o[mb] = M::mma(u32x4_t{lo.x, lo.y, hi.x, hi.y}, kk ? p1 : p0, o[mb]);
+    }
   }
 }
 
@@ -263,8 +289,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   __syncthreads();
 
   // loader roles: thread (lk, lc) moves keys 2*lk and 2*lk+1 (one block: the
-  // block size is a power of two >= 4), 16-byte chunk lc of K and of V; V is
-  // written transposed as 32-bit key pairs.
+  // block size is a power of two >= 4), 16-byte chunk lc of K and of V.
   const int lk = tid >> 4, lc = tid & 15;
   u32x4_t kreg[2], vreg[2];
   auto load_prefix = [&](int k0) {
@@ -295,15 +320,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   };
   auto store_tile = [&](uint16_t* buf) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<u32x4_t*>(buf + (2 * lk + j) * KS_PITCH + lc * 8) = kreg[j];
-    // transpose 2 keys x 8 dims -> 8 dims x 2 keys (4-byte writes)
-    uint16_t* vt = buf + K_TILE + (lc * 8) * VT_PITCH + 2 * lk;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t a0 = vreg[0][w], a1 = vreg[1][w];
-      *reinterpret_cast<uint32_t*>(vt + (2 * w) * VT_PITCH) = (a0 & 0xFFFFu) | (a1 << 16);
-      *reinterpret_cast<uint32_t*>(vt + (2 * w + 1) * VT_PITCH) = (a0 >> 16) | (a1 & 0xFFFF0000u);
+    for (int j = 0; j < 2; ++j) {
+      const int row = 2 * lk + j;
+      *reinterpret_cast<u32x4_t*>(buf + row * KS_PITCH + kchunk(row, lc) * 8) = kreg[j];
+      *reinterpret_cast<u32x4_t*>(buf + K_TILE + row * VS_PITCH + lc * 8) = vreg[j];
     }
   };
   auto store_mask = [&](int bsel, int k0) {
@@ -412,13 +432,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       }
       uint16_t* buf = lds + (grp >> 1) * BUF;
       const int key = (grp & 1) * 32 + slot;
-      *reinterpret_cast<u32x4_t*>(buf + key * KS_PITCH + ch * 8) = kv;
-      uint16_t* vt = buf + K_TILE + (ch * 8) * VT_PITCH + key;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        vt[(2 * w) * VT_PITCH] = (uint16_t)(vv[w] & 0xFFFFu);
-        vt[(2 * w + 1) * VT_PITCH] = (uint16_t)(vv[w] >> 16);
-      }
+      *reinterpret_cast<u32x4_t*>(buf + key * KS_PITCH + kchunk(key, ch) * 8) = kv;
+      *reinterpret_cast<u32x4_t*>(buf + K_TILE + key * VS_PITCH + ch * 8) = vv;
       if (ch == 0) suf_info[grp][slot] = info;
     }
     __syncthreads();
