@@ -42,13 +42,16 @@ constexpr int V_TILE = ST_KEYS * VS_PITCH;
 constexpr int BUF = K_TILE + V_TILE;  // elements per buffer
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESH = 8.0f;
-constexpr int PBT_WIN = 4096;  // prefix block-table entries staged in LDS  // log2 units: rescale O only when the max grows by > 2^8
+constexpr int PBT_WIN = 2048;  // prefix block-table entries staged in LDS
+constexpr int NBUF = 3;        // LDS tile buffers (V of tile t, K of tile t+1, fill of tile t+2)  // log2 units: rescale O only when the max grows by > 2^8
 
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
 typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
 typedef uint32_t u32x4_t __attribute__((__vector_size__(4 * sizeof(uint32_t))));
 typedef uint32_t u32x2_t __attribute__((__vector_size__(2 * sizeof(uint32_t))));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 template <int DT> struct Mma;
 template <> struct Mma<GR_DTYPE_BF16> {
@@ -58,8 +61,7 @@ template <> struct Mma<GR_DTYPE_BF16> {
                                                    __builtin_bit_cast(vec, b), c, 0, 0, 0);
   }
   __device__ static inline uint32_t pack2(float lo, float hi) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+    return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});  // one v_cvt_pk_bf16_f32
   }
 };
 template <> struct Mma<GR_DTYPE_F16> {
@@ -69,8 +71,7 @@ template <> struct Mma<GR_DTYPE_F16> {
                                                   __builtin_bit_cast(vec, b), c, 0, 0, 0);
   }
   __device__ static inline uint32_t pack2(float lo, float hi) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+    return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)lo, (_Float16)hi});
   }
 };
 
@@ -158,9 +159,9 @@ __device__ inline float softmax_tile(f32x16_t& s, uint32_t vis, RowState& st, fl
 
 // One wave: its 32 query rows against one 32-key half-tile in LDS.
 // kbase: first K_s row / V^T column of the half.
-template <int DT, bool SOFTCAP, bool MASKED>
-__device__ inline void tile_step(const uint16_t* buf, int kbase, int lane, const u32x4_t (&qf)[8],
-                                 f32x16_t (&o)[4], RowState& st, uint32_t vis, float c, float cap) {
+// S^T for this wave's 32 rows against the 32-key half-tile at row kbase.
+template <int DT>
+__device__ inline f32x16_t qk(const uint16_t* buf, int kbase, int lane, const u32x4_t (&qf)[8]) {
   using M = Mma<DT>;
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int krow_i = kbase + key_perm(lrow);
@@ -169,14 +170,15 @@ __device__ inline void tile_step(const uint16_t* buf, int kbase, int lane, const
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk)
     s = M::mma(lds_read16(krow + kchunk(krow_i, 2 * kk + lhalf) * 8), qf[kk], s);
-  u32x4_t p0, p1;
-  const float al = softmax_tile<DT, SOFTCAP, MASKED>(s, vis, st, c, cap, p0, p1);
-  if (__ballot(al != 1.f) != 0) {  // wave-uniform: rare after the first tiles
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) o[mb] *= al;
-  }
-  // V^T operand: lane group g = lane/16 covers dims 16*(g&1) .. +15 of the
-  // 32-dim block and keys 8*(g>>1) .. +7 of the 16-key step (two 4-key reads)
+  return s;
+}
+
+// O += V^T . P^T for the 32-key half-tile at row kbase.  The V^T operand:
+// lane group g = lane/16 covers dims 16*(g&1) .. +15 of the 32-dim block and
+// keys 8*(g>>1) .. +7 of the 16-key step (two 4-key transposing reads).
+template <int DT>
+__device__ inline void pv(const uint16_t* buf, int kbase, int lane, u32x4_t p0, u32x4_t p1, f32x16_t (&o)[4]) {
+  using M = Mma<DT>;
   const int g = lane >> 4, sl = lane & 15;
   const uint16_t* vsrc = buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
 #pragma unroll
@@ -191,6 +193,35 @@ __device__ inline void tile_step(const uint16_t* buf, int kbase, int lane, const
   }
 }
 
+// One pipelined step of a wave: the softmax of the current tile's scores
+// (VALU) is interleaved with the QK^T of the next tile (matrix core), then
+// the current tile's PV.  s_cur holds S^T of the current tile on entry and of
+// the next tile on exit (when has_next).
+template <int DT, bool SOFTCAP, bool MASKED>
+__device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_buf, bool has_next, int kbase,
+                                 int lane, const u32x4_t (&qf)[8], f32x16_t& s_cur, f32x16_t (&o)[4],
+                                 RowState& st, uint32_t vis, float c, float cap) {
+  f32x16_t s_next = {};
+  if (has_next) s_next = qk<DT>(next_buf, kbase, lane, qf);
+  u32x4_t p0, p1;
+  const float al = softmax_tile<DT, SOFTCAP, MASKED>(s_cur, vis, st, c, cap, p0, p1);
+  if (has_next) {
+    // interleave: one MFMA of the next tile's QK^T per group of softmax VALU ops
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read (next K fragment)
+      __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
+    }
+  }
+  if (__ballot(al != 1.f) != 0) {  // wave-uniform: rare after the first tiles
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) o[mb] *= al;
+  }
+  pv<DT>(cur_buf, kbase, lane, p0, p1, o);
+  s_cur = s_next;
+}
+
 // Visibility bits of the 16 registers of a lane from a 32-bit key mask of
 // the half-tile (bit k = tile key k visible): register r holds key
 // 16*(r>>3) + 8*lhalf + (r&7).
@@ -200,8 +231,8 @@ __device__ inline uint32_t regs_from_keymask(uint32_t km, int lhalf) {
 
 template <int DT, bool SOFTCAP>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF];
-  __shared__ uint32_t tile_mask[2][2];   // [buffer][half]: visible keys of the prefix super-tile
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF];
+  __shared__ uint32_t tile_mask[NBUF][2];  // [buffer][half]: visible keys of the prefix super-tile
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
   __shared__ int suf_info[4][32];        // per row group slot: (beam << 16) | j, or -1
   __shared__ int pbt_s[PBT_WIN];         // staged prefix block ids (-1 = invalid)
@@ -338,30 +369,44 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     }
   };
 
+  // Three LDS buffers: during step t the wave reads V of tile t, K of tile
+  // t+1, while tile t+2 (loaded into registers at the start of the step) is
+  // stored into the third buffer at its end.
   if (n_st > 0) {
     ensure_window(0);
     load_prefix(0);
     store_tile(lds);
     store_mask(0, 0);
   }
+  if (n_st > 1) {
+    ensure_window(ST_KEYS);
+    load_prefix(ST_KEYS);
+    store_tile(lds + BUF);
+    store_mask(1, ST_KEYS);
+  }
   __syncthreads();
+  f32x16_t s_cur = {};
+  if (n_st > 0) s_cur = qk<DT>(lds, ks * 32, lane, qf);
   for (int it = 0; it < n_st; ++it) {
-    const int cur = it & 1;
-    const bool more = it + 1 < n_st;
-    if (more) {
-      ensure_window((it + 1) * ST_KEYS);
-      load_prefix((it + 1) * ST_KEYS);
+    const int cur = it % NBUF, nxt = (it + 1) % NBUF, fill = (it + 2) % NBUF;
+    const bool fetch = it + 2 < n_st;
+    if (fetch) {
+      ensure_window((it + 2) * ST_KEYS);
+      load_prefix((it + 2) * ST_KEYS);
     }
     const uint16_t* buf = lds + cur * BUF;
+    const uint16_t* nbuf = lds + nxt * BUF;
+    const bool has_next = it + 1 < n_st;
     const uint32_t km = tile_mask[cur][ks];
     if (km == 0xFFFFFFFFu) {
-      tile_step<DT, SOFTCAP, false>(buf, ks * 32, lane, qf, o, st, 0xFFFFu, c, cap);
+      pipe_step<DT, SOFTCAP, false>(buf, nbuf, has_next, ks * 32, lane, qf, s_cur, o, st, 0xFFFFu, c, cap);
     } else {
-      tile_step<DT, SOFTCAP, true>(buf, ks * 32, lane, qf, o, st, regs_from_keymask(km, lhalf), c, cap);
+      pipe_step<DT, SOFTCAP, true>(buf, nbuf, has_next, ks * 32, lane, qf, s_cur, o, st,
+                                   regs_from_keymask(km, lhalf), c, cap);
     }
-    if (more) {
-      store_tile(lds + (cur ^ 1) * BUF);
-      store_mask(cur ^ 1, (it + 1) * ST_KEYS);
+    if (fetch) {
+      store_tile(lds + fill * BUF);
+      store_mask(fill, (it + 2) * ST_KEYS);
     }
     __syncthreads();
   }
@@ -447,7 +492,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         const bool ok = info >= 0 && (info >> 16) == my_b && (info & 0xFFFF) <= lim;
         vis |= (ok ? 1u : 0u) << rr;
       }
-      tile_step<DT, SOFTCAP, true>(lds + (rg >> 1) * BUF, (rg & 1) * 32, lane, qf, o, st, vis, c, cap);
+      const uint16_t* sbuf = lds + (rg >> 1) * BUF;
+      f32x16_t s_t = qk<DT>(sbuf, (rg & 1) * 32, lane, qf);
+      pipe_step<DT, SOFTCAP, true>(sbuf, sbuf, false, (rg & 1) * 32, lane, qf, s_t, o, st, vis, c, cap);
     }
     __syncthreads();
   }
