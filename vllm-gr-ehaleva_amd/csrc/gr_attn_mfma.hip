@@ -278,6 +278,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     for (int kk = 0; kk < 8; ++kk)
       qf[kk] = row_ok ? *reinterpret_cast<const u32x4_t*>(src + kk * 16) : u32x4_t{0, 0, 0, 0};
   }
+  // Retire the Q loads here: the main loop's first read of qf is otherwise
+  // preceded by a full vector-memory wait in every iteration, which also
+  // waits for the tile prefetch issued at the top of the iteration.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   const float c = SOFTCAP ? a.scale / a.softcap : a.scale * LOG2E;
   const float cap = a.softcap;
 
