@@ -84,6 +84,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", choices=["auto", "generic"], default="auto")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a 256 MiB device-to-device copy (5 launches), the reference point "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (requests are "
@@ -91,6 +94,17 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.calibrate_copy:
+        n = 256 << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read_per_launch": n, "bytes_written_per_launch": n,
+                          "launches": 5}), flush=True)
+        return 0
     from vllm_gr_amd import ops, workloads
 
     dev = torch.device("cuda:0")
