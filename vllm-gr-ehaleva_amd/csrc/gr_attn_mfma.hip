@@ -43,7 +43,8 @@ constexpr int BUF = K_TILE + V_TILE;  // elements per buffer
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESH = 8.0f;
 constexpr int PBT_WIN = 2048;  // prefix block-table entries staged in LDS
-constexpr int NBUF = 3;        // LDS tile buffers (V of tile t, K of tile t+1, fill of tile t+2)  // log2 units: rescale O only when the max grows by > 2^8
+constexpr int NBUF = 3;
+constexpr int SB_STAGE = 2;     // suffix block ids staged in LDS per beam (more are read from HBM)        // LDS tile buffers (V of tile t, K of tile t+1, fill of tile t+2)  // log2 units: rescale O only when the max grows by > 2^8
 
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
@@ -235,6 +236,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   __shared__ uint32_t tile_mask[NBUF][2];  // [buffer][half]: visible keys of the prefix super-tile
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
   __shared__ int suf_info[4][32];        // per row group slot: (beam << 16) | j, or -1
+  __shared__ int suf_s0[4][32];          // per row group beam: first suffix position
+  __shared__ int suf_blk[4][32][SB_STAGE];  // per row group beam: its first suffix block ids
   __shared__ int pbt_s[PBT_WIN];         // staged prefix block ids (-1 = invalid)
 
   // ---- XCD-aware tile placement: all m-tiles of a (request, KV head) land on
@@ -278,10 +281,6 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     for (int kk = 0; kk < 8; ++kk)
       qf[kk] = row_ok ? *reinterpret_cast<const u32x4_t*>(src + kk * 16) : u32x4_t{0, 0, 0, 0};
   }
-  // Retire the Q loads here: the main loop's first read of qf is otherwise
-  // preceded by a full vector-memory wait in every iteration, which also
-  // waits for the tile prefetch issued at the top of the iteration.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   const float c = SOFTCAP ? a.scale / a.softcap : a.scale * LOG2E;
   const float cap = a.softcap;
 
@@ -290,14 +289,49 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
   RowState st = {-INFINITY, 0.f};
 
-  // ---- prefix: 64-key super-tiles, double-buffered through LDS ------------
+  // ---- prologue: every read that depends only on the arguments is issued
+  // before the first wait -- the prefix length, the first window of the
+  // prefix block table, and this row group's suffix metadata (lengths, start
+  // positions, first block ids) -- so the set-up costs one memory round trip.
   const int pre_cap = a.prefix_bt_stride * a.bs;
+  const int32_t* pbt = a.prefix_bt + (int64_t)r * a.prefix_bt_stride;
   int P = a.prefix_len[r];
+  constexpr int WIN_PER_THREAD = PBT_WIN / MF_THREADS;
+  static_assert(PBT_WIN % MF_THREADS == 0, "window split");
+  int raw_blk[WIN_PER_THREAD];
+#pragma unroll
+  for (int i = 0; i < WIN_PER_THREAD; ++i) {
+    const int bi = tid + i * MF_THREADS;
+    raw_blk[i] = bi < a.prefix_bt_stride ? pbt[bi] : -1;
+  }
+  // suffix metadata: lane l < nbeams of the key-half-0 wave of row group rg
+  // owns beam b_lo + l of the group
+  const int suf_cap = a.suffix_bt_stride * a.bs;
+  const int rlo = row_base + rg * 32;
+  const int b_lo = rlo / TG;
+  const int nbeams = rlo < rows_r ? min((rlo + 31) / TG, W - 1) - b_lo + 1 : 0;  // <= 32
+  const bool meta_lane = ks == 0 && lane < nbeams;
+  int sL = 0, sS0 = 0, sBlk[SB_STAGE];
+  {
+    const int n = nb0 + b_lo + lane;
+    if (meta_lane) {
+      sL = a.suffix_len[n];
+      sS0 = a.suffix_start ? a.suffix_start[n] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < SB_STAGE; ++j)
+      sBlk[j] = meta_lane && j < a.suffix_bt_stride ? a.suffix_bt[(int64_t)n * a.suffix_bt_stride + j] : -1;
+  }
+  const int my_len = row_ok ? a.suffix_len[nb0 + my_b] : 0;  // this lane's beam (causal limit)
+  // Retire every prologue load (Q included) here: the main loop's first read
+  // of qf is otherwise preceded by a full vector-memory wait in every
+  // iteration, which also waits for the tile prefetch issued at its top.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+
   if (P < 0 || P > pre_cap) {
     if (tid == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
     P = P < 0 ? 0 : pre_cap;
   }
-  const int32_t* pbt = a.prefix_bt + (int64_t)r * a.prefix_bt_stride;
   const int n_st = (P + ST_KEYS - 1) / ST_KEYS;
   const int bsh = a.bs_shift;
 
@@ -320,7 +354,40 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       pbt_s[i] = blk;
     }
   };
-  load_window(0);
+#pragma unroll
+  for (int i = 0; i < WIN_PER_THREAD; ++i) {
+    const int bi = tid + i * MF_THREADS;
+    int blk = -1;
+    if (bi < nblk) {
+      blk = raw_blk[i];
+      if (blk < 0 || blk >= a.num_blocks) {
+        flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
+        blk = -1;
+      }
+    }
+    pbt_s[tid + i * MF_THREADS] = blk;
+  }
+  if (ks == 0) {
+    int len = 0;
+    if (meta_lane) {
+      len = (sL < 0 || sS0 < 0 || sS0 + sL > suf_cap) ? 0 : sL;
+      if (len != sL) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+      suf_s0[rg][lane] = sS0;
+#pragma unroll
+      for (int j = 0; j < SB_STAGE; ++j) suf_blk[rg][lane][j] = sBlk[j];
+    }
+    int incl = len;  // inclusive scan over the first 32 lanes
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if ((lane & 31) >= off) incl += y;
+    }
+    if (lane < 32) suf_cum[rg][lane + 1] = incl;
+    if (lane == 0) {
+      suf_cum[rg][0] = 0;
+      suf_cum[rg][33] = b_lo;  // first beam of the group
+    }
+  }
   __syncthreads();
 
   // loader roles: thread (lk, lc) moves keys 2*lk and 2*lk+1 (one block: the
@@ -416,34 +483,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   }
 
   // ---- suffix: each row group's beams' own tokens, masked 32-key tiles ----
-  // (computed by the key-half-0 wave of each row group; all threads load)
-  const int suf_cap = a.suffix_bt_stride * a.bs;
-  if (ks == 0) {
-    const int rlo = row_base + rg * 32;
-    const int b_lo = rlo / TG;
-    const int b_hi = min((rlo + 31) / TG, W - 1);
-    const int nbeams = rlo < rows_r ? b_hi - b_lo + 1 : 0;  // <= 32
-    int len = 0;
-    if (lane < nbeams) {
-      const int n = nb0 + b_lo + lane;
-      const int L = a.suffix_len[n];
-      const int s0 = a.suffix_start ? a.suffix_start[n] : 0;
-      len = (L < 0 || s0 < 0 || s0 + L > suf_cap) ? 0 : L;
-      if (len != L) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
-    }
-    int incl = len;  // inclusive scan over the first 32 lanes
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) {
-      const int y = __shfl_up(incl, off, 64);
-      if ((lane & 31) >= off) incl += y;
-    }
-    if (lane < 32) suf_cum[rg][lane + 1] = incl;
-    if (lane == 0) {
-      suf_cum[rg][0] = 0;
-      suf_cum[rg][33] = b_lo;  // first beam of the group
-    }
-  }
-  __syncthreads();
+  // (computed by the key-half-0 wave of each row group; all threads load;
+  // the group's metadata was staged in the prologue)
   int max_tot = 0;
 #pragma unroll
   for (int g = 0; g < 4; ++g) max_tot = max(max_tot, suf_cum[g][32]);
@@ -451,13 +492,21 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   for (int it = 0; it < n_sit; ++it) {
     // loader: 4 row groups x 32 slots x 16 chunks; row group g's slots live in
     // buffer g >> 1, rows / columns (g & 1) * 32 .. + 31
-    for (int e = tid; e < 4 * 32 * 16; e += MF_THREADS) {
+    // all loads of the iteration are issued before the first LDS store
+    constexpr int SUF_PER_THREAD = 4 * 32 * 16 / MF_THREADS;
+    static_assert(4 * 32 * 16 % MF_THREADS == 0, "suffix loader split");
+    u32x4_t skv[SUF_PER_THREAD], svv[SUF_PER_THREAD];
+    int sinfo[SUF_PER_THREAD];
+#pragma unroll
+    for (int i = 0; i < SUF_PER_THREAD; ++i) {
+      const int e = tid + i * MF_THREADS;
       const int grp = e >> 9;
       const int slot = (e >> 4) & 31;
       const int ch = e & 15;
       const int gs = it * 32 + slot;
-      u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-      int info = -1;
+      skv[i] = u32x4_t{0, 0, 0, 0};
+      svv[i] = u32x4_t{0, 0, 0, 0};
+      sinfo[i] = -1;
       if (gs < suf_cum[grp][32]) {
         int lo = 0, hi = 31;  // largest beam index i with cum[i] <= gs (skips empty beams)
         while (lo < hi) {
@@ -467,28 +516,36 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         const int b = suf_cum[grp][33] + lo;
         const int j = gs - suf_cum[grp][lo];
         const int n = nb0 + b;
-        const int pos = (a.suffix_start ? a.suffix_start[n] : 0) + j;
-        const int blk = a.suffix_bt[(int64_t)n * a.suffix_bt_stride + pos / a.bs];
+        const int pos = suf_s0[grp][lo] + j;
+        const int bi = bsh >= 0 ? pos >> bsh : pos / a.bs;
+        const int blk = bi < SB_STAGE ? suf_blk[grp][lo][bi] : a.suffix_bt[(int64_t)n * a.suffix_bt_stride + bi];
         if (blk >= 0 && blk < a.num_blocks) {
           const int64_t base = (int64_t)blk * a.kv_block_stride + (int64_t)(pos % a.bs) * a.kv_tok_stride +
                                head_off + ch * 8;
-          kv = *reinterpret_cast<const u32x4_t*>(kc + base);
-          vv = *reinterpret_cast<const u32x4_t*>(vc + base);
-          info = (b << 16) | j;
+          skv[i] = *reinterpret_cast<const u32x4_t*>(kc + base);
+          svv[i] = *reinterpret_cast<const u32x4_t*>(vc + base);
+          sinfo[i] = (b << 16) | j;
         } else {
           flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
         }
       }
+    }
+#pragma unroll
+    for (int i = 0; i < SUF_PER_THREAD; ++i) {
+      const int e = tid + i * MF_THREADS;
+      const int grp = e >> 9;
+      const int slot = (e >> 4) & 31;
+      const int ch = e & 15;
       uint16_t* buf = lds + (grp >> 1) * BUF;
       const int key = (grp & 1) * 32 + slot;
-      *reinterpret_cast<u32x4_t*>(buf + key * KS_PITCH + kchunk(key, ch) * 8) = kv;
-      *reinterpret_cast<u32x4_t*>(buf + K_TILE + key * VS_PITCH + ch * 8) = vv;
-      if (ch == 0) suf_info[grp][slot] = info;
+      *reinterpret_cast<u32x4_t*>(buf + key * KS_PITCH + kchunk(key, ch) * 8) = skv[i];
+      *reinterpret_cast<u32x4_t*>(buf + K_TILE + key * VS_PITCH + ch * 8) = svv[i];
+      if (ch == 0) suf_info[grp][slot] = sinfo[i];
     }
     __syncthreads();
     if (ks == 0) {
       // register r of this lane is slot 16*(r>>3) + 8*lhalf + (r&7) of the group's 32
-      const int lim = row_ok ? a.suffix_len[nb0 + my_b] - a.T + my_qi : -1;
+      const int lim = row_ok ? my_len - a.T + my_qi : -1;
       uint32_t vis = 0;
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
