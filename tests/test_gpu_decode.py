@@ -184,3 +184,19 @@ def test_decode_bad_block_flagged(device):
     wl.prefix_bt[0, 1] = nb + 7
     with pytest.raises(ValueError, match="block id out of range"):
         run_gpu(wl, device)
+
+
+def test_decode_late_dominant_key(device):
+    """A key far above every earlier score of its row, late in the prefix (its
+    weight relative to the running reference exceeds 2^60), must move the
+    softmax reference and rescale the accumulated output."""
+    wl = workloads.make_decode(R=1, W=4, P=1000, L=3, Hq=8, Hkv=2, D=128, dtype=torch.bfloat16,
+                               input_scale=1.0, seed=29)
+    q = wl.q[1, 0].float()
+    pos = 900
+    blk = int(wl.prefix_bt[0, pos // wl.block_size])
+    wl.kv_cache[0, blk, pos % wl.block_size, 0] = (q / q.norm() * 100.0).to(torch.bfloat16)
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    assert ref_lse[1, 0] > 60.0  # the planted key dominates that row by far
+    _check(out, lse, ref, ref_lse, atol=2e-2)

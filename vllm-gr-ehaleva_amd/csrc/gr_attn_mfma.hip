@@ -41,10 +41,11 @@ constexpr int K_TILE = ST_KEYS * KS_PITCH;
 constexpr int V_TILE = ST_KEYS * VS_PITCH;
 constexpr int BUF = K_TILE + V_TILE;  // elements per buffer
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr float RESCALE_THRESH = 8.0f;
+constexpr float RESCALE_THRESH = 60.0f;  // log2 units a key may exceed the reference
+constexpr float RESCALE_SUM = 1.152921504606846976e18f;  // 2^RESCALE_THRESH: a lane weight sum above it forces the exact path
 constexpr int PBT_WIN = 2048;  // prefix block-table entries staged in LDS
-constexpr int NBUF = 3;
-constexpr int SB_STAGE = 2;     // suffix block ids staged in LDS per beam (more are read from HBM)        // LDS tile buffers (V of tile t, K of tile t+1, fill of tile t+2)  // log2 units: rescale O only when the max grows by > 2^8
+constexpr int NBUF = 3;        // LDS tile buffers (V of tile t, K of tile t+1, fill of tile t+2)
+constexpr int SB_STAGE = 2;    // suffix block ids staged in LDS per beam (more are read from HBM)
 
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
@@ -53,6 +54,9 @@ typedef uint32_t u32x4_t __attribute__((__vector_size__(4 * sizeof(uint32_t))));
 typedef uint32_t u32x2_t __attribute__((__vector_size__(2 * sizeof(uint32_t))));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Zero source for loads of keys outside the prefix or in an invalid block.
+__device__ __attribute__((aligned(16))) uint32_t g_zero16[4];
 
 template <int DT> struct Mma;
 template <> struct Mma<GR_DTYPE_BF16> {
@@ -118,122 +122,209 @@ struct RowState {
 // Softmax of one 32-key x 32-row S^T tile held by this lane (16 keys of its
 // row).  vis: bit r set when register r is a visible key.  Returns the
 // rescale factor for O (1 when unchanged) and writes the packed P operand.
-template <int DT, bool SOFTCAP, bool MASKED>
-__device__ inline float softmax_tile(f32x16_t& s, uint32_t vis, RowState& st, float c, float cap,
-                                     u32x4_t& p0, u32x4_t& p1) {
-  float x[16];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    float v = s[r];
-    if (SOFTCAP) v = cap * tanhf(v * c);  // c = scale / softcap here
-    if (MASKED) v = (vis >> r) & 1 ? v : -INFINITY;
-    x[r] = v;
-  }
-#pragma unroll
-  for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(x[r], x[r + 1]));
-  mx = pair_max(mx);
-  // scaled log2-domain maximum of this tile
-  const float cs = SOFTCAP ? LOG2E : c;
-  const float tmax = mx * cs;  // -inf stays -inf (cs > 0)
-  float alpha = 1.f;
-  if (tmax > st.m + RESCALE_THRESH || (st.m == -INFINITY && tmax != -INFINITY)) {
-    alpha = (st.m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(st.m - tmax);
-    st.m = tmax;
-    st.lsum *= alpha;
-  }
-  const float mref = st.m == -INFINITY ? 0.f : st.m;
-  float p[16];
-  float acc = 0.f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    p[r] = __builtin_amdgcn_exp2f(fmaf(x[r], cs, -mref));
-    acc += p[r];
-  }
-  st.lsum += acc;
-  using M = Mma<DT>;
-  p0 = u32x4_t{M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]), M::pack2(p[6], p[7])};
-  p1 = u32x4_t{M::pack2(p[8], p[9]), M::pack2(p[10], p[11]), M::pack2(p[12], p[13]),
-               M::pack2(p[14], p[15])};
-  return alpha;
+// log2-domain score of one S^T entry (c = scale * log2(e), or scale / softcap
+// with the soft cap applied first)
+template <bool SOFTCAP>
+__device__ inline float score_l2(float v, float c, float cap) {
+  return SOFTCAP ? cap * tanhf(v * c) * LOG2E : v * c;
 }
 
-// One wave: its 32 query rows against one 32-key half-tile in LDS.
-// kbase: first K_s row / V^T column of the half.
-// S^T for this wave's 32 rows against the 32-key half-tile at row kbase.
-template <int DT>
-__device__ inline f32x16_t qk(const uint16_t* buf, int kbase, int lane, const u32x4_t (&qf)[8]) {
+// A lane's 16 weights of one half-tile against the row's reference maximum
+// mref (log2 domain), with no tile maximum: the branch-free common case.
+// Weights are packed pairwise as they are produced (p0: registers 0..7, p1:
+// 8..15).  Returns the lane's weight sum.  The caller sends the tile to
+// softmax_exact when any lane's sum exceeds 2^RESCALE_THRESH (some key is
+// more than RESCALE_THRESH above the reference) or is not finite (the row
+// has no reference yet: mref = -inf makes every visible weight +inf).
+template <int DT, bool SOFTCAP, bool MASKED>
+__device__ inline float softmax_fast(const f32x16_t& s, uint32_t vis, float mref, float c, float cap,
+                                     u32x4_t& p0, u32x4_t& p1) {
   using M = Mma<DT>;
-  const int lrow = lane & 31, lhalf = lane >> 5;
-  const int krow_i = kbase + key_perm(lrow);
+  float acc0 = 0.f, acc1 = 0.f;
+  uint32_t pk[8];
+#pragma unroll
+  for (int r = 0; r < 16; r += 2) {
+    float e0 = SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(s[r], c, cap) - mref)
+                       : __builtin_amdgcn_exp2f(fmaf(s[r], c, -mref));
+    float e1 = SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(s[r + 1], c, cap) - mref)
+                       : __builtin_amdgcn_exp2f(fmaf(s[r + 1], c, -mref));
+    if (MASKED) {
+      e0 = (vis >> r) & 1 ? e0 : 0.f;
+      e1 = (vis >> (r + 1)) & 1 ? e1 : 0.f;
+    }
+    acc0 += e0;
+    acc1 += e1;
+    pk[r >> 1] = M::pack2(e0, e1);
+  }
+  p0 = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
+  p1 = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
+  return acc0 + acc1;
+}
+
+// S^T of the wave's 32 rows against the 32-key half-tile at row kbase.
+template <int DT>
+__device__ inline f32x16_t qk_half(const uint16_t* buf, int kbase, int lane, const u32x4_t (&qf)[8]) {
+  using M = Mma<DT>;
+  const int krow_i = kbase + key_perm(lane & 31);
   const uint16_t* krow = buf + krow_i * KS_PITCH;
+  const int lhalf = lane >> 5;
   f32x16_t s = {};
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk)
-    s = M::mma(lds_read16(krow + kchunk(krow_i, 2 * kk + lhalf) * 8), qf[kk], s);
+  for (int kk = 0; kk < 8; ++kk) s = M::mma(lds_read16(krow + kchunk(krow_i, 2 * kk + lhalf) * 8), qf[kk], s);
   return s;
 }
 
-// O += V^T . P^T for the 32-key half-tile at row kbase.  The V^T operand:
-// lane group g = lane/16 covers dims 16*(g&1) .. +15 of the 32-dim block and
-// keys 8*(g>>1) .. +7 of the 16-key step (two 4-key transposing reads).
-template <int DT>
-__device__ inline void pv(const uint16_t* buf, int kbase, int lane, u32x4_t p0, u32x4_t p1, f32x16_t (&o)[4]) {
+// Weight of one score against the reference mref (log2 domain).
+template <bool SOFTCAP>
+__device__ inline float weight1(float v, float c, float cap, float mref) {
+  return SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(v, c, cap) - mref)
+                 : __builtin_amdgcn_exp2f(fmaf(v, c, -mref));
+}
+
+// O += V^T . P^T over NH 32-key halves starting at row kbase.  The V^T
+// operand: lane group g = lane/16 covers dims 16*(g&1) .. +15 of the 32-dim
+// block and keys 8*(g>>1) .. +7 of the 16-key step (two 4-key transposing
+// reads).  The four dim blocks are independent accumulators, issued in turn.
+template <int DT, int NH>
+__device__ inline void pv(const uint16_t* buf, int kbase, int lane, const u32x4_t (&p)[NH][2], f32x16_t (&o)[4]) {
   using M = Mma<DT>;
   const int g = lane >> 4, sl = lane & 15;
   const uint16_t* vsrc = buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
+  for (int h = 0; h < NH; ++h) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const uint16_t* vp = vsrc + (16 * kk) * VS_PITCH + 32 * mb;
-      const uint2 lo = lds_read_tr(vp);
-      const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
-      o[mb] = M::mma(u32x4_t{lo.x, lo.y, hi.x, hi.y}, kk ? p1 : p0, o[mb]);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const uint16_t* vp = vsrc + (32 * h + 16 * kk) * VS_PITCH + 32 * mb;
+        const uint2 lo = lds_read_tr(vp);
+        const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
+        o[mb] = M::mma(u32x4_t{lo.x, lo.y, hi.x, hi.y}, p[h][kk], o[mb]);
+      }
     }
   }
 }
 
-// One pipelined step of a wave: the softmax of the current tile's scores
-// (VALU) is interleaved with the QK^T of the next tile (matrix core), then
-// the current tile's PV.  s_cur holds S^T of the current tile on entry and of
-// the next tile on exit (when has_next).
-template <int DT, bool SOFTCAP, bool MASKED>
-__device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_buf, bool has_next, int kbase,
-                                 int lane, const u32x4_t (&qf)[8], f32x16_t& s_cur, f32x16_t (&o)[4],
-                                 RowState& st, uint32_t vis, float c, float cap) {
-  f32x16_t s_next = {};
-  if (has_next) s_next = qk<DT>(next_buf, kbase, lane, qf);
-  u32x4_t p0, p1;
-  const float al = softmax_tile<DT, SOFTCAP, MASKED>(s_cur, vis, st, c, cap, p0, p1);
-  if (has_next) {
-    // interleave: one MFMA of the next tile's QK^T per group of softmax VALU ops
+// Weights of NH half-tiles of the wave's rows (one row per lane pair): the
+// branch-free fast path against the row's reference, or -- when some weight
+// could exceed 2^RESCALE_THRESH or the row has no reference yet -- the exact
+// path that moves the reference to the maximum over all NH halves and scales
+// O (skipped while the row has accumulated nothing).
+template <int DT, bool SOFTCAP, bool MASKED, int NH>
+__device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH], RowState& st, float c, float cap,
+                               u32x4_t (&p)[NH][2], f32x16_t (&o)[4]) {
+  float acc = 0.f;
+  bool hot = false;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read (next K fragment)
-      __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
+  for (int h = 0; h < NH; ++h) {
+    const float a_h = softmax_fast<DT, SOFTCAP, MASKED>(s[h], vis[h], st.m, c, cap, p[h][0], p[h][1]);
+    hot |= !(a_h <= RESCALE_SUM);
+    acc += a_h;
+  }
+  if (__ballot(hot) == 0) {
+    st.lsum += acc;
+    return;
+  }
+  // exact path (wave-uniform; after a row's first tile it needs a score more
+  // than RESCALE_THRESH log2 units above everything before it).  The empty
+  // volatile asm keeps the compiler from speculating this rare work into the
+  // common path.
+  __asm__ volatile("" ::: "memory");
+  float mx = -INFINITY;
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float v = score_l2<SOFTCAP>(s[h][r], c, cap);
+      mx = (!MASKED || ((vis[h] >> r) & 1)) ? fmaxf(mx, v) : mx;
     }
-  }
-  if (__ballot(al != 1.f) != 0) {  // wave-uniform: rare after the first tiles
+  mx = pair_max(mx);
+  const float new_m = fmaxf(st.m, mx);
+  const float alpha = st.m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m - new_m);
+  const float mref = new_m == -INFINITY ? 0.f : new_m;
+  const bool had_mass = st.lsum > 0.f;
+  st.m = new_m;
+  float acc2 = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) o[mb] *= al;
+  for (int h = 0; h < NH; ++h) acc2 += softmax_fast<DT, SOFTCAP, MASKED>(s[h], vis[h], mref, c, cap, p[h][0], p[h][1]);
+  st.lsum = st.lsum * alpha + acc2;
+  if (__ballot(had_mass && alpha != 1.f) != 0) {
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) o[mb] *= alpha;
   }
-  pv<DT>(cur_buf, kbase, lane, p0, p1, o);
-  s_cur = s_next;
 }
 
-// Visibility bits of the 16 registers of a lane from a 32-bit key mask of
-// the half-tile (bit k = tile key k visible): register r holds key
-// 16*(r>>3) + 8*lhalf + (r&7).
-__device__ inline uint32_t regs_from_keymask(uint32_t km, int lhalf) {
-  return ((km >> (8 * lhalf)) & 0xFFu) | (((km >> (16 + 8 * lhalf)) & 0xFFu) << 8);
+// One pipelined step of a wave over its 32-key half of a fully visible
+// tile.  Phase A interleaves, in 8 fixed segments, one MFMA of the next
+// tile's QK^T (with the LDS read of the fragment two MFMAs ahead) with the
+// weights of two scores of the current tile; phase B checks whether any
+// weight could exceed 2^RESCALE_THRESH (rare: exact path); phase C is the
+// current tile's PV with its transposing reads two MFMAs ahead.  The
+// scheduling barriers pin the segment order so the matrix core and the VALU
+// work side by side.  s_in holds S^T of the current tile, s_out receives that
+// of the next tile (the caller alternates two registers sets: no copies).
+template <int DT, bool SOFTCAP>
+__device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_buf, int kbase, int lane,
+                                 const u32x4_t (&qf)[8], const f32x16_t& s_in, f32x16_t& s_out,
+                                 f32x16_t (&o)[4], RowState& st, float c, float cap) {
+  using M = Mma<DT>;
+  const int lhalf = lane >> 5;
+  const int krow_i = kbase + key_perm(lane & 31);
+  const uint16_t* krow = next_buf + krow_i * KS_PITCH;
+  auto kfrag = [&](int kk) { return lds_read16(krow + kchunk(krow_i, 2 * kk + lhalf) * 8); };
+  const float mref = st.m;
+  u32x4_t kf[8];
+  kf[0] = kfrag(0);
+  kf[1] = kfrag(1);
+  s_out = f32x16_t{};
+  uint32_t pk[8];
+  float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i + 2 < 8) kf[i + 2] = kfrag(i + 2);
+    s_out = M::mma(kf[i], qf[i], s_out);
+    const float e0 = weight1<SOFTCAP>(s_in[2 * i], c, cap, mref);
+    const float e1 = weight1<SOFTCAP>(s_in[2 * i + 1], c, cap, mref);
+    acc0 += e0;
+    acc1 += e1;
+    pk[i] = M::pack2(e0, e1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  u32x4_t p[1][2] = {{u32x4_t{pk[0], pk[1], pk[2], pk[3]}, u32x4_t{pk[4], pk[5], pk[6], pk[7]}}};
+  const float acc = acc0 + acc1;
+  if (__ballot(!(acc <= RESCALE_SUM)) != 0) {
+    __asm__ volatile("" ::: "memory");
+    const uint32_t vis[1] = {0xFFFFu};
+    const f32x16_t s1[1] = {s_in};
+    weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, o);
+  } else {
+    st.lsum += acc;
+  }
+  // phase C: PV of the current tile (MFMA j: step kk = j/4, dim block mb = j%4)
+  const int g = lane >> 4, sl = lane & 15;
+  const uint16_t* vsrc = cur_buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
+  auto vfrag = [&](int j) {
+    const uint16_t* vp = vsrc + (16 * (j >> 2)) * VS_PITCH + 32 * (j & 3);
+    const uint2 lo = lds_read_tr(vp);
+    const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
+    return u32x4_t{lo.x, lo.y, hi.x, hi.y};
+  };
+  u32x4_t vf[8];
+  vf[0] = vfrag(0);
+  vf[1] = vfrag(1);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j + 2 < 8) vf[j + 2] = vfrag(j + 2);
+    o[j & 3] = M::mma(vf[j], p[0][j >> 2], o[j & 3]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 template <int DT, bool SOFTCAP>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF];
-  __shared__ uint32_t tile_mask[NBUF][2];  // [buffer][half]: visible keys of the prefix super-tile
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
   __shared__ int suf_info[4][32];        // per row group slot: (beam << 16) | j, or -1
   __shared__ int suf_s0[4][32];          // per row group beam: first suffix position
@@ -394,19 +485,24 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // block size is a power of two >= 4), 16-byte chunk lc of K and of V.
   const int lk = tid >> 4, lc = tid & 15;
   u32x4_t kreg[2], vreg[2];
-  auto load_prefix = [&](int k0) {
+  // block id of this thread's keys in the tile at k0 (read a step before the
+  // loads that use it, so the LDS latency hides behind a step's compute)
+  auto read_blk = [&](int k0) {
     const int key0 = k0 + 2 * lk;
-    const int blk = key0 < P ? pbt_s[(key0 >> bsh) - win0] : -1;
+    return key0 < P ? pbt_s[(key0 >> bsh) - win0] : -1;
+  };
+  // Branch-free loads: keys outside the prefix or in an invalid block read a
+  // zero source, so every thread issues the same loads.
+  const S* zsrc = reinterpret_cast<const S*>(g_zero16);
+  auto load_prefix = [&](int k0, int blk) {
+    const int key0 = k0 + 2 * lk;
     const int64_t off = (int64_t)(blk < 0 ? 0 : blk) * a.kv_block_stride +
                         (int64_t)(key0 & (a.bs - 1)) * a.kv_tok_stride + head_off + lc * 8;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      kreg[j] = u32x4_t{0, 0, 0, 0};
-      vreg[j] = u32x4_t{0, 0, 0, 0};
-      if (blk >= 0 && key0 + j < P) {
-        kreg[j] = *reinterpret_cast<const u32x4_t*>(kc + off + j * a.kv_tok_stride);
-        vreg[j] = *reinterpret_cast<const u32x4_t*>(vc + off + j * a.kv_tok_stride);
-      }
+      const bool ok = blk >= 0 && key0 + j < P;
+      kreg[j] = *reinterpret_cast<const u32x4_t*>(ok ? kc + off + j * a.kv_tok_stride : zsrc);
+      vreg[j] = *reinterpret_cast<const u32x4_t*>(ok ? vc + off + j * a.kv_tok_stride : zsrc);
     }
   };
   // keep the window over [k0, k0 + 64); switching costs two barriers and
@@ -428,58 +524,68 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       *reinterpret_cast<u32x4_t*>(buf + K_TILE + row * VS_PITCH + lc * 8) = vreg[j];
     }
   };
-  auto store_mask = [&](int bsel, int k0) {
-    if (wave == 0) {
-      const int key = k0 + lane;
-      const bool ok = key < P && pbt_s[(key >> bsh) - win0] >= 0;
-      const uint64_t m = __ballot(ok);
-      if (lane == 0) {
-        tile_mask[bsel][0] = (uint32_t)m;
-        tile_mask[bsel][1] = (uint32_t)(m >> 32);
-      }
-    }
-  };
-
   // Three LDS buffers: during step t the wave reads V of tile t, K of tile
   // t+1, while tile t+2 (loaded into registers at the start of the step) is
   // stored into the third buffer at its end.
   if (n_st > 0) {
     ensure_window(0);
-    load_prefix(0);
+    load_prefix(0, read_blk(0));
     store_tile(lds);
-    store_mask(0, 0);
   }
   if (n_st > 1) {
     ensure_window(ST_KEYS);
-    load_prefix(ST_KEYS);
+    load_prefix(ST_KEYS, read_blk(ST_KEYS));
     store_tile(lds + BUF);
-    store_mask(1, ST_KEYS);
+  }
+  int pf_blk = -1;  // block id for the next tile to load (tile it+2 at step it)
+  if (n_st > 2) {
+    ensure_window(2 * ST_KEYS);
+    pf_blk = read_blk(2 * ST_KEYS);
   }
   __syncthreads();
-  f32x16_t s_cur = {};
-  if (n_st > 0) s_cur = qk<DT>(lds, ks * 32, lane, qf);
-  for (int it = 0; it < n_st; ++it) {
+  f32x16_t s_cur = qk_half<DT>(lds, ks * 32, lane, qf);  // (stale LDS when n_st == 0: never used)
+  // One step over a fully visible tile `it` (not the last): consumes its S^T
+  // from s_in, leaves that of tile it+1 in s_out.  Keys of an invalid block
+  // read as zero rows (the block was flagged when the window was staged).
+  auto prefix_step = [&](int it, const f32x16_t& s_in, f32x16_t& s_out) {
     const int cur = it % NBUF, nxt = (it + 1) % NBUF, fill = (it + 2) % NBUF;
     const bool fetch = it + 2 < n_st;
     if (fetch) {
-      ensure_window((it + 2) * ST_KEYS);
-      load_prefix((it + 2) * ST_KEYS);
+      load_prefix((it + 2) * ST_KEYS, pf_blk);
+      if (it + 3 < n_st) {
+        ensure_window((it + 3) * ST_KEYS);
+        pf_blk = read_blk((it + 3) * ST_KEYS);
+      }
     }
-    const uint16_t* buf = lds + cur * BUF;
-    const uint16_t* nbuf = lds + nxt * BUF;
-    const bool has_next = it + 1 < n_st;
-    const uint32_t km = tile_mask[cur][ks];
-    if (km == 0xFFFFFFFFu) {
-      pipe_step<DT, SOFTCAP, false>(buf, nbuf, has_next, ks * 32, lane, qf, s_cur, o, st, 0xFFFFu, c, cap);
-    } else {
-      pipe_step<DT, SOFTCAP, true>(buf, nbuf, has_next, ks * 32, lane, qf, s_cur, o, st,
-                                   regs_from_keymask(km, lhalf), c, cap);
-    }
-    if (fetch) {
-      store_tile(lds + fill * BUF);
-      store_mask(fill, (it + 2) * ST_KEYS);
-    }
+    pipe_step<DT, SOFTCAP>(lds + cur * BUF, lds + nxt * BUF, ks * 32, lane, qf, s_in, s_out, o, st, c, cap);
+    if (fetch) store_tile(lds + fill * BUF);
     __syncthreads();
+  };
+  // The last tile: no next tile; masked when only p_last of its keys exist.
+  const int p_last = P - (n_st - 1) * ST_KEYS;  // keys in the last tile (1 .. 64)
+  auto last_step = [&](int it, const f32x16_t& s_in) {
+    // register r of lane half lhalf holds tile key ks*32 + 16*(r>>3) + 8*lhalf + (r&7)
+    uint32_t v = 0;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) v |= (ks * 32 + 16 * (rr >> 3) + 8 * lhalf + (rr & 7) < p_last ? 1u : 0u) << rr;
+    const uint32_t vis[1] = {v};
+    const f32x16_t s1[1] = {s_in};
+    u32x4_t pw[1][2];
+    weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o);
+    pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
+    __syncthreads();
+  };
+  f32x16_t s_alt;
+  int it = 0;
+  for (; it + 2 < n_st; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
+    prefix_step(it, s_cur, s_alt);
+    prefix_step(it + 1, s_alt, s_cur);
+  }
+  if (it + 1 < n_st) {
+    prefix_step(it, s_cur, s_alt);
+    last_step(it + 1, s_alt);
+  } else if (it < n_st) {
+    last_step(it, s_cur);
   }
 
   // ---- suffix: each row group's beams' own tokens, masked 32-key tiles ----
@@ -554,8 +660,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         vis |= (ok ? 1u : 0u) << rr;
       }
       const uint16_t* sbuf = lds + (rg >> 1) * BUF;
-      f32x16_t s_t = qk<DT>(sbuf, (rg & 1) * 32, lane, qf);
-      pipe_step<DT, SOFTCAP, true>(sbuf, sbuf, false, (rg & 1) * 32, lane, qf, s_t, o, st, vis, c, cap);
+      const f32x16_t s1[1] = {qk_half<DT>(sbuf, (rg & 1) * 32, lane, qf)};
+      const uint32_t vis1[1] = {vis};
+      u32x4_t pw[1][2];
+      weights<DT, SOFTCAP, true, 1>(s1, vis1, st, c, cap, pw, o);
+      pv<DT, 1>(sbuf, (rg & 1) * 32, lane, pw, o);
     }
     __syncthreads();
   }
