@@ -1,0 +1,166 @@
+"""Host logic of the backend mirror (CPU only, no kernel launch): the static
+backend contract (vllm_gr/v1/attention/backends/beam_attn.py:758-846), the
+impl's argument checks (:579-627, :715-723), the metadata builder's routing
+of mega-decode and standard requests, the resident beam table's position /
+slot arithmetic (engine_core_patch.py:362-365; slot = block * bs + offset,
+beam_attn.py:77-85) and the beam-search step's fork_info / abort set
+(serving_engine.py:141-142, 588-590; tests/test_batch_and_fork_unit.py
+5.10 and 5.15)."""
+
+from __future__ import annotations
+
+import types
+
+import pytest
+import torch
+
+from vllm_gr_amd.entrypoints import beam_search as bsm
+from vllm_gr_amd.v1.attention.backends import beam_attn as ba
+from vllm_gr_amd.v1.beam_kv import BeamKVTable
+
+B = ba.BeamAttentionBackend
+
+
+def test_backend_static_contract():
+    assert B.get_name() == "CUSTOM"
+    assert B.accept_output_buffer is True
+    assert B.get_supported_kernel_block_sizes() == [ba.MultipleOf(16)]
+    assert B.get_kv_cache_shape(10, 16, 8, 128) == (2, 10, 16, 8, 128)
+    assert B.get_kv_cache_stride_order() == (0, 1, 2, 3, 4)
+    assert B.get_kv_cache_stride_order(cache_layout="HND") == (0, 1, 3, 2, 4)
+    assert B.get_kv_cache_stride_order(True) == (2, 0, 1, 3, 4, 5)
+    with pytest.raises(ValueError):
+        B.get_kv_cache_stride_order(cache_layout="XYZ")
+    assert B.get_impl_cls() is ba.BeamAttentionImpl
+    assert B.get_builder_cls() is ba.BeamAttentionMetadataBuilder
+    for hs, ok in ((8, True), (128, True), (256, True), (12, False), (264, False)):
+        assert B.supports_head_size(hs) is ok
+
+
+@pytest.mark.parametrize("kw,reason", [
+    (dict(dtype=torch.float32), "Unsupported dtype"),
+    (dict(head_size=264), "Unsupported head_size"),
+    (dict(kv_cache_dtype="fp8"), "Unsupported kv_cache_dtype"),
+    (dict(block_size=8), "not multiple of 16"),
+    (dict(device_capability="gfx942"), "gfx950"),
+    (dict(has_sink=True), "sink"),
+    (dict(use_mla=True), "MLA"),
+    (dict(use_sparse=True), "sparse"),
+])
+def test_supports_combination_reasons(kw, reason):
+    args = dict(head_size=128, dtype=torch.bfloat16, kv_cache_dtype="auto", block_size=16, use_mla=False,
+                has_sink=False, use_sparse=False, device_capability="gfx950:sramecc+:xnack-")
+    assert B.supports_combination(**args) is None
+    args.update(kw)
+    assert reason in B.supports_combination(**args)
+
+
+def test_impl_rejects_unsupported_features():
+    mk = lambda **kw: ba.BeamAttentionImpl(**{**dict(num_heads=32, head_size=128, scale=0.1, num_kv_heads=8,
+                                                      alibi_slopes=None, sliding_window=None,
+                                                      kv_cache_dtype="auto"), **kw})
+    impl = mk()
+    assert impl.num_queries_per_kv == 4 and impl.logits_soft_cap == 0.0
+    for kw in (dict(alibi_slopes=[0.1] * 32), dict(sliding_window=128), dict(kv_cache_dtype="fp8"),
+               dict(running_sinks=torch.zeros(32))):
+        with pytest.raises(NotImplementedError):
+            mk(**kw)
+    q = torch.zeros(4, 32, 128)
+    kv = torch.zeros(2, 4, 16, 8, 128)
+    with pytest.raises(AssertionError):
+        impl.forward(None, q, None, None, kv, None, output=None)
+    with pytest.raises(NotImplementedError):
+        impl.forward(None, q, None, None, kv, None, output=torch.ones_like(q), output_scale=torch.ones(1))
+    out = torch.ones_like(q)
+    assert torch.equal(impl.forward(None, q, None, None, kv, None, output=out), torch.zeros_like(q))
+
+
+def _table(W=3, P=20, bs=16, lens=(0, 5, 16)):
+    prefix_bt = torch.tensor([[7, 3]], dtype=torch.int32)
+    suffix_bt = torch.tensor([[10, 11], [12, 13], [14, 15]], dtype=torch.int32)[:W]
+    return BeamKVTable(prefix_bt, torch.tensor([P]), W, suffix_bt,
+                       torch.tensor(lens, dtype=torch.int32), block_size=bs)
+
+
+def test_beam_table_positions_and_slots():
+    t = _table()
+    # beam b's j-th suffix token sits at prefix_len + j (engine_core_patch.py:362-365)
+    assert t.positions().tolist() == [20, 25, 36]
+    # next token slot: suffix position L -> block suffix_bt[n][L // 16], offset L % 16
+    assert t.slot_mapping().tolist() == [10 * 16 + 0, 12 * 16 + 5, 15 * 16 + 0]
+    assert t.attention_suffix_len().tolist() == [1, 6, 17]
+    t.advance()
+    assert t.suffix_len.tolist() == [1, 6, 17]
+    full = _table(lens=(31, 32, 0))
+    assert full.slot_mapping().tolist() == [11 * 16 + 15, -1, 14 * 16]
+
+
+def _common(q_lens, seq_lens, bt, bs=16):
+    qs = torch.tensor([0] + list(q_lens)).cumsum(0).to(torch.int32)
+    n = int(qs[-1])
+    slots = torch.arange(1000, 1000 + n, dtype=torch.int64)
+    return ba.CommonAttentionMetadata(
+        query_start_loc=qs, query_start_loc_cpu=qs, seq_lens=torch.tensor(seq_lens, dtype=torch.int32),
+        seq_lens_cpu=torch.tensor(seq_lens, dtype=torch.int32), num_reqs=len(q_lens), num_actual_tokens=n,
+        max_query_len=max(q_lens), max_seq_len=max(seq_lens), block_table_tensor=bt, slot_mapping=slots)
+
+
+def test_builder_routes_mega_and_standard_requests():
+    table = _table()
+    bt = torch.tensor([[7, 3, 0, 0], [20, 21, 22, 23], [30, 31, 32, 33]], dtype=torch.int32)
+    # request "a": mega decode, 3 beams; "b": standard decode; "c": standard prefill of 5 tokens
+    m = _common([3, 1, 5], [20, 40, 45], bt)
+    info = {"req_ids": ["a", "b", "c"],
+            "mega_data": {"a": dict(is_mega_decode=True, mega_beam_width=3, mega_decode_steps=2, prefix_len=20,
+                                    cache_len=20, beam_kv=table)}}
+    builder = ba.BeamAttentionMetadataBuilder(types.SimpleNamespace(block_size=16), ["l0"], None, "cpu")
+    tok = ba.MEGA_DATA_VAR.set(info)
+    try:
+        md = builder.build(0, m)
+    finally:
+        ba.MEGA_DATA_VAR.reset(tok)
+    assert md.mega_req_idxs == [0] and md.std_req_idxs == [1, 2]
+    # mega rows write their K/V into each beam's private block; other rows keep vLLM's slots
+    assert md.slot_mapping[:3].tolist() == table.slot_mapping().tolist()
+    assert md.slot_mapping[3:].tolist() == list(range(1003, 1009))
+    g_mega, g_dec, g_pre = md.groups
+    assert g_mega.q_per_beam == 1 and g_mega.token_index.tolist() == [0, 1, 2]
+    assert g_mega.beam_start.tolist() == [0, 3] and g_mega.prefix_len.tolist() == [20]
+    assert g_mega.suffix_len.tolist() == [1, 6, 17]
+    # standard decode: prefix = the 39 cached tokens, suffix = the new token at position 39
+    assert g_dec.q_per_beam == 1 and g_dec.token_index.tolist() == [3]
+    assert g_dec.prefix_len.tolist() == [39] and g_dec.suffix_len.tolist() == [1]
+    assert g_dec.suffix_start.tolist() == [39] and g_dec.prefix_bt[0, :3].tolist() == [20, 21, 22]
+    # standard prefill chunk: 40 cached + 5 new tokens, causal over the 5
+    assert g_pre.q_per_beam == 5 and g_pre.token_index.tolist() == [4, 5, 6, 7, 8]
+    assert g_pre.prefix_len.tolist() == [40] and g_pre.suffix_start.tolist() == [40]
+
+
+def test_builder_rejects_inconsistent_mega_request():
+    table = _table()
+    bt = torch.zeros(1, 4, dtype=torch.int32)
+    builder = ba.BeamAttentionMetadataBuilder(types.SimpleNamespace(block_size=16), ["l0"], None, "cpu")
+    for md_over, q, exc in ((dict(), 2, ValueError), (dict(cache_len=10), 3, NotImplementedError)):
+        md = dict(is_mega_decode=True, mega_beam_width=3, mega_decode_steps=1, prefix_len=20, cache_len=20,
+                  beam_kv=table)
+        md.update(md_over)
+        tok = ba.MEGA_DATA_VAR.set({"req_ids": ["a"], "mega_data": {"a": md}})
+        try:
+            with pytest.raises(exc):
+                builder.build(0, _common([q], [20], bt))
+        finally:
+            ba.MEGA_DATA_VAR.reset(tok)
+
+
+def test_fork_info_and_abort_set():
+    # tests/test_batch_and_fork_unit.py 5.15: selection (1, 60), (0, 50), (1, 61)
+    res = bsm.PruneResult(parent=torch.tensor([[1, 0, 1]], dtype=torch.int32),
+                          token=torch.tensor([[60, 50, 61]], dtype=torch.int32),
+                          score=torch.tensor([[-0.5, -1.0, -1.5]]), eos_score=torch.full((1, 3), -float("inf")))
+    assert bsm.fork_info(res) == [[(1, 60), (0, 50), (1, 61)]]
+    assert bsm.pruned_parents(res, 3) == [[2]]
+    # 5.10: parents 0, 2, 4 of five selected -> beams 1 and 3 aborted
+    res5 = bsm.PruneResult(parent=torch.tensor([[0, 2, 4, 0, 2]], dtype=torch.int32),
+                           token=torch.zeros(1, 5, dtype=torch.int32), score=torch.zeros(1, 5),
+                           eos_score=torch.zeros(1, 5))
+    assert bsm.pruned_parents(res5, 5) == [[1, 3]]

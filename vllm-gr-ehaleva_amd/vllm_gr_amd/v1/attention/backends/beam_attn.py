@@ -1,0 +1,350 @@
+"""BeamAttention backend: the attention-backend plugin surface of
+vllm_gr/v1/attention/backends/beam_attn.py, over the gfx950 kernels.
+
+Kept from the reference (same names, argument meaning and error behaviour):
+
+* ``MEGA_DATA_VAR`` (beam_attn.py:60): a ContextVar holding
+  ``{"mega_data": {req_id: {...}}, "req_ids": [...]}`` per forward, with the
+  per-request keys ``is_mega_decode``, ``mega_beam_width``,
+  ``mega_decode_steps``, ``prefix_len``, ``cache_len``
+  (engine_core_patch.py:544-554).  One key is added here: ``beam_kv``, the
+  request's :class:`~vllm_gr_amd.v1.beam_kv.BeamKVTable` (the reference has no
+  resident per-beam KV, so it needs none).
+* ``BeamAttentionMetadataBuilder.build(common_prefix_len,
+  common_attn_metadata, fast_build)`` (:480-485) and ``update_block_table``
+  (:561-570).
+* ``BeamAttentionImpl.__init__`` (:579-627) and ``forward(layer, query, key,
+  value, kv_cache, attn_metadata, output, output_scale, output_block_scale)``
+  (:703-755): output buffer required, output quantization rejected with
+  NotImplementedError, zero-fill without metadata, K/V append through the
+  slot mapping, then attention.
+* ``BeamAttentionBackend`` static surface (:758-846): name ``CUSTOM``,
+  fp16/bf16, block size a multiple of 16, KV shape ``(2, NB, bs, Hkv, D)``,
+  NHD/HND stride orders, head size %8 and <= 256, ``supports_combination``
+  returning a reason string or None.
+
+What differs, by design: a mega-decode request's beams attend their resident
+suffix (one new query token per beam) instead of recomputing W*t tokens, and
+the whole step is one ``gr_beam_attn_decode`` launch per query-length group
+(no prefix/suffix/merge passes, beam_attn.py:629-701).  A standard request is
+the one-beam case of the same kernel: prefix = its cached tokens, suffix =
+its new tokens in its own block-table row (bottom-right causal).
+"""
+
+from __future__ import annotations
+
+import contextvars
+import copy
+from dataclasses import dataclass, field
+from enum import Enum
+
+import torch
+
+from vllm_gr_amd import ops
+
+MEGA_DATA_VAR = contextvars.ContextVar("mega_data", default=None)
+
+
+class AttentionType(str, Enum):
+    DECODER = "decoder"
+    ENCODER = "encoder"
+    ENCODER_ONLY = "encoder_only"
+    ENCODER_DECODER = "encoder_decoder"
+
+
+@dataclass(frozen=True)
+class MultipleOf:
+    """Kernel block-size constraint (``MultipleOf(16)`` at beam_attn.py:764-765)."""
+    base: int
+
+
+@dataclass
+class CommonAttentionMetadata:
+    """The per-batch fields of vLLM's CommonAttentionMetadata the builder reads."""
+    query_start_loc: torch.Tensor        # [num_reqs+1] int32 (device)
+    query_start_loc_cpu: torch.Tensor    # [num_reqs+1] int32 (host)
+    seq_lens: torch.Tensor               # [num_reqs] int32 (device)
+    seq_lens_cpu: torch.Tensor           # [num_reqs] int32 (host)
+    num_reqs: int
+    num_actual_tokens: int
+    max_query_len: int
+    max_seq_len: int
+    block_table_tensor: torch.Tensor     # [num_reqs, max_blocks] int32 (device)
+    slot_mapping: torch.Tensor           # [num_actual_tokens] int64 (device)
+    causal: bool = True
+
+
+@dataclass
+class DecodeGroup:
+    """One ``gr_beam_attn_decode`` launch: every beam carries ``q_per_beam``
+    query rows; ``token_index`` maps its rows to batch token positions (None
+    when they are the batch's tokens in order)."""
+    token_index: torch.Tensor | None
+    prefix_bt: torch.Tensor
+    prefix_len: torch.Tensor
+    beam_start: torch.Tensor
+    suffix_bt: torch.Tensor
+    suffix_len: torch.Tensor
+    suffix_start: torch.Tensor | None
+    q_per_beam: int
+    max_beams: int
+
+
+@dataclass
+class BeamAttentionMetadata:
+    num_actual_tokens: int
+    max_query_len: int
+    query_start_loc: torch.Tensor
+    max_seq_len: int
+    seq_lens: torch.Tensor
+    block_table: torch.Tensor
+    slot_mapping: torch.Tensor
+    causal: bool = True
+    groups: list[DecodeGroup] = field(default_factory=list)
+    mega_req_idxs: list[int] = field(default_factory=list)
+    std_req_idxs: list[int] = field(default_factory=list)
+
+
+class BeamAttentionMetadataBuilder:
+    """Routes each request of a batch to a decode group (beam_attn.py:163-570)."""
+
+    supports_update_block_table: bool = True
+
+    def __init__(self, kv_cache_spec, layer_names, vllm_config, device: torch.device):
+        self.kv_cache_spec = kv_cache_spec
+        self.layer_names = layer_names
+        self.vllm_config = vllm_config
+        self.device = torch.device(device)
+        self.block_size = int(kv_cache_spec.block_size)
+
+    def build(self, common_prefix_len: int, common_attn_metadata: CommonAttentionMetadata,
+              fast_build: bool = False) -> BeamAttentionMetadata:
+        m = common_attn_metadata
+        info = MEGA_DATA_VAR.get()
+        mega_data = info["mega_data"] if info else {}
+        req_ids = info["req_ids"] if info else []
+        q_starts = m.query_start_loc_cpu.tolist()
+        seq_lens = m.seq_lens_cpu.tolist()
+        bs = self.block_size
+        dev = self.device
+        slot_mapping = m.slot_mapping
+
+        mega, std = [], []
+        for i in range(m.num_reqs):
+            rid = req_ids[i] if i < len(req_ids) else None
+            md = mega_data.get(rid, {}) if rid is not None else {}
+            (mega if md.get("is_mega_decode", False) else std).append((i, md))
+
+        groups: list[DecodeGroup] = []
+        # ---- mega-decode requests: one query token per beam over the resident suffix
+        if mega:
+            rows, pbt, plen, sbt, slen, widths, slots = [], [], [], [], [], [], []
+            for i, md in mega:
+                table = md["beam_kv"]
+                W = int(md["mega_beam_width"])
+                if W != table.beam_width or table.num_reqs != 1:
+                    raise ValueError(f"request {req_ids[i]}: beam_kv must hold one request of {W} beams")
+                if int(md["cache_len"]) < int(md["prefix_len"]):
+                    raise NotImplementedError(
+                        "mega decode needs the whole prompt prefix cached (prefill it through the "
+                        "standard path first)")
+                q0, q1 = q_starts[i], q_starts[i + 1]
+                if q1 - q0 != W:
+                    raise ValueError(f"request {req_ids[i]}: expected {W} query tokens (one per beam), "
+                                     f"got {q1 - q0}")
+                rows.append(torch.arange(q0, q1, device=dev))
+                pbt.append(table.prefix_bt)
+                plen.append(table.prefix_len)
+                sbt.append(table.suffix_bt)
+                slen.append(table.attention_suffix_len())
+                widths.append(W)
+                slots.append((q0, q1, table.slot_mapping()))
+            idx = torch.cat(rows)
+            slot_mapping = slot_mapping.clone()
+            for q0, q1, s in slots:
+                slot_mapping[q0:q1] = s
+            groups.append(self._group(idx, m.num_actual_tokens, pbt, plen, widths, sbt, slen, None, 1))
+
+        # ---- standard requests: the one-beam case, grouped by query length
+        by_len: dict[int, list[int]] = {}
+        for i, _ in std:
+            ql = q_starts[i + 1] - q_starts[i]
+            if ql > 0:
+                by_len.setdefault(ql, []).append(i)
+        for ql, reqs in sorted(by_len.items()):
+            rows, pbt, plen, sbt, slen, sstart = [], [], [], [], [], []
+            for i in reqs:
+                q0 = q_starts[i]
+                S = int(seq_lens[i])
+                cached = S - ql
+                nb = max(1, (S + bs - 1) // bs)
+                row = m.block_table_tensor[i, :nb].to(torch.int32)
+                rows.append(torch.arange(q0, q0 + ql, device=dev))
+                pbt.append(row[None])
+                plen.append(torch.tensor([cached], dtype=torch.int32, device=dev))
+                sbt.append(row[None])
+                slen.append(torch.tensor([ql], dtype=torch.int32, device=dev))
+                sstart.append(torch.tensor([cached], dtype=torch.int32, device=dev))
+            idx = torch.cat(rows)
+            groups.append(self._group(idx, m.num_actual_tokens, pbt, plen, [1] * len(reqs), sbt, slen,
+                                      sstart, ql))
+        return BeamAttentionMetadata(
+            num_actual_tokens=m.num_actual_tokens, max_query_len=m.max_query_len,
+            query_start_loc=m.query_start_loc, max_seq_len=m.max_seq_len, seq_lens=m.seq_lens,
+            block_table=m.block_table_tensor, slot_mapping=slot_mapping, causal=m.causal,
+            groups=groups, mega_req_idxs=[i for i, _ in mega], std_req_idxs=[i for i, _ in std])
+
+    def _group(self, idx, ntok, pbt, plen, widths, sbt, slen, sstart, T) -> DecodeGroup:
+        dev = self.device
+        pw = max(t.shape[1] for t in pbt)
+        sw = max(t.shape[1] for t in sbt)
+        pad = lambda ts, w: torch.cat([torch.nn.functional.pad(t, (0, w - t.shape[1]), value=-1) for t in ts])
+        beam_start = torch.tensor([0] + widths, dtype=torch.int64).cumsum(0).to(torch.int32).to(dev)
+        in_order = idx.numel() == ntok and bool((idx == torch.arange(ntok, device=dev)).all())
+        return DecodeGroup(
+            token_index=None if in_order else idx, prefix_bt=pad(pbt, pw).contiguous(),
+            prefix_len=torch.cat(plen).contiguous(), beam_start=beam_start,
+            suffix_bt=pad(sbt, sw).contiguous(), suffix_len=torch.cat(slen).to(torch.int32).contiguous(),
+            suffix_start=None if sstart is None else torch.cat(sstart).contiguous(), q_per_beam=T,
+            max_beams=max(widths))
+
+    def update_block_table(self, metadata: BeamAttentionMetadata, blk_table: torch.Tensor,
+                           slot_mapping: torch.Tensor) -> BeamAttentionMetadata:
+        new = copy.copy(metadata)
+        new.block_table = blk_table
+        new.slot_mapping = slot_mapping
+        return new
+
+
+class BeamAttentionImpl:
+    """``AttentionImpl`` of the backend (beam_attn.py:575-755)."""
+
+    can_return_lse_for_decode: bool = True
+
+    def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
+                 alibi_slopes: list[float] | None, sliding_window: int | None, kv_cache_dtype: str,
+                 logits_soft_cap: float | None = None, attn_type: str = AttentionType.DECODER,
+                 kv_sharing_target_layer_name: str | None = None,
+                 running_sinks: torch.Tensor | None = None) -> None:
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.scale = float(scale)
+        self.num_kv_heads = num_kv_heads
+        if num_heads % num_kv_heads != 0:
+            raise ValueError("num_heads must be a multiple of num_kv_heads")
+        self.num_queries_per_kv = num_heads // num_kv_heads
+        if alibi_slopes is not None:
+            raise NotImplementedError("BeamAttention does not support ALiBi slopes.")
+        if sliding_window is not None:
+            raise NotImplementedError("BeamAttention does not support sliding windows.")
+        if kv_cache_dtype not in ("auto", None):
+            raise NotImplementedError(f"BeamAttention does not support kv_cache_dtype={kv_cache_dtype}.")
+        if running_sinks is not None:
+            raise NotImplementedError("BeamAttention does not support attention sinks.")
+        self.kv_cache_dtype = kv_cache_dtype
+        self.logits_soft_cap = float(logits_soft_cap or 0.0)
+        self.attn_type = attn_type
+        self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
+
+    def forward(self, layer, query: torch.Tensor, key: torch.Tensor | None, value: torch.Tensor | None,
+                kv_cache: torch.Tensor, attn_metadata: BeamAttentionMetadata | None,
+                output: torch.Tensor | None = None, output_scale: torch.Tensor | None = None,
+                output_block_scale: torch.Tensor | None = None) -> torch.Tensor:
+        assert output is not None, "Output tensor must be provided."
+        if output_scale is not None or output_block_scale is not None:
+            raise NotImplementedError("fused output quantization is not yet supported for BeamAttentionImpl")
+        if attn_metadata is None:
+            return output.fill_(0)
+        k_cache, v_cache = ops.split_kv_cache(kv_cache)
+        n = attn_metadata.num_actual_tokens
+        if self.kv_sharing_target_layer_name is None and key is not None and value is not None:
+            ops.reshape_and_cache(key[:n], value[:n], k_cache, v_cache, attn_metadata.slot_mapping)
+        for g in attn_metadata.groups:
+            q = query[:n] if g.token_index is None else query.index_select(0, g.token_index)
+            out = output[:n] if g.token_index is None else None
+            res = ops.beam_attn_decode(q, k_cache, v_cache, g.prefix_bt, g.prefix_len, g.beam_start,
+                                       g.suffix_bt, g.suffix_len, g.suffix_start, q_per_beam=g.q_per_beam,
+                                       scale=self.scale, softcap=self.logits_soft_cap,
+                                       max_beams_per_req=g.max_beams, out=out)
+            if g.token_index is not None:
+                output.index_copy_(0, g.token_index, res)
+        return output
+
+
+class BeamAttentionBackend:
+    """Static surface registered as the ``CUSTOM`` backend (beam_attn.py:758-846)."""
+
+    accept_output_buffer = True
+    supported_dtypes = [torch.float16, torch.bfloat16]
+
+    @staticmethod
+    def get_supported_kernel_block_sizes() -> list:
+        return [MultipleOf(16)]
+
+    @staticmethod
+    def get_name() -> str:
+        return "CUSTOM"
+
+    @classmethod
+    def supports_attn_type(cls, attn_type: str) -> bool:
+        return attn_type == AttentionType.DECODER
+
+    @staticmethod
+    def get_impl_cls() -> type[BeamAttentionImpl]:
+        return BeamAttentionImpl
+
+    @staticmethod
+    def get_builder_cls() -> type[BeamAttentionMetadataBuilder]:
+        return BeamAttentionMetadataBuilder
+
+    @staticmethod
+    def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int, head_size: int,
+                           cache_dtype_str: str = "auto") -> tuple[int, ...]:
+        return (2, num_blocks, block_size, num_kv_heads, head_size)
+
+    @staticmethod
+    def get_kv_cache_stride_order(include_num_layers_dimension: bool = False, cache_layout: str = "NHD"):
+        # the kernels take block/token/head strides, so both layouts run as is
+        if cache_layout == "NHD":
+            return (2, 0, 1, 3, 4, 5) if include_num_layers_dimension else (0, 1, 2, 3, 4)
+        if cache_layout == "HND":
+            return (2, 4, 0, 1, 3, 5) if include_num_layers_dimension else (0, 1, 3, 2, 4)
+        raise ValueError(f"Unknown cache layout format {cache_layout}.")
+
+    @classmethod
+    def supports_head_size(cls, head_size: int) -> bool:
+        return head_size % 8 == 0 and head_size <= 256
+
+    @classmethod
+    def supports_kv_cache_dtype(cls, kv_cache_dtype: str | None) -> bool:
+        return kv_cache_dtype is None or kv_cache_dtype == "auto"
+
+    @classmethod
+    def supports_sink(cls) -> bool:
+        return False
+
+    @classmethod
+    def supports_compute_capability(cls, capability) -> bool:
+        """gfx950 (MI355X): the kernels are built for that target only."""
+        return str(capability).startswith("gfx950")
+
+    @classmethod
+    def supports_combination(cls, head_size, dtype, kv_cache_dtype, block_size, use_mla, has_sink,
+                             use_sparse, device_capability) -> str | None:
+        if dtype not in cls.supported_dtypes:
+            return f"Unsupported dtype {dtype}."
+        if not cls.supports_head_size(head_size):
+            return f"Unsupported head_size={head_size}."
+        if not cls.supports_kv_cache_dtype(kv_cache_dtype):
+            return f"Unsupported kv_cache_dtype={kv_cache_dtype}."
+        if block_size is not None and block_size % 16 != 0:
+            return f"block_size={block_size} not multiple of 16."
+        if not cls.supports_compute_capability(device_capability):
+            return "Requires gfx950 (MI355X)."
+        if has_sink and not cls.supports_sink():
+            return "No attention sink support."
+        if use_mla:
+            return "No MLA support."
+        if use_sparse:
+            return "No sparse support."
+        return None
