@@ -77,6 +77,108 @@ def cpu_baseline(wl, budget_s: float = 20.0):
                       f"(prefix pass + suffix pass + LSE merge)"}
 
 
+def _time_launches(step, steps: int, warmup: int) -> float:
+    """Average microseconds per launch over ``steps`` back-to-back launches on
+    the current stream (HIP events), after ``warmup`` untimed launches."""
+    import torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
+def bench_other(args) -> int:
+    """Fork+append (16 requests x 128 beams, old suffix U[1,15], 8 KV heads x
+    128 bf16) or pruning (64 requests x 128 beams x vocab 8192 fp32)."""
+    import numpy as np
+    import torch
+    from vllm_gr_amd import ops, workloads
+
+    dev = torch.device("cuda:0")
+    n_cpu = len(os.sched_getaffinity(0))
+    if args.workload == "fork":
+        host = workloads.fork_beam128(seed=0)
+        wl = host.to(dev)
+        k_cache, v_cache = wl.kv_cache[0], wl.kv_cache[1]
+        bt_out = torch.empty_like(wl.suffix_bt)
+        len_out = torch.empty_like(wl.suffix_len)
+
+        def step():  # out-of-place tables; copies and appends rewrite the same bytes each time
+            ops.beam_kv_fork(wl.parent, wl.suffix_bt, wl.suffix_len, k_cache, v_cache, wl.k_new, wl.v_new,
+                             bt_out=bt_out, len_out=len_out)
+        nbytes = host.algorithmic_bytes()
+        metric = "beam KV fork+append us/step + HBM GB/s at 16 requests x 128 beams"
+        workload = "fork+append: 16 requests x 128 beams, old suffix U[1,15], 8 kv heads x 128, block 16, bf16"
+        dtype = "u16 (bf16 bit copies) + int32 tables"
+    else:
+        host = workloads.prune_beam128(seed=0)
+        wl = host.to(dev)
+        ws = torch.empty(ops.prune_workspace_bytes(64, 128, 8192, 128), dtype=torch.uint8, device=dev)
+        outs = (torch.empty((64, 128), dtype=torch.int32, device=dev),
+                torch.empty((64, 128), dtype=torch.int32, device=dev),
+                torch.empty((64, 128), dtype=torch.float32, device=dev),
+                torch.empty((64, 128), dtype=torch.float32, device=dev))
+
+        def step():
+            ops.beam_prune_topk(wl.logits, wl.cum, 128, -1, workspace=ws, out=outs)
+        nbytes = host.algorithmic_bytes()
+        metric = "fused beam pruning us/step + HBM GB/s at 64 requests x 128 beams x vocab 8192"
+        workload = "prune: log_softmax + cum + top-128 over 128 beams x 8192 vocab, 64 requests, fp32"
+        dtype = "f32 (f64 scores)"
+    us = _time_launches(step, args.steps, args.warmup)
+    gbps = nbytes / (us * 1e-6) / 1e9
+    _log(f"bench: {args.workload}: {us:.2f} us/step, {gbps:.1f} GB/s algorithmic ({nbytes} B/step)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        if args.workload == "fork":
+            from oracle import fork as of
+            bits = lambda t: t.contiguous().view(torch.int16).numpy()
+            par = host.parent[:1].numpy()  # one request of 16 per timing (bounded sample)
+            W = par.shape[1]
+            runs = 0
+            while runs < 3 or time.perf_counter() - t0 < 10.0:
+                of.fork_append(par, host.suffix_bt[:W].numpy(), host.suffix_len[:W].numpy(),
+                               bits(host.kv_cache[0]), bits(host.kv_cache[1]), bits(host.k_new[:W]),
+                               bits(host.v_new[:W]), block_size=host.block_size)
+                runs += 1
+            us_cpu = (time.perf_counter() - t0) / runs * 16 * 1e6
+            sample = f"1 of 16 requests per run, {runs} runs, scaled x16; numpy fork+append restatement"
+            cores = 1
+        else:
+            from oracle import prune as op
+            x = host.logits[:4].numpy()
+            c = host.cum[:4].numpy()
+            runs = 0
+            while runs < 3 or time.perf_counter() - t0 < 10.0:
+                op.prune_topk(x, c, 128)
+                runs += 1
+            us_cpu = (time.perf_counter() - t0) / runs * 16 * 1e6
+            sample = f"4 of 64 requests per run, {runs} runs, scaled x16; scalar C restatement"
+            cores = 1
+        cpu = {"value": round(nbytes / (us_cpu * 1e-6) / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+               "us_per_step": round(us_cpu, 1), "sample": sample}
+        _log(f"bench: cpu {cpu} (host has {n_cpu} cores)")
+    line = {"metric": metric, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 5), "us_per_step": round(us, 3),
+            "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded)",
+            "config": {"workload": workload, "algorithmic_bytes_per_step": nbytes},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+            "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -84,6 +186,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", choices=["auto", "generic"], default="auto")
+    ap.add_argument("--workload", choices=["decode", "fork", "prune"], default="decode",
+                    help="decode (the headline line), or the fork+append / pruning kernels")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 256 MiB device-to-device copy (5 launches), the reference point "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -106,6 +210,9 @@ def main() -> int:
                           "launches": 5}), flush=True)
         return 0
     from vllm_gr_amd import ops, workloads
+
+    if args.workload != "decode":
+        return bench_other(args)
 
     dev = torch.device("cuda:0")
     _log("bench: building decode_beam128 inputs (seed 0)")
