@@ -5,19 +5,15 @@
 // Kernel 1 (prune_rows): one workgroup of 256 threads per beam row.  Reads
 // the row once (float4, rows up to 8192 held in registers), computes the row
 // max, the fixed-order fp32 exp-sum, the float64 LSE, and the row's top-k by
-// (logit desc, token asc):
-//   * the k-th largest of the 256 per-thread maxima bounds the k-th largest
-//     element from below, so only elements >= that bound survive (about
-//     k * 1.4 for random data); survivors are ranked exactly by counting;
-//   * rows with too many survivors (heavy ties) fall back to an exact
-//     bisection over the order-preserving integer image of the logits and
-//     take tied elements in ascending token order.
-// Kernel 2 (prune_merge): one workgroup per request.  The per-row lists are
-// sorted, so "how many candidates score >= t" is one binary search per row.
-// A bisection over the order-preserving integer image of float64 scores
-// narrows [lo, hi) until few candidates remain between, which are ranked
-// exactly; exact ties are resolved by lowest flat index (rows in ascending
-// beam order, tokens ascending inside a row).
+// (logit desc, token asc): a three-pass radix select (11/11/10-bit digits,
+// LDS histograms) over the order-preserving integer image of the logits finds
+// the k-th largest key T exactly; keys above T are taken, then keys equal to
+// T in ascending token order; the k selected are ranked by counting.
+// Kernel 2 (prune_merge): one workgroup of 1024 threads per request.  A
+// six-pass radix select over the order-preserving 64-bit image of the float64
+// scores finds the k-th largest score exactly; candidates above it are taken,
+// then exact ties in ascending flat index (rows in beam order, equal scores
+// of one row in token order); the k selected are ranked by counting.
 //
 // This file is compiled with -ffp-contract=off: every float operation below
 // is a single IEEE operation so the CPU restatement reproduces the scores
@@ -31,10 +27,10 @@ constexpr int PR_THREADS = 256;
 constexpr int PR_VEC = 4;
 constexpr int PR_CHUNK = PR_THREADS * PR_VEC;  // elements per chunk
 constexpr int PR_REG_CHUNKS = 8;               // rows of up to 8192 stay in registers
-constexpr int PR_CAP = 1024;                   // survivor capacity of the fast path
 constexpr int PR_MAXK = 1024;
 constexpr int PR_MAXW = 1024;
-constexpr int PR_CAP2 = 512;                   // merge: candidates ranked exactly at the end
+constexpr int PR_BINS = 2048;                  // radix-select histogram bins (11-bit digits)
+constexpr int MG_THREADS = 1024;               // merge workgroup
 
 typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 
@@ -92,10 +88,6 @@ __device__ inline uint64_t dkey(double x) {
   const uint64_t u = __builtin_bit_cast(uint64_t, x);
   return (u >> 63) ? ~u : (u | (1ull << 63));
 }
-__device__ inline double dval(uint64_t k) {
-  const uint64_t u = (k >> 63) ? (k & ~(1ull << 63)) : ~k;
-  return __builtin_bit_cast(double, u);
-}
 
 struct PruneArgs {
   const float* logits;
@@ -122,7 +114,8 @@ __device__ inline int wave_sum_i(int v) {
   return v;
 }
 
-// block-wide exclusive scan of one int per thread; returns the total
+// block-wide exclusive scan of one int per thread (NT threads); returns the total
+template <int NT = PR_THREADS>
 __device__ int block_scan(int v, int& excl, int* tmp) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int incl = v;
@@ -135,7 +128,7 @@ __device__ int block_scan(int v, int& excl, int* tmp) {
   __syncthreads();
   int base = 0, total = 0;
 #pragma unroll
-  for (int w = 0; w < PR_THREADS / 64; ++w) {
+  for (int w = 0; w < NT / 64; ++w) {
     base += (w < wave) ? tmp[w] : 0;
     total += tmp[w];
   }
@@ -144,22 +137,79 @@ __device__ int block_scan(int v, int& excl, int* tmp) {
   return total;
 }
 
-__device__ int block_sum(int v, int* tmp) {
-  int e;
-  return block_scan(v, e, tmp);
+// Radix select: the need-th largest (1-based) of the unsigned KBITS-bit keys
+// that for_each(f) hands to f (each thread its own keys; at least `need` keys
+// in total).  Digits of 11 bits from the top; a pass histograms the keys that
+// match the digits fixed so far and walks the bins from the top.  Stops early
+// once the bin holding the need-th key holds exactly the keys still needed.
+// Result: keys with (key & mask) > prefix are above the boundary (k_need - need
+// of them); the `need` remaining come from the eq keys with (key & mask) ==
+// prefix -- all of them when eq == need, else (mask all ones) a choice among
+// equal keys left to the caller.
+template <typename K>
+struct RadixSel {
+  K prefix, mask;
+  int need, eq;
+};
+
+template <int NT, typename K, int KBITS, typename ForEach>
+__device__ RadixSel<K> radix_select(ForEach for_each, int need, int* hist, int* itmp, int* sel) {
+  const int tid = threadIdx.x;
+  RadixSel<K> rs{0, 0, need, 0};
+  constexpr int NP = (KBITS + 10) / 11;
+  constexpr int BPT = PR_BINS / NT;  // bins owned per thread in the top-down walk
+#pragma unroll 1
+  for (int pass = 0; pass < NP; ++pass) {
+    const int hi_bit = KBITS - 11 * pass;
+    const int shift = hi_bit > 11 ? hi_bit - 11 : 0;
+    const K dmask = (K(1) << (hi_bit - shift)) - 1;
+    for (int i = tid; i < PR_BINS; i += NT) hist[i] = 0;
+    __syncthreads();
+    const K pm = rs.mask, pp = rs.prefix;
+    for_each([&](K u) {
+      if ((u & pm) == pp) atomicAdd(&hist[(int)((u >> shift) & dmask)], 1);
+    });
+    __syncthreads();
+    int loc = 0;
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) loc += hist[BPT * tid + i];
+    int excl;
+    const int tot = block_scan<NT>(loc, excl, itmp);
+    const int above = tot - excl - loc;  // keys in bins owned by higher threads
+    if (above < rs.need && rs.need <= above + loc) {
+      int acc = above;
+      for (int i = BPT - 1; i >= 0; --i) {
+        const int h = hist[BPT * tid + i];
+        if (acc + h >= rs.need) {
+          sel[0] = BPT * tid + i;
+          sel[1] = acc;
+          sel[2] = h;
+          break;
+        }
+        acc += h;
+      }
+    }
+    __syncthreads();
+    rs.prefix |= (K)sel[0] << shift;
+    rs.mask |= dmask << shift;
+    rs.need -= sel[1];
+    rs.eq = sel[2];
+    __syncthreads();
+    if (rs.eq == rs.need) break;
+  }
+  return rs;
 }
 
 template <int MAXC>  // MAXC > 0: row held in registers (<= MAXC chunks); 0: re-read from memory
 __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
-  __shared__ float sx[PR_CAP];
-  __shared__ int sv[PR_CAP];
+  __shared__ float sx[PR_MAXK];
+  __shared__ int sv[PR_MAXK];
   __shared__ float ox[PR_MAXK];
   __shared__ int ov[PR_MAXK];
-  __shared__ float tmx[PR_THREADS];
-  __shared__ int has[PR_THREADS];
+  __shared__ int hist[PR_BINS];
   __shared__ float wred[PR_THREADS / 64];
   __shared__ int itmp[PR_THREADS / 64];
-  __shared__ float t0_s;
+  __shared__ int sel[3];
   __shared__ int eos_pos;
 
   const int row = blockIdx.x;
@@ -197,8 +247,6 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   }
   const float wm = wave_max(tm);
   if (lane == 0) wred[wave] = wm;
-  tmx[tid] = tm;
-  has[tid] = valid(0) ? 1 : 0;
   __syncthreads();
   float m = wred[0];
 #pragma unroll
@@ -228,82 +276,31 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     c_row = (double)a.cum[row] - lse;
   }
 
-  // ---- stage 1: row top-k1 by (logit desc, token asc) ----
-  int nthr = 0;  // threads owning elements
-  for (int u = 0; u < PR_THREADS; ++u) nthr += has[u];
-  bool fast = k1 <= nthr;
-  if (fast) {
-    if (has[tid]) {
-      int rank = 0;
-      for (int u = 0; u < PR_THREADS; ++u) {
-        const float y = tmx[u];
-        rank += has[u] && (y > tm || (y == tm && u < tid));
-      }
-      if (rank == k1 - 1) t0_s = tm;
-    }
-    __syncthreads();
-    const float t0 = t0_s;
-    int cnt = 0;
-    PR_FOR_CHUNKS(c) {
-      if (valid(c)) {
+  // ---- stage 1: row top-k1 by (logit desc, token asc), radix select ----
+  const RadixSel<uint32_t> rs = radix_select<PR_THREADS, uint32_t, 32>(
+      [&](auto&& f) {
+        PR_FOR_CHUNKS(c) {
+          if (valid(c)) {
 #pragma unroll
-        for (int j = 0; j < PR_VEC; ++j) cnt += get(c, j) >= t0;
-      }
-    }
-    int off;
-    const int total = block_scan(cnt, off, itmp);
-    fast = total <= PR_CAP;
-    if (fast) {
-      PR_FOR_CHUNKS(c) {
-        if (valid(c)) {
-#pragma unroll
-          for (int j = 0; j < PR_VEC; ++j) {
-            const float y = get(c, j);
-            if (y >= t0) {
-              sx[off] = y;
-              sv[off] = c * PR_CHUNK + PR_VEC * tid + j;
-              ++off;
-            }
+            for (int j = 0; j < PR_VEC; ++j) f(fkey(get(c, j)));
           }
         }
-      }
-      __syncthreads();
-      for (int i = tid; i < total; i += PR_THREADS) {
-        const float xi = sx[i];
-        const int vi = sv[i];
-        int rank = 0;
-        for (int q = 0; q < total; ++q) {
-          const float y = sx[q];
-          rank += (y > xi) || (y == xi && sv[q] < vi);
-        }
-        if (rank < k1) {
-          ox[rank] = xi;
-          ov[rank] = vi;
-        }
-      }
-    }
-  }
-  if (!fast) {
-    // exact fallback: largest key T with count(key >= T) >= k1
-    uint64_t lo = 0, hi = 1ull << 32;
-    while (hi - lo > 1) {
-      const uint64_t mid = lo + (hi - lo) / 2;
-      int cnt = 0;
-      PR_FOR_CHUNKS(c) {
-        if (valid(c)) {
-#pragma unroll
-          for (int j = 0; j < PR_VEC; ++j) cnt += (uint64_t)fkey(get(c, j)) >= mid;
-        }
-      }
-      const int tot = block_sum(cnt, itmp);
-      if (tot >= k1) lo = mid; else hi = mid;
-    }
-    const uint32_t T = (uint32_t)lo;
-    int gt = 0;
+      },
+      k1, hist, itmp, sel);
+  const uint32_t T = rs.prefix, Tm = rs.mask;
+  const int need = rs.need, eq_cnt = rs.eq;
+  // keys above the boundary: k1 - need of them, all taken; keys at it: all
+  // when eq_cnt == need, else the first `need` by token
+  {
+    int gt = 0, eq = 0;
     PR_FOR_CHUNKS(c) {
       if (valid(c)) {
 #pragma unroll
-        for (int j = 0; j < PR_VEC; ++j) gt += fkey(get(c, j)) > T;
+        for (int j = 0; j < PR_VEC; ++j) {
+          const uint32_t u = fkey(get(c, j)) & Tm;
+          gt += u > T;
+          eq += u == T;
+        }
       }
     }
     int off;
@@ -313,7 +310,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 #pragma unroll
         for (int j = 0; j < PR_VEC; ++j) {
           const float y = get(c, j);
-          if (fkey(y) > T) {
+          if ((fkey(y) & Tm) > T) {
             sx[off] = y;
             sv[off] = c * PR_CHUNK + PR_VEC * tid + j;
             ++off;
@@ -321,37 +318,56 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
         }
       }
     }
-    // ties at T in ascending token order until k1 are taken
-    int taken = ngt;
-    PR_FOR_CHUNKS(c) {
-      int tc = 0;
-      if (valid(c)) {
+    if (eq_cnt == need) {  // every key equal to T is taken: order is irrelevant here
+      int eoff;
+      block_scan(eq, eoff, itmp);
+      PR_FOR_CHUNKS(c) {
+        if (valid(c)) {
 #pragma unroll
-        for (int j = 0; j < PR_VEC; ++j) tc += fkey(get(c, j)) == T;
-      }
-      int toff;
-      const int ctot = block_scan(tc, toff, itmp);
-      if (valid(c)) {
-#pragma unroll
-        for (int j = 0; j < PR_VEC; ++j) {
-          if (fkey(get(c, j)) == T) {
-            const int pos = taken + toff;
-            if (pos < k1) {
-              sx[pos] = get(c, j);
-              sv[pos] = c * PR_CHUNK + PR_VEC * tid + j;
+          for (int j = 0; j < PR_VEC; ++j) {
+            const float y = get(c, j);
+            if ((fkey(y) & Tm) == T) {
+              sx[ngt + eoff] = y;
+              sv[ngt + eoff] = c * PR_CHUNK + PR_VEC * tid + j;
+              ++eoff;
             }
-            ++toff;
           }
         }
       }
-      taken += ctot;
-      if (taken >= k1) break;
+    } else {  // ties at T: ascending token order (chunk-major, then thread, then lane)
+      int taken = 0;
+      PR_FOR_CHUNKS(c) {
+        int tc = 0;
+        if (valid(c)) {
+#pragma unroll
+          for (int j = 0; j < PR_VEC; ++j) tc += fkey(get(c, j)) == T;
+        }
+        int toff;
+        const int ctot = block_scan(tc, toff, itmp);
+        if (valid(c)) {
+#pragma unroll
+          for (int j = 0; j < PR_VEC; ++j) {
+            if (fkey(get(c, j)) == T) {
+              const int pos = taken + toff;
+              if (pos < need) {
+                sx[ngt + pos] = get(c, j);
+                sv[ngt + pos] = c * PR_CHUNK + PR_VEC * tid + j;
+              }
+              ++toff;
+            }
+          }
+        }
+        taken += ctot;
+        if (taken >= need) break;
+      }
     }
     __syncthreads();
+    // rank the k1 selected: (logit desc, token asc)
     for (int i = tid; i < k1; i += PR_THREADS) {
       const float xi = sx[i];
       const int vi = sv[i];
       int rank = 0;
+#pragma unroll 8
       for (int q = 0; q < k1; ++q) {
         const float y = sx[q];
         rank += (y > xi) || (y == xi && sv[q] < vi);
@@ -385,218 +401,136 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   }
 }
 
-// ---- kernel 2: per-request merge of the sorted row lists --------------------
-struct MergeCtx {
-  const float* xs;  // [W, k1] (LDS copy or workspace)
-  const int32_t* vs;
-  const double* cs;  // [W]
-  int k1;
-  int64_t V;
-};
+// ---- kernel 2: per-request top-k over the rows' candidate lists -----------
+typedef int32_t i32x4_t __attribute__((__vector_size__(4 * sizeof(int32_t))));
 
-__device__ inline double cand_score(const MergeCtx& m, int b, int j) {
-  const int v = m.vs[b * m.k1 + j];
-  if (v < 0) return -INFINITY;
-  const double c = m.cs[b];
-  return c == -INFINITY ? -INFINITY : (double)m.xs[b * m.k1 + j] + c;
-}
-__device__ inline int64_t cand_flat(const MergeCtx& m, int b, int j) {
-  const int v = m.vs[b * m.k1 + j];
-  return v < 0 ? INT64_MAX : (int64_t)b * m.V + v;
-}
-// number of candidates of row b (first nvalid entries) with score >= t
-__device__ inline int count_ge(const MergeCtx& m, int b, int nvalid, double t) {
-  int lo = 0, hi = nvalid;  // first index with score < t
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (cand_score(m, b, mid) >= t) lo = mid + 1; else hi = mid;
-  }
-  return lo;
-}
-
-template <bool LDS_LISTS>
-__global__ __launch_bounds__(PR_THREADS) void prune_merge(PruneArgs a) {
+template <bool LDS_LISTS>  // true: the request's W x k1 lists are staged in LDS
+__global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
   __shared__ double cs[PR_MAXW];
-  __shared__ int nval[PR_MAXW], ge_lo[PR_MAXW], ge_hi[PR_MAXW];
-  __shared__ int between[PR_CAP2];
+  // the radix histogram during the selection, then the selected scores / flats
+  __shared__ __attribute__((aligned(16))) uint8_t work[PR_MAXK * 16];
   __shared__ int fin[PR_MAXK];
-  __shared__ int itmp[PR_THREADS / 64];
-  __shared__ double dred[PR_THREADS / 64][2];
+  __shared__ int itmp[MG_THREADS / 64];
+  __shared__ int sel[3];
+  int* hist = reinterpret_cast<int*>(work);
+  double* fsc = reinterpret_cast<double*>(work);
+  int64_t* ffl = reinterpret_cast<int64_t*>(work + PR_MAXK * 8);
 
   const int r = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int W = a.W, k1 = a.k1, k = a.k;
-  // each thread owns a contiguous row range, so thread order is beam order
-  const int rpt = (W + PR_THREADS - 1) / PR_THREADS;
-  const int rb0 = min(W, tid * rpt), rb1 = min(W, rb0 + rpt);
+  const int n = W * k1;
   const int64_t rbase = (int64_t)r * W;
-  MergeCtx m;
-  m.k1 = k1;
-  m.V = a.V;
-  m.cs = cs;
+  const float* gx = a.cand_x + rbase * k1;
+  const int32_t* gv = a.cand_v + rbase * k1;
+  const float* xs = gx;
+  const int32_t* vs = gv;
   if constexpr (LDS_LISTS) {
-    float* xs = reinterpret_cast<float*>(dyn);
-    int32_t* vs = reinterpret_cast<int32_t*>(dyn + sizeof(float) * (size_t)W * k1);
-    for (int i = tid; i < W * k1; i += PR_THREADS) {
-      xs[i] = a.cand_x[rbase * k1 + i];
-      vs[i] = a.cand_v[rbase * k1 + i];
-    }
-    m.xs = xs;
-    m.vs = vs;
-  } else {
-    m.xs = a.cand_x + rbase * k1;
-    m.vs = a.cand_v + rbase * k1;
-  }
-  for (int b = tid; b < W; b += PR_THREADS) cs[b] = a.row_c[rbase + b];  // any order
-  __syncthreads();
-  // per-row valid counts, global score range
-  double smin = INFINITY, smax = -INFINITY;
-  int nv_loc = 0;
-  for (int b = rb0; b < rb1; ++b) {
-    int nv = 0;
-    {
-      int lo = 0, hi = k1;  // valid entries form a prefix
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (m.vs[b * k1 + mid] >= 0) lo = mid + 1; else hi = mid;
+    float* xl = reinterpret_cast<float*>(dyn);
+    int32_t* vl = reinterpret_cast<int32_t*>(dyn + sizeof(float) * (size_t)n);
+    if ((n & 3) == 0) {  // the request's lists then start 16-byte aligned
+      for (int i = 4 * tid; i < n; i += 4 * MG_THREADS) {
+        *reinterpret_cast<f32x4_t*>(xl + i) = *reinterpret_cast<const f32x4_t*>(gx + i);
+        *reinterpret_cast<i32x4_t*>(vl + i) = *reinterpret_cast<const i32x4_t*>(gv + i);
       }
-      nv = lo;
+    } else {
+      for (int i = tid; i < n; i += MG_THREADS) {
+        xl[i] = gx[i];
+        vl[i] = gv[i];
+      }
     }
-    nval[b] = nv;
-    nv_loc += nv;
-    if (nv > 0) {
-      smax = fmax(smax, cand_score(m, b, 0));
-      smin = fmin(smin, cand_score(m, b, nv - 1));
-    }
+    xs = xl;
+    vs = vl;
   }
-#pragma unroll
-  for (int msk = 32; msk >= 1; msk >>= 1) {
-    smin = fmin(smin, __shfl_xor(smin, msk, 64));
-    smax = fmax(smax, __shfl_xor(smax, msk, 64));
-  }
-  if (lane == 0) {
-    dred[wave][0] = smin;
-    dred[wave][1] = smax;
-  }
-  const int M = block_sum(nv_loc, itmp);  // includes a barrier after dred writes
-  for (int w = 0; w < PR_THREADS / 64; ++w) {
-    smin = fmin(smin, dred[w][0]);
-    smax = fmax(smax, dred[w][1]);
-  }
+  for (int b = tid; b < W; b += MG_THREADS) cs[b] = a.row_c[rbase + b];
+  __syncthreads();
 
-  int n_above = 0;  // candidates certainly selected (score >= value(hi))
-  int q = 0;        // how many to take from the "between" range
-  bool ties = false;
-  if (M <= k) {
-    for (int b = rb0; b < rb1; ++b) {
-      ge_hi[b] = nval[b];
-      ge_lo[b] = nval[b];
-    }
-    n_above = M;
-  } else {
-    uint64_t lo = dkey(smin), hi = dkey(smax) + 1;
-    int cnt_lo = M, cnt_hi = 0;
-    while (hi - lo > 1 && cnt_lo - cnt_hi > PR_CAP2) {
-      const uint64_t mid = lo + (hi - lo) / 2;
-      const double t = dval(mid);
-      int c = 0;
-      for (int b = rb0; b < rb1; ++b) c += count_ge(m, b, nval[b], t);
-      const int tot = block_sum(c, itmp);
-      if (tot >= k) {
-        lo = mid;
-        cnt_lo = tot;
-      } else {
-        hi = mid;
-        cnt_hi = tot;
+  // candidate i = b * k1 + j (row b, list position j), score cum - lse + logit;
+  // thread tid visits i = tid, tid + NT, ... with b stepped incrementally.
+  // Padding entries (token -1) are no candidates.
+  const int db = MG_THREADS / k1, dj = MG_THREADS - db * k1;
+  auto for_cand = [&](auto&& f) {
+    int b = tid / k1, j = tid - b * k1;
+    for (int i = tid; i < n; i += MG_THREADS) {
+      const int v = vs[i];
+      if (v >= 0) {
+        const double c = cs[b];
+        const double sc = c == -INFINITY ? -INFINITY : ((double)xs[i] + c) + 0.0;  // -0 -> +0
+        f(b, v, sc);
+      }
+      b += db;
+      j += dj;
+      if (j >= k1) {
+        j -= k1;
+        ++b;
       }
     }
-    const double tlo = dval(lo), thi = dval(hi);
-    for (int b = rb0; b < rb1; ++b) {
-      ge_lo[b] = count_ge(m, b, nval[b], tlo);
-      ge_hi[b] = count_ge(m, b, nval[b], thi);
-    }
-    n_above = cnt_hi;
-    q = k - cnt_hi;
-    ties = cnt_lo - cnt_hi > PR_CAP2;  // hi == lo + 1: all "between" share one score
-  }
-  __syncthreads();
-  // gather: above-hi candidates and the between set (as b * k1 + j)
-  {
-    int na = 0, nb = 0;
-    for (int b = rb0; b < rb1; ++b) {
-      na += ge_hi[b];
-      nb += ge_lo[b] - ge_hi[b];
-    }
-    int oa, ob;
-    block_scan(na, oa, itmp);
-    const int nbt = block_scan(nb, ob, itmp);
-    (void)nbt;
-    for (int b = rb0; b < rb1; ++b) {
-      for (int j = 0; j < ge_hi[b]; ++j) fin[oa++] = b * k1 + j;
-      if (!ties) {
-        for (int j = ge_hi[b]; j < ge_lo[b]; ++j) between[ob++] = b * k1 + j;
-      }
-    }
-    if (ties) {
-      // exact ties at one score: lowest flat index = ascending beam, then token
-      int tie = 0;
-      for (int b = rb0; b < rb1; ++b) tie += ge_lo[b] - ge_hi[b];
-      int toff;
-      block_scan(tie, toff, itmp);
-      for (int b = rb0; b < rb1; ++b) {
-        for (int j = ge_hi[b]; j < ge_lo[b]; ++j) {
-          if (toff < q) fin[n_above + toff] = b * k1 + j;
-          ++toff;
-        }
-      }
-    }
-  }
-  __syncthreads();
-  if (!ties && M > k) {
-    const int nb = [&] {
-      int s = 0;
-      for (int b = 0; b < W; ++b) s += ge_lo[b] - ge_hi[b];
-      return s;
-    }();
-    for (int i = tid; i < nb; i += PR_THREADS) {
-      const int bi = between[i] / k1, ji = between[i] % k1;
-      const double si = cand_score(m, bi, ji);
-      const int64_t fi = cand_flat(m, bi, ji);
-      int rank = 0;
-      for (int u = 0; u < nb; ++u) {
-        const int bu = between[u] / k1, ju = between[u] % k1;
-        const double su = cand_score(m, bu, ju);
-        rank += (su > si) || (su == si && cand_flat(m, bu, ju) < fi);
-      }
-      if (rank < q) fin[n_above + rank] = between[i];
-    }
-    __syncthreads();
-  }
-  // final order of the selected set: (score desc, flat asc)
+  };
+  int mv = 0;
+  for_cand([&](int, int, double) { ++mv; });
+  int excl;
+  const int M = block_scan<MG_THREADS>(mv, excl, itmp);
   const int nsel = M < k ? M : k;
-  for (int i = tid; i < k; i += PR_THREADS) {
-    const int64_t o = (int64_t)r * k;
-    if (i >= nsel) {
-      a.parent[o + i] = -1;
-      a.token[o + i] = -1;
-      a.score[o + i] = -INFINITY;
+
+  // boundary score (k-th largest), then among exact ties at it the lowest flat
+  // index b * V + v (key ~(b << 32 | v): the largest key is the lowest index)
+  RadixSel<uint64_t> r1{0, 0, 0, 0}, r2{0, 0, 0, 0};
+  bool ties = false;
+  if (M > k) {
+    r1 = radix_select<MG_THREADS, uint64_t, 64>(
+        [&](auto&& f) { for_cand([&](int, int, double sc) { f(dkey(sc)); }); }, k, hist, itmp, sel);
+    if (r1.eq != r1.need) {
+      ties = true;
+      r2 = radix_select<MG_THREADS, uint64_t, 64>(
+          [&](auto&& f) {
+            for_cand([&](int b, int v, double sc) {
+              if (dkey(sc) == r1.prefix) f(~(((uint64_t)b << 32) | (uint32_t)v));
+            });
+          },
+          r1.need, hist, itmp, sel);
     }
   }
-  for (int i = tid; i < nsel; i += PR_THREADS) {
-    const int bi = fin[i] / k1, ji = fin[i] % k1;
-    const double si = cand_score(m, bi, ji);
-    const int64_t fi = cand_flat(m, bi, ji);
+  auto selected = [&](int b, int v, double sc) -> bool {
+    if (M <= k) return true;
+    const uint64_t u = dkey(sc) & r1.mask;
+    if (u != r1.prefix) return u > r1.prefix;
+    if (!ties) return true;
+    return (~(((uint64_t)b << 32) | (uint32_t)v) & r2.mask) >= r2.prefix;
+  };
+  int cnt = 0;
+  for_cand([&](int b, int v, double sc) { cnt += selected(b, v, sc); });
+  int off;
+  block_scan<MG_THREADS>(cnt, off, itmp);  // nsel in total; the histogram is dead from here
+  for_cand([&](int b, int v, double sc) {
+    if (selected(b, v, sc)) {
+      fsc[off] = sc;
+      ffl[off] = (int64_t)b * a.V + v;
+      fin[off] = b;
+      ++off;
+    }
+  });
+  __syncthreads();
+  // final order of the selected set: (score desc, flat asc)
+  for (int i = tid; i < nsel; i += MG_THREADS) {
+    const double si = fsc[i];
+    const int64_t fi = ffl[i];
     int rank = 0;
+#pragma unroll 8
     for (int u = 0; u < nsel; ++u) {
-      const int bu = fin[u] / k1, ju = fin[u] % k1;
-      const double su = cand_score(m, bu, ju);
-      rank += (su > si) || (su == si && cand_flat(m, bu, ju) < fi);
+      const double su = fsc[u];
+      rank += (su > si) || (su == si && ffl[u] < fi);
     }
     const int64_t o = (int64_t)r * k + rank;
-    a.parent[o] = bi;
-    a.token[o] = m.vs[bi * k1 + ji];
+    a.parent[o] = fin[i];
+    a.token[o] = (int32_t)(fi - (int64_t)fin[i] * a.V);
     a.score[o] = (float)si;
+  }
+  for (int i = nsel + tid; i < k; i += MG_THREADS) {
+    const int64_t o = (int64_t)r * k + i;
+    a.parent[o] = -1;
+    a.token[o] = -1;
+    a.score[o] = -INFINITY;
   }
 }
 
@@ -663,9 +597,9 @@ extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_ro
                           hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
       attr_set = true;
     }
-    hipLaunchKernelGGL(prune_merge<true>, dim3((unsigned)num_reqs), dim3(PR_THREADS), list_bytes, stream, a);
+    hipLaunchKernelGGL(prune_merge<true>, dim3((unsigned)num_reqs), dim3(MG_THREADS), list_bytes, stream, a);
   } else {
-    hipLaunchKernelGGL(prune_merge<false>, dim3((unsigned)num_reqs), dim3(PR_THREADS), 0, stream, a);
+    hipLaunchKernelGGL(prune_merge<false>, dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
   }
   return launch_status();
 }
