@@ -20,6 +20,8 @@
 // bit for bit.
 #include "gr_common.h"
 
+#include <type_traits>
+
 namespace gr {
 namespace {
 
@@ -30,6 +32,7 @@ constexpr int PR_REG_CHUNKS = 8;               // rows of up to 8192 stay in reg
 constexpr int PR_MAXK = 1024;
 constexpr int PR_MAXW = 1024;
 constexpr int PR_BINS = 2048;                  // radix-select histogram bins (11-bit digits)
+constexpr int PR_SURV = 512;                   // row survivors ranked directly (at most)
 constexpr int MG_THREADS = 1024;               // merge workgroup
 
 typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
@@ -38,7 +41,8 @@ typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 // exp2 of t <= 0: Taylor series of e^(f ln2) (degree 7, Horner with fma) on the
 // fractional part f = t - rint(t), scaled by 2^rint(t).
 __device__ inline float exp2_neg(float t) {
-  if (!(t >= -125.0f)) return 0.0f;
+  const bool zero = !(t >= -125.0f);  // a select, not a branch: the 32 chains interleave
+  t = zero ? 0.0f : t;
   const float k = __builtin_rintf(t);
   const float f = t - k;
   float p = 0x1.ffcbfcp-17f;
@@ -49,7 +53,8 @@ __device__ inline float exp2_neg(float t) {
   p = __builtin_fmaf(p, f, 0x1.ebfbe0p-3f);
   p = __builtin_fmaf(p, f, 0x1.62e430p-1f);
   p = __builtin_fmaf(p, f, 0x1.000000p+0f);
-  return __builtin_amdgcn_ldexpf(p, (int)k);
+  const float e = __builtin_amdgcn_ldexpf(p, (int)k);
+  return zero ? 0.0f : e;
 }
 
 // natural log of s >= 1 in float64: s = mant * 2^e, mant in [sqrt(1/2), sqrt(2)),
@@ -84,9 +89,19 @@ __device__ inline uint32_t fkey(float x) {
   const uint32_t u = __builtin_bit_cast(uint32_t, x);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+__device__ inline float fval(uint32_t k) {
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+// row order (logit desc, token asc) as one unsigned key: larger key first
+__device__ inline uint64_t row_key(uint32_t fk, int token) {
+  return ((uint64_t)fk << 32) | (uint32_t)~(uint32_t)token;
+}
 __device__ inline uint64_t dkey(double x) {
   const uint64_t u = __builtin_bit_cast(uint64_t, x);
   return (u >> 63) ? ~u : (u | (1ull << 63));
+}
+__device__ inline double dval(uint64_t k) {
+  return __builtin_bit_cast(double, (k >> 63) ? (k & ~(1ull << 63)) : ~k);
 }
 
 struct PruneArgs {
@@ -137,30 +152,40 @@ __device__ int block_scan(int v, int& excl, int* tmp) {
   return total;
 }
 
-// Radix select: the need-th largest (1-based) of the unsigned KBITS-bit keys
-// that for_each(f) hands to f (each thread its own keys; at least `need` keys
-// in total).  Digits of 11 bits from the top; a pass histograms the keys that
-// match the digits fixed so far and walks the bins from the top.  Stops early
-// once the bin holding the need-th key holds exactly the keys still needed.
-// Result: keys with (key & mask) > prefix are above the boundary (k_need - need
-// of them); the `need` remaining come from the eq keys with (key & mask) ==
-// prefix -- all of them when eq == need, else (mask all ones) a choice among
-// equal keys left to the caller.
+// Radix select: the need-th largest (1-based) of the unsigned keys that
+// for_each(f) hands to f (each thread its own keys; at least `need` keys in
+// total, all within [kmin, kmax]).  The bits above the highest bit in which
+// kmin and kmax differ are common to every key; below it, digits of 11 bits
+// from the top: a pass histograms the keys that match the digits fixed so far
+// and walks the bins from the top.  Stops early once the bin holding the
+// need-th key holds exactly the keys still needed.
+// Result: keys with (key & mask) > prefix are above the boundary (need_in -
+// need of them); the `need` remaining come from the eq keys with (key & mask)
+// == prefix -- all of them when eq == need, else (mask all ones) a choice
+// among equal keys left to the caller.
 template <typename K>
 struct RadixSel {
   K prefix, mask;
   int need, eq;
 };
 
-template <int NT, typename K, int KBITS, typename ForEach>
-__device__ RadixSel<K> radix_select(ForEach for_each, int need, int* hist, int* itmp, int* sel) {
-  const int tid = threadIdx.x;
-  RadixSel<K> rs{0, 0, need, 0};
-  constexpr int NP = (KBITS + 10) / 11;
+__device__ inline int clz_key(uint32_t x) { return __builtin_clz(x); }
+__device__ inline int clz_key(uint64_t x) { return __builtin_clzll(x); }
+
+template <int NT, typename K, typename ForEach>
+__device__ RadixSel<K> radix_select(ForEach for_each, int need, K kmin, K kmax, int* hist, int* itmp, int* sel) {
+  constexpr int KB = 8 * sizeof(K);
   constexpr int BPT = PR_BINS / NT;  // bins owned per thread in the top-down walk
+  const int tid = threadIdx.x;
+  const K dx = kmin ^ kmax;
+  const int nbits = dx == 0 ? 1 : KB - clz_key(dx);
+  RadixSel<K> rs;
+  rs.mask = nbits >= KB ? K(0) : ~((K(1) << nbits) - 1);
+  rs.prefix = kmax & rs.mask;
+  rs.need = need;
+  rs.eq = 0;
 #pragma unroll 1
-  for (int pass = 0; pass < NP; ++pass) {
-    const int hi_bit = KBITS - 11 * pass;
+  for (int hi_bit = nbits; hi_bit > 0; hi_bit -= 11) {
     const int shift = hi_bit > 11 ? hi_bit - 11 : 0;
     const K dmask = (K(1) << (hi_bit - shift)) - 1;
     for (int i = tid; i < PR_BINS; i += NT) hist[i] = 0;
@@ -200,16 +225,118 @@ __device__ RadixSel<K> radix_select(ForEach for_each, int need, int* hist, int* 
   return rs;
 }
 
+// Row top-k1 by (logit desc, token asc) through a radix select of the k1-th
+// largest key T over the keys >= t0, re-reading the row from memory: the path
+// for rows with many keys near the top (ties, flat rows), kept out of line so
+// the register-resident path does not carry its state.  Leaves the k1
+// selected, ranked, in ox / ov.
+__device__ __noinline__ void row_topk_radix(const float* xg, int V, int k1, uint32_t t0, uint32_t kmax, uint64_t* sk,
+                                            float* ox, int* ov, int* hist, int* itmp, int* sel) {
+  const int tid = threadIdx.x;
+  const int nch = (V + PR_CHUNK - 1) / PR_CHUNK;
+  auto valid = [&](int c) { return c * PR_CHUNK + PR_VEC * tid < V; };
+  auto getk = [&](int c, int j) -> uint32_t { return fkey(xg[c * PR_CHUNK + PR_VEC * tid + j] + 0.0f); };
+  const RadixSel<uint32_t> rs = radix_select<PR_THREADS, uint32_t>(
+      [&](auto&& f) {
+        for (int c = 0; c < nch; ++c) {
+          if (valid(c)) {
+#pragma unroll
+            for (int j = 0; j < PR_VEC; ++j) {
+              const uint32_t u = getk(c, j);
+              if (u >= t0) f(u);
+            }
+          }
+        }
+      },
+      k1, t0, kmax, hist, itmp, sel);
+  const uint32_t T = rs.prefix, Tm = rs.mask;
+  const int need = rs.need, eq_cnt = rs.eq;
+  // keys above the boundary: k1 - need of them, all taken; keys at it: all
+  // when eq_cnt == need, else the first `need` by token
+  int gt = 0, eq = 0;
+  for (int c = 0; c < nch; ++c) {
+    if (valid(c)) {
+#pragma unroll
+      for (int j = 0; j < PR_VEC; ++j) {
+        const uint32_t u = getk(c, j);
+        gt += (u & Tm) > T;
+        eq += (u & Tm) == T && u >= t0;
+      }
+    }
+  }
+  int off;
+  const int ngt = block_scan(gt, off, itmp);
+  for (int c = 0; c < nch; ++c) {
+    if (valid(c)) {
+#pragma unroll
+      for (int j = 0; j < PR_VEC; ++j) {
+        const uint32_t u = getk(c, j);
+        if ((u & Tm) > T) sk[off++] = row_key(u, c * PR_CHUNK + PR_VEC * tid + j);
+      }
+    }
+  }
+  if (eq_cnt == need) {  // every key at the boundary is taken: order is irrelevant here
+    int eoff;
+    block_scan(eq, eoff, itmp);
+    for (int c = 0; c < nch; ++c) {
+      if (valid(c)) {
+#pragma unroll
+        for (int j = 0; j < PR_VEC; ++j) {
+          const uint32_t u = getk(c, j);
+          if ((u & Tm) == T && u >= t0) sk[ngt + eoff++] = row_key(u, c * PR_CHUNK + PR_VEC * tid + j);
+        }
+      }
+    }
+  } else {  // ties at T (all bits fixed): ascending token order (chunk, then thread, then lane)
+    int taken = 0;
+    for (int c = 0; c < nch; ++c) {
+      int tc = 0;
+      if (valid(c)) {
+#pragma unroll
+        for (int j = 0; j < PR_VEC; ++j) tc += getk(c, j) == T;
+      }
+      int toff;
+      const int ctot = block_scan(tc, toff, itmp);
+      if (valid(c)) {
+#pragma unroll
+        for (int j = 0; j < PR_VEC; ++j) {
+          if (getk(c, j) == T) {
+            const int pos = taken + toff;
+            if (pos < need) sk[ngt + pos] = row_key(T, c * PR_CHUNK + PR_VEC * tid + j);
+            ++toff;
+          }
+        }
+      }
+      taken += ctot;
+      if (taken >= need) break;
+    }
+  }
+  __syncthreads();
+  // rank the k1 selected: (logit desc, token asc)
+  for (int i = tid; i < k1; i += PR_THREADS) {
+    const uint64_t ki = sk[i];
+    int rank = 0;
+#pragma unroll 8
+    for (int q = 0; q < k1; ++q) rank += sk[q] > ki;
+    ox[rank] = fval((uint32_t)(ki >> 32));
+    ov[rank] = (int)~(uint32_t)ki;
+  }
+}
+
 template <int MAXC>  // MAXC > 0: row held in registers (<= MAXC chunks); 0: re-read from memory
 __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
-  __shared__ float sx[PR_MAXK];
-  __shared__ int sv[PR_MAXK];
+  __shared__ uint64_t sk[PR_MAXK];  // candidates as row_key
   __shared__ float ox[PR_MAXK];
   __shared__ int ov[PR_MAXK];
-  __shared__ int hist[PR_BINS];
+  // radix histogram (fallback path) or the survivors' partial ranks
+  __shared__ int hist_part[PR_BINS > PR_SURV * (PR_THREADS / 64) ? PR_BINS : PR_SURV * (PR_THREADS / 64)];
+  int* hist = hist_part;
+  int* part = hist_part;
+  __shared__ int scnt;
   __shared__ float wred[PR_THREADS / 64];
   __shared__ int itmp[PR_THREADS / 64];
   __shared__ int sel[3];
+  __shared__ uint32_t wkey[PR_THREADS / 64];
   __shared__ int eos_pos;
 
   const int row = blockIdx.x;
@@ -217,6 +344,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   const float* xg = a.logits + (int64_t)row * a.row_stride;
   const int V = a.V, k1 = a.k1;
   const int nch = (V + PR_CHUNK - 1) / PR_CHUNK;
+  if (tid == 0) scnt = 0;  // ordered before its use by the barriers below
 
   float xr[MAXC > 0 ? MAXC : 1][PR_VEC];
   if constexpr (MAXC > 0) {
@@ -230,6 +358,11 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     }
   }
   auto valid = [&](int c) { return c * PR_CHUNK + PR_VEC * tid < V; };
+  // row max, exp-sum and survivor scan: with the row in registers the
+  // padding past V is -inf -- neutral for the max, +0 for the sum, and a
+  // survivor only when t0 admits every key, which sends the row to the
+  // radix path (more than PR_SURV survivors) where valid() is checked
+  auto live = [&](int c) { return MAXC > 0 || valid(c); };
   auto get = [&](int c, int j) -> float {
     if constexpr (MAXC > 0) return xr[c][j];
     else return xg[c * PR_CHUNK + PR_VEC * tid + j] + 0.0f;
@@ -240,7 +373,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   // ---- row max ----
   float tm = -INFINITY;
   PR_FOR_CHUNKS(c) {
-    if (valid(c)) {
+    if (live(c)) {
 #pragma unroll
       for (int j = 0; j < PR_VEC; ++j) tm = fmaxf(tm, get(c, j));
     }
@@ -258,7 +391,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   if (m != -INFINITY) {
     float acc = 0.0f;
     PR_FOR_CHUNKS(c) {
-      if (valid(c)) {
+      if (live(c)) {
 #pragma unroll
         for (int j = 0; j < PR_VEC; ++j) {
           const float d = get(c, j) - m;
@@ -276,105 +409,122 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     c_row = (double)a.cum[row] - lse;
   }
 
-  // ---- stage 1: row top-k1 by (logit desc, token asc), radix select ----
-  const RadixSel<uint32_t> rs = radix_select<PR_THREADS, uint32_t, 32>(
-      [&](auto&& f) {
-        PR_FOR_CHUNKS(c) {
-          if (valid(c)) {
-#pragma unroll
-            for (int j = 0; j < PR_VEC; ++j) f(fkey(get(c, j)));
-          }
-        }
-      },
-      k1, hist, itmp, sel);
-  const uint32_t T = rs.prefix, Tm = rs.mask;
-  const int need = rs.need, eq_cnt = rs.eq;
-  // keys above the boundary: k1 - need of them, all taken; keys at it: all
-  // when eq_cnt == need, else the first `need` by token
-  {
-    int gt = 0, eq = 0;
-    PR_FOR_CHUNKS(c) {
-      if (valid(c)) {
-#pragma unroll
-        for (int j = 0; j < PR_VEC; ++j) {
-          const uint32_t u = fkey(get(c, j)) & Tm;
-          gt += u > T;
-          eq += u == T;
-        }
-      }
+  // ---- stage 1: row top-k1 by (logit desc, token asc) ----
+  // Lower bound t0 of the k1-th largest key: per wave, the ceil(k1/4)-th
+  // largest thread maximum (bisection over the key range with wave ballots),
+  // least over the waves.  Every wave then has that many threads holding a
+  // key >= t0: at least k1 keys in all.  Only keys >= t0 can be selected; with
+  // few of them they are ranked directly.
+  uint32_t t0 = 0;
+  if (k1 <= PR_THREADS) {
+    const int kw = (k1 + 3) >> 2;
+    const uint32_t a0 = fkey(tm);
+    // invariant: at least kw lanes have a0 >= lo; the answer is <= hi (bounds
+    // are wave-uniform, kept in scalar registers)
+    uint32_t lo = 0, hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)fkey(m));
+    while (lo < hi) {
+      const uint32_t mid = lo + ((hi - lo + 1) >> 1);
+      const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(a0 >= mid));
+      if (c >= kw) lo = mid;
+      else hi = mid - 1;
     }
-    int off;
-    const int ngt = block_scan(gt, off, itmp);
+    if (lane == 0) wkey[wave] = lo;
+    __syncthreads();
+    t0 = wkey[0];
+#pragma unroll
+    for (int w = 1; w < PR_THREADS / 64; ++w) t0 = min(t0, wkey[w]);
+  }
+  // the same bound on the logits (t0 = 0 admits every key; keys 0 .. fkey(-inf)
+  // are NaN patterns)
+  const float t0f = t0 == 0 ? -INFINITY : fval(t0);
+  // survivors -> LDS in any order (an LDS counter hands out each thread's slots)
+  int ns = 0;
+  PR_FOR_CHUNKS(c) {
+    if (live(c)) {
+#pragma unroll
+      for (int j = 0; j < PR_VEC; ++j) ns += get(c, j) >= t0f;
+    }
+  }
+  if (ns > 0) {
+    int pos = atomicAdd(&scnt, ns);
     PR_FOR_CHUNKS(c) {
-      if (valid(c)) {
+      if (live(c)) {
 #pragma unroll
         for (int j = 0; j < PR_VEC; ++j) {
           const float y = get(c, j);
-          if ((fkey(y) & Tm) > T) {
-            sx[off] = y;
-            sv[off] = c * PR_CHUNK + PR_VEC * tid + j;
-            ++off;
+          if (y >= t0f) {  // (logit bits, token); made a row key once, below
+            if (pos < PR_SURV)
+              sk[pos] = ((uint64_t)__builtin_bit_cast(uint32_t, y) << 32) | (uint32_t)(c * PR_CHUNK + PR_VEC * tid + j);
+            ++pos;
           }
         }
       }
     }
-    if (eq_cnt == need) {  // every key equal to T is taken: order is irrelevant here
-      int eoff;
-      block_scan(eq, eoff, itmp);
-      PR_FOR_CHUNKS(c) {
-        if (valid(c)) {
-#pragma unroll
-          for (int j = 0; j < PR_VEC; ++j) {
-            const float y = get(c, j);
-            if ((fkey(y) & Tm) == T) {
-              sx[ngt + eoff] = y;
-              sv[ngt + eoff] = c * PR_CHUNK + PR_VEC * tid + j;
-              ++eoff;
-            }
-          }
-        }
-      }
-    } else {  // ties at T: ascending token order (chunk-major, then thread, then lane)
-      int taken = 0;
-      PR_FOR_CHUNKS(c) {
-        int tc = 0;
-        if (valid(c)) {
-#pragma unroll
-          for (int j = 0; j < PR_VEC; ++j) tc += fkey(get(c, j)) == T;
-        }
-        int toff;
-        const int ctot = block_scan(tc, toff, itmp);
-        if (valid(c)) {
-#pragma unroll
-          for (int j = 0; j < PR_VEC; ++j) {
-            if (fkey(get(c, j)) == T) {
-              const int pos = taken + toff;
-              if (pos < need) {
-                sx[ngt + pos] = get(c, j);
-                sv[ngt + pos] = c * PR_CHUNK + PR_VEC * tid + j;
-              }
-              ++toff;
-            }
-          }
-        }
-        taken += ctot;
-        if (taken >= need) break;
-      }
-    }
+  }
+  __syncthreads();
+  const int S = scnt;
+  if (S <= PR_SURV && k1 <= PR_THREADS) {
+    // each thread's survivors (slots tid, tid + 256) as row keys: distinct
+    const bool ha = tid < S, hb = tid + PR_THREADS < S;
+    auto to_key = [](uint64_t raw) { return row_key(fkey(__builtin_bit_cast(float, (uint32_t)(raw >> 32))), (int)(uint32_t)raw); };
+    const uint64_t ka = ha ? to_key(sk[tid]) : 0, kb = hb ? to_key(sk[tid + PR_THREADS]) : 0;
+    // the k1-th largest survivor key: all keys are distinct, so the selection
+    // ends with the boundary bin holding exactly the keys still needed
+    const RadixSel<uint64_t> rs = radix_select<PR_THREADS, uint64_t>(
+        [&](auto&& f) {
+          if (ha) f(ka);
+          if (hb) f(kb);
+        },
+        k1, (uint64_t)t0 << 32, ((uint64_t)fkey(m) << 32) | 0xffffffffu, hist, itmp, sel);
+    const bool sa = ha && (ka & rs.mask) >= rs.prefix, sb = hb && (kb & rs.mask) >= rs.prefix;
+    int off;
+    block_scan((int)sa + (int)sb, off, itmp);  // k1 in total; its barriers end all reads of sk above
+    if (sa) sk[off++] = ka;
+    if (sb) sk[off] = kb;
     __syncthreads();
-    // rank the k1 selected: (logit desc, token asc)
-    for (int i = tid; i < k1; i += PR_THREADS) {
-      const float xi = sx[i];
-      const int vi = sv[i];
-      int rank = 0;
-#pragma unroll 8
-      for (int q = 0; q < k1; ++q) {
-        const float y = sx[q];
-        rank += (y > xi) || (y == xi && sv[q] < vi);
+    // rank of selected key i = number of selected keys greater than it.  Wave
+    // w counts over the keys [w*Q, (w+1)*Q) for every target; lane l holds the
+    // targets l, l + 64, ...; the four partial counts are summed in LDS.
+    const int Q = (k1 + 3) >> 2, q0 = wave * Q, q1 = min(k1, q0 + Q);
+    auto partial = [&](auto tg_c) {
+      constexpr int TG = decltype(tg_c)::value;
+      uint64_t kt[TG];
+      int rk[TG];
+#pragma unroll
+      for (int mi = 0; mi < TG; ++mi) {
+        const int i = lane + 64 * mi;
+        kt[mi] = i < k1 ? sk[i] : ~0ull;
+        rk[mi] = 0;
       }
-      ox[rank] = xi;
-      ov[rank] = vi;
+#pragma unroll 4
+      for (int q = q0; q < q1; ++q) {
+        const uint64_t kq = sk[q];
+#pragma unroll
+        for (int mi = 0; mi < TG; ++mi) rk[mi] += kq > kt[mi];
+      }
+#pragma unroll
+      for (int mi = 0; mi < TG; ++mi) {
+        const int i = lane + 64 * mi;
+        if (i < k1) part[wave * PR_SURV + i] = rk[mi];
+      }
+    };
+    if (k1 <= 128) partial(std::integral_constant<int, 2>{});
+    else partial(std::integral_constant<int, 4>{});
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < PR_SURV / PR_THREADS; ++h) {
+      const int i = tid + h * PR_THREADS;
+      if (i < k1) {
+        int rank = 0;
+#pragma unroll
+        for (int w = 0; w < PR_THREADS / 64; ++w) rank += part[w * PR_SURV + i];
+        const uint64_t ki = sk[i];
+        ox[rank] = fval((uint32_t)(ki >> 32));
+        ov[rank] = (int)~(uint32_t)ki;
+      }
     }
+  } else {
+    row_topk_radix(xg, V, k1, t0, fkey(m), sk, ox, ov, hist, itmp, sel);
   }
 #undef PR_FOR_CHUNKS
   if (tid == 0) eos_pos = -1;
@@ -402,16 +552,17 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 }
 
 // ---- kernel 2: per-request top-k over the rows' candidate lists -----------
-typedef int32_t i32x4_t __attribute__((__vector_size__(4 * sizeof(int32_t))));
+constexpr int MG_REG = 16;  // candidates per thread staged on chip (W * k1 <= 16384)
 
-template <bool LDS_LISTS>  // true: the request's W x k1 lists are staged in LDS
+template <int MPT>  // > 0: MPT candidates per thread staged on chip; 0: re-read from memory per pass
 __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+  extern __shared__ uint64_t ckl[];  // [MPT * MG_THREADS] candidate keys (MPT > 0)
   __shared__ double cs[PR_MAXW];
   // the radix histogram during the selection, then the selected scores / flats
   __shared__ __attribute__((aligned(16))) uint8_t work[PR_MAXK * 16];
   __shared__ int fin[PR_MAXK];
   __shared__ int itmp[MG_THREADS / 64];
+  __shared__ uint64_t kred[MG_THREADS / 64][2];
   __shared__ int sel[3];
   int* hist = reinterpret_cast<int*>(work);
   double* fsc = reinterpret_cast<double*>(work);
@@ -424,41 +575,34 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
   const int64_t rbase = (int64_t)r * W;
   const float* gx = a.cand_x + rbase * k1;
   const int32_t* gv = a.cand_v + rbase * k1;
-  const float* xs = gx;
-  const int32_t* vs = gv;
-  if constexpr (LDS_LISTS) {
-    float* xl = reinterpret_cast<float*>(dyn);
-    int32_t* vl = reinterpret_cast<int32_t*>(dyn + sizeof(float) * (size_t)n);
-    if ((n & 3) == 0) {  // the request's lists then start 16-byte aligned
-      for (int i = 4 * tid; i < n; i += 4 * MG_THREADS) {
-        *reinterpret_cast<f32x4_t*>(xl + i) = *reinterpret_cast<const f32x4_t*>(gx + i);
-        *reinterpret_cast<i32x4_t*>(vl + i) = *reinterpret_cast<const i32x4_t*>(gv + i);
-      }
-    } else {
-      for (int i = tid; i < n; i += MG_THREADS) {
-        xl[i] = gx[i];
-        vl[i] = gv[i];
-      }
-    }
-    xs = xl;
-    vs = vl;
-  }
   for (int b = tid; b < W; b += MG_THREADS) cs[b] = a.row_c[rbase + b];
   __syncthreads();
 
-  // candidate i = b * k1 + j (row b, list position j), score cum - lse + logit;
-  // thread tid visits i = tid, tid + NT, ... with b stepped incrementally.
-  // Padding entries (token -1) are no candidates.
+  // candidate i = b * k1 + j (row b, list position j), score cum - lse + logit
+  // as its order-preserving key; thread tid owns i = tid, tid + NT, ... with b
+  // stepped incrementally.  Padding entries (token -1) are no candidates.
   const int db = MG_THREADS / k1, dj = MG_THREADS - db * k1;
-  auto for_cand = [&](auto&& f) {
+  auto cand = [&](int i, int b, int& v) -> uint64_t {
+    v = gv[i];
+    const double c = cs[b];
+    const double sc = c == -INFINITY ? -INFINITY : ((double)gx[i] + c) + 0.0;  // -0 -> +0
+    return dkey(sc);
+  };
+  // MPT > 0: the keys in LDS (0 = no candidate; every real score has a
+  // nonzero key), the tokens in registers
+  constexpr int NR = MPT > 0 ? MPT : 1;
+  int cv[NR];
+  if constexpr (MPT > 0) {
     int b = tid / k1, j = tid - b * k1;
-    for (int i = tid; i < n; i += MG_THREADS) {
-      const int v = vs[i];
-      if (v >= 0) {
-        const double c = cs[b];
-        const double sc = c == -INFINITY ? -INFINITY : ((double)xs[i] + c) + 0.0;  // -0 -> +0
-        f(b, v, sc);
-      }
+#pragma unroll
+    for (int q = 0; q < MPT; ++q) {
+      const int i = tid + q * MG_THREADS;
+      const int ic = i < n ? i : n - 1;  // loads stay in range; the entry is dropped below
+      int v;
+      const uint64_t u = cand(ic, b < W ? b : W - 1, v);
+      cv[q] = i < n ? v : -1;
+      ckl[i] = cv[q] >= 0 ? u : 0;
+      if ((q & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // at most 4 candidates' loads in flight
       b += db;
       j += dj;
       if (j >= k1) {
@@ -466,11 +610,59 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
         ++b;
       }
     }
+  }
+  auto for_cand = [&](auto&& f) {
+    if constexpr (MPT > 0) {
+      int b = tid / k1, j = tid - b * k1;
+#pragma unroll
+      for (int q = 0; q < MPT; ++q) {
+        const uint64_t u = ckl[tid + q * MG_THREADS];
+        if (u != 0) f(b, cv[q], u);
+        b += db;
+        j += dj;
+        if (j >= k1) {
+          j -= k1;
+          ++b;
+        }
+      }
+    } else {
+      int b = tid / k1, j = tid - b * k1;
+      for (int i = tid; i < n; i += MG_THREADS) {
+        int v;
+        const uint64_t u = cand(i, b, v);
+        if (v >= 0) f(b, v, u);
+        b += db;
+        j += dj;
+        if (j >= k1) {
+          j -= k1;
+          ++b;
+        }
+      }
+    }
   };
   int mv = 0;
-  for_cand([&](int, int, double) { ++mv; });
+  uint64_t kmin = ~0ull, kmax = 0;
+  for_cand([&](int, int, uint64_t u) {
+    ++mv;
+    kmin = u < kmin ? u : kmin;
+    kmax = u > kmax ? u : kmax;
+  });
+#pragma unroll
+  for (int msk = 32; msk >= 1; msk >>= 1) {
+    const uint64_t a0 = __shfl_xor(kmin, msk, 64), a1 = __shfl_xor(kmax, msk, 64);
+    kmin = a0 < kmin ? a0 : kmin;
+    kmax = a1 > kmax ? a1 : kmax;
+  }
+  if ((tid & 63) == 0) {
+    kred[tid >> 6][0] = kmin;
+    kred[tid >> 6][1] = kmax;
+  }
   int excl;
-  const int M = block_scan<MG_THREADS>(mv, excl, itmp);
+  const int M = block_scan<MG_THREADS>(mv, excl, itmp);  // its barriers order the kred writes
+  for (int w = 0; w < MG_THREADS / 64; ++w) {
+    kmin = kred[w][0] < kmin ? kred[w][0] : kmin;
+    kmax = kred[w][1] > kmax ? kred[w][1] : kmax;
+  }
   const int nsel = M < k ? M : k;
 
   // boundary score (k-th largest), then among exact ties at it the lowest flat
@@ -478,33 +670,34 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
   RadixSel<uint64_t> r1{0, 0, 0, 0}, r2{0, 0, 0, 0};
   bool ties = false;
   if (M > k) {
-    r1 = radix_select<MG_THREADS, uint64_t, 64>(
-        [&](auto&& f) { for_cand([&](int, int, double sc) { f(dkey(sc)); }); }, k, hist, itmp, sel);
+    r1 = radix_select<MG_THREADS, uint64_t>(
+        [&](auto&& f) { for_cand([&](int, int, uint64_t u) { f(u); }); }, k, kmin, kmax, hist, itmp, sel);
     if (r1.eq != r1.need) {
       ties = true;
-      r2 = radix_select<MG_THREADS, uint64_t, 64>(
+      const uint64_t tmin = ~(((uint64_t)(W - 1) << 32) | (uint32_t)(a.V - 1));
+      r2 = radix_select<MG_THREADS, uint64_t>(
           [&](auto&& f) {
-            for_cand([&](int b, int v, double sc) {
-              if (dkey(sc) == r1.prefix) f(~(((uint64_t)b << 32) | (uint32_t)v));
+            for_cand([&](int b, int v, uint64_t u) {
+              if (u == r1.prefix) f(~(((uint64_t)b << 32) | (uint32_t)v));
             });
           },
-          r1.need, hist, itmp, sel);
+          r1.need, tmin, ~0ull, hist, itmp, sel);
     }
   }
-  auto selected = [&](int b, int v, double sc) -> bool {
+  auto selected = [&](int b, int v, uint64_t key) -> bool {
     if (M <= k) return true;
-    const uint64_t u = dkey(sc) & r1.mask;
+    const uint64_t u = key & r1.mask;
     if (u != r1.prefix) return u > r1.prefix;
     if (!ties) return true;
     return (~(((uint64_t)b << 32) | (uint32_t)v) & r2.mask) >= r2.prefix;
   };
   int cnt = 0;
-  for_cand([&](int b, int v, double sc) { cnt += selected(b, v, sc); });
+  for_cand([&](int b, int v, uint64_t u) { cnt += selected(b, v, u); });
   int off;
   block_scan<MG_THREADS>(cnt, off, itmp);  // nsel in total; the histogram is dead from here
-  for_cand([&](int b, int v, double sc) {
-    if (selected(b, v, sc)) {
-      fsc[off] = sc;
+  for_cand([&](int b, int v, uint64_t u) {
+    if (selected(b, v, u)) {
+      fsc[off] = dval(u);
       ffl[off] = (int64_t)b * a.V + v;
       fin[off] = b;
       ++off;
@@ -519,7 +712,8 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
 #pragma unroll 8
     for (int u = 0; u < nsel; ++u) {
       const double su = fsc[u];
-      rank += (su > si) || (su == si && ffl[u] < fi);
+      const int64_t fu = ffl[u];
+      rank += (su > si) | ((su == si) & (fu < fi));
     }
     const int64_t o = (int64_t)r * k + rank;
     a.parent[o] = fin[i];
@@ -589,17 +783,17 @@ extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_ro
     hipLaunchKernelGGL(prune_rows<0>, dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
   gr_status_t st = launch_status();
   if (st != GR_OK) return st;
-  const size_t list_bytes = (size_t)beam_width * k1 * 8;
-  if (list_bytes <= 128 * 1024) {
-    static bool attr_set = false;
+  if ((size_t)beam_width * k1 <= (size_t)MG_REG * MG_THREADS) {
+    static bool attr_set = false;  // the key staging exceeds the default dynamic LDS limit
     if (!attr_set) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prune_merge<true>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prune_merge<MG_REG>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, MG_REG * MG_THREADS * 8);
       attr_set = true;
     }
-    hipLaunchKernelGGL(prune_merge<true>, dim3((unsigned)num_reqs), dim3(MG_THREADS), list_bytes, stream, a);
+    hipLaunchKernelGGL(prune_merge<MG_REG>, dim3((unsigned)num_reqs), dim3(MG_THREADS),
+                       MG_REG * MG_THREADS * 8, stream, a);
   } else {
-    hipLaunchKernelGGL(prune_merge<false>, dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
+    hipLaunchKernelGGL(prune_merge<0>, dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
   }
   return launch_status();
 }
