@@ -552,20 +552,19 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 }
 
 // ---- kernel 2: per-request top-k over the rows' candidate lists -----------
-constexpr int MG_REG = 16;  // candidates per thread staged on chip (W * k1 <= 16384)
+typedef int32_t i32x4_t __attribute__((__vector_size__(4 * sizeof(int32_t))));
+constexpr int MG_REG = 16;  // candidates per thread held in registers (W * k1 <= 16384)
 
-template <int MPT>  // > 0: MPT candidates per thread staged on chip; 0: re-read from memory per pass
+template <int MPT>  // > 0: thread t holds candidates [MPT t, MPT t + MPT) in registers; 0: re-read per pass
 __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
-  extern __shared__ uint64_t ckl[];  // [MPT * MG_THREADS] candidate keys (MPT > 0)
   __shared__ double cs[PR_MAXW];
-  // the radix histogram during the selection, then the selected scores / flats
+  // the radix histogram during the selection, then the selected keys / flats
   __shared__ __attribute__((aligned(16))) uint8_t work[PR_MAXK * 16];
-  __shared__ int fin[PR_MAXK];
   __shared__ int itmp[MG_THREADS / 64];
   __shared__ uint64_t kred[MG_THREADS / 64][2];
   __shared__ int sel[3];
   int* hist = reinterpret_cast<int*>(work);
-  double* fsc = reinterpret_cast<double*>(work);
+  uint64_t* fkeys = reinterpret_cast<uint64_t*>(work);
   int64_t* ffl = reinterpret_cast<int64_t*>(work + PR_MAXK * 8);
 
   const int r = blockIdx.x;
@@ -578,71 +577,70 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
   for (int b = tid; b < W; b += MG_THREADS) cs[b] = a.row_c[rbase + b];
   __syncthreads();
 
-  // candidate i = b * k1 + j (row b, list position j), score cum - lse + logit
-  // as its order-preserving key; thread tid owns i = tid, tid + NT, ... with b
-  // stepped incrementally.  Padding entries (token -1) are no candidates.
-  const int db = MG_THREADS / k1, dj = MG_THREADS - db * k1;
-  auto cand = [&](int i, int b, int& v) -> uint64_t {
-    v = gv[i];
+  // candidate i = b * k1 + j (row b, list position j): score cum - lse + logit
+  // as its order-preserving key; padding entries (token -1) are no candidates
+  // and get key 0, which no score has
+  auto score_key = [&](float x, int b) -> uint64_t {
     const double c = cs[b];
-    const double sc = c == -INFINITY ? -INFINITY : ((double)gx[i] + c) + 0.0;  // -0 -> +0
-    return dkey(sc);
+    return dkey(c == -INFINITY ? -INFINITY : ((double)x + c) + 0.0);  // -0 -> +0
   };
-  // MPT > 0: the keys in LDS (0 = no candidate; every real score has a
-  // nonzero key), the tokens in registers
   constexpr int NR = MPT > 0 ? MPT : 1;
+  uint64_t ck[NR];
   int cv[NR];
+  const int i0 = NR * tid;
   if constexpr (MPT > 0) {
-    int b = tid / k1, j = tid - b * k1;
+    float xv[MPT];
+    if (i0 + MPT <= n) {  // the request's lists start 16-byte aligned (n % 4 == 0 on this path)
 #pragma unroll
-    for (int q = 0; q < MPT; ++q) {
-      const int i = tid + q * MG_THREADS;
-      const int ic = i < n ? i : n - 1;  // loads stay in range; the entry is dropped below
-      int v;
-      const uint64_t u = cand(ic, b < W ? b : W - 1, v);
-      cv[q] = i < n ? v : -1;
-      ckl[i] = cv[q] >= 0 ? u : 0;
-      if ((q & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // at most 4 candidates' loads in flight
-      b += db;
-      j += dj;
-      if (j >= k1) {
-        j -= k1;
-        ++b;
-      }
-    }
-  }
-  auto for_cand = [&](auto&& f) {
-    if constexpr (MPT > 0) {
-      int b = tid / k1, j = tid - b * k1;
+      for (int q = 0; q < MPT; q += 4) {
+        const f32x4_t x4 = *reinterpret_cast<const f32x4_t*>(gx + i0 + q);
+        const i32x4_t v4 = *reinterpret_cast<const i32x4_t*>(gv + i0 + q);
 #pragma unroll
-      for (int q = 0; q < MPT; ++q) {
-        const uint64_t u = ckl[tid + q * MG_THREADS];
-        if (u != 0) f(b, cv[q], u);
-        b += db;
-        j += dj;
-        if (j >= k1) {
-          j -= k1;
-          ++b;
+        for (int e = 0; e < 4; ++e) {
+          xv[q + e] = x4[e];
+          cv[q + e] = v4[e];
         }
       }
     } else {
-      int b = tid / k1, j = tid - b * k1;
+#pragma unroll
+      for (int q = 0; q < MPT; ++q) {
+        const bool in = i0 + q < n;
+        xv[q] = in ? gx[in ? i0 + q : 0] : 0.0f;
+        cv[q] = in ? gv[in ? i0 + q : 0] : -1;
+      }
+    }
+    int b = min(i0 / k1, W - 1), j = i0 - b * k1;
+#pragma unroll
+    for (int q = 0; q < MPT; ++q) {
+      ck[q] = cv[q] >= 0 ? score_key(xv[q], b) : 0;
+      if (++j == k1) {
+        j = 0;
+        b = min(b + 1, W - 1);
+      }
+    }
+  }
+  // f(q, key) for this thread's candidates (MPT = 0: keys recomputed from memory)
+  auto for_cand = [&](auto&& f) {
+    if constexpr (MPT > 0) {
+#pragma unroll
+      for (int q = 0; q < MPT; ++q)
+        if (ck[q] != 0) f(q, ck[q]);
+    } else {
       for (int i = tid; i < n; i += MG_THREADS) {
-        int v;
-        const uint64_t u = cand(i, b, v);
-        if (v >= 0) f(b, v, u);
-        b += db;
-        j += dj;
-        if (j >= k1) {
-          j -= k1;
-          ++b;
-        }
+        const int v = gv[i];
+        if (v >= 0) f(i, score_key(gx[i], i / k1));
       }
     }
   };
+  // (row, token) of candidate q (MPT > 0: index i0 + q; else flat index i)
+  auto cand_bv = [&](int q, int& b, int& v) {
+    const int i = MPT > 0 ? i0 + q : q;
+    b = i / k1;
+    v = MPT > 0 ? cv[MPT > 0 ? q : 0] : gv[i];
+  };
   int mv = 0;
   uint64_t kmin = ~0ull, kmax = 0;
-  for_cand([&](int, int, uint64_t u) {
+  for_cand([&](int, uint64_t u) {
     ++mv;
     kmin = u < kmin ? u : kmin;
     kmax = u > kmax ? u : kmax;
@@ -671,54 +669,62 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
   bool ties = false;
   if (M > k) {
     r1 = radix_select<MG_THREADS, uint64_t>(
-        [&](auto&& f) { for_cand([&](int, int, uint64_t u) { f(u); }); }, k, kmin, kmax, hist, itmp, sel);
+        [&](auto&& f) { for_cand([&](int, uint64_t u) { f(u); }); }, k, kmin, kmax, hist, itmp, sel);
     if (r1.eq != r1.need) {
       ties = true;
       const uint64_t tmin = ~(((uint64_t)(W - 1) << 32) | (uint32_t)(a.V - 1));
       r2 = radix_select<MG_THREADS, uint64_t>(
           [&](auto&& f) {
-            for_cand([&](int b, int v, uint64_t u) {
-              if (u == r1.prefix) f(~(((uint64_t)b << 32) | (uint32_t)v));
+            for_cand([&](int q, uint64_t u) {
+              if (u == r1.prefix) {
+                int b, v;
+                cand_bv(q, b, v);
+                f(~(((uint64_t)b << 32) | (uint32_t)v));
+              }
             });
           },
           r1.need, tmin, ~0ull, hist, itmp, sel);
     }
   }
-  auto selected = [&](int b, int v, uint64_t key) -> bool {
+  auto selected = [&](int q, uint64_t key) -> bool {
     if (M <= k) return true;
     const uint64_t u = key & r1.mask;
     if (u != r1.prefix) return u > r1.prefix;
     if (!ties) return true;
+    int b, v;
+    cand_bv(q, b, v);
     return (~(((uint64_t)b << 32) | (uint32_t)v) & r2.mask) >= r2.prefix;
   };
   int cnt = 0;
-  for_cand([&](int b, int v, uint64_t u) { cnt += selected(b, v, u); });
+  for_cand([&](int q, uint64_t u) { cnt += selected(q, u); });
   int off;
   block_scan<MG_THREADS>(cnt, off, itmp);  // nsel in total; the histogram is dead from here
-  for_cand([&](int b, int v, uint64_t u) {
-    if (selected(b, v, u)) {
-      fsc[off] = dval(u);
+  for_cand([&](int q, uint64_t u) {
+    if (selected(q, u)) {
+      int b, v;
+      cand_bv(q, b, v);
+      fkeys[off] = u;
       ffl[off] = (int64_t)b * a.V + v;
-      fin[off] = b;
       ++off;
     }
   });
   __syncthreads();
   // final order of the selected set: (score desc, flat asc)
   for (int i = tid; i < nsel; i += MG_THREADS) {
-    const double si = fsc[i];
+    const uint64_t ki = fkeys[i];
     const int64_t fi = ffl[i];
     int rank = 0;
 #pragma unroll 8
     for (int u = 0; u < nsel; ++u) {
-      const double su = fsc[u];
-      const int64_t fu = ffl[u];
-      rank += (su > si) | ((su == si) & (fu < fi));
+      const uint64_t kq = fkeys[u];
+      const int64_t fq = ffl[u];
+      rank += (kq > ki) | ((kq == ki) & (fq < fi));
     }
     const int64_t o = (int64_t)r * k + rank;
-    a.parent[o] = fin[i];
-    a.token[o] = (int32_t)(fi - (int64_t)fin[i] * a.V);
-    a.score[o] = (float)si;
+    const int b = (int)(fi / a.V);
+    a.parent[o] = b;
+    a.token[o] = (int32_t)(fi - (int64_t)b * a.V);
+    a.score[o] = (float)dval(ki);
   }
   for (int i = nsel + tid; i < k; i += MG_THREADS) {
     const int64_t o = (int64_t)r * k + i;
@@ -783,17 +789,9 @@ extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_ro
     hipLaunchKernelGGL(prune_rows<0>, dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
   gr_status_t st = launch_status();
   if (st != GR_OK) return st;
-  if ((size_t)beam_width * k1 <= (size_t)MG_REG * MG_THREADS) {
-    static bool attr_set = false;  // the key staging exceeds the default dynamic LDS limit
-    if (!attr_set) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prune_merge<MG_REG>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, MG_REG * MG_THREADS * 8);
-      attr_set = true;
-    }
-    hipLaunchKernelGGL(prune_merge<MG_REG>, dim3((unsigned)num_reqs), dim3(MG_THREADS),
-                       MG_REG * MG_THREADS * 8, stream, a);
-  } else {
+  if ((size_t)beam_width * k1 <= (size_t)MG_REG * MG_THREADS && ((size_t)beam_width * k1) % 4 == 0)
+    hipLaunchKernelGGL(prune_merge<MG_REG>, dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
+  else
     hipLaunchKernelGGL(prune_merge<0>, dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
-  }
   return launch_status();
 }
