@@ -3,13 +3,14 @@
 // All three kernels move K/V rows of head_dim elements in 16-byte vectors;
 // they are pure HBM copy work (no arithmetic), so the design goal is wide
 // coalesced accesses and no serialisation:
-//  * beam_fork: one workgroup per (request, group of children).  Every
-//    workgroup recomputes its request's row assignment from the read-only
-//    input tables (a few hundred integer ops), so there is no inter-workgroup
-//    dependency and no atomics on the tables; the new tables are written out
-//    of place.  Copy-on-write destinations are rows of childless parents,
-//    which nobody reads, and in-place appends write positions past every
-//    copied range, so the single launch is race-free.
+//  * beam_fork: one workgroup per child.  Every workgroup recomputes its
+//    request's row assignment from the read-only input tables (LDS atomics
+//    for each parent's lowest child and child count, wave ballots for the
+//    ranks), so there is no inter-workgroup dependency and no atomics on the
+//    tables; the new tables are written out of place.  Copy-on-write
+//    destinations are rows of childless parents, which nobody reads, and
+//    in-place appends write positions past every copied range, so the single
+//    launch is race-free.  Copies issue a batch of loads before the stores.
 //  * beam_append / reshape_and_cache: one wave per beam / token.
 #include "gr_common.h"
 
@@ -19,8 +20,9 @@ namespace {
 typedef uint32_t u32x4_t __attribute__((__vector_size__(4 * sizeof(uint32_t))));
 
 constexpr int FORK_THREADS = 256;
-constexpr int FORK_CHILDREN_PER_WG = 4;
 constexpr int FORK_MAX_W = 1024;
+constexpr int FORK_STAGE_S = 256;  // block-table rows of up to this many blocks are staged in LDS
+constexpr int FORK_BATCH = 4;      // 16-byte K and V vectors per thread in flight
 
 struct KvGeom {
   void* k_cache;
@@ -34,143 +36,172 @@ __device__ inline int64_t kv_byte_off(const KvGeom& g, int64_t blk, int off, int
   return (blk * g.block_stride + (int64_t)off * g.tok_stride + (int64_t)h * g.head_stride) * g.esize;
 }
 
-// Exclusive scan of flags[0..n) (n <= FORK_MAX_W) into out[]; returns total.
-__device__ int block_exclusive_scan(const int* flags, int* out, int n, int* tmp) {
-  const int tid = threadIdx.x;
-  // each thread scans 4 consecutive entries
-  const int base = tid * 4;
-  int loc[4], s = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    loc[j] = s;
-    s += (base + j < n) ? flags[base + j] : 0;
-  }
-  tmp[tid] = s;
-  __syncthreads();
-  for (int off = 1; off < FORK_THREADS; off <<= 1) {
-    int v = tid >= off ? tmp[tid - off] : 0;
-    __syncthreads();
-    tmp[tid] += v;
-    __syncthreads();
-  }
-  const int excl = tmp[tid] - s;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (base + j < n) out[base + j] = excl + loc[j];
-  const int total = tmp[FORK_THREADS - 1];
-  __syncthreads();
-  return total;
-}
-
 __global__ __launch_bounds__(FORK_THREADS) void beam_fork(
     const int32_t* __restrict__ parent, int R, int W, const int32_t* __restrict__ bt_in,
     const int32_t* __restrict__ len_in, int32_t* __restrict__ bt_out, int32_t* __restrict__ len_out,
     int S, KvGeom g, const uint8_t* k_new, const uint8_t* v_new, int64_t new_tok_stride,
     int32_t* dev_status) {
   __shared__ int par[FORK_MAX_W], first[FORK_MAX_W], cnt[FORK_MAX_W];
-  __shared__ int cow_flag[FORK_MAX_W], cow_rank[FORK_MAX_W];
-  __shared__ int free_flag[FORK_MAX_W], free_rank[FORK_MAX_W], free_list[FORK_MAX_W];
-  __shared__ int scan_tmp[FORK_THREADS];
+  __shared__ uint64_t cow_mask[FORK_MAX_W / 64], free_mask[FORK_MAX_W / 64];
+  __shared__ int src_row[FORK_STAGE_S], dst_row[FORK_STAGE_S];
   __shared__ int bad;
-  const int chunks = (W + FORK_CHILDREN_PER_WG - 1) / FORK_CHILDREN_PER_WG;
-  const int r = blockIdx.x / chunks;
-  const int chunk = blockIdx.x % chunks;
-  const int tid = threadIdx.x;
+  const int r = blockIdx.x / W;
+  const int c = blockIdx.x - r * W;  // this workgroup's child
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (r >= R) return;
   if (tid == 0) bad = 0;
-  for (int c = tid; c < W; c += FORK_THREADS) {
-    first[c] = W;
-    cnt[c] = 0;
+  for (int i = tid; i < W; i += FORK_THREADS) {
+    first[i] = W;
+    cnt[i] = 0;
   }
   __syncthreads();
-  for (int c = tid; c < W; c += FORK_THREADS) {
-    int p = parent[(int64_t)r * W + c];
+  for (int i = tid; i < W; i += FORK_THREADS) {
+    int p = parent[(int64_t)r * W + i];
     if (p < 0 || p >= W) {
       bad = 1;
-      p = c;
+      p = i;
     }
-    par[c] = p;
-    atomicMin(&first[p], c);
+    par[i] = p;
+    atomicMin(&first[p], i);
     atomicAdd(&cnt[p], 1);
   }
   __syncthreads();
   const bool req_bad = bad != 0;
-  if (req_bad && chunk == 0 && tid == 0) flag_status(dev_status, GR_DEV_BAD_PARENT);
-  for (int c = tid; c < W; c += FORK_THREADS) {
-    cow_flag[c] = (!req_bad && first[par[c]] != c) ? 1 : 0;
-    free_flag[c] = (!req_bad && cnt[c] == 0) ? 1 : 0;
+  if (req_bad && c == 0 && tid == 0) flag_status(dev_status, GR_DEV_BAD_PARENT);
+  // per 64-entry group: the children that copy (not their parent's lowest
+  // child) and the parents without children
+  for (int base = 0; base < W; base += FORK_THREADS) {
+    const int i = base + tid;
+    const bool in = i < W;
+    const bool cw = in && first[par[in ? i : 0]] != i;
+    const bool fr = in && cnt[in ? i : 0] == 0;
+    const uint64_t cm = __builtin_amdgcn_ballot_w64(cw);
+    const uint64_t fm = __builtin_amdgcn_ballot_w64(fr);
+    if (lane == 0 && base + 64 * wave < W) {
+      cow_mask[(base >> 6) + wave] = cm;
+      free_mask[(base >> 6) + wave] = fm;
+    }
   }
   __syncthreads();
-  block_exclusive_scan(cow_flag, cow_rank, W, scan_tmp);
-  block_exclusive_scan(free_flag, free_rank, W, scan_tmp);
-  for (int p = tid; p < W; p += FORK_THREADS)
-    if (free_flag[p]) free_list[free_rank[p]] = p;
-  __syncthreads();
-
+  const int p = par[c];
+  const bool cow = !req_bad && first[p] != c;
+  int owner = req_bad ? c : p;  // beam whose old row child c receives
+  if (cow) {
+    // k = rank of c among the copying children; owner = the k-th childless
+    // parent (both ascending; the two counts are equal)
+    const int gc = c >> 6;
+    int k = __builtin_popcountll(cow_mask[gc] & ((1ull << (c & 63)) - 1));
+    for (int gi = 0; gi < gc; ++gi) k += __builtin_popcountll(cow_mask[gi]);
+    const int ngroups = (W + 63) >> 6;
+    int gi = 0;
+    uint64_t m = free_mask[0];
+    while (gi + 1 < ngroups && k >= __builtin_popcountll(m)) {
+      k -= __builtin_popcountll(m);
+      m = free_mask[++gi];
+    }
+    for (; k > 0 && m != 0; --k) m &= m - 1;
+    owner = m != 0 ? gi * 64 + __builtin_ctzll(m) : c;
+  }
+  const int64_t n_c = (int64_t)r * W + c, n_p = (int64_t)r * W + p, n_o = (int64_t)r * W + owner;
+  const bool staged = S <= FORK_STAGE_S;
+  for (int j = tid; j < S; j += FORK_THREADS) {
+    const int b = bt_in[n_o * S + j];
+    bt_out[n_c * S + j] = b;
+    if (staged) {
+      dst_row[j] = b;
+      if (cow) src_row[j] = bt_in[n_p * S + j];
+    }
+  }
+  if (req_bad) {  // a request with a bad parent keeps its tables
+    if (tid == 0) len_out[n_c] = len_in[n_c];
+    return;
+  }
   const int cap = S * g.bs;
-  const int row_vecs = g.D * g.esize / 16;  // 16-byte vectors per (token, head) row
+  int len = len_in[n_p];
+  if (len < 0 || len > cap) {
+    if (tid == 0) flag_status(dev_status, GR_DEV_BAD_LENGTH);
+    len = len < 0 ? 0 : cap;
+  }
+  __syncthreads();  // staged rows visible
+  auto src_blk = [&](int i) { return staged ? src_row[i] : bt_in[n_p * S + i]; };
+  auto dst_blk = [&](int i) { return staged ? dst_row[i] : bt_in[n_o * S + i]; };
   uint8_t* kc = static_cast<uint8_t*>(g.k_cache);
   uint8_t* vc = static_cast<uint8_t*>(g.v_cache);
-  const int c_end = min(W, (chunk + 1) * FORK_CHILDREN_PER_WG);
-  for (int c = chunk * FORK_CHILDREN_PER_WG; c < c_end; ++c) {
-    const int p = par[c];
-    const bool cow = cow_flag[c] != 0;
-    // beam whose old row c receives; a request with a bad parent keeps its tables
-    const int owner = req_bad ? c : (cow ? free_list[cow_rank[c]] : p);
-    const int64_t n_c = (int64_t)r * W + c;
-    const int64_t n_p = (int64_t)r * W + p;
-    const int64_t n_o = (int64_t)r * W + owner;
-    int len = len_in[n_p];
-    if (len < 0 || len > cap) {
-      if (tid == 0) flag_status(dev_status, GR_DEV_BAD_LENGTH);
-      len = len < 0 ? 0 : cap;
-    }
-    for (int j = tid; j < S; j += FORK_THREADS) bt_out[n_c * S + j] = bt_in[n_o * S + j];
-    if (req_bad) {
-      if (tid == 0) len_out[n_c] = len_in[n_c];
-      continue;
-    }
-    if (cow) {
-      // copy tokens [0, len) of the parent's row into the owner's row
-      const int work = len * g.Hkv * row_vecs;
-      for (int e = tid; e < work; e += FORK_THREADS) {
-        const int vec = e % row_vecs;
-        const int h = (e / row_vecs) % g.Hkv;
-        const int pos = e / (row_vecs * g.Hkv);
-        const int bsrc = bt_in[n_p * S + pos / g.bs];
-        const int bdst = bt_in[n_o * S + pos / g.bs];
+  const int row_vecs = g.D * g.esize / 16;  // 16-byte vectors per (token, head) row
+  const int tv = g.Hkv * row_vecs;          // 16-byte vectors per token, all heads
+  if (cow) {
+    // copy tokens [0, len) of the parent's row into the owner's row
+    if (FORK_THREADS % tv == 0 && g.num_blocks > 0) {
+      // a token's vectors divide the workgroup: each thread keeps one (head,
+      // vector) and steps over tokens with FORK_BATCH loads in flight; lanes
+      // past the end or on a bad block load an in-range row and skip the store
+      const int tpp = FORK_THREADS / tv;  // tokens per pass
+      const int h = (tid % tv) / row_vecs, vec = (tid % tv) % row_vecs;
+#pragma unroll 1
+      for (int p0 = tid / tv; p0 < len; p0 += tpp * FORK_BATCH) {
+        u32x4_t kb[FORK_BATCH], vb[FORK_BATCH];
+        int64_t dof[FORK_BATCH];
+        bool ok[FORK_BATCH];
+#pragma unroll
+        for (int u = 0; u < FORK_BATCH; ++u) {
+          const int pos = min(p0 + u * tpp, len - 1);
+          const int bi = pos / g.bs, off = pos - bi * g.bs;
+          const int bsrc = src_blk(bi), bdst = dst_blk(bi);
+          const bool valid = bsrc >= 0 && bsrc < g.num_blocks && bdst >= 0 && bdst < g.num_blocks;
+          ok[u] = valid && p0 + u * tpp < len;
+          if (!valid) flag_status(dev_status, GR_DEV_BAD_BLOCK);
+          const int64_t so = kv_byte_off(g, valid ? bsrc : 0, off, h) + vec * 16;
+          dof[u] = kv_byte_off(g, valid ? bdst : 0, off, h) + vec * 16;
+          kb[u] = *reinterpret_cast<const u32x4_t*>(kc + so);
+          vb[u] = *reinterpret_cast<const u32x4_t*>(vc + so);
+        }
+#pragma unroll
+        for (int u = 0; u < FORK_BATCH; ++u) {
+          if (ok[u]) {
+            *reinterpret_cast<u32x4_t*>(kc + dof[u]) = kb[u];
+            *reinterpret_cast<u32x4_t*>(vc + dof[u]) = vb[u];
+          }
+        }
+      }
+    } else {
+#pragma unroll 1
+      for (int e = tid; e < len * tv; e += FORK_THREADS) {
+        const int pos = e / tv, rem = e - pos * tv;
+        const int h = rem / row_vecs, vec = rem - h * row_vecs;
+        const int bi = pos / g.bs, off = pos - bi * g.bs;
+        const int bsrc = src_blk(bi), bdst = dst_blk(bi);
         if (bsrc < 0 || bsrc >= g.num_blocks || bdst < 0 || bdst >= g.num_blocks) {
           flag_status(dev_status, GR_DEV_BAD_BLOCK);
           continue;
         }
-        const int64_t so = kv_byte_off(g, bsrc, pos % g.bs, h) + vec * 16;
-        const int64_t dof = kv_byte_off(g, bdst, pos % g.bs, h) + vec * 16;
-        *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(kc + so);
-        *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(vc + so);
+        const int64_t so = kv_byte_off(g, bsrc, off, h) + vec * 16;
+        const int64_t dst = kv_byte_off(g, bdst, off, h) + vec * 16;
+        *reinterpret_cast<u32x4_t*>(kc + dst) = *reinterpret_cast<const u32x4_t*>(kc + so);
+        *reinterpret_cast<u32x4_t*>(vc + dst) = *reinterpret_cast<const u32x4_t*>(vc + so);
       }
     }
-    int new_len = len;
-    if (k_new) {
-      if (len < cap) {
-        const int bdst = bt_in[n_o * S + len / g.bs];
-        if (bdst >= 0 && bdst < g.num_blocks) {
-          for (int e = tid; e < g.Hkv * row_vecs; e += FORK_THREADS) {
-            const int vec = e % row_vecs, h = e / row_vecs;
-            const int64_t src = (n_c * new_tok_stride + (int64_t)h * g.D) * g.esize + vec * 16;
-            const int64_t dof = kv_byte_off(g, bdst, len % g.bs, h) + vec * 16;
-            *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(k_new + src);
-            *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(v_new + src);
-          }
-          new_len = len + 1;
-        } else if (tid == 0) {
-          flag_status(dev_status, GR_DEV_BAD_BLOCK);
-        }
-      } else if (tid == 0) {
-        flag_status(dev_status, GR_DEV_SUFFIX_FULL);
-      }
-    }
-    if (tid == 0) len_out[n_c] = new_len;
   }
+  int new_len = len;
+  if (k_new) {
+    if (len < cap) {
+      const int bdst = dst_blk(len / g.bs);
+      if (bdst >= 0 && bdst < g.num_blocks) {
+        for (int e = tid; e < tv; e += FORK_THREADS) {
+          const int h = e / row_vecs, vec = e - h * row_vecs;
+          const int64_t src = (n_c * new_tok_stride + (int64_t)h * g.D) * g.esize + vec * 16;
+          const int64_t dof = kv_byte_off(g, bdst, len % g.bs, h) + vec * 16;
+          *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(k_new + src);
+          *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(v_new + src);
+        }
+        new_len = len + 1;
+      } else if (tid == 0) {
+        flag_status(dev_status, GR_DEV_BAD_BLOCK);
+      }
+    } else if (tid == 0) {
+      flag_status(dev_status, GR_DEV_SUFFIX_FULL);
+    }
+  }
+  if (tid == 0) len_out[n_c] = new_len;
 }
 
 // One 64-lane wave per beam: append its token at suffix_len[n], then bump it.
@@ -285,8 +316,8 @@ extern "C" gr_status_t gr_beam_kv_fork(const int32_t* parent, int num_reqs, int 
   if (k_new && (!aligned16(k_new) || !aligned16(v_new) || (new_tok_stride * g.esize) % 16 ||
                 new_tok_stride < (int64_t)num_kv_heads * head_dim))
     return GR_ERR_INVALID_ARG;
-  const int chunks = (beam_width + FORK_CHILDREN_PER_WG - 1) / FORK_CHILDREN_PER_WG;
-  hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * chunks)), dim3(FORK_THREADS), 0, stream, parent,
+  if ((int64_t)num_reqs * beam_width > INT32_MAX) return GR_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * beam_width)), dim3(FORK_THREADS), 0, stream, parent,
                      num_reqs, beam_width, bt_in, len_in, bt_out, len_out, bt_stride, g,
                      static_cast<const uint8_t*>(k_new), static_cast<const uint8_t*>(v_new), new_tok_stride,
                      dev_status);
