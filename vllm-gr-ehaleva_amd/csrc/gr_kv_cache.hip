@@ -21,8 +21,9 @@ typedef uint32_t u32x4_t __attribute__((__vector_size__(4 * sizeof(uint32_t))));
 
 constexpr int FORK_THREADS = 256;
 constexpr int FORK_MAX_W = 1024;
-constexpr int FORK_STAGE_S = 256;  // block-table rows of up to this many blocks are staged in LDS
-constexpr int FORK_BATCH = 4;      // 16-byte K and V vectors per thread in flight
+constexpr int FORK_STAGE_BT = 1024;  // a request's whole block table is staged in LDS up to this many entries
+constexpr int FORK_STAGE_S = 256;    // else the two rows a child uses, up to this many blocks each
+constexpr int FORK_BATCH = 4;        // 16-byte K and V vectors per thread in flight
 
 struct KvGeom {
   void* k_cache;
@@ -41,29 +42,59 @@ __global__ __launch_bounds__(FORK_THREADS) void beam_fork(
     const int32_t* __restrict__ len_in, int32_t* __restrict__ bt_out, int32_t* __restrict__ len_out,
     int S, KvGeom g, const uint8_t* k_new, const uint8_t* v_new, int64_t new_tok_stride,
     int32_t* dev_status) {
-  __shared__ int par[FORK_MAX_W], first[FORK_MAX_W], cnt[FORK_MAX_W];
+  __shared__ int par[FORK_MAX_W], first[FORK_MAX_W], cnt[FORK_MAX_W], lens[FORK_MAX_W];
   __shared__ uint64_t cow_mask[FORK_MAX_W / 64], free_mask[FORK_MAX_W / 64];
+  __shared__ int bts[FORK_STAGE_BT];
   __shared__ int src_row[FORK_STAGE_S], dst_row[FORK_STAGE_S];
   __shared__ int bad;
   const int r = blockIdx.x / W;
   const int c = blockIdx.x - r * W;  // this workgroup's child
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (r >= R) return;
+  const int64_t n_c = (int64_t)r * W + c;
+  const int row_vecs = g.D * g.esize / 16;  // 16-byte vectors per (token, head) row
+  const int tv = g.Hkv * row_vecs;          // 16-byte vectors per token, all heads
+  // the appended token's vectors, loaded before the tables are worked out
+  const bool pre_new = k_new && tv <= FORK_THREADS && tid < tv;
+  u32x4_t knew{}, vnew{};
+  const int nh = tid / row_vecs, nvec = tid - (tid / row_vecs) * row_vecs;
+  if (pre_new) {
+    const int64_t src = (n_c * new_tok_stride + (int64_t)nh * g.D) * g.esize + nvec * 16;
+    knew = *reinterpret_cast<const u32x4_t*>(k_new + src);
+    vnew = *reinterpret_cast<const u32x4_t*>(v_new + src);
+  }
   if (tid == 0) bad = 0;
   for (int i = tid; i < W; i += FORK_THREADS) {
     first[i] = W;
     cnt[i] = 0;
   }
-  __syncthreads();
-  for (int i = tid; i < W; i += FORK_THREADS) {
-    int p = parent[(int64_t)r * W + i];
-    if (p < 0 || p >= W) {
-      bad = 1;
-      p = i;
+  // the request's parents, lengths and (when small) block table in one round trip
+  const bool all_staged = W * S <= FORK_STAGE_BT;
+  int pv[FORK_MAX_W / FORK_THREADS];
+#pragma unroll
+  for (int u = 0; u < FORK_MAX_W / FORK_THREADS; ++u) {
+    const int i = tid + u * FORK_THREADS;
+    if (i < W) {
+      pv[u] = parent[(int64_t)r * W + i];
+      lens[i] = len_in[(int64_t)r * W + i];
     }
-    par[i] = p;
-    atomicMin(&first[p], i);
-    atomicAdd(&cnt[p], 1);
+  }
+  if (all_staged)
+    for (int j = tid; j < W * S; j += FORK_THREADS) bts[j] = bt_in[(int64_t)r * W * S + j];
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < FORK_MAX_W / FORK_THREADS; ++u) {
+    const int i = tid + u * FORK_THREADS;
+    if (i < W) {
+      int p = pv[u];
+      if (p < 0 || p >= W) {
+        bad = 1;
+        p = i;
+      }
+      par[i] = p;
+      atomicMin(&first[p], i);
+      atomicAdd(&cnt[p], 1);
+    }
   }
   __syncthreads();
   const bool req_bad = bad != 0;
@@ -102,10 +133,10 @@ __global__ __launch_bounds__(FORK_THREADS) void beam_fork(
     for (; k > 0 && m != 0; --k) m &= m - 1;
     owner = m != 0 ? gi * 64 + __builtin_ctzll(m) : c;
   }
-  const int64_t n_c = (int64_t)r * W + c, n_p = (int64_t)r * W + p, n_o = (int64_t)r * W + owner;
-  const bool staged = S <= FORK_STAGE_S;
+  const int64_t n_p = (int64_t)r * W + p, n_o = (int64_t)r * W + owner;
+  const bool staged = !all_staged && S <= FORK_STAGE_S;
   for (int j = tid; j < S; j += FORK_THREADS) {
-    const int b = bt_in[n_o * S + j];
+    const int b = all_staged ? bts[owner * S + j] : bt_in[n_o * S + j];
     bt_out[n_c * S + j] = b;
     if (staged) {
       dst_row[j] = b;
@@ -113,22 +144,24 @@ __global__ __launch_bounds__(FORK_THREADS) void beam_fork(
     }
   }
   if (req_bad) {  // a request with a bad parent keeps its tables
-    if (tid == 0) len_out[n_c] = len_in[n_c];
+    if (tid == 0) len_out[n_c] = lens[c];
     return;
   }
   const int cap = S * g.bs;
-  int len = len_in[n_p];
+  int len = lens[p];
   if (len < 0 || len > cap) {
     if (tid == 0) flag_status(dev_status, GR_DEV_BAD_LENGTH);
     len = len < 0 ? 0 : cap;
   }
-  __syncthreads();  // staged rows visible
-  auto src_blk = [&](int i) { return staged ? src_row[i] : bt_in[n_p * S + i]; };
-  auto dst_blk = [&](int i) { return staged ? dst_row[i] : bt_in[n_o * S + i]; };
+  if (staged) __syncthreads();  // staged rows visible
+  auto src_blk = [&](int i) {
+    return all_staged ? bts[p * S + i] : staged ? src_row[i] : bt_in[n_p * S + i];
+  };
+  auto dst_blk = [&](int i) {
+    return all_staged ? bts[owner * S + i] : staged ? dst_row[i] : bt_in[n_o * S + i];
+  };
   uint8_t* kc = static_cast<uint8_t*>(g.k_cache);
   uint8_t* vc = static_cast<uint8_t*>(g.v_cache);
-  const int row_vecs = g.D * g.esize / 16;  // 16-byte vectors per (token, head) row
-  const int tv = g.Hkv * row_vecs;          // 16-byte vectors per token, all heads
   if (cow) {
     // copy tokens [0, len) of the parent's row into the owner's row
     if (FORK_THREADS % tv == 0 && g.num_blocks > 0) {
@@ -186,12 +219,20 @@ __global__ __launch_bounds__(FORK_THREADS) void beam_fork(
     if (len < cap) {
       const int bdst = dst_blk(len / g.bs);
       if (bdst >= 0 && bdst < g.num_blocks) {
-        for (int e = tid; e < tv; e += FORK_THREADS) {
-          const int h = e / row_vecs, vec = e - h * row_vecs;
-          const int64_t src = (n_c * new_tok_stride + (int64_t)h * g.D) * g.esize + vec * 16;
-          const int64_t dof = kv_byte_off(g, bdst, len % g.bs, h) + vec * 16;
-          *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(k_new + src);
-          *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(v_new + src);
+        if (tv <= FORK_THREADS) {
+          if (pre_new) {
+            const int64_t dof = kv_byte_off(g, bdst, len % g.bs, nh) + nvec * 16;
+            *reinterpret_cast<u32x4_t*>(kc + dof) = knew;
+            *reinterpret_cast<u32x4_t*>(vc + dof) = vnew;
+          }
+        } else {
+          for (int e = tid; e < tv; e += FORK_THREADS) {
+            const int h = e / row_vecs, vec = e - h * row_vecs;
+            const int64_t src = (n_c * new_tok_stride + (int64_t)h * g.D) * g.esize + vec * 16;
+            const int64_t dof = kv_byte_off(g, bdst, len % g.bs, h) + vec * 16;
+            *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(k_new + src);
+            *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(v_new + src);
+          }
         }
         new_len = len + 1;
       } else if (tid == 0) {
