@@ -200,3 +200,26 @@ def test_decode_late_dominant_key(device):
     ref, ref_lse = run_oracle(wl)
     assert ref_lse[1, 0] > 60.0  # the planted key dominates that row by far
     _check(out, lse, ref, ref_lse, atol=2e-2)
+
+
+def test_decode_prefix_beyond_staged_window(device):
+    """A prefix longer than the 2048 block ids the matrix-core kernel stages in
+    LDS (33,000 tokens at block size 16): the staged window moves mid-prefix."""
+    wl = workloads.make_decode(R=1, W=2, P=33000, L=(1, 8), Hq=8, Hkv=2, D=128, dtype=torch.bfloat16,
+                               input_scale=1.0, seed=31, pool_factor=1.0)
+    assert wl.prefix_bt.shape[1] > 2048
+    out, lse = run_gpu(wl, device)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2, rel=5e-2)
+
+
+@pytest.mark.parametrize("kernel", ["auto", "generic"])
+def test_decode_long_suffix(device, kernel):
+    """Suffixes spanning several blocks (37 and 60 tokens at block size 16):
+    block ids past the ones staged per beam are read from the table."""
+    wl = workloads.make_decode(R=2, W=8, P=200, L=[37, 60], Hq=16, Hkv=4, D=128, dtype=torch.bfloat16,
+                               input_scale=1.0, seed=37)
+    assert wl.suffix_bt.shape[1] == 4
+    out, lse = run_gpu(wl, device, kernel)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2)
