@@ -109,3 +109,14 @@ def test_append_full_row_flagged(device):
     wl = workloads.make_fork(R=1, W=4, Hkv=2, D=64, S=1, L_old=(16, 16), seed=14)
     with pytest.raises(ValueError, match="suffix full"):
         run_fork(wl, device)
+
+
+@pytest.mark.parametrize("W,S,Hkv,L", [
+    (128, 12, 2, (100, 180)),  # request table too big to stage whole: each child's two rows staged
+    (4, 300, 2, (200, 600)),   # rows longer than the row staging: block ids read from the table
+    (300, 1, 2, (1, 15)),      # more children than threads per workgroup
+    (16, 2, 3, (1, 30)),       # a token's vectors (3 heads x 16) do not divide the workgroup
+])
+def test_fork_table_sizes(device, W, S, Hkv, L):
+    wl = workloads.make_fork(R=2, W=W, Hkv=Hkv, D=128, S=S, L_old=L, seed=W + S)
+    _assert_same(run_fork(wl, device), run_oracle(wl))

@@ -31,7 +31,8 @@ def test_prune_beam128_full(device):
     _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), wl.k))
 
 
-@pytest.mark.parametrize("R,W,V,k", [(3, 16, 512, 16), (2, 4, 12288, 32), (1, 1, 64, 8), (2, 300, 256, 100)])
+@pytest.mark.parametrize("R,W,V,k", [(3, 16, 512, 16), (2, 4, 12288, 32), (1, 1, 64, 8), (2, 300, 256, 100),
+                                     (2, 4, 2048, 300)])
 def test_prune_shapes(device, R, W, V, k):
     wl = workloads.make_prune(R=R, W=W, V=V, k=k, seed=R + W + V)
     _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), k))
