@@ -116,6 +116,9 @@ struct PruneArgs {
   int32_t* token;
   float* score;
   float* eos_score;
+  uint64_t* part_key;  // [R, ng, k] stage-1 selections: score key (0 = empty) ...
+  int64_t* part_flat;  // ... and flat index b * V + v
+  int ng, gr;          // row groups per request, rows per group
 };
 
 __device__ inline float wave_max(float v) {
@@ -734,6 +737,347 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
   }
 }
 
+// ---- two-stage merge -------------------------------------------------------
+// Stage 1 (prune_merge_part): one workgroup per (request, group of gr rows,
+// gr * k1 <= MG_GROUP_CAND candidates, MG_PART_PER_THREAD per thread): the
+// group's top-k by (score desc, flat asc), sorted, into the part buffer as
+// (score key, flat index) pairs.  Stage 2, one workgroup per request, merges
+// the groups' sorted lists (prune_merge_lists: each entry's rank is its
+// position plus, per other list, a binary search) or, for very many groups,
+// selects again (prune_merge_final).  A candidate of
+// the request's top-k is within its group's top-k under the same order, so
+// both stages together select what a single pass over all candidates does;
+// the work of stage 1 is spread over every request's groups.
+constexpr int MG_PART_PER_THREAD = 4;
+constexpr int MG_GROUP_CAND = MG_PART_PER_THREAD * MG_THREADS;
+
+// Top-k by (key desc, flat asc) of the candidates the NT threads hold
+// (thread's ck[q] = 0: no candidate).  Sets take[q] for the selected ones and
+// returns their number, min(valid, k); *off is this thread's first output
+// slot (exclusive scan over the threads in thread order).
+template <int NT, int MPT>
+__device__ int merge_select(const uint64_t (&ck)[MPT], const int64_t (&cf)[MPT], int k, int64_t flat_end,
+                            bool (&take)[MPT], int& off, int* hist, int* itmp, int* sel, uint64_t (*kred)[2]) {
+  const int tid = threadIdx.x;
+  int mv = 0;
+  uint64_t kmin = ~0ull, kmax = 0;
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) {
+    if (ck[q] != 0) {
+      ++mv;
+      kmin = ck[q] < kmin ? ck[q] : kmin;
+      kmax = ck[q] > kmax ? ck[q] : kmax;
+    }
+  }
+#pragma unroll
+  for (int msk = 32; msk >= 1; msk >>= 1) {
+    const uint64_t a0 = __shfl_xor(kmin, msk, 64), a1 = __shfl_xor(kmax, msk, 64);
+    kmin = a0 < kmin ? a0 : kmin;
+    kmax = a1 > kmax ? a1 : kmax;
+  }
+  if ((tid & 63) == 0) {
+    kred[tid >> 6][0] = kmin;
+    kred[tid >> 6][1] = kmax;
+  }
+  int excl;
+  const int M = block_scan<NT>(mv, excl, itmp);  // its barriers order the kred writes
+  for (int w = 0; w < NT / 64; ++w) {
+    kmin = kred[w][0] < kmin ? kred[w][0] : kmin;
+    kmax = kred[w][1] > kmax ? kred[w][1] : kmax;
+  }
+  // boundary key (k-th largest), then among exact ties at it the lowest flat
+  // indices (tie key ~flat: the largest is the lowest index)
+  RadixSel<uint64_t> r1{0, 0, 0, 0}, r2{0, 0, 0, 0};
+  bool ties = false;
+  if (M > k) {
+    r1 = radix_select<NT, uint64_t>(
+        [&](auto&& f) {
+#pragma unroll
+          for (int q = 0; q < MPT; ++q)
+            if (ck[q] != 0) f(ck[q]);
+        },
+        k, kmin, kmax, hist, itmp, sel);
+    if (r1.eq != r1.need) {
+      ties = true;
+      r2 = radix_select<NT, uint64_t>(
+          [&](auto&& f) {
+#pragma unroll
+            for (int q = 0; q < MPT; ++q)
+              if (ck[q] != 0 && ck[q] == r1.prefix) f(~(uint64_t)cf[q]);
+          },
+          r1.need, ~(uint64_t)(flat_end - 1), ~0ull, hist, itmp, sel);
+    }
+  }
+  int cnt = 0;
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) {
+    bool t = ck[q] != 0;
+    if (t && M > k) {
+      const uint64_t u = ck[q] & r1.mask;
+      if (u != r1.prefix) t = u > r1.prefix;
+      else if (ties) t = (~(uint64_t)cf[q] & r2.mask) >= r2.prefix;
+    }
+    take[q] = t;
+    cnt += t;
+  }
+  block_scan<NT>(cnt, off, itmp);
+  return M < k ? M : k;
+}
+
+__global__ __launch_bounds__(MG_THREADS) void prune_merge_part(PruneArgs a) {
+  __shared__ double cs[PR_MAXW];
+  __shared__ int hist[PR_BINS];
+  __shared__ uint64_t fkeys[PR_MAXK];
+  __shared__ int64_t ffl[PR_MAXK];
+  __shared__ int itmp[MG_THREADS / 64];
+  __shared__ uint64_t kred[MG_THREADS / 64][2];
+  __shared__ int sel[3];
+  constexpr int MPT = MG_PART_PER_THREAD;
+  const int r = blockIdx.x / a.ng, g = blockIdx.x - r * a.ng;
+  const int tid = threadIdx.x;
+  const int k1 = a.k1;
+  const int b0 = g * a.gr, b1 = min(a.W, b0 + a.gr);
+  const int n = (b1 - b0) * k1;  // <= MG_GROUP_CAND
+  const int64_t row0 = (int64_t)r * a.W + b0;
+  const float* gx = a.cand_x + row0 * k1;
+  const int32_t* gv = a.cand_v + row0 * k1;
+  for (int b = tid; b < b1 - b0; b += MG_THREADS) cs[b] = a.row_c[row0 + b];
+  __syncthreads();
+  // thread t: candidates i = MPT t .. MPT t + MPT - 1 of the group (row i / k1)
+  uint64_t ck[MPT];
+  int64_t cf[MPT];
+  const int i0 = MPT * tid;
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) {
+    const int i = i0 + q;
+    ck[q] = 0;
+    cf[q] = 0;
+    if (i < n) {
+      const int v = gv[i];
+      if (v >= 0) {
+        const int bl = i / k1;
+        const double c = cs[bl];
+        ck[q] = dkey(c == -INFINITY ? -INFINITY : ((double)gx[i] + c) + 0.0);  // -0 -> +0
+        cf[q] = (int64_t)(b0 + bl) * a.V + v;
+      }
+    }
+  }
+  bool take[MPT];
+  int off;
+  const int nsel = merge_select<MG_THREADS, MPT>(ck, cf, a.k, (int64_t)a.W * a.V, take, off, hist, itmp, sel, kred);
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) {
+    if (take[q]) {
+      fkeys[off] = ck[q];
+      ffl[off] = cf[q];
+      ++off;
+    }
+  }
+  __syncthreads();
+  // the group's list, sorted by (score desc, flat asc); empty tail entries
+  // have key 0, below every score.  Rank of entry i = entries ordered before
+  // it: wave w counts over the entries [w*Q, (w+1)*Q) for every target, lane
+  // l holding targets l, l + 64, ...; the partial counts meet in LDS.
+  const int64_t o = ((int64_t)r * a.ng + g) * a.k;
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int i = tid; i < nsel; i += MG_THREADS) hist[i] = 0;  // the histogram is dead: rank counters
+  __syncthreads();
+  {
+    constexpr int NW = MG_THREADS / 64;
+    const int Q = (nsel + NW - 1) / NW, q0 = wave * Q, q1 = min(nsel, q0 + Q);
+    for (int t0 = 0; t0 < nsel; t0 += 64 * 4) {
+      uint64_t kt[4];
+      int64_t ft[4];
+      int rk[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int i = t0 + lane + 64 * m;
+        kt[m] = i < nsel ? fkeys[i] : 0;
+        ft[m] = i < nsel ? ffl[i] : 0;
+        rk[m] = 0;
+      }
+      for (int q = q0; q < q1; ++q) {
+        const uint64_t kq = fkeys[q];
+        const int64_t fq = ffl[q];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) rk[m] += (kq > kt[m]) | ((kq == kt[m]) & (fq < ft[m]));
+      }
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int i = t0 + lane + 64 * m;
+        if (i < nsel && rk[m]) atomicAdd(&hist[i], rk[m]);
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < nsel; i += MG_THREADS) {
+    const int rank = hist[i];
+    a.part_key[o + rank] = fkeys[i];
+    a.part_flat[o + rank] = ffl[i];
+  }
+  for (int i = nsel + tid; i < a.k; i += MG_THREADS) a.part_key[o + i] = 0;
+}
+
+template <int NT, int MPT>  // threads, candidates per thread: ng * k <= MPT * NT
+__global__ __launch_bounds__(NT) void prune_merge_final(PruneArgs a) {
+  __shared__ int hist[PR_BINS];
+  __shared__ uint64_t fkeys[PR_MAXK];
+  __shared__ int64_t ffl[PR_MAXK];
+  __shared__ int itmp[NT / 64];
+  __shared__ uint64_t kred[NT / 64][2];
+  __shared__ int sel[3];
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int k = a.k;
+  const int n = a.ng * k;
+  const uint64_t* pk = a.part_key + (int64_t)r * n;
+  const int64_t* pf = a.part_flat + (int64_t)r * n;
+  uint64_t ck[MPT];
+  int64_t cf[MPT];
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) {
+    const int i = tid + q * NT;
+    ck[q] = i < n ? pk[i] : 0;
+    cf[q] = ck[q] != 0 ? pf[i] : 0;
+  }
+  bool take[MPT];
+  int off;
+  const int nsel = merge_select<NT, MPT>(ck, cf, k, (int64_t)a.W * a.V, take, off, hist, itmp, sel, kred);
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) {
+    if (take[q]) {
+      fkeys[off] = ck[q];
+      ffl[off] = cf[q];
+      ++off;
+    }
+  }
+  __syncthreads();
+  // final order of the selected set: (score desc, flat asc)
+  for (int i = tid; i < nsel; i += NT) {
+    const uint64_t ki = fkeys[i];
+    const int64_t fi = ffl[i];
+    int rank = 0;
+#pragma unroll 8
+    for (int u = 0; u < nsel; ++u) {
+      const uint64_t kq = fkeys[u];
+      const int64_t fq = ffl[u];
+      rank += (kq > ki) | ((kq == ki) & (fq < fi));
+    }
+    const int64_t o = (int64_t)r * k + rank;
+    const int b = (int)(fi / a.V);
+    a.parent[o] = b;
+    a.token[o] = (int32_t)(fi - (int64_t)b * a.V);
+    a.score[o] = (float)dval(ki);
+  }
+  for (int i = nsel + tid; i < k; i += NT) {
+    const int64_t o = (int64_t)r * k + i;
+    a.parent[o] = -1;
+    a.token[o] = -1;
+    a.score[o] = -INFINITY;
+  }
+}
+
+// Stage 2 over sorted lists: entry i of list g has rank i + (entries of the
+// other lists ordered before it); those below k are written out at their
+// rank.  Unfilled output slots (fewer than k candidates) get -1, -1, -inf.
+constexpr int MG_LIST_MAX = 4096;  // ng * k staged in LDS
+constexpr int MG_LIST_THREADS = 512;
+constexpr int MG_LIST_MAXG = 16;   // lists searched side by side
+__global__ __launch_bounds__(MG_LIST_THREADS) void prune_merge_lists(PruneArgs a) {
+  __shared__ uint64_t lk[MG_LIST_MAX];
+  __shared__ int64_t lf[MG_LIST_MAX];
+  __shared__ int cnt_s;
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int k = a.k, ng = a.ng;
+  const int n = ng * k;
+  const uint64_t* pk = a.part_key + (int64_t)r * n;
+  const int64_t* pf = a.part_flat + (int64_t)r * n;
+  if (tid == 0) cnt_s = 0;
+  constexpr int PER = MG_LIST_MAX / MG_LIST_THREADS;
+  uint64_t ek[PER];
+  int64_t ef[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {  // all loads in flight together
+    const int e = tid + u * MG_LIST_THREADS;
+    ek[u] = e < n ? pk[e] : 0;
+    ef[u] = e < n ? pf[e] : 0;
+  }
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = tid + u * MG_LIST_THREADS;
+    if (e < n) {
+      lk[e] = ek[u];
+      lf[e] = ef[u];
+    }
+  }
+  __syncthreads();
+  int filled = 0;
+#pragma unroll 1
+  for (int u = 0; u < PER; ++u) {
+    const int e = tid + u * MG_LIST_THREADS;
+    if (__builtin_amdgcn_readfirstlane(e - tid) >= n) break;  // wave-uniform: no entries left
+    const uint64_t ke = ek[u];
+    const int64_t fe = ef[u];
+    const int g = e / k;
+    int rank = e - g * k;
+    // per other list, the first position ordered after (ke, fe); the
+    // searches run side by side, MG_LIST_MAXG lists at a time
+    for (int h0 = 0; h0 < ng; h0 += MG_LIST_MAXG) {
+      int lo[MG_LIST_MAXG], hi[MG_LIST_MAXG];
+#pragma unroll
+      for (int j = 0; j < MG_LIST_MAXG; ++j) {
+        lo[j] = 0;
+        hi[j] = h0 + j < ng && h0 + j != g ? k : 0;
+      }
+      for (int span = k; span > 0; span >>= 1) {
+#pragma unroll
+        for (int j = 0; j < MG_LIST_MAXG; ++j) {
+          if (h0 + j < ng) {  // wave-uniform
+            // branch-free step: both words are read whether or not the
+            // search is still open (an open search reads inside its list)
+            const bool open = lo[j] < hi[j];
+            const int mid = (lo[j] + hi[j]) >> 1;
+            const int idx = (h0 + j) * k + (open ? mid : 0);
+            const uint64_t km = lk[idx];
+            const int64_t fm = lf[idx];
+            const bool before = (km > ke) | ((km == ke) & (fm < fe));
+            lo[j] = open & before ? mid + 1 : lo[j];
+            hi[j] = open & !before ? mid : hi[j];
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < MG_LIST_MAXG; ++j) rank += lo[j];
+    }
+    if (e < n && ke != 0 && rank < k) {
+      const int64_t o = (int64_t)r * k + rank;
+      const int b = (int)(fe / a.V);
+      a.parent[o] = b;
+      a.token[o] = (int32_t)(fe - (int64_t)b * a.V);
+      a.score[o] = (float)dval(ke);
+      ++filled;
+    }
+  }
+  if (filled) atomicAdd(&cnt_s, filled);
+  __syncthreads();
+  for (int i = cnt_s + tid; i < k; i += MG_LIST_THREADS) {
+    const int64_t o = (int64_t)r * k + i;
+    a.parent[o] = -1;
+    a.token[o] = -1;
+    a.score[o] = -INFINITY;
+  }
+}
+
+// merge layout: rows per stage-1 group and groups per request
+void merge_groups(int W, int k1, int k, int& gr, int& ng) {
+  gr = MG_GROUP_CAND / k1;
+  if (gr < 1) gr = 1;
+  if (gr > W) gr = W;
+  ng = (W + gr - 1) / gr;
+  (void)k;
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace
@@ -745,8 +1089,11 @@ extern "C" size_t gr_beam_prune_workspace_size(int num_reqs, int beam_width, int
   if (num_reqs < 0 || beam_width < 1 || vocab < 1 || k < 1) return 0;
   const int k1 = k < vocab ? k : vocab;
   const size_t rows = (size_t)num_reqs * beam_width;
+  int gr, ng;
+  merge_groups(beam_width, k1, k, gr, ng);
+  const size_t parts = (size_t)num_reqs * ng * k;
   return align256(rows * k1 * sizeof(float)) + align256(rows * k1 * sizeof(int32_t)) +
-         align256(rows * sizeof(double));
+         align256(rows * sizeof(double)) + align256(parts * sizeof(uint64_t)) + align256(parts * sizeof(int64_t));
 }
 
 extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_row_stride, const float* cum,
@@ -783,15 +1130,32 @@ extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_ro
   a.token = token;
   a.score = score;
   a.eos_score = eos_score;
+  merge_groups(beam_width, k1, k, a.gr, a.ng);
+  const size_t parts = (size_t)num_reqs * a.ng * k;
+  uint8_t* part_base = ws + align256(rows * k1 * sizeof(float)) + align256(rows * k1 * sizeof(int32_t)) +
+                       align256(rows * sizeof(double));
+  a.part_key = reinterpret_cast<uint64_t*>(part_base);
+  a.part_flat = reinterpret_cast<int64_t*>(part_base + align256(parts * sizeof(uint64_t)));
   if (vocab <= PR_CHUNK * PR_REG_CHUNKS)
     hipLaunchKernelGGL(prune_rows<PR_REG_CHUNKS>, dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
   else
     hipLaunchKernelGGL(prune_rows<0>, dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
   gr_status_t st = launch_status();
   if (st != GR_OK) return st;
-  if ((size_t)beam_width * k1 <= (size_t)MG_REG * MG_THREADS && ((size_t)beam_width * k1) % 4 == 0)
-    hipLaunchKernelGGL(prune_merge<MG_REG>, dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
-  else
+  const size_t per_req = (size_t)a.ng * k;  // stage-2 candidates per request
+  if (per_req > (size_t)MG_REG * MG_THREADS) {
+    // very wide requests: one pass over all candidates, re-read from memory
     hipLaunchKernelGGL(prune_merge<0>, dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
+    return launch_status();
+  }
+  hipLaunchKernelGGL(prune_merge_part, dim3((unsigned)(num_reqs * a.ng)), dim3(MG_THREADS), 0, stream, a);
+  st = launch_status();
+  if (st != GR_OK) return st;
+  if (per_req <= MG_LIST_MAX)
+    hipLaunchKernelGGL(prune_merge_lists, dim3((unsigned)num_reqs), dim3(MG_LIST_THREADS), 0, stream, a);
+  else if (per_req <= 4 * MG_THREADS)
+    hipLaunchKernelGGL((prune_merge_final<MG_THREADS, 4>), dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
+  else
+    hipLaunchKernelGGL((prune_merge_final<MG_THREADS, MG_REG>), dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
   return launch_status();
 }
