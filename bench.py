@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import re
 import sys
@@ -179,6 +180,102 @@ def bench_other(args) -> int:
     return 0
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def e2e_cpu_baseline(cfg, prompt, n_req: int, budget_s: float = 15.0):
+    """The prefill phase of the batch on the host cores: one decoder layer
+    over one 2048-token prompt in torch float32 (the oracle's full forward),
+    timed and scaled by layers x requests."""
+    import dataclasses
+    import torch
+    from oracle import sid_beam as so
+    from vllm_gr_amd.v1.sid_decoder import init_weights
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    one = dataclasses.replace(cfg, num_layers=1, dtype=torch.float32)
+    w = init_weights(one, seed=0)
+    times = []
+    t0 = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t0 < budget_s and len(times) < 10):
+        t1 = time.perf_counter()
+        with torch.no_grad():
+            so.decoder_logits(w, one, prompt)
+        times.append(time.perf_counter() - t1)
+    times.sort()
+    per_layer = times[len(times) // 2]
+    ms = per_layer * cfg.num_layers * n_req * 1e3
+    return {"value": round(ms, 1), "unit": "ms (prefill phase)", "cores": n, "kind": "port",
+            "sample": f"1 decoder layer (+ embedding/lm_head) over one {len(prompt)}-token prompt, torch "
+                      f"float32, median of {len(times)}, scaled x{cfg.num_layers} layers x{n_req} requests"}
+
+
+def bench_e2e(args) -> int:
+    """Semantic-ID beam decode of 4 prompts x 2048 tokens, 128 beams, 3 SID
+    tokens through the 28-layer decoder: prefill once, then per step decode
+    -> prune -> fork.  One timed step = one whole batch (every request of it
+    completes together), host wall clock from the call to the results on the
+    host."""
+    import torch
+    from vllm_gr_amd.entrypoints.beam_search import BeamSearchParams
+    from vllm_gr_amd.entrypoints.llm import LLM
+    from vllm_gr_amd.v1.sid_decoder import SID_DECODER_1P7B as cfg
+    from vllm_gr_amd.v1.sid_runner import blocks_needed
+
+    R, P, W, T = 4, 2048, 128, 3
+    _log("bench: e2e: initialising the 28-layer decoder (seed 0, N(0, 0.02) bf16)")
+    llm = LLM(cfg, seed=0, num_blocks=blocks_needed(R, P, W, T, 16) + 64)
+    g = torch.Generator().manual_seed(0)
+    prompts = [torch.randint(0, cfg.vocab, (P,), generator=g).tolist() for _ in range(R)]
+    params = BeamSearchParams(beam_width=W, max_tokens=T)
+    for _ in range(args.warmup):
+        llm.beam_search(prompts, params)
+    torch.cuda.synchronize()
+    walls, pre, steps = [], [], []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        llm.beam_search(prompts, params)
+        t = llm.last_times
+        walls.append(t.wall_ms)
+        pre.append(t.prefill_ms)
+        steps.append(t.step_ms)
+        if (i + 1) % 10 == 0:
+            _log(f"bench: e2e batch {i + 1}/{args.steps}: wall {t.wall_ms:.2f} ms")
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    srt = sorted(walls)
+    p99 = srt[min(len(srt) - 1, int(math.ceil(0.99 * len(srt))) - 1)]
+    med = srt[len(srt) // 2]
+    pre_med = sorted(pre)[len(pre) // 2]
+    step_med = [sorted(s[j] for s in steps)[len(steps) // 2] for j in range(len(steps[0]))]
+    tokens = R * P
+    prefill_flops = 2 * cfg.num_params() * tokens + 4 * cfg.num_layers * cfg.num_heads * cfg.head_dim * R * P * (P + 1) // 2
+    tflops = prefill_flops / (pre_med * 1e-3) / 1e12
+    _log(f"bench: e2e p99 {p99:.2f} ms, median {med:.2f} ms, prefill {pre_med:.2f} ms ({tflops:.0f} TFLOP/s), "
+         f"steps {[round(x, 3) for x in step_med]} ms")
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = e2e_cpu_baseline(cfg, prompts[0], R)
+        _log(f"bench: cpu {cpu}")
+    line = {"metric": "semantic-ID beam decode request latency (p99) at 4 prompts x 2048 tokens, "
+                      "128 beams, 3 SID tokens, 28-layer decoder",
+            "value": round(p99, 3), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(elapsed * 1e3 / args.steps, 3), "median_ms": round(med, 3),
+            "prefill_ms": round(pre_med, 3), "decode_step_ms": [round(x, 3) for x in step_med],
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (random-init N(0,0.02) weights, seeded random prompt ids)",
+            "config": {"workload": "e2e semantic-ID beam decode: 4 requests x 2048-token prompt, beam 128, "
+                                   "3 tokens; 28 layers, hidden 2048, 16/8 heads x 128, FFN 6144, vocab 8192",
+                       "requests": R, "prompt": P, "beams": W, "max_tokens": T},
+            "roofline": {"bound": "mfma", "scope": "prefill phase (GEMM-dominated)",
+                         "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+            "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -186,8 +283,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", choices=["auto", "generic"], default="auto")
-    ap.add_argument("--workload", choices=["decode", "fork", "prune"], default="decode",
-                    help="decode (the headline line), or the fork+append / pruning kernels")
+    ap.add_argument("--workload", choices=["decode", "fork", "prune", "e2e"], default="decode",
+                    help="decode (the headline line), the fork+append / pruning kernels, or e2e "
+                         "(whole semantic-ID beam decode through a 28-layer decoder; a step is one batch)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 256 MiB device-to-device copy (5 launches), the reference point "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -211,6 +309,8 @@ def main() -> int:
         return 0
     from vllm_gr_amd import ops, workloads
 
+    if args.workload == "e2e":
+        return bench_e2e(args)
     if args.workload != "decode":
         return bench_other(args)
 

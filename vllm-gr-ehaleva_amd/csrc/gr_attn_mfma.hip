@@ -719,6 +719,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 bool mfma_decode_supported(const DecodeArgs& a) {
   if (a.D != HD || (a.dtype != GR_DTYPE_BF16 && a.dtype != GR_DTYPE_F16)) return false;
   if (a.bs_shift < 2) return false;  // power-of-two block size >= 4
+  // the suffix tiles tag each key with its 16-bit index within the beam's suffix
+  if ((int64_t)a.suffix_bt_stride * a.bs > 0xFFFF) return false;
   // 16-byte vector access: base pointers and element strides multiples of 8 elements
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!al(a.q) || !al(a.out) || !al(a.k_cache) || !al(a.v_cache)) return false;

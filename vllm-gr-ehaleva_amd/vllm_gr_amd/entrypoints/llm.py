@@ -1,0 +1,216 @@
+"""Offline semantic-ID beam search over the resident-KV path.
+
+Mirrors ``LLM.beam_search`` of the reference (vllm_gr/entrypoints/llm.py:31-280):
+same parameters (beam width, max tokens, ignore_eos, length penalty, the
+``begin_token`` / ``end_token`` pair), the same per-step candidate rule (each
+beam's top ``beam_width`` tokens by logprob, candidate score = cumulative
+logprob + logprob, EOS candidates finish with their score and leave the
+pool, the top ``beam_width`` of the union become the new beams, :201-271) and
+the same output (per prompt the best ``beam_width`` of finished + live
+sequences by vLLM's beam-search score, :273-292).
+
+What differs is how a step is computed.  The reference re-submits every
+beam's whole token list as a new one-token request each step (:183-199).
+Here a batch of prompts is prefilled once, then each step decodes exactly one
+token per beam against the shared prompt prefix and the beam's resident
+suffix (gr_beam_attn_decode), prunes on the device (gr_beam_prune_topk) and
+forks the beams' suffix KV (gr_beam_kv_fork) -- no host round trip between
+steps.  There is no tokenizer: ``begin_token`` / ``end_token`` of the
+:class:`BeamSearchParams` are token ids, or strings looked up in the
+``special_tokens`` map given to :class:`LLM` (an unknown one is ignored with
+a warning, as at llm.py:60-74), and ``text`` stays None.
+"""
+
+from __future__ import annotations
+
+import logging
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from ..v1.beam_kv import BeamKVTable
+from ..v1.sid_decoder import SID_DECODER_1P7B, DecoderConfig, SidDecoder, init_weights
+from ..v1.sid_runner import SidModelRunner
+from . import beam_search as bsm
+from .beam_search import BeamSearchParams
+
+logger = logging.getLogger(__name__)
+
+
+@dataclass
+class BeamSearchSequence:
+    """vLLM's BeamSearchSequence, the fields the offline path fills."""
+    tokens: list[int]
+    cum_logprob: float = 0.0
+    finish_reason: str | None = None
+    stop_reason: int | None = None
+    text: str | None = None
+
+
+@dataclass
+class BeamSearchOutput:
+    sequences: list[BeamSearchSequence]
+
+
+@dataclass
+class StepTimes:
+    """Device time of each phase of the last batch, milliseconds (HIP
+    events on the current stream), and the host wall time of the whole
+    batch including the final copy of the results."""
+    prefill_ms: float = 0.0
+    step_ms: list[float] = field(default_factory=list)
+    total_ms: float = 0.0
+    wall_ms: float = 0.0
+
+
+def beam_search_score(tokens: list[int], cum_logprob: float, eos_token_id: int | None,
+                      length_penalty: float) -> float:
+    """vLLM's beam-search sort key: ``cum_logprob / len ** length_penalty``,
+    the length excluding a final EOS (llm.py:75-79)."""
+    n = len(tokens)
+    if eos_token_id is not None and n and tokens[-1] == eos_token_id:
+        n -= 1
+    return cum_logprob / (n ** length_penalty)
+
+
+class LLM:
+    """A random-init Qwen-style decoder served through the beam path.
+
+    ``weights`` (from :func:`init_weights`) default to ``init_weights(cfg,
+    seed, device)``.  ``num_blocks`` KV-cache blocks of ``block_size``
+    tokens are allocated per layer up front; a batch needs
+    :func:`~vllm_gr_amd.v1.sid_runner.blocks_needed` of them."""
+
+    def __init__(self, cfg: DecoderConfig = SID_DECODER_1P7B, *, seed: int = 0, device="cuda",
+                 num_blocks: int = 4096, block_size: int = 16, eos_token_id: int | None = None,
+                 special_tokens: dict[str, int] | None = None, weights: dict | None = None,
+                 max_position: int = 32768):
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise ValueError("the beam path runs on a HIP device (torch 'cuda')")
+        if weights is None:
+            weights = init_weights(cfg, seed, dev)
+        self.cfg = cfg
+        self.model = SidDecoder(cfg, weights, max_position=max_position)
+        self.runner = SidModelRunner(self.model, num_blocks, block_size)
+        self.eos_token_id = eos_token_id
+        self.special_tokens = dict(special_tokens or {})
+        self.last_times = StepTimes()
+        self._batch = 0
+
+    def _token_id(self, tok, what: str) -> int | None:
+        if tok is None:
+            return None
+        tid = tok if isinstance(tok, int) else self.special_tokens.get(tok)
+        if tid is None or not 0 <= tid < self.cfg.vocab:
+            logger.warning("%s must be a valid token in the vocabulary, got token %s", what, tok)
+            return None
+        return int(tid)
+
+    def beam_search(self, prompts, params: BeamSearchParams) -> list[BeamSearchOutput]:
+        """``prompts``: token-id lists or ``{"prompt_token_ids": [...]}``
+        dicts.  Returns one :class:`BeamSearchOutput` per prompt."""
+        W = int(params.beam_width)
+        if W < 1:
+            raise ValueError("beam_width must be >= 1")
+        toks = [list(p["prompt_token_ids"]) if isinstance(p, dict) else list(p) for p in prompts]
+        if not toks:
+            return []
+        begin = self._token_id(params.begin_token, "begin_token")
+        end = self._token_id(params.end_token, "end_token")
+        if begin is not None:
+            toks = [t + [begin] for t in toks]
+        pre_calc = (begin is not None) + (end is not None)
+        steps = max(0, int(params.max_tokens) - pre_calc)
+        eos = None if params.ignore_eos else self.eos_token_id
+        if W > self.cfg.vocab:
+            raise ValueError("beam_width must not exceed the vocabulary")
+        for t in toks:
+            if any(not 0 <= x < self.cfg.vocab for x in t):
+                raise ValueError("prompt token id outside the vocabulary")
+
+        R, dev, bs = len(toks), self.model.device, self.runner.block_size
+        self._batch += 1
+        rids = [f"beam-{self._batch}-{r}" for r in range(R)]
+        lens = [len(t) for t in toks]
+        times = StepTimes()
+        t_wall = time.perf_counter()
+        stream = torch.cuda.current_stream(dev)
+        ev = [torch.cuda.Event(enable_timing=True)]
+        ev[0].record(stream)
+
+        hist = torch.empty(R, W, 0, dtype=torch.int32, device=dev)
+        score = torch.zeros(R, W, dtype=torch.float32, device=dev)
+        finished: list[tuple[torch.Tensor, torch.Tensor]] = []  # (eos_score [R, W_old], hist_old)
+        blocks: list[int] = []
+        try:
+            if steps > 0:
+                logits, prefix_bt, prefix_len, pblocks = self.runner.prefill(toks, rids)
+                blocks += [b for bl in pblocks for b in bl]
+                ev.append(torch.cuda.Event(enable_timing=True))
+                ev[-1].record(stream)
+                # the prompt is the one beam of every request (llm.py:118-146)
+                res = bsm.prune_step(logits[:, None], torch.zeros(R, 1, device=dev), W, eos)
+                finished.append((res.eos_score, torch.empty(R, 1, 0, dtype=torch.int32, device=dev)))
+                hist = res.token[..., None]
+                score = res.score
+                table = None
+                if steps > 1:
+                    per_beam = -(-(steps - 1) // bs)
+                    sblocks = self.runner.pool.allocate(R * W * per_beam)
+                    blocks += sblocks
+                    sbt = torch.tensor(sblocks, dtype=torch.int32).view(R * W, per_beam).to(dev)
+                    table = BeamKVTable(prefix_bt, prefix_len, W, sbt, block_size=bs)
+                for s in range(1, steps):
+                    tok = res.token.clamp(min=0).view(-1).to(torch.int64)
+                    logits = self.runner.decode(table, tok, rids, lens, step=s - 1)
+                    table.advance()
+                    if s + 1 < steps:
+                        res = bsm.beam_search_step(table, logits, score, self.runner.kv_caches, eos)
+                    else:
+                        res = bsm.prune_step(logits, score, W, eos)
+                    finished.append((res.eos_score, hist))
+                    par = res.parent.clamp(min=0).to(torch.int64)
+                    hist = torch.cat((hist.gather(1, par[..., None].expand(-1, -1, hist.shape[2])),
+                                      res.token[..., None]), dim=2)
+                    score = res.score
+                    ev.append(torch.cuda.Event(enable_timing=True))
+                    ev[-1].record(stream)
+            hist_h, score_h = hist.cpu().tolist(), score.cpu().tolist()
+            fin_h = [(e.cpu().tolist(), h.cpu().tolist()) for e, h in finished]
+        finally:
+            self.runner.pool.release(blocks)
+        times.wall_ms = (time.perf_counter() - t_wall) * 1e3
+        if len(ev) > 1:
+            times.prefill_ms = ev[0].elapsed_time(ev[1])
+            times.step_ms = [a.elapsed_time(b) for a, b in zip(ev[1:-1], ev[2:])]
+            times.total_ms = ev[0].elapsed_time(ev[-1])
+        self.last_times = times
+        return self._outputs(toks, hist_h, score_h, fin_h, steps, eos, end, params.length_penalty, W)
+
+    @staticmethod
+    def _outputs(toks, hist, score, finished, steps, eos, end, length_penalty, W):
+        outs = []
+        for r, prompt in enumerate(toks):
+            done = []
+            for eos_sc, hist_old in finished:
+                for b, sc in enumerate(eos_sc[r]):
+                    if sc != float("-inf"):
+                        done.append(BeamSearchSequence(prompt + hist_old[r][b] + [eos], sc,
+                                                       finish_reason="stop", stop_reason=eos))
+            live = []
+            tail = [] if end is None else [end]
+            if steps == 0:
+                live.append(BeamSearchSequence(prompt + tail, 0.0, finish_reason="length"))
+            else:
+                for b in range(W):
+                    if score[r][b] == float("-inf"):
+                        continue  # a slot no candidate filled
+                    live.append(BeamSearchSequence(prompt + hist[r][b] + tail, score[r][b],
+                                                   finish_reason="length"))
+            allseq = done + live
+            allseq.sort(key=lambda x: beam_search_score(x.tokens, x.cum_logprob, eos, length_penalty),
+                        reverse=True)
+            outs.append(BeamSearchOutput(allseq[:W]))
+        return outs

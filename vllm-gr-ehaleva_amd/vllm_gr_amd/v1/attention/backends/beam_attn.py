@@ -136,34 +136,48 @@ class BeamAttentionMetadataBuilder:
             (mega if md.get("is_mega_decode", False) else std).append((i, md))
 
         groups: list[DecodeGroup] = []
-        # ---- mega-decode requests: one query token per beam over the resident suffix
+        # ---- mega-decode requests: one query token per beam over the resident suffix.
+        # A table may hold several requests: then exactly that many consecutive batch
+        # requests name it, its i-th request being the i-th of them, and their query
+        # rows are contiguous, so the table's tensors are used whole.
         if mega:
-            rows, pbt, plen, sbt, slen, widths, slots = [], [], [], [], [], [], []
+            runs: list[tuple[object, list[tuple[int, dict]]]] = []
             for i, md in mega:
                 table = md["beam_kv"]
-                W = int(md["mega_beam_width"])
-                if W != table.beam_width or table.num_reqs != 1:
-                    raise ValueError(f"request {req_ids[i]}: beam_kv must hold one request of {W} beams")
-                if int(md["cache_len"]) < int(md["prefix_len"]):
-                    raise NotImplementedError(
-                        "mega decode needs the whole prompt prefix cached (prefill it through the "
-                        "standard path first)")
-                q0, q1 = q_starts[i], q_starts[i + 1]
-                if q1 - q0 != W:
-                    raise ValueError(f"request {req_ids[i]}: expected {W} query tokens (one per beam), "
-                                     f"got {q1 - q0}")
-                rows.append(torch.arange(q0, q1, device=dev))
+                if runs and runs[-1][0] is table and runs[-1][1][-1][0] == i - 1:
+                    runs[-1][1].append((i, md))
+                else:
+                    runs.append((table, [(i, md)]))
+            rows, pbt, plen, sbt, slen, widths, slots = [], [], [], [], [], [], []
+            for table, members in runs:
+                W = table.beam_width
+                if len(members) != table.num_reqs:
+                    raise ValueError(
+                        f"request {req_ids[members[0][0]]}: its beam_kv table holds {table.num_reqs} "
+                        f"requests but {len(members)} consecutive requests name it")
+                for i, md in members:
+                    if int(md["mega_beam_width"]) != W:
+                        raise ValueError(f"request {req_ids[i]}: beam_kv must hold requests of "
+                                         f"{int(md['mega_beam_width'])} beams")
+                    if int(md["cache_len"]) < int(md["prefix_len"]):
+                        raise NotImplementedError(
+                            "mega decode needs the whole prompt prefix cached (prefill it through the "
+                            "standard path first)")
+                    if q_starts[i + 1] - q_starts[i] != W:
+                        raise ValueError(f"request {req_ids[i]}: expected {W} query tokens (one per "
+                                         f"beam), got {q_starts[i + 1] - q_starts[i]}")
+                q0, q1 = q_starts[members[0][0]], q_starts[members[-1][0] + 1]
+                rows.append((q0, q1))
                 pbt.append(table.prefix_bt)
                 plen.append(table.prefix_len)
                 sbt.append(table.suffix_bt)
                 slen.append(table.attention_suffix_len())
-                widths.append(W)
+                widths.extend([W] * table.num_reqs)
                 slots.append((q0, q1, table.slot_mapping()))
-            idx = torch.cat(rows)
             slot_mapping = slot_mapping.clone()
             for q0, q1, s in slots:
                 slot_mapping[q0:q1] = s
-            groups.append(self._group(idx, m.num_actual_tokens, pbt, plen, widths, sbt, slen, None, 1))
+            groups.append(self._group(rows, m.num_actual_tokens, pbt, plen, widths, sbt, slen, None, 1))
 
         # ---- standard requests: the one-beam case, grouped by query length
         by_len: dict[int, list[int]] = {}
@@ -179,14 +193,13 @@ class BeamAttentionMetadataBuilder:
                 cached = S - ql
                 nb = max(1, (S + bs - 1) // bs)
                 row = m.block_table_tensor[i, :nb].to(torch.int32)
-                rows.append(torch.arange(q0, q0 + ql, device=dev))
+                rows.append((q0, q0 + ql))
                 pbt.append(row[None])
                 plen.append(torch.tensor([cached], dtype=torch.int32, device=dev))
                 sbt.append(row[None])
                 slen.append(torch.tensor([ql], dtype=torch.int32, device=dev))
                 sstart.append(torch.tensor([cached], dtype=torch.int32, device=dev))
-            idx = torch.cat(rows)
-            groups.append(self._group(idx, m.num_actual_tokens, pbt, plen, [1] * len(reqs), sbt, slen,
+            groups.append(self._group(rows, m.num_actual_tokens, pbt, plen, [1] * len(reqs), sbt, slen,
                                       sstart, ql))
         return BeamAttentionMetadata(
             num_actual_tokens=m.num_actual_tokens, max_query_len=m.max_query_len,
@@ -194,15 +207,21 @@ class BeamAttentionMetadataBuilder:
             block_table=m.block_table_tensor, slot_mapping=slot_mapping, causal=m.causal,
             groups=groups, mega_req_idxs=[i for i, _ in mega], std_req_idxs=[i for i, _ in std])
 
-    def _group(self, idx, ntok, pbt, plen, widths, sbt, slen, sstart, T) -> DecodeGroup:
+    def _group(self, rows, ntok, pbt, plen, widths, sbt, slen, sstart, T) -> DecodeGroup:
+        """``rows``: the group's batch token ranges ``(q0, q1)`` in beam order."""
         dev = self.device
         pw = max(t.shape[1] for t in pbt)
         sw = max(t.shape[1] for t in sbt)
         pad = lambda ts, w: torch.cat([torch.nn.functional.pad(t, (0, w - t.shape[1]), value=-1) for t in ts])
         beam_start = torch.tensor([0] + widths, dtype=torch.int64).cumsum(0).to(torch.int32).to(dev)
-        in_order = idx.numel() == ntok and bool((idx == torch.arange(ntok, device=dev)).all())
+        pos, in_order = 0, True
+        for q0, q1 in rows:
+            in_order &= q0 == pos
+            pos = q1
+        in_order &= pos == ntok
+        idx = None if in_order else torch.cat([torch.arange(q0, q1) for q0, q1 in rows]).to(dev)
         return DecodeGroup(
-            token_index=None if in_order else idx, prefix_bt=pad(pbt, pw).contiguous(),
+            token_index=idx, prefix_bt=pad(pbt, pw).contiguous(),
             prefix_len=torch.cat(plen).contiguous(), beam_start=beam_start,
             suffix_bt=pad(sbt, sw).contiguous(), suffix_len=torch.cat(slen).to(torch.int32).contiguous(),
             suffix_start=None if sstart is None else torch.cat(sstart).contiguous(), q_per_beam=T,

@@ -1,0 +1,187 @@
+"""Random-init Qwen-style decoder for end-to-end semantic-ID beam decode.
+
+The reference serves a Qwen3 checkpoint through vLLM's model executor
+(vllm==0.14, not vendored; the semantic-ID tasks use Qwen3 chat templates,
+benchmarks/open_one_rec/tasks/recommendation/config.py:19).  This is the
+same architecture, sized by a :class:`DecoderConfig`, with weights drawn
+from N(0, std) -- there are no checkpoints here:
+
+* token embedding, tied to the lm_head by default;
+* per layer: RMSNorm, q/k/v projections (no bias), per-head RMSNorm of q and
+  k, rotary embedding with rotate-half pairing (theta 1e6) at the positions
+  the caller gives, attention through the BeamAttention backend, o
+  projection, residual add; RMSNorm, SwiGLU MLP (silu(gate) * up, down),
+  residual add;
+* final RMSNorm; logits = lm_head rows in float32.
+
+GEMMs are ``torch.nn.functional.linear`` (hipBLASLt on ROCm).  Attention --
+K/V append through the slot mapping, then shared-prefix + resident-suffix
+decode -- is :class:`BeamAttentionImpl.forward`, the same call vLLM's
+Attention layer makes (beam_attn.py:703-755).  Positions follow the
+reference's rule (a beam's j-th suffix token sits at prefix_len + j,
+engine_core_patch.py:362-365); logits are taken for one row per beam, the
+beam's newest token (:367-369).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .attention.backends.beam_attn import BeamAttentionImpl
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    num_layers: int = 28
+    hidden: int = 2048
+    num_heads: int = 16
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 6144
+    vocab: int = 8192
+    rope_theta: float = 1.0e6
+    rms_eps: float = 1.0e-6
+    tie_embeddings: bool = True
+    init_std: float = 0.02
+    dtype: torch.dtype = torch.bfloat16
+
+    @property
+    def q_size(self) -> int:
+        return self.num_heads * self.head_dim
+
+    @property
+    def kv_size(self) -> int:
+        return self.num_kv_heads * self.head_dim
+
+    def num_params(self) -> int:
+        H, L = self.hidden, self.num_layers
+        per_layer = (H * (self.q_size + 2 * self.kv_size) + self.q_size * H + 3 * H * self.ffn
+                     + 2 * H + 2 * self.head_dim)
+        emb = self.vocab * H * (1 if self.tie_embeddings else 2)
+        return L * per_layer + emb + H
+
+
+#: the 28-layer, 2048-hidden, 16/8-head, 6144-FFN, 8192-token decoder
+SID_DECODER_1P7B = DecoderConfig()
+
+
+def init_weights(cfg: DecoderConfig, seed: int, device="cpu") -> dict[str, torch.Tensor]:
+    """Weights in nn.Linear layout ``[out, in]``, drawn from one generator on
+    ``device`` in a fixed order (embedding, then per layer qkv, o, gate_up,
+    down), N(0, init_std) in float32 rounded to ``cfg.dtype``; norm weights
+    are ones.  The same seed and device give the same weights."""
+    dev = torch.device(device)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def normal(*shape):
+        w = torch.randn(*shape, generator=g, device=dev, dtype=torch.float32)
+        return w.mul_(cfg.init_std).to(cfg.dtype)
+
+    ones = lambda n: torch.ones(n, device=dev, dtype=cfg.dtype)
+    H = cfg.hidden
+    w = {"embed": normal(cfg.vocab, H)}
+    for i in range(cfg.num_layers):
+        p = f"layers.{i}."
+        w[p + "qkv"] = normal(cfg.q_size + 2 * cfg.kv_size, H)
+        w[p + "o"] = normal(H, cfg.q_size)
+        w[p + "gate_up"] = normal(2 * cfg.ffn, H)
+        w[p + "down"] = normal(H, cfg.ffn)
+        w[p + "input_norm"] = ones(H)
+        w[p + "post_norm"] = ones(H)
+        w[p + "q_norm"] = ones(cfg.head_dim)
+        w[p + "k_norm"] = ones(cfg.head_dim)
+    w["final_norm"] = ones(H)
+    w["lm_head"] = w["embed"] if cfg.tie_embeddings else normal(cfg.vocab, H)
+    return w
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm over the last dim in float32, rounded once to x's dtype."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (y * weight.float()).to(x.dtype)
+
+
+class RotaryEmbedding:
+    """Rotate-half rotary embedding: pair (i, i + D/2) turns by
+    ``pos * theta^(-2i/D)``; cos/sin in float32 from a cached table."""
+
+    def __init__(self, head_dim: int, theta: float, max_pos: int, device):
+        half = head_dim // 2
+        inv = 1.0 / (theta ** (torch.arange(0, half, dtype=torch.float64) * 2.0 / head_dim))
+        ang = torch.arange(max_pos, dtype=torch.float64)[:, None] * inv[None]
+        self.cos = ang.cos().float().to(device)
+        self.sin = ang.sin().float().to(device)
+        self.max_pos = max_pos
+
+    def __call__(self, positions: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """x [T, heads, D] -> rotated, same dtype."""
+        half = x.shape[-1] // 2
+        c = self.cos[positions][:, None]
+        s = self.sin[positions][:, None]
+        xf = x.float()
+        x1, x2 = xf[..., :half], xf[..., half:]
+        return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
+
+
+class SidDecoder:
+    """The decoder's forward over a flat batch of tokens.
+
+    ``forward(input_ids, positions, attn_metadata, kv_caches)`` runs every
+    layer; ``kv_caches[i]`` is layer i's ``[2, num_blocks, block_size, Hkv,
+    D]`` cache and ``attn_metadata`` the backend metadata of the batch (its
+    slot mapping says where each token's K/V is written).  Positions must lie
+    below ``max_position`` (the caller checks; the rotary table is indexed on
+    the device without a bounds check).  Returns the final
+    normalised hidden states ``[T, hidden]``; :meth:`compute_logits` maps
+    selected rows to float32 logits."""
+
+    def __init__(self, cfg: DecoderConfig, weights: dict[str, torch.Tensor], *, max_position: int = 32768):
+        self.cfg = cfg
+        self.w = weights
+        dev = weights["embed"].device
+        self.rope = RotaryEmbedding(cfg.head_dim, cfg.rope_theta, max_position, dev)
+        self.layer_names = [f"model.layers.{i}.self_attn.attn" for i in range(cfg.num_layers)]
+        self.attn = [BeamAttentionImpl(cfg.num_heads, cfg.head_dim, 1.0 / math.sqrt(cfg.head_dim),
+                                       cfg.num_kv_heads, None, None, "auto")
+                     for _ in range(cfg.num_layers)]
+
+    @property
+    def device(self) -> torch.device:
+        return self.w["embed"].device
+
+    def _attention(self, i: int, x: torch.Tensor, positions: torch.Tensor, attn_metadata,
+                   kv_cache: torch.Tensor) -> torch.Tensor:
+        cfg, p = self.cfg, f"layers.{i}."
+        T = x.shape[0]
+        qkv = F.linear(x, self.w[p + "qkv"])
+        q, k, v = qkv.split([cfg.q_size, cfg.kv_size, cfg.kv_size], dim=-1)
+        q = rms_norm(q.view(T, cfg.num_heads, cfg.head_dim), self.w[p + "q_norm"], cfg.rms_eps)
+        k = rms_norm(k.view(T, cfg.num_kv_heads, cfg.head_dim), self.w[p + "k_norm"], cfg.rms_eps)
+        q = self.rope(positions, q)
+        k = self.rope(positions, k)
+        v = v.reshape(T, cfg.num_kv_heads, cfg.head_dim)
+        out = torch.empty_like(q)
+        self.attn[i].forward(None, q, k, v, kv_cache, attn_metadata, output=out)
+        return F.linear(out.view(T, cfg.q_size), self.w[p + "o"])
+
+    def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, attn_metadata,
+                kv_caches) -> torch.Tensor:
+        cfg = self.cfg
+        h = self.w["embed"][input_ids]
+        for i in range(cfg.num_layers):
+            p = f"layers.{i}."
+            h = h + self._attention(i, rms_norm(h, self.w[p + "input_norm"], cfg.rms_eps), positions,
+                                    attn_metadata, kv_caches[i])
+            x = rms_norm(h, self.w[p + "post_norm"], cfg.rms_eps)
+            gate, up = F.linear(x, self.w[p + "gate_up"]).chunk(2, dim=-1)
+            h = h + F.linear(F.silu(gate) * up, self.w[p + "down"])
+        return rms_norm(h, self.w["final_norm"], cfg.rms_eps)
+
+    def compute_logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        return F.linear(hidden, self.w["lm_head"]).float()
