@@ -92,6 +92,34 @@ gr_status_t gr_beam_attn_decode(
     float scale, float softcap, float* lse_out, int32_t* dev_status, hipStream_t stream);
 
 /*
+ * Varlen causal attention of the standard (non-beam) requests of a batch --
+ * prefill chunks and single-token decodes -- over the paged KV cache.
+ *
+ * Replaces flash_attn_varlen_func(cu_seqlens_q, seqused_k, causal=True,
+ * block_table) on the standard path of the reference's cascade attention
+ * (vllm_gr/v1/attention/backends/beam_attn.py:643-654).
+ *
+ * Request r owns query rows query_start[r] .. query_start[r+1]-1 of q/out
+ * (ql = their count <= max_query_len) and seq_len[r] keys in block-table row
+ * block_table[r * bt_stride ...], its new tokens' K/V already written there.
+ * Query i of request r sees keys 0 .. seq_len[r] - ql + i (bottom-right
+ * causal).  GQA, scale, softcap, LSE and row layout as in
+ * gr_beam_attn_decode; q/out [num_tokens, num_q_heads, head_dim].  Table
+ * contents are checked on the device (GR_DEV_BAD_LENGTH for an inconsistent
+ * request, which is then skipped; GR_DEV_BAD_BLOCK for a block id outside
+ * the pool, whose keys read as zeros).
+ */
+gr_status_t gr_paged_attn_prefill(
+    void* out, int64_t out_tok_stride,
+    const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* block_table, int bt_stride, const int32_t* query_start,
+    const int32_t* seq_len, int num_reqs, int num_tokens, int max_query_len,
+    int num_q_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
+    float scale, float softcap, float* lse_out, int32_t* dev_status, hipStream_t stream);
+
+/*
  * Scatter new K/V tokens into the paged cache by flat slot
  * (slot = block * block_size + offset; slot < 0 is skipped).
  *

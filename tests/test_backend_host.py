@@ -123,17 +123,26 @@ def test_builder_routes_mega_and_standard_requests():
     # mega rows write their K/V into each beam's private block; other rows keep vLLM's slots
     assert md.slot_mapping[:3].tolist() == table.slot_mapping().tolist()
     assert md.slot_mapping[3:].tolist() == list(range(1003, 1009))
-    g_mega, g_dec, g_pre = md.groups
+    (g_mega,) = md.groups
     assert g_mega.q_per_beam == 1 and g_mega.token_index.tolist() == [0, 1, 2]
     assert g_mega.beam_start.tolist() == [0, 3] and g_mega.prefix_len.tolist() == [20]
     assert g_mega.suffix_len.tolist() == [1, 6, 17]
-    # standard decode: prefix = the 39 cached tokens, suffix = the new token at position 39
-    assert g_dec.q_per_beam == 1 and g_dec.token_index.tolist() == [3]
-    assert g_dec.prefix_len.tolist() == [39] and g_dec.suffix_len.tolist() == [1]
-    assert g_dec.suffix_start.tolist() == [39] and g_dec.prefix_bt[0, :3].tolist() == [20, 21, 22]
-    # standard prefill chunk: 40 cached + 5 new tokens, causal over the 5
-    assert g_pre.q_per_beam == 5 and g_pre.token_index.tolist() == [4, 5, 6, 7, 8]
-    assert g_pre.prefix_len.tolist() == [40] and g_pre.suffix_start.tolist() == [40]
+    # standard decode (1 new token of 40) and prefill chunk (5 new of 45): one varlen causal
+    # launch over their own block-table rows (flash_attn_varlen_func, beam_attn.py:643-654)
+    p = md.prefill
+    assert p.token_index.tolist() == [3, 4, 5, 6, 7, 8]
+    assert p.query_start.tolist() == [0, 1, 6] and p.seq_len.tolist() == [40, 45]
+    assert p.block_table.tolist() == bt[1:].tolist() and p.max_query_len == 5
+
+
+def test_builder_standard_only_batch_uses_batch_tensors():
+    bt = torch.tensor([[1, 2, 0], [3, 4, 5]], dtype=torch.int32)
+    m = _common([17, 40], [17, 40], bt)
+    builder = ba.BeamAttentionMetadataBuilder(types.SimpleNamespace(block_size=16), ["l0"], None, "cpu")
+    md = builder.build(0, m)
+    assert md.groups == [] and md.prefill.token_index is None and md.prefill.max_query_len == 40
+    assert md.prefill.block_table is m.block_table_tensor and md.prefill.seq_len is m.seq_lens
+    assert md.prefill.query_start is m.query_start_loc
 
 
 def test_builder_rejects_inconsistent_mega_request():

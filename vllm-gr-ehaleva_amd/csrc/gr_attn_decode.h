@@ -32,6 +32,8 @@ struct DecodeArgs {
 // MFMA path (gr_attn_mfma.hip): bf16/fp16, head_dim 128, 16-byte aligned rows.
 bool mfma_decode_supported(const DecodeArgs& a);
 gr_status_t launch_mfma_decode(const DecodeArgs& a, hipStream_t stream);
+// Varlen causal mode of the same kernel (see gr_paged_attn_prefill).
+gr_status_t launch_mfma_prefill(const DecodeArgs& a, hipStream_t stream);
 
 // 0 = choose automatically, 1 = always the generic kernel (testing hook).
 extern int g_decode_kernel_override;

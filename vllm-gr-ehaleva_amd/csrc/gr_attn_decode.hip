@@ -30,7 +30,11 @@ __device__ inline int find_request(const int32_t* beam_start, int num_reqs, int 
   return lo;
 }
 
-template <int DT>
+// PREFILL: the varlen causal mode (gr_paged_attn_prefill): blockIdx.x / chunks
+// is the request, prefix_bt / prefix_len its block table and sequence length,
+// beam_start its query start, T the largest query count; query i of a request
+// with ql queries sees keys 0 .. seq - ql + i, and there is no suffix.
+template <int DT, bool PREFILL = false>
 __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   using E = Elem<DT>;
   using S = typename E::storage;
@@ -52,18 +56,37 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   const int chunk = blockIdx.x % chunks;
   const int hk = blockIdx.y;
   const int t = threadIdx.x;
-  if (n >= a.num_beams) return;
-  const int r = find_request(a.beam_start, a.num_reqs, n);
-  const int P = a.prefix_len[r];
-  const int L = a.suffix_len[n];
-  const int s0 = a.suffix_start ? a.suffix_start[n] : 0;
+  if (n >= (PREFILL ? a.num_reqs : a.num_beams)) return;
   const int row0 = chunk * GEN_ROWS;
-  const int nrows = min(GEN_ROWS, rows_total - row0);
   const int pre_cap = a.prefix_bt_stride * a.bs;
-  const int suf_cap = a.suffix_bt_stride * a.bs;
-  const int Pc = min(max(P, 0), pre_cap);
-  const int Lc = (L < 0 || s0 < 0 || s0 + L > suf_cap) ? 0 : L;
-  if (t == 0 && (Pc != P || Lc != L)) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+  int r, P, L, s0, nrows, Pc, Lc, ctx = 0;
+  int64_t tok0;  // token row of query 0 of this beam / request
+  if constexpr (PREFILL) {
+    r = n;
+    const int q0 = a.beam_start[r], ql = a.beam_start[r + 1] - q0, seq = a.prefix_len[r];
+    if (q0 < 0 || ql < 0 || q0 + ql > a.num_beams || ql > a.T || seq < ql || seq > pre_cap) {
+      if (t == 0 && chunk == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+      return;
+    }
+    if (row0 >= G * ql) return;
+    nrows = min(GEN_ROWS, G * ql - row0);
+    ctx = seq - ql;
+    // keys up to the chunk's last query token
+    P = Pc = ctx + (row0 + nrows - 1) / G + 1;
+    L = Lc = s0 = 0;
+    tok0 = q0;
+  } else {
+    r = find_request(a.beam_start, a.num_reqs, n);
+    P = a.prefix_len[r];
+    L = a.suffix_len[n];
+    s0 = a.suffix_start ? a.suffix_start[n] : 0;
+    nrows = min(GEN_ROWS, rows_total - row0);
+    const int suf_cap = a.suffix_bt_stride * a.bs;
+    Pc = min(max(P, 0), pre_cap);
+    Lc = (L < 0 || s0 < 0 || s0 + L > suf_cap) ? 0 : L;
+    if (t == 0 && (Pc != P || Lc != L)) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+    tok0 = (int64_t)n * a.T;
+  }
 
   const S* q = static_cast<const S*>(a.q);
   const S* kc = static_cast<const S*>(a.k_cache);
@@ -75,7 +98,7 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
     if (row < nrows) {
       int rho = row0 + row;
       int qi = rho / G, g = rho % G;
-      v = E::to_float(q[(int64_t)(n * a.T + qi) * a.q_tok_stride + (int64_t)(hk * G + g) * D + d]);
+      v = E::to_float(q[(tok0 + qi) * a.q_tok_stride + (int64_t)(hk * G + g) * D + d]);
     }
     q_s[e] = v;
   }
@@ -134,7 +157,8 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
         s *= a.scale;
         if (a.softcap > 0.f) s = a.softcap * tanhf(s / a.softcap);
         bool vis = row < nrows && kk < total && kv_ok[key];
-        if (vis && kk >= Pc) {
+        if (PREFILL) vis = vis && kk <= ctx + (row0 + row) / G;
+        if (!PREFILL && vis && kk >= Pc) {
           int qi = (row0 + row) / G;
           vis = (kk - Pc) <= Lc - a.T + qi;
         }
@@ -187,7 +211,7 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
         int qi = rho / G, g = rho % G;
         float l = l_s[row];
         float o = l > 0.f ? acc[i] / l : 0.f;
-        out[(int64_t)(n * a.T + qi) * a.out_tok_stride + (int64_t)(hk * G + g) * D + d] = E::from_float(o);
+        out[(tok0 + qi) * a.out_tok_stride + (int64_t)(hk * G + g) * D + d] = E::from_float(o);
       }
     }
   }
@@ -195,7 +219,7 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
     int rho = row0 + t;
     int qi = rho / G, g = rho % G;
     float l = l_s[t];
-    a.lse_out[(int64_t)(n * a.T + qi) * a.Hq + hk * G + g] = l > 0.f ? m_s[t] + logf(l) : -INFINITY;
+    a.lse_out[(tok0 + qi) * a.Hq + hk * G + g] = l > 0.f ? m_s[t] + logf(l) : -INFINITY;
   }
 }
 
@@ -206,28 +230,32 @@ static size_t generic_smem_bytes(int D) {
 
 int g_decode_kernel_override = 0;
 
+template <bool PREFILL>
 static gr_status_t launch_generic(const DecodeArgs& a, hipStream_t stream) {
   const int G = a.Hq / a.Hkv;
-  const int chunks = (G * a.T + GEN_ROWS - 1) / GEN_ROWS;
-  dim3 grid((unsigned)((int64_t)a.num_beams * chunks), (unsigned)a.Hkv);
+  const int64_t chunks = ((int64_t)G * a.T + GEN_ROWS - 1) / GEN_ROWS;
+  const int64_t gx = (int64_t)(PREFILL ? a.num_reqs : a.num_beams) * chunks;
+  if (gx == 0) return GR_OK;
+  if (gx > 0x7fffffff || a.Hkv > 65535) return GR_ERR_INVALID_ARG;
+  dim3 grid((unsigned)gx, (unsigned)a.Hkv);
   size_t smem = generic_smem_bytes(a.D);
-  static bool attr_done[3] = {false, false, false};
-  if (!attr_done[a.dtype]) {  // head_dim 256 needs more than the default 64 KB
-    const void* fn = a.dtype == GR_DTYPE_F32 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F32>)
-                     : a.dtype == GR_DTYPE_F16 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F16>)
-                                               : reinterpret_cast<const void*>(decode_generic<GR_DTYPE_BF16>);
+  static bool attr_done[2][3] = {};
+  if (!attr_done[PREFILL][a.dtype]) {  // head_dim 256 needs more than the default 64 KB
+    const void* fn = a.dtype == GR_DTYPE_F32 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F32, PREFILL>)
+                     : a.dtype == GR_DTYPE_F16 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F16, PREFILL>)
+                                               : reinterpret_cast<const void*>(decode_generic<GR_DTYPE_BF16, PREFILL>);
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)generic_smem_bytes(256));
-    attr_done[a.dtype] = true;
+    attr_done[PREFILL][a.dtype] = true;
   }
   switch (a.dtype) {
     case GR_DTYPE_F32:
-      hipLaunchKernelGGL(decode_generic<GR_DTYPE_F32>, grid, dim3(GEN_THREADS), smem, stream, a);
+      hipLaunchKernelGGL((decode_generic<GR_DTYPE_F32, PREFILL>), grid, dim3(GEN_THREADS), smem, stream, a);
       break;
     case GR_DTYPE_F16:
-      hipLaunchKernelGGL(decode_generic<GR_DTYPE_F16>, grid, dim3(GEN_THREADS), smem, stream, a);
+      hipLaunchKernelGGL((decode_generic<GR_DTYPE_F16, PREFILL>), grid, dim3(GEN_THREADS), smem, stream, a);
       break;
     default:
-      hipLaunchKernelGGL(decode_generic<GR_DTYPE_BF16>, grid, dim3(GEN_THREADS), smem, stream, a);
+      hipLaunchKernelGGL((decode_generic<GR_DTYPE_BF16, PREFILL>), grid, dim3(GEN_THREADS), smem, stream, a);
       break;
   }
   return launch_status();
@@ -274,7 +302,42 @@ extern "C" gr_status_t gr_beam_attn_decode(
   a.scale = scale; a.softcap = softcap; a.lse_out = lse_out; a.dev_status = dev_status;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   if (g_decode_kernel_override == 0 && mfma_decode_supported(a)) return launch_mfma_decode(a, stream);
-  return launch_generic(a, stream);
+  return launch_generic<false>(a, stream);
+}
+
+extern "C" gr_status_t gr_paged_attn_prefill(
+    void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* block_table, int bt_stride, const int32_t* query_start, const int32_t* seq_len,
+    int num_reqs, int num_tokens, int max_query_len, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
+    hipStream_t stream) {
+  if (num_reqs < 0 || num_tokens < 0 || max_query_len < 0 || num_q_heads < 1 || num_kv_heads < 1 ||
+      num_q_heads % num_kv_heads != 0 || block_size < 1 || head_dim < 8 || head_dim % 8 != 0 ||
+      num_blocks < 0 || bt_stride < 0 || !dtype_valid(dtype) || !(softcap >= 0.f))
+    return GR_ERR_INVALID_ARG;
+  if (head_dim > 256) return GR_ERR_UNSUPPORTED;
+  if (num_reqs == 0 || num_tokens == 0 || max_query_len == 0) return GR_OK;
+  if (!out || !q || !k_cache || !v_cache || !block_table || !query_start || !seq_len)
+    return GR_ERR_INVALID_ARG;
+  if (q_tok_stride < (int64_t)num_q_heads * head_dim || out_tok_stride < (int64_t)num_q_heads * head_dim ||
+      kv_block_stride < 1 || kv_tok_stride < 1 || kv_head_stride < 1)
+    return GR_ERR_INVALID_ARG;
+  DecodeArgs a = {};
+  a.out = out; a.out_tok_stride = out_tok_stride;
+  a.q = q; a.q_tok_stride = q_tok_stride;
+  a.k_cache = k_cache; a.v_cache = v_cache; a.num_blocks = num_blocks;
+  a.kv_block_stride = kv_block_stride; a.kv_tok_stride = kv_tok_stride; a.kv_head_stride = kv_head_stride;
+  a.prefix_bt = block_table; a.prefix_bt_stride = bt_stride; a.prefix_len = seq_len;
+  a.beam_start = query_start;
+  a.suffix_bt = nullptr; a.suffix_bt_stride = 0; a.suffix_len = nullptr; a.suffix_start = nullptr;
+  a.num_reqs = num_reqs; a.max_beams = 1; a.num_beams = num_tokens; a.T = max_query_len;
+  a.Hq = num_q_heads; a.Hkv = num_kv_heads; a.D = head_dim; a.bs = block_size; a.dtype = dtype;
+  a.scale = scale; a.softcap = softcap; a.lse_out = lse_out; a.dev_status = dev_status;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  if (g_decode_kernel_override == 0 && mfma_decode_supported(a)) return launch_mfma_prefill(a, stream);
+  return launch_generic<true>(a, stream);
 }
 
 extern "C" int gr_set_decode_kernel(int which) {

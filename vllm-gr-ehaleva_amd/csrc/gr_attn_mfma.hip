@@ -322,7 +322,13 @@ __device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_b
   }
 }
 
-template <int DT, bool SOFTCAP>
+// PREFILL: the varlen causal mode (gr_paged_attn_prefill).  The argument
+// block is read as: prefix_bt = block table, prefix_len = sequence length,
+// beam_start = query start per request, num_beams = query tokens, T = the
+// largest query count; a request's rows are its query tokens x GQA group,
+// query i sees keys 0 .. seq - ql + i, all read through the prefix machinery
+// (fully visible tiles pipelined, the causal edge masked per row), no suffix.
+template <int DT, bool SOFTCAP, bool PREFILL = false>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF];
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
@@ -335,19 +341,38 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // the same XCD (round-robin dispatch puts workgroup i on XCD i % 8)
   const int bid = blockIdx.x;
   const int xcd = bid & 7, local = bid >> 3;
-  const int unit = (local / mtiles) * 8 + xcd;
-  const int mt = local % mtiles;
+  // prefill: tile rank is the slow index and runs last-token-first, so every
+  // (request, head)'s longest causal range is dispatched in the first wave
+  const int ugroups = (units + 7) >> 3;
+  const int unit = PREFILL ? (local % ugroups) * 8 + xcd : (local / mtiles) * 8 + xcd;
+  const int mt = PREFILL ? mtiles - 1 - local / ugroups : local % mtiles;
   if (unit >= units) return;
   const int r = unit / a.Hkv, hk = unit % a.Hkv;
-  const int nb0 = a.beam_start[r];
-  const int W = a.beam_start[r + 1] - nb0;
-  const int G = a.Hq / a.Hkv, TG = a.T * G;
-  const int rows_r = W * TG;
-  const int row_base = mt * MF_ROWS;
-  if (nb0 < 0 || W < 0 || nb0 + W > a.num_beams) {  // beam_start is device data: never trust it
-    if (threadIdx.x == 0 && mt == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
-    return;
+  const int G = a.Hq / a.Hkv;
+  const int nb0 = a.beam_start[r];  // prefill: first query token of the request
+  int W, TG, rows_r, ctx = 0;
+  if constexpr (PREFILL) {
+    const int ql = a.beam_start[r + 1] - nb0;
+    const int seq = a.prefix_len[r];
+    ctx = seq - ql;  // keys before the request's first query token
+    if (nb0 < 0 || ql < 0 || nb0 + ql > a.num_beams || ql > a.T || ctx < 0 ||
+        seq > a.prefix_bt_stride * a.bs) {
+      if (threadIdx.x == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+      return;
+    }
+    W = 1;
+    TG = G;
+    rows_r = ql * G;
+  } else {
+    W = a.beam_start[r + 1] - nb0;
+    TG = a.T * G;
+    rows_r = W * TG;
+    if (nb0 < 0 || W < 0 || nb0 + W > a.num_beams) {  // beam_start is device data: never trust it
+      if (threadIdx.x == 0 && mt == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+      return;
+    }
   }
+  const int row_base = mt * MF_ROWS;
   if (row_base >= rows_r) return;
 
   const int tid = threadIdx.x;
@@ -363,11 +388,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // ---- Q fragments (B operand of S^T): this lane's query row ----
   const int my_rho = row_base + rg * 32 + lrow;
   const bool row_ok = my_rho < rows_r;
-  const int my_b = my_rho / TG, my_qi = (my_rho / G) % a.T, my_g = my_rho % G;
+  const int my_b = PREFILL ? 0 : my_rho / TG;
+  const int my_qi = PREFILL ? my_rho / G : (my_rho / G) % a.T, my_g = my_rho % G;
+  const int64_t my_tok = PREFILL ? (int64_t)(nb0 + my_qi) : (int64_t)((nb0 + my_b) * a.T + my_qi);
   u32x4_t qf[8];
   {
-    const S* src = qp + (int64_t)((nb0 + my_b) * a.T + my_qi) * a.q_tok_stride +
-                   (int64_t)(hk * G + my_g) * HD + lhalf * 8;
+    const S* src = qp + my_tok * a.q_tok_stride + (int64_t)(hk * G + my_g) * HD + lhalf * 8;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
       qf[kk] = row_ok ? *reinterpret_cast<const u32x4_t*>(src + kk * 16) : u32x4_t{0, 0, 0, 0};
@@ -386,7 +412,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // positions, first block ids) -- so the set-up costs one memory round trip.
   const int pre_cap = a.prefix_bt_stride * a.bs;
   const int32_t* pbt = a.prefix_bt + (int64_t)r * a.prefix_bt_stride;
-  int P = a.prefix_len[r];
+  // prefill: the workgroup reads keys up to its last query token's
+  int P = PREFILL ? ctx + (min(row_base + MF_ROWS, rows_r) - 1) / G + 1 : a.prefix_len[r];
   constexpr int WIN_PER_THREAD = PBT_WIN / MF_THREADS;
   static_assert(PBT_WIN % MF_THREADS == 0, "window split");
   int raw_blk[WIN_PER_THREAD];
@@ -400,7 +427,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   const int suf_cap = a.suffix_bt_stride * a.bs;
   const int rlo = row_base + rg * 32;
   const int b_lo = rlo / TG;
-  const int nbeams = rlo < rows_r ? min((rlo + 31) / TG, W - 1) - b_lo + 1 : 0;  // <= 32
+  const int nbeams = !PREFILL && rlo < rows_r ? min((rlo + 31) / TG, W - 1) - b_lo + 1 : 0;  // <= 32
   const bool meta_lane = ks == 0 && lane < nbeams;
   int sL = 0, sS0 = 0, sBlk[SB_STAGE];
   {
@@ -413,7 +440,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     for (int j = 0; j < SB_STAGE; ++j)
       sBlk[j] = meta_lane && j < a.suffix_bt_stride ? a.suffix_bt[(int64_t)n * a.suffix_bt_stride + j] : -1;
   }
-  const int my_len = row_ok ? a.suffix_len[nb0 + my_b] : 0;  // this lane's beam (causal limit)
+  const int my_len = !PREFILL && row_ok ? a.suffix_len[nb0 + my_b] : 0;  // this lane's beam (causal limit)
   // Retire every prologue load (Q included) here: the main loop's first read
   // of qf is otherwise preceded by a full vector-memory wait in every
   // iteration, which also waits for the tile prefetch issued at its top.
@@ -577,15 +604,54 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   };
   f32x16_t s_alt;
   int it = 0;
-  for (; it + 2 < n_st; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
-    prefix_step(it, s_cur, s_alt);
-    prefix_step(it + 1, s_alt, s_cur);
-  }
-  if (it + 1 < n_st) {
-    prefix_step(it, s_cur, s_alt);
-    last_step(it + 1, s_alt);
-  } else if (it < n_st) {
-    last_step(it, s_cur);
+  if constexpr (PREFILL) {
+    // tiles below the workgroup's first query token's position are visible to
+    // every row: pipelined steps; the rest (the causal edge, at most three
+    // tiles for 128 rows) step one at a time with a per-row mask
+    const int n_pipe = min((ctx + row_base / G + 1) / ST_KEYS, n_st - 1);
+    const int lim = row_ok ? ctx + my_qi : -1;  // last key this lane's row sees
+    for (; it + 2 <= n_pipe; it += 2) {
+      prefix_step(it, s_cur, s_alt);
+      prefix_step(it + 1, s_alt, s_cur);
+    }
+    if (it < n_pipe) {
+      prefix_step(it, s_cur, s_alt);
+      s_cur = s_alt;
+      ++it;
+    }
+    for (; it < n_st; ++it) {
+      const bool fetch = it + 2 < n_st;
+      if (fetch) {
+        load_prefix((it + 2) * ST_KEYS, pf_blk);
+        if (it + 3 < n_st) {
+          ensure_window((it + 3) * ST_KEYS);
+          pf_blk = read_blk((it + 3) * ST_KEYS);
+        }
+      }
+      uint32_t v = 0;
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr)
+        v |= (it * ST_KEYS + ks * 32 + 16 * (rr >> 3) + 8 * lhalf + (rr & 7) <= lim ? 1u : 0u) << rr;
+      const uint32_t vis[1] = {v};
+      const f32x16_t s1[1] = {s_cur};
+      u32x4_t pw[1][2];
+      weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o);
+      pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
+      if (it + 1 < n_st) s_cur = qk_half<DT>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf);
+      if (fetch) store_tile(lds + ((it + 2) % NBUF) * BUF);
+      __syncthreads();
+    }
+  } else {
+    for (; it + 2 < n_st; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
+      prefix_step(it, s_cur, s_alt);
+      prefix_step(it + 1, s_alt, s_cur);
+    }
+    if (it + 1 < n_st) {
+      prefix_step(it, s_cur, s_alt);
+      last_step(it + 1, s_alt);
+    } else if (it < n_st) {
+      last_step(it, s_cur);
+    }
   }
 
   // ---- suffix: each row group's beams' own tokens, masked 32-key tiles ----
@@ -690,7 +756,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const float lrow_sum = pair_sum(l0 * a0 + l1 * a1);
     const float inv = lrow_sum > 0.f ? 1.f / lrow_sum : 0.f;
     if (row_ok) {
-      const int64_t tok = (int64_t)(nb0 + my_b) * a.T + my_qi;
+      const int64_t tok = PREFILL ? (int64_t)(nb0 + my_qi) : (int64_t)(nb0 + my_b) * a.T + my_qi;
       S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + my_g) * HD + 4 * lhalf;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
@@ -730,24 +796,29 @@ bool mfma_decode_supported(const DecodeArgs& a) {
   return true;
 }
 
-gr_status_t launch_mfma_decode(const DecodeArgs& a, hipStream_t stream) {
+template <bool PREFILL>
+static gr_status_t launch_mfma(const DecodeArgs& a, hipStream_t stream) {
   const int G = a.Hq / a.Hkv;
-  const int64_t rows = (int64_t)a.max_beams * a.T * G;
-  const int mtiles = (int)((rows + MF_ROWS - 1) / MF_ROWS);
+  const int64_t rows = (int64_t)(PREFILL ? 1 : a.max_beams) * a.T * G;
+  const int64_t mt64 = (rows + MF_ROWS - 1) / MF_ROWS;
   const int units = a.num_reqs * a.Hkv;
-  if (mtiles == 0 || units == 0) return GR_OK;
-  const int64_t nwg = (int64_t)((units + 7) / 8) * 8 * mtiles;
+  if (mt64 == 0 || units == 0) return GR_OK;
+  const int64_t nwg = (int64_t)((units + 7) / 8) * 8 * mt64;
   if (nwg > 0x7fffffff) return GR_ERR_INVALID_ARG;
+  const int mtiles = (int)mt64;
   dim3 grid((unsigned)nwg);
   const bool cap = a.softcap > 0.f;
   if (a.dtype == GR_DTYPE_BF16) {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
   } else {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
   }
   return launch_status();
 }
+
+gr_status_t launch_mfma_decode(const DecodeArgs& a, hipStream_t stream) { return launch_mfma<false>(a, stream); }
+gr_status_t launch_mfma_prefill(const DecodeArgs& a, hipStream_t stream) { return launch_mfma<true>(a, stream); }
 
 }  // namespace gr

@@ -50,6 +50,15 @@ SIGNATURES = {
         _I, _I, _I, _I, _I,             # Hq, Hkv, head_dim, block_size, dtype
         _F, _F, _P, _P, _P,             # scale, softcap, lse_out, dev_status, stream
     ]),
+    "gr_paged_attn_prefill": (_I, [
+        _P, _L, _P, _L,                 # out, out_tok_stride, q, q_tok_stride
+        _P, _P, _L,                     # k_cache, v_cache, num_blocks
+        _L, _L, _L,                     # kv block/tok/head strides
+        _P, _I, _P, _P,                 # block_table, bt_stride, query_start, seq_len
+        _I, _I, _I,                     # num_reqs, num_tokens, max_query_len
+        _I, _I, _I, _I, _I,             # Hq, Hkv, head_dim, block_size, dtype
+        _F, _F, _P, _P, _P,             # scale, softcap, lse_out, dev_status, stream
+    ]),
     "gr_reshape_and_cache": (_I, [
         _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _I, _I, _I, _I, _P, _P,
     ]),

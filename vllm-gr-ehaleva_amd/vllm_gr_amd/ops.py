@@ -145,6 +145,47 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return out
 
 
+def paged_attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       block_table: torch.Tensor, query_start: torch.Tensor, seq_len: torch.Tensor, *,
+                       max_query_len: int, scale: float, softcap: float = 0.0,
+                       out: torch.Tensor | None = None, lse: torch.Tensor | None = None,
+                       status: torch.Tensor | None = None) -> torch.Tensor:
+    """Varlen causal attention of standard requests over the paged cache; see
+    ``gr_paged_attn_prefill`` in gr_beam.h.  ``q``: ``[num_tokens, Hq, D]``,
+    ``block_table [R, blocks]``, ``query_start [R+1]``, ``seq_len [R]`` int32.
+    ``max_query_len`` must bound every request's query count (it sizes the
+    grid; a request above it is flagged and skipped)."""
+    dev = _need_cuda(q, k_cache, v_cache, block_table, query_start, seq_len, out, lse, status)
+    if q.dim() != 3 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
+        raise ValueError("q must be [tokens, Hq, D] with heads and dims contiguous")
+    for name, t in (("block_table", block_table), ("query_start", query_start), ("seq_len", seq_len)):
+        _need_i32(name, t)
+    if q.dtype != k_cache.dtype:
+        raise ValueError("q and KV cache dtype must match")
+    NT, Hq, D = q.shape
+    NB, bs, Hkv, Dk = k_cache.shape
+    if Dk != D:
+        raise ValueError("head_dim mismatch between q and KV cache")
+    R = seq_len.numel()
+    if block_table.dim() != 2 or block_table.shape[0] != R or query_start.numel() != R + 1:
+        raise ValueError("block_table must be [R, blocks] and query_start [R+1]")
+    bstr, tstr, hstr = _cache_strides(k_cache, v_cache)
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 or out.stride(1) != D:
+        raise ValueError("out must match q's shape/dtype with heads and dims contiguous")
+    if lse is not None and (lse.shape != (NT, Hq) or lse.dtype != torch.float32 or not lse.is_contiguous()):
+        raise ValueError("lse must be a contiguous float32 [tokens, Hq] tensor")
+    code = _C.lib().gr_paged_attn_prefill(
+        out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), NB, bstr, tstr, hstr,
+        block_table.data_ptr(), block_table.shape[1], query_start.data_ptr(), seq_len.data_ptr(),
+        R, NT, int(max_query_len), Hq, Hkv, D, bs, _dtype_code(q), float(scale), float(softcap or 0.0),
+        _ptr(lse), _ptr(status), _stream(dev))
+    _C.check("gr_paged_attn_prefill", code)
+    return out
+
+
 def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
                       v_cache: torch.Tensor, slot_mapping: torch.Tensor,
                       status: torch.Tensor | None = None) -> None:

@@ -25,10 +25,11 @@ Kept from the reference (same names, argument meaning and error behaviour):
 
 What differs, by design: a mega-decode request's beams attend their resident
 suffix (one new query token per beam) instead of recomputing W*t tokens, and
-the whole step is one ``gr_beam_attn_decode`` launch per query-length group
-(no prefix/suffix/merge passes, beam_attn.py:629-701).  A standard request is
-the one-beam case of the same kernel: prefix = its cached tokens, suffix =
-its new tokens in its own block-table row (bottom-right causal).
+the mega requests of a batch are one ``gr_beam_attn_decode`` launch (no
+prefix/suffix/merge passes, beam_attn.py:656-701).  The standard requests
+(prefill chunks, plain decodes) are one ``gr_paged_attn_prefill`` launch:
+varlen causal attention over their block-table rows, the
+``flash_attn_varlen_func`` call of the standard path (:643-654).
 """
 
 from __future__ import annotations
@@ -91,6 +92,20 @@ class DecodeGroup:
 
 
 @dataclass
+class PrefillGroup:
+    """One ``gr_paged_attn_prefill`` launch over the standard requests:
+    request i's queries are rows ``query_start[i] .. query_start[i+1]-1`` of
+    the gathered query (``token_index`` maps them to batch positions; None
+    when they are the batch's tokens in order) and it sees ``seq_len[i]``
+    keys of ``block_table`` row i, causally."""
+    token_index: torch.Tensor | None
+    block_table: torch.Tensor
+    query_start: torch.Tensor
+    seq_len: torch.Tensor
+    max_query_len: int
+
+
+@dataclass
 class BeamAttentionMetadata:
     num_actual_tokens: int
     max_query_len: int
@@ -101,6 +116,7 @@ class BeamAttentionMetadata:
     slot_mapping: torch.Tensor
     causal: bool = True
     groups: list[DecodeGroup] = field(default_factory=list)
+    prefill: PrefillGroup | None = None
     mega_req_idxs: list[int] = field(default_factory=list)
     std_req_idxs: list[int] = field(default_factory=list)
 
@@ -179,33 +195,40 @@ class BeamAttentionMetadataBuilder:
                 slot_mapping[q0:q1] = s
             groups.append(self._group(rows, m.num_actual_tokens, pbt, plen, widths, sbt, slen, None, 1))
 
-        # ---- standard requests: the one-beam case, grouped by query length
-        by_len: dict[int, list[int]] = {}
-        for i, _ in std:
-            ql = q_starts[i + 1] - q_starts[i]
-            if ql > 0:
-                by_len.setdefault(ql, []).append(i)
-        for ql, reqs in sorted(by_len.items()):
-            rows, pbt, plen, sbt, slen, sstart = [], [], [], [], [], []
-            for i in reqs:
-                q0 = q_starts[i]
-                S = int(seq_lens[i])
-                cached = S - ql
-                nb = max(1, (S + bs - 1) // bs)
-                row = m.block_table_tensor[i, :nb].to(torch.int32)
-                rows.append((q0, q0 + ql))
-                pbt.append(row[None])
-                plen.append(torch.tensor([cached], dtype=torch.int32, device=dev))
-                sbt.append(row[None])
-                slen.append(torch.tensor([ql], dtype=torch.int32, device=dev))
-                sstart.append(torch.tensor([cached], dtype=torch.int32, device=dev))
-            groups.append(self._group(rows, m.num_actual_tokens, pbt, plen, [1] * len(reqs), sbt, slen,
-                                      sstart, ql))
+        # ---- standard requests: one varlen causal launch over their own rows
+        prefill = None
+        reqs = [i for i, _ in std if q_starts[i + 1] > q_starts[i]]
+        if reqs:
+            rows = [(q_starts[i], q_starts[i + 1]) for i in reqs]
+            qlens = [q1 - q0 for q0, q1 in rows]
+            every = reqs == list(range(m.num_reqs))
+            if every:  # the batch's own tensors serve as they are
+                bt, qs, sl = m.block_table_tensor, m.query_start_loc, m.seq_lens
+            else:
+                idx = torch.tensor(reqs, dtype=torch.int64).to(dev)
+                bt = m.block_table_tensor.index_select(0, idx)
+                qs = torch.tensor([0] + qlens, dtype=torch.int64).cumsum(0).to(torch.int32).to(dev)
+                sl = m.seq_lens_cpu.index_select(0, torch.tensor(reqs)).to(torch.int32).to(dev)
+            prefill = PrefillGroup(
+                token_index=self._token_index(rows, m.num_actual_tokens),
+                block_table=bt.to(torch.int32).contiguous(), query_start=qs.to(torch.int32).contiguous(),
+                seq_len=sl.to(torch.int32).contiguous(), max_query_len=max(qlens))
         return BeamAttentionMetadata(
             num_actual_tokens=m.num_actual_tokens, max_query_len=m.max_query_len,
             query_start_loc=m.query_start_loc, max_seq_len=m.max_seq_len, seq_lens=m.seq_lens,
             block_table=m.block_table_tensor, slot_mapping=slot_mapping, causal=m.causal,
-            groups=groups, mega_req_idxs=[i for i, _ in mega], std_req_idxs=[i for i, _ in std])
+            groups=groups, prefill=prefill, mega_req_idxs=[i for i, _ in mega], std_req_idxs=[i for i, _ in std])
+
+    def _token_index(self, rows, ntok) -> torch.Tensor | None:
+        """Batch positions of token ranges ``(q0, q1)``; None when they are
+        the batch's tokens in order."""
+        pos, in_order = 0, True
+        for q0, q1 in rows:
+            in_order &= q0 == pos
+            pos = q1
+        if in_order and pos == ntok:
+            return None
+        return torch.cat([torch.arange(q0, q1) for q0, q1 in rows]).to(self.device)
 
     def _group(self, rows, ntok, pbt, plen, widths, sbt, slen, sstart, T) -> DecodeGroup:
         """``rows``: the group's batch token ranges ``(q0, q1)`` in beam order."""
@@ -214,14 +237,8 @@ class BeamAttentionMetadataBuilder:
         sw = max(t.shape[1] for t in sbt)
         pad = lambda ts, w: torch.cat([torch.nn.functional.pad(t, (0, w - t.shape[1]), value=-1) for t in ts])
         beam_start = torch.tensor([0] + widths, dtype=torch.int64).cumsum(0).to(torch.int32).to(dev)
-        pos, in_order = 0, True
-        for q0, q1 in rows:
-            in_order &= q0 == pos
-            pos = q1
-        in_order &= pos == ntok
-        idx = None if in_order else torch.cat([torch.arange(q0, q1) for q0, q1 in rows]).to(dev)
         return DecodeGroup(
-            token_index=idx, prefix_bt=pad(pbt, pw).contiguous(),
+            token_index=self._token_index(rows, ntok), prefix_bt=pad(pbt, pw).contiguous(),
             prefix_len=torch.cat(plen).contiguous(), beam_start=beam_start,
             suffix_bt=pad(sbt, sw).contiguous(), suffix_len=torch.cat(slen).to(torch.int32).contiguous(),
             suffix_start=None if sstart is None else torch.cat(sstart).contiguous(), q_per_beam=T,
@@ -287,6 +304,15 @@ class BeamAttentionImpl:
                                        max_beams_per_req=g.max_beams, out=out)
             if g.token_index is not None:
                 output.index_copy_(0, g.token_index, res)
+        p = attn_metadata.prefill
+        if p is not None:
+            q = query[:n] if p.token_index is None else query.index_select(0, p.token_index)
+            out = output[:n] if p.token_index is None else None
+            res = ops.paged_attn_prefill(q, k_cache, v_cache, p.block_table, p.query_start, p.seq_len,
+                                         max_query_len=p.max_query_len, scale=self.scale,
+                                         softcap=self.logits_soft_cap, out=out)
+            if p.token_index is not None:
+                output.index_copy_(0, p.token_index, res)
         return output
 
 
