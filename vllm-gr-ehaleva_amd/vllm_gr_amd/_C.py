@@ -1,4 +1,5 @@
-"""ctypes binding of libgr_beam.so (declared in include/gr_beam.h).
+"""ctypes binding of libgr_beam.so (declared in include/gr_beam.h and
+include/gr_decoder.h).
 
 The library is the product: there is no Python or CPU fallback.  Loading
 fails loudly with an ImportError-like RuntimeError when the shared object is
@@ -34,7 +35,7 @@ _L = ctypes.c_int64
 _F = ctypes.c_float
 _SZ = ctypes.c_size_t
 
-# name -> (restype, argtypes); mirrors include/gr_beam.h one to one
+# name -> (restype, argtypes); mirrors include/gr_beam.h and include/gr_decoder.h one to one
 SIGNATURES = {
     "gr_status_string": (ctypes.c_char_p, [_I]),
     "gr_version": (_I, []),
@@ -59,6 +60,15 @@ SIGNATURES = {
         _I, _I, _I, _I, _I,             # Hq, Hkv, head_dim, block_size, dtype
         _F, _F, _P, _P, _P,             # scale, softcap, lse_out, dev_status, stream
     ]),
+    "gr_rms_norm": (_I, [_P, _L, _P, _L, _P, _L, _P, _I, _I, _F, _I, _P]),
+    "gr_qk_norm_rope_cache": (_I, [
+        _P, _L, _P, _L, _P,             # q_out, q_out_stride, qkv, qkv_stride, positions
+        _P, _P, _L, _P, _P,             # cos, sin, table_len, q_norm, k_norm
+        _P, _P, _L, _L, _L, _L,         # k_cache, v_cache, num_blocks, kv strides
+        _P, _I, _I,                     # slot_mapping, block_size, num_tokens
+        _I, _I, _I, _F, _I, _P, _P,     # Hq, Hkv, head_dim, eps, dtype, dev_status, stream
+    ]),
+    "gr_silu_mul": (_I, [_P, _L, _P, _L, _I, _I, _I, _P]),
     "gr_reshape_and_cache": (_I, [
         _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _I, _I, _I, _I, _P, _P,
     ]),

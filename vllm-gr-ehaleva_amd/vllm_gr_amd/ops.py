@@ -1,4 +1,5 @@
-"""torch-tensor entry points over the C ABI (include/gr_beam.h).
+"""torch-tensor entry points over the C ABI (include/gr_beam.h,
+include/gr_decoder.h).
 
 Each function validates shapes/devices on the host, allocates outputs with
 the torch caching allocator when the caller passes none, and launches on
@@ -309,3 +310,103 @@ def beam_prune_topk(logits: torch.Tensor, cum: torch.Tensor, k: int, eos_token_i
         workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(dev))
     _C.check("gr_beam_prune_topk", code)
     return parent, token, score, eos_score
+
+
+# ---- fused decoder stages (include/gr_decoder.h) ---------------------------
+
+
+def _rows(name: str, t: torch.Tensor) -> None:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a [tokens, features] tensor with contiguous features")
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """``out = RMSNorm(x [+ residual]) * weight``; with ``residual`` the sum is
+    also written back into it (vLLM's fused_add_rms_norm).  ``x [T, H]``."""
+    dev = _need_cuda(x, weight, residual, out)
+    _rows("x", x)
+    T, H = x.shape
+    if weight.shape != (H,) or not weight.is_contiguous() or weight.dtype != x.dtype:
+        raise ValueError("weight must be a contiguous [hidden] tensor of x's dtype")
+    if residual is not None:
+        _rows("residual", residual)
+        if residual.shape != x.shape or residual.dtype != x.dtype:
+            raise ValueError("residual must match x")
+    if out is None:
+        out = torch.empty((T, H), dtype=x.dtype, device=x.device)
+    _rows("out", out)
+    if out.shape != x.shape or out.dtype != x.dtype:
+        raise ValueError("out must match x")
+    code = _C.lib().gr_rms_norm(out.data_ptr(), out.stride(0), x.data_ptr(), x.stride(0), _ptr(residual),
+                                0 if residual is None else residual.stride(0), weight.data_ptr(), T, H,
+                                float(eps), _dtype_code(x), _stream(dev))
+    _C.check("gr_rms_norm", code)
+    return out
+
+
+def qk_norm_rope_cache(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                       q_norm: torch.Tensor | None, k_norm: torch.Tensor | None, k_cache: torch.Tensor | None,
+                       v_cache: torch.Tensor | None, slot_mapping: torch.Tensor | None, *, num_q_heads: int,
+                       num_kv_heads: int, head_dim: int, eps: float, q_out: torch.Tensor | None = None,
+                       status: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-head q/k RMSNorm + rotate-half rotary at ``positions`` (int64)
+    with the ``cos``/``sin`` tables ``[max_pos, head_dim/2]`` float32;
+    rotated keys and the values are written to the cache at ``slot_mapping``.
+    ``qkv [T, (Hq + 2 Hkv) * D]``.  Returns the rotated queries ``[T, Hq, D]``."""
+    dev = _need_cuda(qkv, positions, cos, sin, q_norm, k_norm, k_cache, v_cache, slot_mapping, q_out, status)
+    _rows("qkv", qkv)
+    T = qkv.shape[0]
+    Hq, Hkv, D = num_q_heads, num_kv_heads, head_dim
+    if qkv.shape[1] != (Hq + 2 * Hkv) * D:
+        raise ValueError("qkv must hold Hq + 2*Hkv heads of head_dim per token")
+    if positions.dtype != torch.int64 or not positions.is_contiguous() or positions.numel() != T:
+        raise ValueError("positions must be a contiguous int64 [tokens] tensor")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.dim() != 2 or t.shape[1] != D // 2:
+            raise ValueError(f"{name} must be a contiguous float32 [max_pos, head_dim/2] table")
+    if cos.shape != sin.shape:
+        raise ValueError("cos and sin tables differ in shape")
+    for name, t in (("q_norm", q_norm), ("k_norm", k_norm)):
+        if t is not None and (t.shape != (D,) or not t.is_contiguous() or t.dtype != qkv.dtype):
+            raise ValueError(f"{name} must be a contiguous [head_dim] tensor of qkv's dtype")
+    NB = bstr = tstr = hstr = bs = 0
+    if slot_mapping is not None:
+        if slot_mapping.dtype != torch.int64 or not slot_mapping.is_contiguous() or slot_mapping.numel() < T:
+            raise ValueError("slot_mapping must be a contiguous int64 tensor covering the tokens")
+        if k_cache is None or v_cache is None or k_cache.dtype != qkv.dtype:
+            raise ValueError("the KV cache (of qkv's dtype) is needed with a slot mapping")
+        NB, bs, Hc, Dc = k_cache.shape
+        if (Hc, Dc) != (Hkv, D):
+            raise ValueError("KV cache heads / head_dim do not match")
+        bstr, tstr, hstr = _cache_strides(k_cache, v_cache)
+    if q_out is None:
+        q_out = torch.empty((T, Hq, D), dtype=qkv.dtype, device=qkv.device)
+    if q_out.shape != (T, Hq, D) or q_out.dtype != qkv.dtype or q_out.stride(2) != 1 or q_out.stride(1) != D:
+        raise ValueError("q_out must be [tokens, Hq, D] with heads and dims contiguous")
+    code = _C.lib().gr_qk_norm_rope_cache(
+        q_out.data_ptr(), q_out.stride(0), qkv.data_ptr(), qkv.stride(0), positions.data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), cos.shape[0], _ptr(q_norm), _ptr(k_norm),
+        _ptr(k_cache), _ptr(v_cache), NB, bstr, tstr, hstr, _ptr(slot_mapping), bs or 1, T, Hq, Hkv, D,
+        float(eps), _dtype_code(qkv), _ptr(status), _stream(dev))
+    _C.check("gr_qk_norm_rope_cache", code)
+    return q_out
+
+
+def silu_mul(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(x[:, :F]) * x[:, F:]`` for ``x [T, 2F]`` (vLLM's silu_and_mul)."""
+    dev = _need_cuda(x, out)
+    _rows("x", x)
+    T, F2 = x.shape
+    if F2 % 2:
+        raise ValueError("x must hold gate and up halves")
+    F = F2 // 2
+    if out is None:
+        out = torch.empty((T, F), dtype=x.dtype, device=x.device)
+    _rows("out", out)
+    if out.shape != (T, F) or out.dtype != x.dtype:
+        raise ValueError("out must be [tokens, F] of x's dtype")
+    code = _C.lib().gr_silu_mul(out.data_ptr(), out.stride(0), x.data_ptr(), x.stride(0), T, F,
+                                _dtype_code(x), _stream(dev))
+    _C.check("gr_silu_mul", code)
+    return out

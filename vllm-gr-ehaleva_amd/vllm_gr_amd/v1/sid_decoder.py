@@ -14,11 +14,13 @@ from N(0, std) -- there are no checkpoints here:
   residual add;
 * final RMSNorm; logits = lm_head rows in float32.
 
-GEMMs are ``torch.nn.functional.linear`` (hipBLASLt on ROCm).  Attention --
-K/V append through the slot mapping, then shared-prefix + resident-suffix
-decode -- is :class:`BeamAttentionImpl.forward`, the same call vLLM's
-Attention layer makes (beam_attn.py:703-755).  Positions follow the
-reference's rule (a beam's j-th suffix token sits at prefix_len + j,
+GEMMs are ``torch.nn.functional.linear`` (hipBLASLt on ROCm).  The
+elementwise stages are fused HIP kernels (include/gr_decoder.h): residual add
++ RMSNorm, per-head q/k RMSNorm + rotary + K/V cache write through the slot
+mapping, and the SiLU-gated product.  Attention is
+:class:`BeamAttentionImpl.forward`, the call vLLM's Attention layer makes
+(beam_attn.py:703-755), with the K/V already written (key/value None).
+Positions follow the reference's rule (a beam's j-th suffix token sits at prefix_len + j,
 engine_core_patch.py:362-365); logits are taken for one row per beam, the
 beam's newest token (:367-369).
 """
@@ -31,6 +33,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from .. import ops
 from .attention.backends.beam_attn import BeamAttentionImpl
 
 
@@ -100,16 +103,10 @@ def init_weights(cfg: DecoderConfig, seed: int, device="cpu") -> dict[str, torch
     return w
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """RMSNorm over the last dim in float32, rounded once to x's dtype."""
-    xf = x.float()
-    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return (y * weight.float()).to(x.dtype)
-
-
 class RotaryEmbedding:
-    """Rotate-half rotary embedding: pair (i, i + D/2) turns by
-    ``pos * theta^(-2i/D)``; cos/sin in float32 from a cached table."""
+    """Tables of the rotate-half rotary embedding: pair (i, i + D/2) turns by
+    ``pos * theta^(-2i/D)``; cos/sin ``[max_pos, D/2]`` evaluated in float64
+    and stored as float32 on the device (read by gr_qk_norm_rope_cache)."""
 
     def __init__(self, head_dim: int, theta: float, max_pos: int, device):
         half = head_dim // 2
@@ -119,15 +116,6 @@ class RotaryEmbedding:
         self.sin = ang.sin().float().to(device)
         self.max_pos = max_pos
 
-    def __call__(self, positions: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-        """x [T, heads, D] -> rotated, same dtype."""
-        half = x.shape[-1] // 2
-        c = self.cos[positions][:, None]
-        s = self.sin[positions][:, None]
-        xf = x.float()
-        x1, x2 = xf[..., :half], xf[..., half:]
-        return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
-
 
 class SidDecoder:
     """The decoder's forward over a flat batch of tokens.
@@ -135,11 +123,11 @@ class SidDecoder:
     ``forward(input_ids, positions, attn_metadata, kv_caches)`` runs every
     layer; ``kv_caches[i]`` is layer i's ``[2, num_blocks, block_size, Hkv,
     D]`` cache and ``attn_metadata`` the backend metadata of the batch (its
-    slot mapping says where each token's K/V is written).  Positions must lie
-    below ``max_position`` (the caller checks; the rotary table is indexed on
-    the device without a bounds check).  Returns the final
-    normalised hidden states ``[T, hidden]``; :meth:`compute_logits` maps
-    selected rows to float32 logits."""
+    slot mapping says where each token's K/V is written).  Positions lie
+    below ``max_position`` (the rotary table's length; the kernel flags and
+    skips a token beyond it).  Returns the final normalised hidden states
+    ``[T, hidden]``; :meth:`compute_logits` maps selected rows to float32
+    logits."""
 
     def __init__(self, cfg: DecoderConfig, weights: dict[str, torch.Tensor], *, max_position: int = 32768):
         self.cfg = cfg
@@ -155,33 +143,29 @@ class SidDecoder:
     def device(self) -> torch.device:
         return self.w["embed"].device
 
-    def _attention(self, i: int, x: torch.Tensor, positions: torch.Tensor, attn_metadata,
-                   kv_cache: torch.Tensor) -> torch.Tensor:
-        cfg, p = self.cfg, f"layers.{i}."
-        T = x.shape[0]
-        qkv = F.linear(x, self.w[p + "qkv"])
-        q, k, v = qkv.split([cfg.q_size, cfg.kv_size, cfg.kv_size], dim=-1)
-        q = rms_norm(q.view(T, cfg.num_heads, cfg.head_dim), self.w[p + "q_norm"], cfg.rms_eps)
-        k = rms_norm(k.view(T, cfg.num_kv_heads, cfg.head_dim), self.w[p + "k_norm"], cfg.rms_eps)
-        q = self.rope(positions, q)
-        k = self.rope(positions, k)
-        v = v.reshape(T, cfg.num_kv_heads, cfg.head_dim)
-        out = torch.empty_like(q)
-        self.attn[i].forward(None, q, k, v, kv_cache, attn_metadata, output=out)
-        return F.linear(out.view(T, cfg.q_size), self.w[p + "o"])
-
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, attn_metadata,
                 kv_caches) -> torch.Tensor:
-        cfg = self.cfg
-        h = self.w["embed"][input_ids]
+        cfg, w, eps = self.cfg, self.w, self.cfg.rms_eps
+        T = input_ids.shape[0]
+        slots = attn_metadata.slot_mapping if attn_metadata is not None else None
+        h = w["embed"][input_ids]  # the residual stream
+        x = ops.rms_norm(h, w["layers.0.input_norm"], eps)
+        mlp = None
         for i in range(cfg.num_layers):
             p = f"layers.{i}."
-            h = h + self._attention(i, rms_norm(h, self.w[p + "input_norm"], cfg.rms_eps), positions,
-                                    attn_metadata, kv_caches[i])
-            x = rms_norm(h, self.w[p + "post_norm"], cfg.rms_eps)
-            gate, up = F.linear(x, self.w[p + "gate_up"]).chunk(2, dim=-1)
-            h = h + F.linear(F.silu(gate) * up, self.w[p + "down"])
-        return rms_norm(h, self.w["final_norm"], cfg.rms_eps)
+            if i:
+                x = ops.rms_norm(mlp, w[p + "input_norm"], eps, residual=h, out=x)
+            qkv = F.linear(x, w[p + "qkv"])
+            k_cache, v_cache = ops.split_kv_cache(kv_caches[i])
+            q = ops.qk_norm_rope_cache(qkv, positions, self.rope.cos, self.rope.sin, w[p + "q_norm"],
+                                       w[p + "k_norm"], k_cache, v_cache, slots, num_q_heads=cfg.num_heads,
+                                       num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, eps=eps)
+            attn = torch.empty_like(q)
+            self.attn[i].forward(None, q, None, None, kv_caches[i], attn_metadata, output=attn)
+            x = ops.rms_norm(F.linear(attn.view(T, cfg.q_size), w[p + "o"]), w[p + "post_norm"], eps,
+                             residual=h, out=x)
+            mlp = F.linear(ops.silu_mul(F.linear(x, w[p + "gate_up"])), w[p + "down"])
+        return ops.rms_norm(mlp, w["final_norm"], eps, residual=h)
 
     def compute_logits(self, hidden: torch.Tensor) -> torch.Tensor:
         return F.linear(hidden, self.w["lm_head"]).float()
