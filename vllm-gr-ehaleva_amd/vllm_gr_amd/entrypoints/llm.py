@@ -146,6 +146,12 @@ class LLM:
         blocks: list[int] = []
         try:
             if steps > 0:
+                sbt = None
+                if steps > 1:  # the beams' suffix blocks (host-to-device copy before any kernel)
+                    per_beam = -(-(steps - 1) // bs)
+                    sblocks = self.runner.pool.allocate(R * W * per_beam)
+                    blocks += sblocks
+                    sbt = torch.tensor(sblocks, dtype=torch.int32).view(R * W, per_beam).to(dev)
                 logits, prefix_bt, prefix_len, pblocks = self.runner.prefill(toks, rids)
                 blocks += [b for bl in pblocks for b in bl]
                 ev.append(torch.cuda.Event(enable_timing=True))
@@ -155,13 +161,7 @@ class LLM:
                 finished.append((res.eos_score, torch.empty(R, 1, 0, dtype=torch.int32, device=dev)))
                 hist = res.token[..., None]
                 score = res.score
-                table = None
-                if steps > 1:
-                    per_beam = -(-(steps - 1) // bs)
-                    sblocks = self.runner.pool.allocate(R * W * per_beam)
-                    blocks += sblocks
-                    sbt = torch.tensor(sblocks, dtype=torch.int32).view(R * W, per_beam).to(dev)
-                    table = BeamKVTable(prefix_bt, prefix_len, W, sbt, block_size=bs)
+                table = None if sbt is None else BeamKVTable(prefix_bt, prefix_len, W, sbt, block_size=bs)
                 for s in range(1, steps):
                     tok = res.token.clamp(min=0).view(-1).to(torch.int64)
                     logits = self.runner.decode(table, tok, rids, lens, step=s - 1)

@@ -190,10 +190,19 @@ class BeamAttentionMetadataBuilder:
                 slen.append(table.attention_suffix_len())
                 widths.extend([W] * table.num_reqs)
                 slots.append((q0, q1, table.slot_mapping()))
-            slot_mapping = slot_mapping.clone()
-            for q0, q1, s in slots:
-                slot_mapping[q0:q1] = s
-            groups.append(self._group(rows, m.num_actual_tokens, pbt, plen, widths, sbt, slen, None, 1))
+            if len(runs) == 1 and rows[0] == (0, m.num_actual_tokens):
+                # one table covering the batch: its tensors as they are (no host copies)
+                slot_mapping = slots[0][2]
+                table = runs[0][0]
+                groups.append(DecodeGroup(
+                    token_index=None, prefix_bt=table.prefix_bt, prefix_len=table.prefix_len,
+                    beam_start=table.beam_start, suffix_bt=table.suffix_bt, suffix_len=slen[0],
+                    suffix_start=None, q_per_beam=1, max_beams=table.beam_width))
+            else:
+                slot_mapping = slot_mapping.clone()
+                for q0, q1, s in slots:
+                    slot_mapping[q0:q1] = s
+                groups.append(self._group(rows, m.num_actual_tokens, pbt, plen, widths, sbt, slen, None, 1))
 
         # ---- standard requests: one varlen causal launch over their own rows
         prefill = None

@@ -2,10 +2,12 @@
 per-forward backend metadata and the decoder's forward.
 
 It plays the part of vLLM's GPU model runner for one batch of beam-search
-requests: the prompts go through the backend's standard path once (a
-standard request is the one-beam case of the decode kernel, its new tokens
-its own suffix), then every step runs one query token per beam through the
-mega-decode path over the batch's :class:`BeamKVTable`.  The side channel is
+requests: the prompts go through the backend's standard path once (varlen
+causal attention, gr_paged_attn_prefill), then every step runs one query
+token per beam through the mega-decode path over the batch's
+:class:`BeamKVTable`.  Host-to-device copies are issued before the forward
+they feed (a copy from pageable host memory waits for the stream), so a
+whole batch is enqueued without a host round trip.  The side channel is
 the reference's ``MEGA_DATA_VAR`` (engine_core_patch.py:544-554) with the
 ``beam_kv`` key the backend adds.
 """
@@ -114,10 +116,11 @@ class SidModelRunner:
             num_reqs=R, num_actual_tokens=int(qsl[-1]), max_query_len=max(lens), max_seq_len=max(lens),
             block_table_tensor=bt.to(dev), slot_mapping=slots.to(dev))
         ids = torch.tensor([t for p in prompts for t in p], dtype=torch.int64).to(dev)
-        hidden = self._forward(ids, pos.to(dev), m, {"mega_data": {}, "req_ids": list(req_ids)})
+        # every host-to-device copy precedes the forward: none waits for it
         last = (qsl[1:].to(torch.int64) - 1).to(dev)
+        hidden = self._forward(ids, pos.to(dev), m, {"mega_data": {}, "req_ids": list(req_ids)})
         logits = self.model.compute_logits(hidden.index_select(0, last))
-        return logits, bt.to(dev), seq.to(dev), blocks
+        return logits, m.block_table_tensor, m.seq_lens, blocks
 
     def decode(self, table: BeamKVTable, tokens: torch.Tensor, req_ids: list[str],
                prompt_lens: list[int], step: int) -> torch.Tensor:
@@ -134,8 +137,11 @@ class SidModelRunner:
             raise ValueError("beam suffix blocks are full")
         qsl = torch.arange(0, N + 1, W, dtype=torch.int32)
         seq = torch.tensor([p + step + 1 for p in prompt_lens], dtype=torch.int32)
+        # device copies come from device tensors: a host-to-device copy here would
+        # wait for the previous step's kernels
         m = CommonAttentionMetadata(
-            query_start_loc=qsl.to(dev), query_start_loc_cpu=qsl, seq_lens=seq.to(dev), seq_lens_cpu=seq,
+            query_start_loc=table.beam_start, query_start_loc_cpu=qsl,
+            seq_lens=table.prefix_len + (step + 1), seq_lens_cpu=seq,
             num_reqs=R, num_actual_tokens=N, max_query_len=1, max_seq_len=int(seq.max()),
             block_table_tensor=table.prefix_bt, slot_mapping=table.slot_mapping())
         side = {"req_ids": list(req_ids), "mega_data": {
