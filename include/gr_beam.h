@@ -92,6 +92,37 @@ gr_status_t gr_beam_attn_decode(
     float scale, float softcap, float* lse_out, int32_t* dev_status, hipStream_t stream);
 
 /*
+ * gr_beam_attn_decode with a split prefix for small batches.
+ *
+ * Same arguments and results as gr_beam_attn_decode.  When the batch's row
+ * tiles (requests x KV heads x beam rows / 128) would leave the GPU's 256
+ * compute units idle, each tile's prefix is split over several workgroups
+ * that write partial outputs and LSEs to `workspace`, and a second kernel on
+ * the same stream merges them as merge_attn_states does
+ * (beam_attn.py:697-699).  max_prefix_len (host hint, 0 = unknown) keeps at
+ * least 256 prefix keys per split.  workspace: device memory of
+ * gr_beam_attn_decode_workspace_size() bytes (0 = no split: workspace may be
+ * NULL), 256-byte aligned, no initial contents.  Calls that share one
+ * workspace must not overlap (one stream).
+ */
+size_t gr_beam_attn_decode_workspace_size(int num_reqs, int max_beams_per_req, int q_per_beam,
+                                          int num_q_heads, int num_kv_heads, int head_dim,
+                                          int max_prefix_len);
+gr_status_t gr_beam_attn_decode_ws(
+    void* out, int64_t out_tok_stride,
+    const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* prefix_bt, int prefix_bt_stride, const int32_t* prefix_len,
+    const int32_t* beam_start,
+    const int32_t* suffix_bt, int suffix_bt_stride, const int32_t* suffix_len,
+    const int32_t* suffix_start,
+    int num_reqs, int max_beams_per_req, int num_beams, int q_per_beam,
+    int num_q_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
+    float scale, float softcap, float* lse_out, int32_t* dev_status,
+    int max_prefix_len, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
  * Varlen causal attention of the standard (non-beam) requests of a batch --
  * prefill chunks and single-token decodes -- over the paged KV cache.
  *

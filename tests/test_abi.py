@@ -125,3 +125,19 @@ def test_python_wrapper_rejects_host_tensors(built_lib):
         ops.beam_prune_topk(torch.zeros(1, 4, 64), torch.zeros(1, 4), 4)
     with pytest.raises(ValueError):
         ops.split_kv_cache(torch.zeros(3, 2, 2, 2, 8))
+
+
+def test_split_decode_workspace_plan_and_check(built_lib):
+    """The split plan: a 1-request x 128-beam decode splits (workspace > 0), the
+    8-request one fills the GPU unsplit (0), and the _ws entry point rejects a
+    missing workspace before any HIP call (pointer values are never used)."""
+    ws = built_lib.gr_beam_attn_decode_workspace_size
+    assert ws(1, 128, 1, 32, 8, 128, 2048) > 0
+    assert ws(8, 128, 1, 32, 8, 128, 2048) == 0
+    assert ws(1, 128, 1, 32, 8, 64, 2048) == 0  # generic kernel: no split
+    assert ws(1, 128, 1, 32, 8, 128, 200) == 0  # under 4 tiles per split
+    P = 0x1000  # aligned, non-null, never dereferenced
+    code = built_lib.gr_beam_attn_decode_ws(
+        P, 4096, P, 4096, P, P, 100, 16 * 8 * 128, 8 * 128, 128, P, 128, P, P, P, 1, P, None,
+        1, 128, 128, 1, 32, 8, 128, 16, 2, 0.088, 0.0, None, None, 2048, None, 0, None)
+    assert code == 4  # GR_ERR_WORKSPACE

@@ -23,7 +23,7 @@ def _host(t):
     return t.detach().cpu().to(torch.float64).numpy()
 
 
-def run_gpu(wl, device, kernel="auto"):
+def run_gpu(wl, device, kernel="auto", split=True, max_prefix_len=None):
     d = wl.to(device)
     out = torch.empty_like(d.q)
     lse = torch.empty((d.q.shape[0], d.q.shape[1]), dtype=torch.float32, device=device)
@@ -33,7 +33,7 @@ def run_gpu(wl, device, kernel="auto"):
         ops.beam_attn_decode(d.q, d.k_cache, d.v_cache, d.prefix_bt, d.prefix_len, d.beam_start,
                              d.suffix_bt, d.suffix_len, q_per_beam=d.q_per_beam, scale=d.scale,
                              softcap=d.softcap, max_beams_per_req=d.max_beams, out=out, lse=lse,
-                             status=status)
+                             status=status, split=split, max_prefix_len=max_prefix_len)
         torch.cuda.synchronize()
     finally:
         ops.set_decode_kernel("auto")
@@ -223,3 +223,28 @@ def test_decode_long_suffix(device, kernel):
     out, lse = run_gpu(wl, device, kernel)
     ref, ref_lse = run_oracle(wl)
     _check(out, lse, ref, ref_lse, atol=2e-2)
+
+
+@pytest.mark.parametrize("R,W,P,hint,dtype,softcap", [
+    (1, 128, 2048, 2048, torch.bfloat16, 0.0),   # one request x 128 beams: 8 splits of 4 tiles
+    (1, 128, 2048, 0, torch.bfloat16, 0.0),      # no hint: 8 splits
+    (2, 32, 1000, 1000, torch.float16, 0.0),     # splits of uneven tile counts
+    (1, 16, 100, 0, torch.bfloat16, 0.0),        # 16 splits over 2 tiles: most splits empty
+    (3, 8, 300, 0, torch.bfloat16, 30.0),        # soft cap, 11 splits over 5 tiles
+])
+def test_decode_split_prefix(device, R, W, P, hint, dtype, softcap):
+    """Small batches spread each row tile's prefix over several workgroups and
+    merge the partials by LSE in a second kernel: same result as the oracle
+    and as the unsplit kernel; a repeated call is bit-identical."""
+    from vllm_gr_amd import _C
+    assert _C.lib().gr_beam_attn_decode_workspace_size(R, W, 1, 32, 8, 128, hint) > 0
+    wl = workloads.make_decode(R=R, W=W, P=P, L=(1, 8), Hq=32, Hkv=8, D=128, dtype=dtype, input_scale=1.0,
+                               seed=R * 7 + W, softcap=softcap)
+    print(f"[decode] split R={R} W={W} P={P} hint={hint} {dtype} softcap={softcap}", flush=True)
+    out, lse = run_gpu(wl, device, split=True, max_prefix_len=hint)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, atol=2e-2)
+    whole, whole_lse = run_gpu(wl, device, split=False)
+    assert np.abs(out - whole).max() <= 1e-2 and np.abs(lse - whole_lse).max() <= 1e-4
+    again, again_lse = run_gpu(wl, device, split=True, max_prefix_len=hint)
+    assert np.array_equal(out, again) and np.array_equal(lse, again_lse)

@@ -27,6 +27,11 @@ struct DecodeArgs {
   float scale, softcap;
   float* lse_out;
   int32_t* dev_status;
+  // split prefix (MFMA decode only): nsplit workgroups share each row tile's
+  // prefix; each writes its normalised partial O / LSE, a second kernel merges
+  int nsplit;
+  float* ws_o;    // [tiles * nsplit][128 rows][128] float32
+  float* ws_lse;  // [tiles * nsplit][128 rows] float32 (natural log)
 };
 
 // MFMA path (gr_attn_mfma.hip): bf16/fp16, head_dim 128, 16-byte aligned rows.
@@ -34,6 +39,12 @@ bool mfma_decode_supported(const DecodeArgs& a);
 gr_status_t launch_mfma_decode(const DecodeArgs& a, hipStream_t stream);
 // Varlen causal mode of the same kernel (see gr_paged_attn_prefill).
 gr_status_t launch_mfma_prefill(const DecodeArgs& a, hipStream_t stream);
+// Split-prefix decode (a.nsplit > 1, workspace set): the decode kernel, then
+// the merge of its partials.
+gr_status_t launch_mfma_decode_split(const DecodeArgs& a, hipStream_t stream);
+// Row tiles of the MFMA decode grid and the prefix split it would use.
+void mfma_decode_plan(int num_reqs, int max_beams, int q_per_beam, int Hq, int Hkv, int max_prefix_len,
+                      int* tiles, int* nsplit);
 
 // 0 = choose automatically, 1 = always the generic kernel (testing hook).
 extern int g_decode_kernel_override;

@@ -265,30 +265,35 @@ static gr_status_t launch_generic(const DecodeArgs& a, hipStream_t stream) {
 
 using namespace gr;
 
-extern "C" gr_status_t gr_beam_attn_decode(
-    void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
+// Validates the decode arguments and fills the argument block; GR_OK means
+// "launch" unless *empty is set (nothing to do).
+static gr_status_t decode_args(
+    DecodeArgs& a, bool& empty, void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
     const void* k_cache, const void* v_cache, int64_t num_blocks,
     int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
     const int32_t* prefix_bt, int prefix_bt_stride, const int32_t* prefix_len,
     const int32_t* beam_start, const int32_t* suffix_bt, int suffix_bt_stride,
     const int32_t* suffix_len, const int32_t* suffix_start, int num_reqs, int max_beams_per_req,
     int num_beams, int q_per_beam, int num_q_heads, int num_kv_heads, int head_dim,
-    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
-    hipStream_t stream) {
+    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status) {
+  empty = false;
   if (num_beams < 0 || num_reqs < 0 || q_per_beam < 1 || num_q_heads < 1 || num_kv_heads < 1 ||
       num_q_heads % num_kv_heads != 0 || block_size < 1 || head_dim < 8 || head_dim % 8 != 0 ||
       num_blocks < 0 || prefix_bt_stride < 0 || suffix_bt_stride < 0 || max_beams_per_req < 0 ||
       !dtype_valid(dtype) || !(softcap >= 0.f))
     return GR_ERR_INVALID_ARG;
   if (head_dim > 256) return GR_ERR_UNSUPPORTED;
-  if (num_beams == 0) return GR_OK;
+  if (num_beams == 0) {
+    empty = true;
+    return GR_OK;
+  }
   if (num_reqs == 0 || !out || !q || !k_cache || !v_cache || !prefix_bt || !prefix_len ||
       !beam_start || !suffix_bt || !suffix_len)
     return GR_ERR_INVALID_ARG;
   if (q_tok_stride < (int64_t)num_q_heads * head_dim || out_tok_stride < (int64_t)num_q_heads * head_dim ||
       kv_block_stride < 1 || kv_tok_stride < 1 || kv_head_stride < 1)
     return GR_ERR_INVALID_ARG;
-  DecodeArgs a;
+  a = DecodeArgs{};
   a.out = out; a.out_tok_stride = out_tok_stride;
   a.q = q; a.q_tok_stride = q_tok_stride;
   a.k_cache = k_cache; a.v_cache = v_cache; a.num_blocks = num_blocks;
@@ -301,8 +306,88 @@ extern "C" gr_status_t gr_beam_attn_decode(
   a.Hq = num_q_heads; a.Hkv = num_kv_heads; a.D = head_dim; a.bs = block_size; a.dtype = dtype;
   a.scale = scale; a.softcap = softcap; a.lse_out = lse_out; a.dev_status = dev_status;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  a.nsplit = 1;
+  return GR_OK;
+}
+
+#define GR_DECODE_ARG_NAMES                                                                         \
+  out, out_tok_stride, q, q_tok_stride, k_cache, v_cache, num_blocks, kv_block_stride, kv_tok_stride, \
+      kv_head_stride, prefix_bt, prefix_bt_stride, prefix_len, beam_start, suffix_bt, suffix_bt_stride, \
+      suffix_len, suffix_start, num_reqs, max_beams_per_req, num_beams, q_per_beam, num_q_heads,       \
+      num_kv_heads, head_dim, block_size, dtype, scale, softcap, lse_out, dev_status
+
+extern "C" gr_status_t gr_beam_attn_decode(
+    void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* prefix_bt, int prefix_bt_stride, const int32_t* prefix_len,
+    const int32_t* beam_start, const int32_t* suffix_bt, int suffix_bt_stride,
+    const int32_t* suffix_len, const int32_t* suffix_start, int num_reqs, int max_beams_per_req,
+    int num_beams, int q_per_beam, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
+    hipStream_t stream) {
+  DecodeArgs a;
+  bool empty;
+  const gr_status_t st = decode_args(a, empty, GR_DECODE_ARG_NAMES);
+  if (st != GR_OK || empty) return st;
   if (g_decode_kernel_override == 0 && mfma_decode_supported(a)) return launch_mfma_decode(a, stream);
   return launch_generic<false>(a, stream);
+}
+
+// Workspace layout of the split decode: partial LSEs, then partial outputs
+// (256-byte aligned).
+struct SplitLayout {
+  size_t lse_off, o_off, total;
+};
+static SplitLayout split_layout(int tiles, int nsplit) {
+  SplitLayout l;
+  const size_t slots = (size_t)tiles * nsplit;
+  l.lse_off = 0;
+  l.o_off = (sizeof(float) * slots * 128 + 255) & ~(size_t)255;
+  l.total = l.o_off + sizeof(float) * slots * 128 * 128;
+  return l;
+}
+
+extern "C" size_t gr_beam_attn_decode_workspace_size(int num_reqs, int max_beams_per_req, int q_per_beam,
+                                                     int num_q_heads, int num_kv_heads, int head_dim,
+                                                     int max_prefix_len) {
+  if (num_reqs <= 0 || max_beams_per_req <= 0 || q_per_beam <= 0 || num_kv_heads <= 0 ||
+      num_q_heads % num_kv_heads != 0 || head_dim != 128)
+    return 0;
+  int tiles, nsplit;
+  mfma_decode_plan(num_reqs, max_beams_per_req, q_per_beam, num_q_heads, num_kv_heads, max_prefix_len, &tiles,
+                   &nsplit);
+  return nsplit > 1 ? split_layout(tiles, nsplit).total : 0;
+}
+
+extern "C" gr_status_t gr_beam_attn_decode_ws(
+    void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* prefix_bt, int prefix_bt_stride, const int32_t* prefix_len,
+    const int32_t* beam_start, const int32_t* suffix_bt, int suffix_bt_stride,
+    const int32_t* suffix_len, const int32_t* suffix_start, int num_reqs, int max_beams_per_req,
+    int num_beams, int q_per_beam, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
+    int max_prefix_len, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  DecodeArgs a;
+  bool empty;
+  const gr_status_t st = decode_args(a, empty, GR_DECODE_ARG_NAMES);
+  if (st != GR_OK || empty) return st;
+  if (max_prefix_len < 0) return GR_ERR_INVALID_ARG;
+  if (g_decode_kernel_override != 0 || !mfma_decode_supported(a)) return launch_generic<false>(a, stream);
+  int tiles, nsplit;
+  mfma_decode_plan(num_reqs, max_beams_per_req, q_per_beam, num_q_heads, num_kv_heads, max_prefix_len, &tiles,
+                   &nsplit);
+  if (nsplit <= 1) return launch_mfma_decode(a, stream);
+  const SplitLayout l = split_layout(tiles, nsplit);
+  if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || workspace_bytes < l.total)
+    return GR_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  a.nsplit = nsplit;
+  a.ws_lse = reinterpret_cast<float*>(ws + l.lse_off);
+  a.ws_o = reinterpret_cast<float*>(ws + l.o_off);
+  return launch_mfma_decode_split(a, stream);
 }
 
 extern "C" gr_status_t gr_paged_attn_prefill(

@@ -26,6 +26,8 @@
 // gfx950's transposing LDS read (ds_read_b64_tr_b16): in each 16-lane group,
 // source lane s addresses V[k0 + s/4][d0 + 4*(s%4) .. +3] and lane i receives
 // V[k0 .. k0+3][d0 + i].
+#include <algorithm>
+
 #include "gr_attn_decode.h"
 
 namespace gr {
@@ -328,7 +330,10 @@ __device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_b
 // largest query count; a request's rows are its query tokens x GQA group,
 // query i sees keys 0 .. seq - ql + i, all read through the prefix machinery
 // (fully visible tiles pipelined, the causal edge masked per row), no suffix.
-template <int DT, bool SOFTCAP, bool PREFILL = false>
+// SPLIT: a.nsplit workgroups per row tile, each over a contiguous share of
+// the prefix's 64-key tiles (the last one also takes the suffix), writing its
+// normalised partial O and LSE to the workspace; split_merge combines them.
+template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF];
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
@@ -344,8 +349,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // prefill: tile rank is the slow index and runs last-token-first, so every
   // (request, head)'s longest causal range is dispatched in the first wave
   const int ugroups = (units + 7) >> 3;
-  const int unit = PREFILL ? (local % ugroups) * 8 + xcd : (local / mtiles) * 8 + xcd;
-  const int mt = PREFILL ? mtiles - 1 - local / ugroups : local % mtiles;
+  // split: the splits of a row tile are adjacent in dispatch order, on one XCD
+  const int nsplit = SPLIT ? a.nsplit : 1;
+  const int split = SPLIT ? local % nsplit : 0;
+  const int lt = SPLIT ? local / nsplit : local;
+  const int unit = PREFILL ? (lt % ugroups) * 8 + xcd : (lt / mtiles) * 8 + xcd;
+  const int mt = PREFILL ? mtiles - 1 - lt / ugroups : lt % mtiles;
   if (unit >= units) return;
   const int r = unit / a.Hkv, hk = unit % a.Hkv;
   const int G = a.Hq / a.Hkv;
@@ -450,7 +459,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     if (tid == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
     P = P < 0 ? 0 : pre_cap;
   }
-  const int n_st = (P + ST_KEYS - 1) / ST_KEYS;
+  const int n_all = (P + ST_KEYS - 1) / ST_KEYS;
+  const int ts0 = SPLIT ? (int)((int64_t)split * n_all / nsplit) : 0;  // first tile of this workgroup
+  const int n_st = SPLIT ? (int)((int64_t)(split + 1) * n_all / nsplit) - ts0 : n_all;
+  const int kb = ts0 * ST_KEYS;  // first key of this workgroup's prefix range
   const int bsh = a.bs_shift;
 
   // The request's prefix block-table row is staged in LDS (a window of
@@ -555,19 +567,19 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // t+1, while tile t+2 (loaded into registers at the start of the step) is
   // stored into the third buffer at its end.
   if (n_st > 0) {
-    ensure_window(0);
-    load_prefix(0, read_blk(0));
+    ensure_window(kb);
+    load_prefix(kb, read_blk(kb));
     store_tile(lds);
   }
   if (n_st > 1) {
-    ensure_window(ST_KEYS);
-    load_prefix(ST_KEYS, read_blk(ST_KEYS));
+    ensure_window(kb + ST_KEYS);
+    load_prefix(kb + ST_KEYS, read_blk(kb + ST_KEYS));
     store_tile(lds + BUF);
   }
   int pf_blk = -1;  // block id for the next tile to load (tile it+2 at step it)
   if (n_st > 2) {
-    ensure_window(2 * ST_KEYS);
-    pf_blk = read_blk(2 * ST_KEYS);
+    ensure_window(kb + 2 * ST_KEYS);
+    pf_blk = read_blk(kb + 2 * ST_KEYS);
   }
   __syncthreads();
   f32x16_t s_cur = qk_half<DT>(lds, ks * 32, lane, qf);  // (stale LDS when n_st == 0: never used)
@@ -578,10 +590,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const int cur = it % NBUF, nxt = (it + 1) % NBUF, fill = (it + 2) % NBUF;
     const bool fetch = it + 2 < n_st;
     if (fetch) {
-      load_prefix((it + 2) * ST_KEYS, pf_blk);
+      load_prefix(kb + (it + 2) * ST_KEYS, pf_blk);
       if (it + 3 < n_st) {
-        ensure_window((it + 3) * ST_KEYS);
-        pf_blk = read_blk((it + 3) * ST_KEYS);
+        ensure_window(kb + (it + 3) * ST_KEYS);
+        pf_blk = read_blk(kb + (it + 3) * ST_KEYS);
       }
     }
     pipe_step<DT, SOFTCAP>(lds + cur * BUF, lds + nxt * BUF, ks * 32, lane, qf, s_in, s_out, o, st, c, cap);
@@ -589,7 +601,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     __syncthreads();
   };
   // The last tile: no next tile; masked when only p_last of its keys exist.
-  const int p_last = P - (n_st - 1) * ST_KEYS;  // keys in the last tile (1 .. 64)
+  const int p_last = min(ST_KEYS, P - kb - (n_st - 1) * ST_KEYS);  // keys in the last tile (1 .. 64)
   auto last_step = [&](int it, const f32x16_t& s_in) {
     // register r of lane half lhalf holds tile key ks*32 + 16*(r>>3) + 8*lhalf + (r&7)
     uint32_t v = 0;
@@ -660,7 +672,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   int max_tot = 0;
 #pragma unroll
   for (int g = 0; g < 4; ++g) max_tot = max(max_tot, suf_cum[g][32]);
-  const int n_sit = (max_tot + 31) / 32;
+  const int n_sit = !SPLIT || split == nsplit - 1 ? (max_tot + 31) / 32 : 0;
   for (int it = 0; it < n_sit; ++it) {
     // loader: 4 row groups x 32 slots x 16 chunks; row group g's slots live in
     // buffer g >> 1, rows / columns (g & 1) * 32 .. + 31
@@ -755,7 +767,27 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
     const float lrow_sum = pair_sum(l0 * a0 + l1 * a1);
     const float inv = lrow_sum > 0.f ? 1.f / lrow_sum : 0.f;
-    if (row_ok) {
+    if constexpr (SPLIT) {
+      // this split's normalised partial O and LSE, every row of the tile
+      const int64_t slot = (int64_t)(unit * mtiles + mt) * nsplit + split;
+      float* po = a.ws_o + (slot * MF_ROWS + rg * 32 + lrow) * HD + 4 * lhalf;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          float v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int rr = qd * 4 + u;
+            v[u] = (o[mb][rr] * a0 + xo[(mb * 16 + rr) * 64 + lane] * a1) * inv;
+          }
+          *reinterpret_cast<float4*>(po + mb * 32 + qd * 8) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      }
+      if (lhalf == 0)
+        a.ws_lse[slot * MF_ROWS + rg * 32 + lrow] =
+            lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
+    } else if (row_ok) {
       const int64_t tok = PREFILL ? (int64_t)(nb0 + my_qi) : (int64_t)(nb0 + my_b) * a.T + my_qi;
       S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + my_g) * HD + 4 * lhalf;
 #pragma unroll
@@ -780,6 +812,52 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   }
 }
 
+// Merge of the split decode's partials: one thread per (row, 4 dims), 8 rows
+// of one row tile per workgroup.  LSE* = log sum_s exp(LSE_s), O = sum_s
+// exp(LSE_s - LSE*) O_s (the merge_attn_states rule), written as the final
+// output and LSE.
+constexpr int MG_ROWS = 8;
+template <int DT>
+__global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
+  using S = uint16_t;
+  constexpr int PER_TILE = MF_ROWS / MG_ROWS;
+  const int tile = blockIdx.x / PER_TILE;
+  const int row = (blockIdx.x % PER_TILE) * MG_ROWS + threadIdx.x / (HD / 4);
+  const int d4 = (threadIdx.x % (HD / 4)) * 4;
+  const int unit = tile / mtiles, mt = tile % mtiles;
+  const int r = unit / a.Hkv, hk = unit % a.Hkv;
+  const int nb0 = a.beam_start[r], W = a.beam_start[r + 1] - nb0;
+  if (nb0 < 0 || W < 0 || nb0 + W > a.num_beams) return;  // flagged by the decode kernel
+  const int G = a.Hq / a.Hkv, TG = a.T * G, rows_r = W * TG;
+  const int rho = mt * MF_ROWS + row;
+  if (rho >= rows_r) return;
+  const int nsplit = a.nsplit;
+  const float* lse = a.ws_lse + (int64_t)tile * nsplit * MF_ROWS + row;
+  const float* po = a.ws_o + ((int64_t)tile * nsplit * MF_ROWS + row) * HD + d4;
+  float mx = -INFINITY;
+#pragma unroll 4
+  for (int s2 = 0; s2 < nsplit; ++s2) mx = fmaxf(mx, lse[s2 * MF_ROWS]);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f}, sum = 0.f;
+  if (mx != -INFINITY) {
+#pragma unroll 4
+    for (int s2 = 0; s2 < nsplit; ++s2) {
+      const float w = __expf(lse[s2 * MF_ROWS] - mx);
+      const float4 pv = *reinterpret_cast<const float4*>(po + (int64_t)s2 * MF_ROWS * HD);
+      sum += w;
+      acc[0] += w * pv.x;
+      acc[1] += w * pv.y;
+      acc[2] += w * pv.z;
+      acc[3] += w * pv.w;
+    }
+  }
+  const float inv = sum > 0.f ? 1.f / sum : 0.f;
+  const int b = rho / TG, qi = (rho / G) % a.T, g = rho % G;
+  const int64_t tok = (int64_t)(nb0 + b) * a.T + qi;
+  const u32x2_t wv = {Mma<DT>::pack2(acc[0] * inv, acc[1] * inv), Mma<DT>::pack2(acc[2] * inv, acc[3] * inv)};
+  *reinterpret_cast<u32x2_t*>(static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g) * HD + d4) = wv;
+  if (a.lse_out && d4 == 0) a.lse_out[tok * a.Hq + hk * G + g] = mx == -INFINITY ? -INFINITY : mx + __logf(sum);
+}
+
 }  // namespace
 
 bool mfma_decode_supported(const DecodeArgs& a) {
@@ -796,29 +874,58 @@ bool mfma_decode_supported(const DecodeArgs& a) {
   return true;
 }
 
-template <bool PREFILL>
+template <bool PREFILL, bool SPLIT>
 static gr_status_t launch_mfma(const DecodeArgs& a, hipStream_t stream) {
   const int G = a.Hq / a.Hkv;
   const int64_t rows = (int64_t)(PREFILL ? 1 : a.max_beams) * a.T * G;
   const int64_t mt64 = (rows + MF_ROWS - 1) / MF_ROWS;
   const int units = a.num_reqs * a.Hkv;
   if (mt64 == 0 || units == 0) return GR_OK;
-  const int64_t nwg = (int64_t)((units + 7) / 8) * 8 * mt64;
+  const int64_t nwg = (int64_t)((units + 7) / 8) * 8 * mt64 * (SPLIT ? a.nsplit : 1);
   if (nwg > 0x7fffffff) return GR_ERR_INVALID_ARG;
   const int mtiles = (int)mt64;
   dim3 grid((unsigned)nwg);
   const bool cap = a.softcap > 0.f;
   if (a.dtype == GR_DTYPE_BF16) {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL, SPLIT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL, SPLIT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
   } else {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL, SPLIT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL, SPLIT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
   }
   return launch_status();
 }
 
-gr_status_t launch_mfma_decode(const DecodeArgs& a, hipStream_t stream) { return launch_mfma<false>(a, stream); }
-gr_status_t launch_mfma_prefill(const DecodeArgs& a, hipStream_t stream) { return launch_mfma<true>(a, stream); }
+gr_status_t launch_mfma_decode(const DecodeArgs& a, hipStream_t stream) { return launch_mfma<false, false>(a, stream); }
+gr_status_t launch_mfma_prefill(const DecodeArgs& a, hipStream_t stream) { return launch_mfma<true, false>(a, stream); }
+gr_status_t launch_mfma_decode_split(const DecodeArgs& a, hipStream_t stream) {
+  const gr_status_t st = launch_mfma<false, true>(a, stream);
+  if (st != GR_OK) return st;
+  const int G = a.Hq / a.Hkv;
+  const int mtiles = (int)(((int64_t)a.max_beams * a.T * G + MF_ROWS - 1) / MF_ROWS);
+  const int64_t nwg = (int64_t)a.num_reqs * a.Hkv * mtiles * (MF_ROWS / MG_ROWS);
+  if (nwg == 0) return GR_OK;
+  if (nwg > 0x7fffffff) return GR_ERR_INVALID_ARG;
+  if (a.dtype == GR_DTYPE_BF16)
+    hipLaunchKernelGGL(split_merge<GR_DTYPE_BF16>, dim3((unsigned)nwg), dim3(256), 0, stream, a, mtiles);
+  else
+    hipLaunchKernelGGL(split_merge<GR_DTYPE_F16>, dim3((unsigned)nwg), dim3(256), 0, stream, a, mtiles);
+  return launch_status();
+}
+
+// Enough splits to give the grid ~256 workgroups (one per CU at this kernel's
+// LDS use), at most 16, and no fewer than 4 prefix tiles per split when the
+// longest prefix is known.
+void mfma_decode_plan(int num_reqs, int max_beams, int q_per_beam, int Hq, int Hkv, int max_prefix_len,
+                      int* tiles, int* nsplit) {
+  const int G = Hq / Hkv;
+  const int64_t mtiles = ((int64_t)max_beams * q_per_beam * G + MF_ROWS - 1) / MF_ROWS;
+  const int64_t units = (int64_t)num_reqs * Hkv;
+  const int64_t wg = (units + 7) / 8 * 8 * mtiles;
+  *tiles = (int)(units * mtiles);
+  int ns = wg <= 0 || wg >= 256 ? 1 : (int)((256 + wg - 1) / wg);
+  if (max_prefix_len > 0) ns = std::min(ns, std::max(1, max_prefix_len / (4 * ST_KEYS)));
+  *nsplit = std::min(ns, 16);
+}
 
 }  // namespace gr

@@ -102,18 +102,22 @@ struct RopeArgs {
   int32_t* dev_status;
 };
 
-// Wave w handles heads w, w + 4, ... of the token's Hq query, Hkv key and
-// Hkv value heads; lane l holds the rotary pairs (i, i + D/2), i = l, l + 64.
+// One wave per head: workgroup g covers heads 4*(g % hgroups) .. +3 of token
+// g / hgroups, over the token's Hq query, Hkv key and Hkv value heads (in
+// that order); lane l holds the rotary pairs (i, i + D/2), i = l, l + 64.
 template <int DT>
-__global__ __launch_bounds__(EW_THREADS) void qk_norm_rope_k(RopeArgs a) {
+__global__ __launch_bounds__(EW_THREADS) void qk_norm_rope_k(RopeArgs a, int hgroups) {
   using E = Elem<DT>;
   using S = typename E::storage;
-  const int64_t t = blockIdx.x;
+  const int64_t t = blockIdx.x / hgroups;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = (blockIdx.x % hgroups) * (EW_THREADS / 64) + wave;
+  const int nheads = a.Hq + 2 * a.Hkv;
+  if (h >= nheads) return;
   const int D = a.D, half = D >> 1;
   const int64_t pos = a.positions[t];
   if (pos < 0 || pos >= a.table_len) {
-    if (threadIdx.x == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+    if (h == 0 && lane == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
     return;
   }
   int64_t kv_off = -1;  // element offset of this token's slot in the cache
@@ -123,7 +127,7 @@ __global__ __launch_bounds__(EW_THREADS) void qk_norm_rope_k(RopeArgs a) {
       const int64_t blk = slot / a.bs;
       if (blk < a.num_blocks) {
         kv_off = blk * a.kv_block_stride + (slot % a.bs) * a.kv_tok_stride;
-      } else if (threadIdx.x == 0) {
+      } else if (h == 0 && lane == 0) {
         flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
       }
     }
@@ -131,15 +135,14 @@ __global__ __launch_bounds__(EW_THREADS) void qk_norm_rope_k(RopeArgs a) {
   const S* src = static_cast<const S*>(a.qkv) + t * a.qkv_stride;
   const float* ct = a.cos_t + pos * half;
   const float* st = a.sin_t + pos * half;
-  const int nheads = a.Hq + 2 * a.Hkv;
-  for (int h = wave; h < nheads; h += EW_THREADS / 64) {
+  {
     const S* hp = src + (int64_t)h * D;
     if (h >= a.Hq + a.Hkv) {  // value head: copy into the cache
       if (kv_off >= 0) {
         S* dst = static_cast<S*>(a.v_cache) + kv_off + (int64_t)(h - a.Hq - a.Hkv) * a.kv_head_stride;
         for (int i = lane; i < D; i += 64) dst[i] = hp[i];
       }
-      continue;
+      return;
     }
     const bool is_q = h < a.Hq;
     const S* nw = static_cast<const S*>(is_q ? a.q_norm : a.k_norm);
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(EW_THREADS) void qk_norm_rope_k(RopeArgs a) {
     if (is_q) {
       dst = static_cast<S*>(a.q_out) + t * a.q_out_stride + (int64_t)h * D;
     } else {
-      if (kv_off < 0) continue;
+      if (kv_off < 0) return;
       dst = static_cast<S*>(a.k_cache) + kv_off + (int64_t)(h - a.Hq) * a.kv_head_stride;
     }
 #pragma unroll
@@ -260,11 +263,14 @@ extern "C" gr_status_t gr_qk_norm_rope_cache(
   RopeArgs a{q_out, q_out_stride, qkv, qkv_stride, positions, cos_table, sin_table, table_len,
              q_norm_weight, k_norm_weight, k_cache, v_cache, num_blocks, kv_block_stride, kv_tok_stride,
              kv_head_stride, slot_mapping, block_size, num_q_heads, num_kv_heads, head_dim, eps, dev_status};
-  dim3 grid((unsigned)num_tokens);
+  const int hgroups = (num_q_heads + 2 * num_kv_heads + EW_THREADS / 64 - 1) / (EW_THREADS / 64);
+  const int64_t nwg = (int64_t)num_tokens * hgroups;
+  if (nwg > 0x7fffffff) return GR_ERR_INVALID_ARG;
+  dim3 grid((unsigned)nwg);
   switch (dtype) {
-    case GR_DTYPE_F32: hipLaunchKernelGGL(qk_norm_rope_k<GR_DTYPE_F32>, grid, dim3(EW_THREADS), 0, stream, a); break;
-    case GR_DTYPE_F16: hipLaunchKernelGGL(qk_norm_rope_k<GR_DTYPE_F16>, grid, dim3(EW_THREADS), 0, stream, a); break;
-    default: hipLaunchKernelGGL(qk_norm_rope_k<GR_DTYPE_BF16>, grid, dim3(EW_THREADS), 0, stream, a); break;
+    case GR_DTYPE_F32: hipLaunchKernelGGL(qk_norm_rope_k<GR_DTYPE_F32>, grid, dim3(EW_THREADS), 0, stream, a, hgroups); break;
+    case GR_DTYPE_F16: hipLaunchKernelGGL(qk_norm_rope_k<GR_DTYPE_F16>, grid, dim3(EW_THREADS), 0, stream, a, hgroups); break;
+    default: hipLaunchKernelGGL(qk_norm_rope_k<GR_DTYPE_BF16>, grid, dim3(EW_THREADS), 0, stream, a, hgroups); break;
   }
   return launch_status();
 }

@@ -51,6 +51,12 @@ SIGNATURES = {
         _I, _I, _I, _I, _I,             # Hq, Hkv, head_dim, block_size, dtype
         _F, _F, _P, _P, _P,             # scale, softcap, lse_out, dev_status, stream
     ]),
+    "gr_beam_attn_decode_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I, _I]),
+    "gr_beam_attn_decode_ws": (_I, [
+        _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _P, _P, _P, _I, _P, _P,
+        _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _P,
+        _I, _P, _SZ, _P,                # max_prefix_len, workspace, workspace_bytes, stream
+    ]),
     "gr_paged_attn_prefill": (_I, [
         _P, _L, _P, _L,                 # out, out_tok_stride, q, q_tok_stride
         _P, _P, _L,                     # k_cache, v_cache, num_blocks

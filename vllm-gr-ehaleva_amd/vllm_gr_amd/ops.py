@@ -98,11 +98,15 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                      suffix_start: torch.Tensor | None = None, *, q_per_beam: int = 1,
                      scale: float, softcap: float = 0.0, max_beams_per_req: int | None = None,
                      out: torch.Tensor | None = None, lse: torch.Tensor | None = None,
-                     status: torch.Tensor | None = None) -> torch.Tensor:
-    """BeamAttention decode step; see ``gr_beam_attn_decode`` in gr_beam.h.
+                     status: torch.Tensor | None = None, max_prefix_len: int | None = None,
+                     split: bool = True) -> torch.Tensor:
+    """BeamAttention decode step; see ``gr_beam_attn_decode`` / ``_ws`` in gr_beam.h.
 
     ``q``: ``[num_beams*q_per_beam, Hq, D]`` (token stride free, heads and dims
-    contiguous).  Returns ``out`` (same shape/dtype as ``q``)."""
+    contiguous).  Returns ``out`` (same shape/dtype as ``q``).  With ``split``
+    a small batch spreads each tile's prefix over several workgroups (a
+    per-device workspace is kept for it); ``max_prefix_len`` (host hint) is
+    the longest prefix, 0 or None when unknown."""
     dev = _need_cuda(q, k_cache, v_cache, prefix_bt, prefix_len, beam_start, suffix_bt, suffix_len,
                      suffix_start, out, lse, status)
     if q.dim() != 3 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
@@ -135,15 +139,36 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
         raise ValueError("out must match q's shape/dtype with heads and dims contiguous")
     if lse is not None and (lse.shape != (NT, Hq) or lse.dtype != torch.float32 or not lse.is_contiguous()):
         raise ValueError("lse must be a contiguous float32 [tokens, Hq] tensor")
-    code = _C.lib().gr_beam_attn_decode(
-        out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0),
-        k_cache.data_ptr(), v_cache.data_ptr(), NB, bstr, tstr, hstr,
-        prefix_bt.data_ptr(), prefix_bt.shape[1], prefix_len.data_ptr(), beam_start.data_ptr(),
-        suffix_bt.data_ptr(), suffix_bt.shape[1], suffix_len.data_ptr(), _ptr(suffix_start),
-        R, max_beams_per_req, N, q_per_beam, Hq, Hkv, D, bs, _dtype_code(q),
-        float(scale), float(softcap or 0.0), _ptr(lse), _ptr(status), _stream(dev))
-    _C.check("gr_beam_attn_decode", code)
+    args = (out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0),
+            k_cache.data_ptr(), v_cache.data_ptr(), NB, bstr, tstr, hstr,
+            prefix_bt.data_ptr(), prefix_bt.shape[1], prefix_len.data_ptr(), beam_start.data_ptr(),
+            suffix_bt.data_ptr(), suffix_bt.shape[1], suffix_len.data_ptr(), _ptr(suffix_start),
+            R, max_beams_per_req, N, q_per_beam, Hq, Hkv, D, bs, _dtype_code(q),
+            float(scale), float(softcap or 0.0), _ptr(lse), _ptr(status))
+    hint = int(max_prefix_len or 0)
+    ws_bytes = (_C.lib().gr_beam_attn_decode_workspace_size(R, max_beams_per_req, q_per_beam, Hq, Hkv, D, hint)
+                if split and R else 0)
+    if ws_bytes:
+        ws = _split_workspace(dev, ws_bytes)
+        code = _C.lib().gr_beam_attn_decode_ws(*args, hint, ws.data_ptr(), ws_bytes, _stream(dev))
+        _C.check("gr_beam_attn_decode_ws", code)
+    else:
+        code = _C.lib().gr_beam_attn_decode(*args, _stream(dev))
+        _C.check("gr_beam_attn_decode", code)
     return out
+
+
+_SPLIT_WS: dict = {}
+
+
+def _split_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device workspace of the split decode (partials only, no initial
+    contents); launches on one stream share it in order."""
+    ws = _SPLIT_WS.get(dev)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _SPLIT_WS[dev] = ws
+    return ws
 
 
 def paged_attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,

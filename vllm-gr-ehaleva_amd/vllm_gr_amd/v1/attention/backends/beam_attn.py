@@ -89,6 +89,7 @@ class DecodeGroup:
     suffix_start: torch.Tensor | None
     q_per_beam: int
     max_beams: int
+    max_prefix_len: int = 0  # host hint for the split decode (0 = unknown)
 
 
 @dataclass
@@ -165,6 +166,7 @@ class BeamAttentionMetadataBuilder:
                 else:
                     runs.append((table, [(i, md)]))
             rows, pbt, plen, sbt, slen, widths, slots = [], [], [], [], [], [], []
+            max_prefix = max(int(md["prefix_len"]) for _, md in mega)
             for table, members in runs:
                 W = table.beam_width
                 if len(members) != table.num_reqs:
@@ -197,12 +199,13 @@ class BeamAttentionMetadataBuilder:
                 groups.append(DecodeGroup(
                     token_index=None, prefix_bt=table.prefix_bt, prefix_len=table.prefix_len,
                     beam_start=table.beam_start, suffix_bt=table.suffix_bt, suffix_len=slen[0],
-                    suffix_start=None, q_per_beam=1, max_beams=table.beam_width))
+                    suffix_start=None, q_per_beam=1, max_beams=table.beam_width, max_prefix_len=max_prefix))
             else:
                 slot_mapping = slot_mapping.clone()
                 for q0, q1, s in slots:
                     slot_mapping[q0:q1] = s
                 groups.append(self._group(rows, m.num_actual_tokens, pbt, plen, widths, sbt, slen, None, 1))
+                groups[-1].max_prefix_len = max_prefix
 
         # ---- standard requests: one varlen causal launch over their own rows
         prefill = None
@@ -310,7 +313,7 @@ class BeamAttentionImpl:
             res = ops.beam_attn_decode(q, k_cache, v_cache, g.prefix_bt, g.prefix_len, g.beam_start,
                                        g.suffix_bt, g.suffix_len, g.suffix_start, q_per_beam=g.q_per_beam,
                                        scale=self.scale, softcap=self.logits_soft_cap,
-                                       max_beams_per_req=g.max_beams, out=out)
+                                       max_beams_per_req=g.max_beams, out=out, max_prefix_len=g.max_prefix_len)
             if g.token_index is not None:
                 output.index_copy_(0, g.token_index, res)
         p = attn_metadata.prefill
