@@ -56,7 +56,8 @@ def test_rms_norm(device, dtype, H, with_res):
 
 
 @pytest.mark.parametrize("dtype,D,heads", [(torch.bfloat16, 128, (16, 8)), (torch.float32, 32, (4, 2)),
-                                           (torch.float16, 256, (4, 4)), (torch.bfloat16, 64, (6, 2))])
+                                           (torch.float16, 256, (4, 4)), (torch.bfloat16, 64, (6, 2)),
+                                           (torch.bfloat16, 40, (3, 1))])  # 40: the scalar form
 def test_qk_norm_rope_cache(device, dtype, D, heads):
     Hq, Hkv = heads
     g = torch.Generator().manual_seed(D + Hq)
