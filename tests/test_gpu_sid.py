@@ -120,6 +120,31 @@ def test_sid_beam_search_bf16_mfma_rescored():
             assert abs(cum - s.cum_logprob) < 0.05 * steps, (s.tokens[len(p):], cum, s.cum_logprob)
 
 
+@pytest.mark.parametrize("cfg", [F32, BF16_128], ids=["f32", "bf16_mfma"])
+def test_sid_graph_replays_match_eager(cfg):
+    """Decode steps replayed from captured graphs give the eager run's beams
+    and scores; several replays, with eager batches and host syncs between
+    them, all agree."""
+    seed, lens, W, steps = 7, [19, 44], 8, 4
+    w = init_weights(cfg, seed)
+    prompts = _prompts(seed, lens, cfg.vocab)
+    nb = blocks_needed(len(lens), max(lens), W, steps, 16) + 8
+    wd = {k: v.cuda() for k, v in w.items()}
+    eager = LLM(cfg, weights=wd, num_blocks=nb, use_graphs=False)
+    graphed = LLM(cfg, weights=wd, num_blocks=nb, use_graphs=True)
+    params = BeamSearchParams(W, steps)
+    ref = eager.beam_search(prompts, params)
+    for i in range(3):
+        got = graphed.beam_search(prompts, params)  # first call captures, later ones replay
+        torch.cuda.synchronize()
+        for o, r in zip(got, ref):
+            assert [s.tokens for s in o.sequences] == [s.tokens for s in r.sequences], i
+            assert np.allclose([s.cum_logprob for s in o.sequences], [s.cum_logprob for s in r.sequences],
+                               rtol=0, atol=1e-5), i
+        eager.beam_search(prompts, params)
+    assert len(graphed.runner._graphs) == 1
+
+
 def test_sid_beam_search_full_size_self_consistent():
     """4 x 2048-token prompts, 128 beams, 3 SID tokens through the 28-layer
     decoder; two returned beams per request rescored by prefilling their

@@ -80,12 +80,13 @@ class LLM:
     ``weights`` (from :func:`init_weights`) default to ``init_weights(cfg,
     seed, device)``.  ``num_blocks`` KV-cache blocks of ``block_size``
     tokens are allocated per layer up front; a batch needs
-    :func:`~vllm_gr_amd.v1.sid_runner.blocks_needed` of them."""
+    :func:`~vllm_gr_amd.v1.sid_runner.blocks_needed` of them.  With
+    ``use_graphs`` each decode step shape is captured once and replayed."""
 
     def __init__(self, cfg: DecoderConfig = SID_DECODER_1P7B, *, seed: int = 0, device="cuda",
                  num_blocks: int = 4096, block_size: int = 16, eos_token_id: int | None = None,
                  special_tokens: dict[str, int] | None = None, weights: dict | None = None,
-                 max_position: int = 32768):
+                 max_position: int = 32768, use_graphs: bool = True):
         dev = torch.device(device)
         if dev.type != "cuda":
             raise ValueError("the beam path runs on a HIP device (torch 'cuda')")
@@ -93,7 +94,7 @@ class LLM:
             weights = init_weights(cfg, seed, dev)
         self.cfg = cfg
         self.model = SidDecoder(cfg, weights, max_position=max_position)
-        self.runner = SidModelRunner(self.model, num_blocks, block_size)
+        self.runner = SidModelRunner(self.model, num_blocks, block_size, use_graphs=use_graphs)
         self.eos_token_id = eos_token_id
         self.special_tokens = dict(special_tokens or {})
         self.last_times = StepTimes()

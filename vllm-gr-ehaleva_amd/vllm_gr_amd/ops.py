@@ -159,13 +159,17 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
 
 
 _SPLIT_WS: dict = {}
+_SPLIT_WS_RETIRED: list = []
 
 
 def _split_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     """Per-device workspace of the split decode (partials only, no initial
-    contents); launches on one stream share it in order."""
+    contents); launches on one stream share it in order.  A workspace that is
+    outgrown stays allocated: a captured graph may still name it."""
     ws = _SPLIT_WS.get(dev)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _SPLIT_WS_RETIRED.append(ws)
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _SPLIT_WS[dev] = ws
     return ws

@@ -63,10 +63,51 @@ def blocks_needed(num_reqs: int, prompt_len: int, beam_width: int, new_tokens: i
     return num_reqs * (per_prompt + beam_width * per_beam)
 
 
-class SidModelRunner:
-    """Owns one ``[2, num_blocks, block_size, Hkv, D]`` cache per layer."""
+class _DecodeGraph:
+    """The decode forward of one batch shape captured as a HIP graph.
 
-    def __init__(self, model: SidDecoder, num_blocks: int, block_size: int = 16):
+    It owns a static :class:`BeamKVTable` and token buffer; capturing runs the
+    metadata builder and the decoder once, so the builder's device work
+    (positions, slot mapping, attention suffix lengths) is recorded too and
+    replays from whatever the static table holds.  A replay copies the live
+    table and tokens in (six small device copies) and returns the captured
+    logits buffer, valid until the next replay."""
+
+    def __init__(self, runner: "SidModelRunner", table: BeamKVTable, tokens: torch.Tensor, req_ids, prompt_lens,
+                 step: int):
+        self.table = BeamKVTable(table.prefix_bt.clone(), table.prefix_len.clone(), table.beam_width,
+                                 table.suffix_bt.clone(), table.suffix_len.clone(), block_size=table.block_size)
+        self.tokens = tokens.clone()
+        args = (self.table, self.tokens, list(req_ids), list(prompt_lens), step)
+        side = torch.cuda.Stream(device=runner.device)  # warm-up off the main stream, as capture expects
+        side.wait_stream(torch.cuda.current_stream(runner.device))
+        with torch.cuda.stream(side):
+            runner._decode_eager(*args)
+        torch.cuda.current_stream(runner.device).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = runner._decode_eager(*args)
+
+    def replay(self, table: BeamKVTable, tokens: torch.Tensor) -> torch.Tensor:
+        st = self.table
+        st.prefix_bt.copy_(table.prefix_bt)
+        st.prefix_len.copy_(table.prefix_len)
+        st.beam_start.copy_(table.beam_start)
+        st.suffix_bt.copy_(table.suffix_bt)
+        st.suffix_len.copy_(table.suffix_len)
+        self.tokens.copy_(tokens)
+        self.graph.replay()
+        return self.logits
+
+
+class SidModelRunner:
+    """Owns one ``[2, num_blocks, block_size, Hkv, D]`` cache per layer.
+
+    With ``use_graphs`` the decode forward of each batch shape (requests,
+    beams, table widths, longest prompt) runs eagerly once and is then
+    captured; later steps of that shape replay the graph."""
+
+    def __init__(self, model: SidDecoder, num_blocks: int, block_size: int = 16, use_graphs: bool = True):
         cfg = model.cfg
         if block_size % 16 != 0:
             raise ValueError("block_size must be a multiple of 16")
@@ -80,6 +121,8 @@ class SidModelRunner:
         self.builder = BeamAttentionMetadataBuilder(_KVSpec(block_size), model.layer_names, None,
                                                     self.device)
         self.pool = BlockPool(num_blocks)
+        self.use_graphs = use_graphs
+        self._graphs: dict = {}
 
     def _forward(self, ids, positions, m: CommonAttentionMetadata, side: dict):
         token = MEGA_DATA_VAR.set(side)
@@ -129,12 +172,26 @@ class SidModelRunner:
         suffix slot.  ``step`` = tokens already resident per beam (host
         copy of ``table.suffix_len``, equal for every beam).  Returns logits
         ``[R, W, V]`` float32."""
-        R, W, dev = table.num_reqs, table.beam_width, self.device
-        N = R * W
+        R, W = table.num_reqs, table.beam_width
         if max(prompt_lens) + step >= self.model.rope.max_pos:
             raise ValueError(f"position beyond the rotary table ({self.model.rope.max_pos})")
         if step >= table.suffix_capacity:
             raise ValueError("beam suffix blocks are full")
+        if tokens.shape != (R * W,):
+            raise ValueError("tokens must hold one query token per beam")
+        if not self.use_graphs:
+            return self._decode_eager(table, tokens, req_ids, prompt_lens, step)
+        key = (R, W, table.prefix_bt.shape[1], table.suffix_bt.shape[1], max(prompt_lens))
+        g = self._graphs.get(key)
+        if g is None:
+            out = self._decode_eager(table, tokens, req_ids, prompt_lens, step)
+            self._graphs[key] = _DecodeGraph(self, table, tokens, req_ids, prompt_lens, step)
+            return out
+        return g.replay(table, tokens)
+
+    def _decode_eager(self, table: BeamKVTable, tokens: torch.Tensor, req_ids, prompt_lens, step: int):
+        R, W = table.num_reqs, table.beam_width
+        N = R * W
         qsl = torch.arange(0, N + 1, W, dtype=torch.int32)
         seq = torch.tensor([p + step + 1 for p in prompt_lens], dtype=torch.int32)
         # device copies come from device tensors: a host-to-device copy here would
