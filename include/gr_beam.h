@@ -39,7 +39,8 @@ enum {
   GR_DEV_BAD_BLOCK = 1,   /* block id outside [0, num_blocks) */
   GR_DEV_BAD_LENGTH = 2,  /* length beyond the block-table row capacity */
   GR_DEV_BAD_PARENT = 4,  /* parent index outside [0, beam width) */
-  GR_DEV_SUFFIX_FULL = 8  /* append past the row capacity (token dropped) */
+  GR_DEV_SUFFIX_FULL = 8, /* append past the row capacity (token dropped) */
+  GR_DEV_BAD_NODE = 16    /* catalog node id or child range outside the trie */
 };
 
 enum { GR_DTYPE_F32 = 0, GR_DTYPE_F16 = 1, GR_DTYPE_BF16 = 2 };
@@ -234,6 +235,33 @@ gr_status_t gr_beam_kv_append(
  * gr_beam_prune_workspace_size() bytes, 256-byte aligned.
  */
 size_t gr_beam_prune_workspace_size(int num_reqs, int beam_width, int vocab, int k);
+
+/*
+ * gr_beam_prune_topk constrained by a catalog of valid semantic-ID token
+ * sequences (the reference's Catalog trie, vllm_gr/entrypoints/openai/
+ * serving_models.py:18-49, applied at serving_engine.py:381-394, 504-506,
+ * 526-528).
+ *
+ * The trie is given in CSR form: node n's children are
+ * child_token[node_start[n] .. node_start[n+1]) (ascending) with node ids
+ * child_node[...]; node 0 is the root.  beam_node[b] (int32 [R*W]) is the
+ * node reached by beam b's generated tokens (-1: none, as Catalog.valid
+ * returns the empty set).  Stage 1 is unchanged -- each beam's top-k by
+ * (logit desc, token asc) -- and then, as the reference masks after the
+ * sampler's per-beam top-K, every candidate that is not a child of the
+ * beam's node leaves the pool (EOS reports its score only when it is a
+ * child).  node_out [R, k] receives each selected beam's new node (-1 for an
+ * unfilled slot).  Same workspace as gr_beam_prune_topk.  Node ids and child
+ * ranges outside the trie flag GR_DEV_BAD_NODE in *dev_status (nullable) and
+ * read as childless.
+ */
+gr_status_t gr_beam_prune_topk_catalog(
+    const float* logits, int64_t logits_row_stride, const float* cum,
+    int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
+    const int32_t* beam_node, const int32_t* node_start, const int32_t* child_token,
+    const int32_t* child_node, int num_nodes, int num_edges,
+    int32_t* parent, int32_t* token, float* score, float* eos_score, int32_t* node_out,
+    void* workspace, size_t workspace_bytes, int32_t* dev_status, hipStream_t stream);
 
 gr_status_t gr_beam_prune_topk(
     const float* logits, int64_t logits_row_stride, const float* cum,

@@ -59,7 +59,7 @@ def _load():
         lib.oracle_prune_row_stats.argtypes = [P, P, ctypes.c_int, ctypes.c_int, P, P, P, P]
         lib.oracle_prune_topk.restype = ctypes.c_int
         lib.oracle_prune_topk.argtypes = [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                          ctypes.c_int, ctypes.c_int, P, P, P, P, P]
+                                          ctypes.c_int, ctypes.c_int, P, P, P, P, P, P]
         _lib = lib
     return _lib
 
@@ -89,8 +89,10 @@ def row_stats(logits: np.ndarray, cum: np.ndarray):
     return m, S, lse, c
 
 
-def prune_topk(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id: int = -1):
-    """Bit-exact oracle.  ``logits [R, W, V]`` fp32, ``cum [R, W]`` fp32.
+def prune_topk(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id: int = -1, allowed=None):
+    """Bit-exact oracle.  ``logits [R, W, V]`` fp32, ``cum [R, W]`` fp32;
+    ``allowed [R, W, V]`` bool (optional): the catalog mask applied to each
+    beam's top-k candidates.
 
     Returns dict with ``parent, token [R, k]`` int32, ``score [R, k]`` fp32,
     ``score64 [R, k]`` fp64 and ``eos_score [R, W]`` fp32.
@@ -103,22 +105,26 @@ def prune_topk(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id: int = 
     score = np.empty((R, k), np.float32)
     score64 = np.empty((R, k), np.float64)
     eos_score = np.empty((R, W), np.float32)
+    al = None if allowed is None else np.ascontiguousarray(allowed, dtype=np.uint8).reshape(R, W, V)
     rc = _load().oracle_prune_topk(_ptr(x), _ptr(cm), R, W, V, int(k), int(eos_token_id),
                                    _ptr(parent), _ptr(token), _ptr(score), _ptr(score64),
-                                   _ptr(eos_score))
+                                   _ptr(eos_score), None if al is None else _ptr(al))
     if rc != 0:
         raise ValueError("oracle_prune_topk: bad arguments")
     return dict(parent=parent, token=token, score=score, score64=score64, eos_score=eos_score)
 
 
-def prune_topk_float64(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id: int = -1):
+def prune_topk_float64(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id: int = -1, valid_sets=None):
     """Plain numpy float64 restatement of the reference's pruning arithmetic.
 
     Per beam: ``log_softmax`` then the beam's top-k candidates
     (``serving_engine.py:300-308`` asks the sampler for ``logprobs=W``);
     ``score = cum + logprob`` (``:511``) in float64 (``:538-539``); EOS
     candidates leave the pool (``:541-562``); top-k over the union
-    (``:566-567``), sorted by (score desc, flat asc).
+    (``:566-567``), sorted by (score desc, flat asc).  ``valid_sets`` (one
+    set of tokens per beam, ``[R][W]``): the catalog's valid continuations;
+    the beam's other candidates become -inf (``:504-506``) and, being
+    -inf, are never selected here.
     """
     x = np.asarray(logits, dtype=np.float64)
     R, W, V = x.shape
@@ -133,6 +139,8 @@ def prune_topk_float64(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id
         for b in range(W):
             order = np.lexsort((np.arange(V), -x[r, b]))[:min(k, V)]
             for v in order:
+                if valid_sets is not None and int(v) not in valid_sets[r][b]:
+                    continue
                 if v == eos_token_id:
                     continue
                 cand_s.append(float(cum[r][b]) + logp[r, b, v])

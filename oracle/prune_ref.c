@@ -200,11 +200,15 @@ static void topk_push(topk_t* t, cand_t c) {
  * parent (beam within request), token, score (fp32 of the fp64 score),
  * score64 (nullable); eos_score [R*W] (nullable; -inf when the beam's top-k
  * holds no EOS).  Slots past the available candidates get -1/-1/-inf.
+ * allowed [R*W, V] (nullable): the catalog mask -- a stage-1 candidate whose
+ * token is not allowed for its beam leaves the pool (the reference sets its
+ * logprob to -inf after the per-beam top-K, serving_engine.py:504-506); EOS
+ * reports a score only when allowed.
  * Returns 0, or -1 on bad arguments.
  */
 int oracle_prune_topk(const float* logits, const float* cum, int R, int W, int V, int k,
                       int eos, int32_t* parent, int32_t* token, float* score,
-                      double* score64, float* eos_score) {
+                      double* score64, float* eos_score, const uint8_t* allowed) {
   if (R < 0 || W <= 0 || V <= 0 || k <= 0) return -1;
   int k1 = k < V ? k : V;
   cand_t* row_heap = (cand_t*)malloc(sizeof(cand_t) * (size_t)k1);
@@ -226,6 +230,7 @@ int oracle_prune_topk(const float* logits, const float* cum, int R, int W, int V
       if (eos_score) eos_score[r * W + b] = -INFINITY;
       for (int i = 0; i < row.n; ++i) {
         int v = (int)row.h[i].idx;
+        if (allowed && !allowed[((size_t)r * W + b) * V + v]) continue;
         double s = (m == -INFINITY) ? -INFINITY : (double)x[v] + c;
         if (v == eos) {
           if (eos_score) eos_score[r * W + b] = (float)s;

@@ -116,27 +116,35 @@ def beam_score(tokens, cum, eos, length_penalty) -> float:
 
 
 def beam_search(next_logprobs, prompts, beam_width: int, max_tokens: int, eos_token_id=None,
-                length_penalty: float = 1.0, begin_token=None, end_token=None, trace=None):
+                length_penalty: float = 1.0, begin_token=None, end_token=None, trace=None, valid_fn=None):
     """Returns, per prompt, the list of :class:`Seq` the reference outputs.
     ``trace`` (a list) receives, per step and prompt, the sorted scores of
     the candidates left after the EOS split, and per prompt the sorted
     final scores of completed + live sequences -- the gap between entries
     ``beam_width - 1`` and ``beam_width`` of each is how close that cut came
-    to a different selection."""
+    to a different selection.  ``valid_fn(generated_tokens) -> set`` is the
+    catalog (serving_engine.py:381-394): a beam's candidates outside the set
+    are masked to -inf after its top-W (:504-506); such a candidate is never
+    kept as a beam here (the reference keeps -inf beams when fewer than W
+    valid ones exist)."""
     W = beam_width
-    insts = []
+    insts, plen = [], []
     for p in prompts:
         toks = list(p) + ([begin_token] if begin_token is not None else [])
         insts.append(_Instance([Seq(toks, 0.0)]))
+        plen.append(len(toks))
     pre_calc = (begin_token is not None) + (end_token is not None)
     for _ in range(max(0, max_tokens - pre_calc)):
-        for inst in insts:
+        for ii, inst in enumerate(insts):
             cand = []  # (score, beam index, token)
             for bi, beam in enumerate(inst.beams):
                 lp = np.asarray(next_logprobs(beam.tokens), dtype=np.float64)
                 V = lp.shape[0]
                 top = np.lexsort((np.arange(V), -lp))[:W]  # (logprob desc, token asc)
+                ok = None if valid_fn is None else valid_fn(beam.tokens[plen[ii]:])
                 for t in top:
+                    if ok is not None and int(t) not in ok:
+                        continue
                     cand.append((beam.cum_logprob + float(lp[t]), bi, int(t)))
             keep = []
             for sc, bi, t in cand:

@@ -69,3 +69,55 @@ def test_prune_masked_logits(device):
     wl.logits[0, :, 100:] = float("-inf")
     wl.logits[1, 3, :] = float("-inf")
     _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), 8))
+
+
+def test_prune_catalog_matches_oracle(device):
+    """Catalog-constrained pruning: each beam's top-k candidates outside its
+    trie node's children leave the pool (serving_engine.py:504-506), bit for
+    bit against the masked C oracle; node_out is each new beam's trie node."""
+    from vllm_gr_amd.entrypoints.catalog import Catalog
+    rng = np.random.default_rng(11)
+    R, W, V, k, eos = 4, 32, 8192, 32, 5
+    cat = Catalog()
+    seqs = [rng.integers(0, V, size=3).tolist() for _ in range(3000)]
+    seqs += [[s[0], eos] for s in seqs[:40]]  # EOS valid after some first tokens
+    for s in seqs:
+        cat.add(s)
+    # beam prefixes: root, inside the trie, dead (-1) and complete (no children)
+    prefixes = []
+    for r in range(R):
+        row = []
+        for b in range(W):
+            s = seqs[int(rng.integers(0, len(seqs)))]
+            kind = b % 5
+            # kind 1: a first token that has EOS among its children
+            row.append([] if kind == 0 else seqs[int(rng.integers(0, 40))][:1] if kind == 1 else s[:2]
+                       if kind == 2 else [V - 1, V - 2] if kind == 3 else s[:3])
+        prefixes.append(row)
+    node = torch.tensor([[cat.node_of(p) for p in row] for row in prefixes], dtype=torch.int32)
+    allowed = np.zeros((R, W, V), bool)
+    for r in range(R):
+        for b in range(W):
+            allowed[r, b, list(cat.valid(prefixes[r][b]))] = True
+    logits = torch.from_numpy((rng.standard_normal((R, W, V)) * 3).astype(np.float32))
+    # make the valid tokens competitive so the beams' top-k hold several of them
+    logits += torch.from_numpy(allowed.astype(np.float32) * 6.0)
+    cum = torch.from_numpy(rng.uniform(-20, 0, (R, W)).astype(np.float32))
+    status = ops.new_status(device)
+    print(f"[prune] catalog R={R} W={W} V={V} k={k} nodes={cat.to_device('cpu').num_nodes}", flush=True)
+    parent, token, score, eos_score, node_out = ops.beam_prune_topk(
+        logits.to(device), cum.to(device), k, eos, catalog=cat.to_device(device), beam_node=node.to(device),
+        status=status)
+    torch.cuda.synchronize()
+    ops.check_status(status)
+    want = op.prune_topk(logits.numpy(), cum.numpy(), k, eos, allowed=allowed)
+    assert np.array_equal(parent.cpu().numpy(), want["parent"])
+    assert np.array_equal(token.cpu().numpy(), want["token"])
+    assert np.array_equal(score.cpu().numpy().view(np.int32), want["score"].view(np.int32))
+    assert np.array_equal(eos_score.cpu().numpy().view(np.int32), want["eos_score"].reshape(R, W).view(np.int32))
+    assert (want["parent"] >= 0).sum() > R * k // 2 and np.isfinite(want["eos_score"]).any()
+    no = node_out.cpu().numpy()
+    for r in range(R):
+        for j in range(k):
+            p, t = int(want["parent"][r, j]), int(want["token"][r, j])
+            assert no[r, j] == (cat.node_of(prefixes[r][p] + [t]) if p >= 0 else -1)

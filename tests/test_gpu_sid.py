@@ -104,6 +104,39 @@ def test_sid_beam_search_f32_eos_begin_end():
             assert abs(got[k][0] - exp[k][0]) < 1e-4 and (got[k][1] == "stop") == (exp[k][1] == "stop")
 
 
+def test_sid_beam_search_f32_catalog():
+    """A catalog of 3-token semantic IDs restricts every beam to valid
+    continuations of its generated tokens: same beams as the oracle with the
+    catalog rule, every output a catalog entry."""
+    from vllm_gr_amd.entrypoints.catalog import Catalog
+    seed, lens, W = 10, [14, 27], 8
+    w = init_weights(F32, seed)
+    prompts = _prompts(seed, lens, F32.vocab)
+    rng = np.random.default_rng(seed)
+    cat = Catalog()
+    sids = set()  # about half the vocabulary valid at each level (57,600 IDs)
+    for a in rng.choice(F32.vocab, 48, replace=False):
+        for b in rng.choice(F32.vocab, 40, replace=False):
+            for c in rng.choice(F32.vocab, 30, replace=False):
+                sids.add((int(a), int(b), int(c)))
+    for sid in sids:
+        cat.add(sid)
+    f = so.decoder_next_logprobs(so.weights_f64(w), F32)
+    trace = []
+    ref = so.beam_search(f, prompts, W, 3, trace=trace, valid_fn=cat.valid)
+    assert _min_margin(trace, W) > 1e-3
+    llm = _llm(F32, w, len(lens), max(lens), W, 3)
+    llm.catalog = cat
+    out = llm.beam_search(prompts, BeamSearchParams(W, 3))
+    for o, r, p in zip(out, ref, prompts):
+        got = {tuple(s.tokens): s.cum_logprob for s in o.sequences}
+        exp = {tuple(s.tokens): s.cum_logprob for s in r if math.isfinite(s.cum_logprob)}
+        assert set(got) == set(exp) and len(got) > 0
+        for kk in exp:
+            assert abs(got[kk] - exp[kk]) < 1e-4
+            assert kk[len(p):] in sids
+
+
 def test_sid_beam_search_bf16_mfma_rescored():
     seed, lens, W, steps = 5, [70, 129], 16, 4
     w = init_weights(BF16_128, seed)

@@ -141,6 +141,20 @@ def test_beam_search_eos_and_length_penalty():
     assert math.isclose(got[1].cum_logprob, math.log(.4))
 
 
+def test_beam_search_catalog_mask_after_top_w():
+    """The catalog masks a beam's candidates after its top-W (serving_engine.py:
+    504-506): a valid token outside the beam's top-W is not a candidate."""
+    P = [3]
+    table = {(): [.5, .3, .15, .05], (0,): [.7, .2, .05, .05], (3,): [.1, .2, .3, .4]}
+    valid = {(): {0, 3}, (0,): {1, 3}, (3,): {0}}
+    got = so.beam_search(_table_logprobs(table, 4, len(P)), [P], 2, 2,
+                         valid_fn=lambda g: valid.get(tuple(g), set()))[0]
+    # step 0: top-2 = {0 (.5), 1 (.3)}; 3 is valid but outside the top-2, 1 is invalid -> beam [0]
+    # step 1 from (0,): top-2 = {0 (.7), 1 (.2)}; only 1 is valid -> [0, 1] = .5 * .2
+    assert [s.tokens for s in got] == [P + [0, 1]]
+    assert math.isclose(got[0].cum_logprob, math.log(.1))
+
+
 def test_beam_search_begin_end_tokens():
     P = [1]
     f = _hash_logprobs(5, seed=2)

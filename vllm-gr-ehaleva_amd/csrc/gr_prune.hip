@@ -119,7 +119,45 @@ struct PruneArgs {
   uint64_t* part_key;  // [R, ng, k] stage-1 selections: score key (0 = empty) ...
   int64_t* part_flat;  // ... and flat index b * V + v
   int ng, gr;          // row groups per request, rows per group
+  // catalog (nullable): the trie in CSR form -- node n's children are
+  // child_token / child_node[node_start[n] .. node_start[n+1]), tokens
+  // ascending; beam_node[b] is beam b's node (-1: no valid continuation)
+  const int32_t* beam_node;
+  const int32_t* node_start;
+  const int32_t* child_token;
+  const int32_t* child_node;
+  int num_nodes, num_edges;
+  int32_t* dev_status;
 };
+
+// Position of token t among the children [c0, c1) of a trie node, or -1.
+__device__ inline int catalog_find(const int32_t* child_token, int c0, int c1, int t) {
+  int lo = c0, hi = c1;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (child_token[mid] < t) lo = mid + 1; else hi = mid;
+  }
+  return lo < c1 && child_token[lo] == t ? lo : -1;
+}
+
+// Children range of beam b's trie node; empty for -1 and, flagged, for an
+// id or range outside the trie.
+__device__ inline void catalog_range(const PruneArgs& a, int b, int& c0, int& c1) {
+  const int node = a.beam_node[b];
+  c0 = c1 = 0;
+  if (node < 0) return;
+  if (node >= a.num_nodes) {
+    flag_status(a.dev_status, GR_DEV_BAD_NODE);
+    return;
+  }
+  const int s0 = a.node_start[node], s1 = a.node_start[node + 1];
+  if (s0 < 0 || s1 < s0 || s1 > a.num_edges) {
+    flag_status(a.dev_status, GR_DEV_BAD_NODE);
+    return;
+  }
+  c0 = s0;
+  c1 = s1;
+}
 
 __device__ inline float wave_max(float v) {
 #pragma unroll
@@ -326,7 +364,11 @@ __device__ __noinline__ void row_topk_radix(const float* xg, int V, int k1, uint
   }
 }
 
-template <int MAXC>  // MAXC > 0: row held in registers (<= MAXC chunks); 0: re-read from memory
+// MAXC > 0: row held in registers (<= MAXC chunks); 0: re-read from memory.
+// CATALOG: the beam's top-k candidates outside its trie node's children are
+// dropped (the reference masks them to -inf after the sampler's per-beam
+// top-K, serving_engine.py:504-506, 526-528).
+template <int MAXC, bool CATALOG = false>
 __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   __shared__ uint64_t sk[PR_MAXK];  // candidates as row_key
   __shared__ float ox[PR_MAXK];
@@ -532,18 +574,55 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 #undef PR_FOR_CHUNKS
   if (tid == 0) eos_pos = -1;
   __syncthreads();
-  if (a.eos >= 0)
-    for (int i = tid; i < k1; i += PR_THREADS)
-      if (ov[i] == a.eos) eos_pos = i;
-  __syncthreads();
-  const int e = eos_pos;
   float* cx = a.cand_x + (int64_t)row * k1;
   int32_t* cv = a.cand_v + (int64_t)row * k1;
-  for (int i = tid; i < k1; i += PR_THREADS) {
-    const int src = (e >= 0 && i >= e) ? i + 1 : i;
-    cx[i] = src < k1 ? ox[src] : -INFINITY;
-    cv[i] = src < k1 ? ov[src] : -1;
+  if constexpr (CATALOG) {
+    // keep the candidates among the node's children, in order; EOS (when a
+    // child) leaves the pool with its score
+    int c0, c1;
+    catalog_range(a, row, c0, c1);
+    constexpr int PER = PR_MAXK / PR_THREADS;
+    bool kf[PER];
+    int keep = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = tid * PER + j;
+      bool k = false;
+      if (i < k1 && catalog_find(a.child_token, c0, c1, ov[i]) >= 0) {
+        if (ov[i] == a.eos) eos_pos = i;
+        else k = true;
+      }
+      kf[j] = k;
+      keep += k;
+    }
+    int dst;
+    const int total = block_scan(keep, dst, itmp);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = tid * PER + j;
+      if (kf[j]) {
+        cx[dst] = ox[i];
+        cv[dst] = ov[i];
+        ++dst;
+      }
+    }
+    for (int i = total + tid; i < k1; i += PR_THREADS) {
+      cx[i] = -INFINITY;
+      cv[i] = -1;
+    }
+  } else {
+    if (a.eos >= 0)
+      for (int i = tid; i < k1; i += PR_THREADS)
+        if (ov[i] == a.eos) eos_pos = i;
+    __syncthreads();
+    const int e = eos_pos;
+    for (int i = tid; i < k1; i += PR_THREADS) {
+      const int src = (e >= 0 && i >= e) ? i + 1 : i;
+      cx[i] = src < k1 ? ox[src] : -INFINITY;
+      cv[i] = src < k1 ? ov[src] : -1;
+    }
   }
+  const int e = eos_pos;
   if (tid == 0) {
     a.row_c[row] = c_row;
     if (a.eos_score) {
@@ -1096,10 +1175,26 @@ extern "C" size_t gr_beam_prune_workspace_size(int num_reqs, int beam_width, int
          align256(rows * sizeof(double)) + align256(parts * sizeof(uint64_t)) + align256(parts * sizeof(int64_t));
 }
 
-extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_row_stride, const float* cum,
-                                          int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
-                                          int32_t* parent, int32_t* token, float* score, float* eos_score,
-                                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
+// The new beam's trie node: the child of its parent's node reached by its
+// token (a selected candidate is always such a child).
+__global__ void catalog_advance(PruneArgs a, int32_t* node_out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.R * a.k) return;
+  const int r = i / a.k, p = a.parent[i], t = a.token[i];
+  int node = -1;
+  if (p >= 0 && p < a.W && t >= 0) {
+    int c0, c1;
+    catalog_range(a, r * a.W + p, c0, c1);
+    const int e = catalog_find(a.child_token, c0, c1, t);
+    node = e >= 0 ? a.child_node[e] : -1;
+  }
+  node_out[i] = node;
+}
+
+static gr_status_t prune_launch(PruneArgs& a, const float* logits, int64_t logits_row_stride, const float* cum,
+                                int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
+                                int32_t* parent, int32_t* token, float* score, float* eos_score,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (num_reqs < 0 || beam_width < 1 || vocab < 4 || vocab % 4 != 0 || k < 1 || k > PR_MAXK || k > vocab ||
       beam_width > PR_MAXW || logits_row_stride < vocab || logits_row_stride % 4 != 0)
     return GR_ERR_INVALID_ARG;
@@ -1111,7 +1206,6 @@ extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_ro
     return GR_ERR_WORKSPACE;
   const int k1 = k;
   const size_t rows = (size_t)num_reqs * beam_width;
-  PruneArgs a;
   a.logits = logits;
   a.row_stride = logits_row_stride;
   a.cum = cum;
@@ -1136,10 +1230,14 @@ extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_ro
                        align256(rows * sizeof(double));
   a.part_key = reinterpret_cast<uint64_t*>(part_base);
   a.part_flat = reinterpret_cast<int64_t*>(part_base + align256(parts * sizeof(uint64_t)));
-  if (vocab <= PR_CHUNK * PR_REG_CHUNKS)
-    hipLaunchKernelGGL(prune_rows<PR_REG_CHUNKS>, dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
-  else
-    hipLaunchKernelGGL(prune_rows<0>, dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
+  const bool cat = a.beam_node != nullptr;
+  if (vocab <= PR_CHUNK * PR_REG_CHUNKS) {
+    if (cat) hipLaunchKernelGGL((prune_rows<PR_REG_CHUNKS, true>), dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
+    else hipLaunchKernelGGL((prune_rows<PR_REG_CHUNKS, false>), dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
+  } else {
+    if (cat) hipLaunchKernelGGL((prune_rows<0, true>), dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
+    else hipLaunchKernelGGL((prune_rows<0, false>), dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
+  }
   gr_status_t st = launch_status();
   if (st != GR_OK) return st;
   const size_t per_req = (size_t)a.ng * k;  // stage-2 candidates per request
@@ -1157,5 +1255,40 @@ extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_ro
     hipLaunchKernelGGL((prune_merge_final<MG_THREADS, 4>), dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
   else
     hipLaunchKernelGGL((prune_merge_final<MG_THREADS, MG_REG>), dim3((unsigned)num_reqs), dim3(MG_THREADS), 0, stream, a);
+  return launch_status();
+}
+
+extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_row_stride, const float* cum,
+                                          int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
+                                          int32_t* parent, int32_t* token, float* score, float* eos_score,
+                                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  PruneArgs a = {};
+  return prune_launch(a, logits, logits_row_stride, cum, num_reqs, beam_width, vocab, k, eos_token_id, parent,
+                      token, score, eos_score, workspace, workspace_bytes, stream);
+}
+
+extern "C" gr_status_t gr_beam_prune_topk_catalog(
+    const float* logits, int64_t logits_row_stride, const float* cum,
+    int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
+    const int32_t* beam_node, const int32_t* node_start, const int32_t* child_token,
+    const int32_t* child_node, int num_nodes, int num_edges,
+    int32_t* parent, int32_t* token, float* score, float* eos_score, int32_t* node_out,
+    void* workspace, size_t workspace_bytes, int32_t* dev_status, hipStream_t stream) {
+  if (num_nodes < 1 || num_edges < 0 || !beam_node || !node_start || !node_out ||
+      (num_edges > 0 && (!child_token || !child_node)))
+    return GR_ERR_INVALID_ARG;
+  PruneArgs a = {};
+  a.beam_node = beam_node;
+  a.node_start = node_start;
+  a.child_token = child_token;
+  a.child_node = child_node;
+  a.num_nodes = num_nodes;
+  a.num_edges = num_edges;
+  a.dev_status = dev_status;
+  gr_status_t st = prune_launch(a, logits, logits_row_stride, cum, num_reqs, beam_width, vocab, k, eos_token_id,
+                                parent, token, score, eos_score, workspace, workspace_bytes, stream);
+  if (st != GR_OK || num_reqs == 0) return st;
+  const int n = num_reqs * k;
+  hipLaunchKernelGGL(catalog_advance, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, node_out);
   return launch_status();
 }

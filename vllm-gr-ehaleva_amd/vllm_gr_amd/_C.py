@@ -24,6 +24,7 @@ GR_DEV_BAD_BLOCK = 1
 GR_DEV_BAD_LENGTH = 2
 GR_DEV_BAD_PARENT = 4
 GR_DEV_SUFFIX_FULL = 8
+GR_DEV_BAD_NODE = 16
 
 GR_DTYPE_F32 = 0
 GR_DTYPE_F16 = 1
@@ -87,6 +88,12 @@ SIGNATURES = {
         _P, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P,
     ]),
     "gr_beam_prune_workspace_size": (_SZ, [_I, _I, _I, _I]),
+    "gr_beam_prune_topk_catalog": (_I, [
+        _P, _L, _P, _I, _I, _I, _I, _I,    # logits, stride, cum, R, W, V, k, eos
+        _P, _P, _P, _P, _I, _I,            # beam_node, node_start, child_token, child_node, nodes, edges
+        _P, _P, _P, _P, _P,                # parent, token, score, eos_score, node_out
+        _P, _SZ, _P, _P,                   # workspace, bytes, dev_status, stream
+    ]),
     "gr_beam_prune_topk": (_I, [
         _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _SZ, _P,
     ]),

@@ -47,16 +47,26 @@ class PruneResult:
     token: torch.Tensor      # [R, W] int32
     score: torch.Tensor      # [R, W] float32: new cumulative logprob, descending per request
     eos_score: torch.Tensor  # [R, W_old] float32: score of a beam's EOS candidate (-inf if none)
+    node: torch.Tensor | None = None  # [R, W] int32: each new beam's catalog trie node (with a catalog)
 
 
 def prune_step(logits: torch.Tensor, cum_logprob: torch.Tensor, beam_width: int,
-               eos_token_id: int | None = None, *, workspace: torch.Tensor | None = None) -> PruneResult:
+               eos_token_id: int | None = None, *, workspace: torch.Tensor | None = None,
+               catalog=None, beam_node: torch.Tensor | None = None) -> PruneResult:
     """Fused log_softmax + cumulative logprob + top-``beam_width`` over
-    beams x vocab per request.  ``logits [R, W, V]`` float32, ``cum [R, W]``."""
+    beams x vocab per request.  ``logits [R, W, V]`` float32, ``cum [R, W]``.
+    With ``catalog`` (device trie) and ``beam_node [R, W]``, each beam's
+    candidates outside its valid continuations leave the pool (the catalog
+    mask of serving_engine.py:381-394, 504-506) and the result carries the
+    new beams' trie nodes."""
     eos = -1 if eos_token_id is None else int(eos_token_id)
-    parent, token, score, eos_score = ops.beam_prune_topk(logits, cum_logprob, beam_width, eos,
-                                                           workspace=workspace)
-    return PruneResult(parent, token, score, eos_score)
+    if catalog is None:
+        parent, token, score, eos_score = ops.beam_prune_topk(logits, cum_logprob, beam_width, eos,
+                                                               workspace=workspace)
+        return PruneResult(parent, token, score, eos_score)
+    parent, token, score, eos_score, node = ops.beam_prune_topk(
+        logits, cum_logprob, beam_width, eos, workspace=workspace, catalog=catalog, beam_node=beam_node)
+    return PruneResult(parent, token, score, eos_score, node)
 
 
 def fork_info(res: PruneResult) -> list[list[tuple[int, int]]]:
@@ -78,7 +88,8 @@ def pruned_parents(res: PruneResult, beam_width: int) -> list[list[int]]:
 
 
 def beam_search_step(table, logits: torch.Tensor, cum_logprob: torch.Tensor, kv_caches,
-                     eos_token_id: int | None = None, status: torch.Tensor | None = None):
+                     eos_token_id: int | None = None, status: torch.Tensor | None = None, *,
+                     catalog=None, beam_node: torch.Tensor | None = None):
     """Prune the candidates of every beam and fork the beams' resident KV.
 
     ``table``: the batch's :class:`~vllm_gr_amd.v1.beam_kv.BeamKVTable`;
@@ -88,7 +99,7 @@ def beam_search_step(table, logits: torch.Tensor, cum_logprob: torch.Tensor, kv_
     its ``score`` the new cumulative logprobs.  Unfilled slots (fewer live
     candidates than beams) keep their parent's KV."""
     W = table.beam_width
-    res = prune_step(logits, cum_logprob, W, eos_token_id)
+    res = prune_step(logits, cum_logprob, W, eos_token_id, catalog=catalog, beam_node=beam_node)
     parent = torch.where(res.parent >= 0, res.parent,
                          torch.arange(W, device=res.parent.device, dtype=res.parent.dtype)[None])
     table.fork(parent, kv_caches, status=status)

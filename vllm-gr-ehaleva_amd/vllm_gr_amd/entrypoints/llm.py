@@ -81,12 +81,18 @@ class LLM:
     seed, device)``.  ``num_blocks`` KV-cache blocks of ``block_size``
     tokens are allocated per layer up front; a batch needs
     :func:`~vllm_gr_amd.v1.sid_runner.blocks_needed` of them.  With
-    ``use_graphs`` each decode step shape is captured once and replayed."""
+    ``use_graphs`` each decode step shape is captured once and replayed.
+    With a :class:`~vllm_gr_amd.entrypoints.catalog.Catalog`, every beam's
+    candidates are restricted to the catalog's valid continuations of its
+    generated tokens; a candidate the catalog rules out never becomes a beam
+    (the reference keeps it as a -inf-score beam, serving_engine.py:504-506,
+    which only reaches the output when fewer than beam_width valid sequences
+    exist)."""
 
     def __init__(self, cfg: DecoderConfig = SID_DECODER_1P7B, *, seed: int = 0, device="cuda",
                  num_blocks: int = 4096, block_size: int = 16, eos_token_id: int | None = None,
                  special_tokens: dict[str, int] | None = None, weights: dict | None = None,
-                 max_position: int = 32768, use_graphs: bool = True):
+                 max_position: int = 32768, use_graphs: bool = True, catalog=None):
         dev = torch.device(device)
         if dev.type != "cuda":
             raise ValueError("the beam path runs on a HIP device (torch 'cuda')")
@@ -97,6 +103,9 @@ class LLM:
         self.runner = SidModelRunner(self.model, num_blocks, block_size, use_graphs=use_graphs)
         self.eos_token_id = eos_token_id
         self.special_tokens = dict(special_tokens or {})
+        # the catalog of valid semantic IDs (serving_models.py:52-65 loads it per server)
+        self.catalog = catalog
+        self._catalog_dev = None
         self.last_times = StepTimes()
         self._batch = 0
 
@@ -141,6 +150,11 @@ class LLM:
         ev = [torch.cuda.Event(enable_timing=True)]
         ev[0].record(stream)
 
+        cat = None
+        if self.catalog is not None:
+            if self._catalog_dev is None:
+                self._catalog_dev = self.catalog.to_device(dev)
+            cat = self._catalog_dev
         hist = torch.empty(R, W, 0, dtype=torch.int32, device=dev)
         score = torch.zeros(R, W, dtype=torch.float32, device=dev)
         finished: list[tuple[torch.Tensor, torch.Tensor]] = []  # (eos_score [R, W_old], hist_old)
@@ -157,8 +171,10 @@ class LLM:
                 blocks += [b for bl in pblocks for b in bl]
                 ev.append(torch.cuda.Event(enable_timing=True))
                 ev[-1].record(stream)
-                # the prompt is the one beam of every request (llm.py:118-146)
-                res = bsm.prune_step(logits[:, None], torch.zeros(R, 1, device=dev), W, eos)
+                # the prompt is the one beam of every request (llm.py:118-146), at the trie's root
+                node0 = None if cat is None else torch.zeros(R, 1, dtype=torch.int32, device=dev)
+                res = bsm.prune_step(logits[:, None], torch.zeros(R, 1, device=dev), W, eos, catalog=cat,
+                                     beam_node=node0)
                 finished.append((res.eos_score, torch.empty(R, 1, 0, dtype=torch.int32, device=dev)))
                 hist = res.token[..., None]
                 score = res.score
@@ -167,10 +183,12 @@ class LLM:
                     tok = res.token.clamp(min=0).view(-1).to(torch.int64)
                     logits = self.runner.decode(table, tok, rids, lens, step=s - 1)
                     table.advance()
+                    node = res.node
                     if s + 1 < steps:
-                        res = bsm.beam_search_step(table, logits, score, self.runner.kv_caches, eos)
+                        res = bsm.beam_search_step(table, logits, score, self.runner.kv_caches, eos, catalog=cat,
+                                                   beam_node=node)
                     else:
-                        res = bsm.prune_step(logits, score, W, eos)
+                        res = bsm.prune_step(logits, score, W, eos, catalog=cat, beam_node=node)
                     finished.append((res.eos_score, hist))
                     par = res.parent.clamp(min=0).to(torch.int64)
                     hist = torch.cat((hist.gather(1, par[..., None].expand(-1, -1, hist.shape[2])),

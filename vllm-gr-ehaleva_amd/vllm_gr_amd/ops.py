@@ -82,7 +82,8 @@ def check_status(status: torch.Tensor) -> None:
         names = [n for b, n in ((_C.GR_DEV_BAD_BLOCK, "block id out of range"),
                                 (_C.GR_DEV_BAD_LENGTH, "length beyond table capacity"),
                                 (_C.GR_DEV_BAD_PARENT, "parent index out of range"),
-                                (_C.GR_DEV_SUFFIX_FULL, "suffix full")) if bits & b]
+                                (_C.GR_DEV_SUFFIX_FULL, "suffix full"),
+                                (_C.GR_DEV_BAD_NODE, "catalog node out of range")) if bits & b]
         raise ValueError("device tables rejected: " + ", ".join(names))
 
 
@@ -310,13 +311,19 @@ def prune_workspace_bytes(num_reqs: int, beam_width: int, vocab: int, k: int) ->
 
 
 def beam_prune_topk(logits: torch.Tensor, cum: torch.Tensor, k: int, eos_token_id: int = -1, *,
-                    workspace: torch.Tensor | None = None, out=None):
+                    workspace: torch.Tensor | None = None, out=None, catalog=None,
+                    beam_node: torch.Tensor | None = None, node_out: torch.Tensor | None = None,
+                    status: torch.Tensor | None = None):
     """Fused log_softmax + cum + top-k over beams x vocab per request.
 
     ``logits``: ``[R, W, V]`` float32 (vocab contiguous), ``cum``: ``[R, W]``.
     Returns ``(parent [R,k] int32, token [R,k] int32, score [R,k] float32,
-    eos_score [R,W] float32)``."""
-    dev = _need_cuda(logits, cum, workspace)
+    eos_score [R,W] float32)``.  With ``catalog`` (a
+    :class:`~vllm_gr_amd.entrypoints.catalog.CatalogTensors`) and ``beam_node
+    [R, W]`` int32, candidates outside each beam's trie node are dropped
+    (gr_beam_prune_topk_catalog) and a fifth value, ``node_out [R, k]``, is
+    returned."""
+    dev = _need_cuda(logits, cum, workspace, beam_node, node_out, status)
     if logits.dim() != 3 or logits.dtype != torch.float32 or logits.stride(2) != 1 \
             or logits.stride(0) != logits.shape[1] * logits.stride(1):
         raise ValueError("logits must be float32 [R, W, V] with rows at a uniform stride")
@@ -333,12 +340,34 @@ def beam_prune_topk(logits: torch.Tensor, cum: torch.Tensor, k: int, eos_token_i
         eos_score = torch.empty((R, W), dtype=torch.float32, device=dev)
     else:
         parent, token, score, eos_score = out
-    code = _C.lib().gr_beam_prune_topk(
+    ws_bytes = workspace.numel() * workspace.element_size()
+    if catalog is None:
+        code = _C.lib().gr_beam_prune_topk(
+            logits.data_ptr(), logits.stride(1), cum.data_ptr(), R, W, V, int(k), int(eos_token_id),
+            parent.data_ptr(), token.data_ptr(), score.data_ptr(), eos_score.data_ptr(),
+            workspace.data_ptr(), ws_bytes, _stream(dev))
+        _C.check("gr_beam_prune_topk", code)
+        return parent, token, score, eos_score
+    _need_cuda(catalog.node_start, catalog.child_token, catalog.child_node)
+    for name, t in (("node_start", catalog.node_start), ("child_token", catalog.child_token),
+                    ("child_node", catalog.child_node)):
+        _need_i32(name, t)
+    if beam_node is None or beam_node.shape != (R, W):
+        raise ValueError("beam_node must be an int32 [R, W] tensor")
+    _need_i32("beam_node", beam_node)
+    if node_out is None:
+        node_out = torch.empty((R, k), dtype=torch.int32, device=dev)
+    if node_out.shape != (R, k):
+        raise ValueError("node_out must be [R, k]")
+    _need_i32("node_out", node_out)
+    code = _C.lib().gr_beam_prune_topk_catalog(
         logits.data_ptr(), logits.stride(1), cum.data_ptr(), R, W, V, int(k), int(eos_token_id),
-        parent.data_ptr(), token.data_ptr(), score.data_ptr(), eos_score.data_ptr(),
-        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(dev))
-    _C.check("gr_beam_prune_topk", code)
-    return parent, token, score, eos_score
+        beam_node.data_ptr(), catalog.node_start.data_ptr(), _ptr(catalog.child_token if catalog.num_edges else None),
+        _ptr(catalog.child_node if catalog.num_edges else None), catalog.num_nodes, catalog.num_edges,
+        parent.data_ptr(), token.data_ptr(), score.data_ptr(), eos_score.data_ptr(), node_out.data_ptr(),
+        workspace.data_ptr(), ws_bytes, _ptr(status), _stream(dev))
+    _C.check("gr_beam_prune_topk_catalog", code)
+    return parent, token, score, eos_score, node_out
 
 
 # ---- fused decoder stages (include/gr_decoder.h) ---------------------------
