@@ -137,14 +137,26 @@ class SidModelRunner:
         Returns ``(logits [R, V] float32 of each prompt's last token,
         prefix_bt [R, blocks] int32, prefix_len [R] int32, blocks per
         request)``."""
-        bs, dev = self.block_size, self.device
+        bs = self.block_size
         lens = [len(p) for p in prompts]
         if min(lens) < 1:
             raise ValueError("empty prompt")
         if max(lens) > self.model.rope.max_pos:
             raise ValueError(f"prompt longer than the rotary table ({self.model.rope.max_pos})")
         nbs = [-(-n // bs) for n in lens]
-        blocks = [self.pool.allocate(n) for n in nbs]
+        flat = self.pool.allocate(sum(nbs))
+        try:
+            return self._prefill(prompts, req_ids, lens, nbs, flat)
+        except BaseException:
+            self.pool.release(flat)
+            raise
+
+    def _prefill(self, prompts, req_ids, lens, nbs, flat):
+        bs, dev = self.block_size, self.device
+        offs = [0]
+        for n in nbs:
+            offs.append(offs[-1] + n)
+        blocks = [flat[offs[r]:offs[r + 1]] for r in range(len(nbs))]
         R, width = len(prompts), max(nbs)
         bt = torch.zeros(R, width, dtype=torch.int32)
         for r, b in enumerate(blocks):
