@@ -11,6 +11,11 @@ counted once + suffix K/V + Q + O + tables) over the average step time;
 roofline for the decode kernel against 8 TB/s; cpu_baseline = the torch
 float32 cascade restatement of the reference (oracle/cpu_baseline.py) on the
 host cores for the same step.
+
+--workload fork | prune measure the fork+append and pruning kernels the same
+way; --workload e2e runs the end-to-end semantic-ID beam decode (4 prompts x
+2048 tokens, 128 beams, 3 tokens, 28-layer decoder) and reports the p99
+request latency.
 """
 
 from __future__ import annotations
