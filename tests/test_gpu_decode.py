@@ -248,3 +248,25 @@ def test_decode_split_prefix(device, R, W, P, hint, dtype, softcap):
     assert np.abs(out - whole).max() <= 1e-2 and np.abs(lse - whole_lse).max() <= 1e-4
     again, again_lse = run_gpu(wl, device, split=True, max_prefix_len=hint)
     assert np.array_equal(out, again) and np.array_equal(lse, again_lse)
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("pos", [5, 70, 200, 470, 520])
+def test_decode_dominant_key(device, split, pos):
+    """One prefix key planted to dominate one row by far more than the
+    kernels' lazy-rescale margin, in the first tile, the pipelined tiles, the
+    second-to-last and the last tile (P = 530: nine 64-key tiles), with and
+    without the split prefix: the exact path gives the oracle's result for
+    every row."""
+    wl = workloads.make_decode(R=2, W=32, P=530, L=(1, 6), Hq=32, Hkv=8, D=128, dtype=torch.bfloat16,
+                               input_scale=1.0, seed=41)
+    r, b, h = 1, 3, 2  # request 1's beam 3, query head 2 (KV head 0)
+    n = int(wl.beam_start[r]) + b
+    q = wl.q[n, h].float()
+    blk = int(wl.prefix_bt[r, pos // wl.block_size])
+    wl.kv_cache[0, blk, pos % wl.block_size, 0] = (q / q.norm() * 60.0).to(torch.bfloat16)
+    print(f"[decode] dominant key pos={pos} split={split}", flush=True)
+    out, lse = run_gpu(wl, device, split=split, max_prefix_len=530 if split else None)
+    ref, ref_lse = run_oracle(wl)
+    assert ref_lse[n, h] > 50.0
+    _check(out, lse, ref, ref_lse, atol=2e-2)

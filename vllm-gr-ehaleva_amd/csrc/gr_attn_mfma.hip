@@ -257,19 +257,18 @@ __device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH
   }
 }
 
-// One pipelined step of a wave over its 32-key half of a fully visible
-// tile.  Phase A interleaves, in 8 fixed segments, one MFMA of the next
-// tile's QK^T (with the LDS read of the fragment two MFMAs ahead) with the
-// weights of two scores of the current tile; phase B checks whether any
-// weight could exceed 2^RESCALE_THRESH (rare: exact path); phase C is the
-// current tile's PV with its transposing reads two MFMAs ahead.  The
-// scheduling barriers pin the segment order so the matrix core and the VALU
-// work side by side.  s_in holds S^T of the current tile, s_out receives that
-// of the next tile (the caller alternates two registers sets: no copies).
+// Phase A of a pipelined step of a wave over its 32-key half of a fully
+// visible tile: in 8 fixed segments, one MFMA of the next tile's QK^T (with
+// the LDS read of the fragment two MFMAs ahead) beside the weights of two
+// scores of the current tile against the row's reference.  s_in holds S^T of
+// the current tile, s_out receives that of the next tile (the caller
+// alternates two register sets: no copies).  Returns true when some weight
+// could exceed 2^RESCALE_THRESH or the row has no reference yet (the tile then
+// needs the exact path); otherwise adds the weight sum to the row's state.
 template <int DT, bool SOFTCAP>
-__device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_buf, int kbase, int lane,
-                                 const u32x4_t (&qf)[8], const f32x16_t& s_in, f32x16_t& s_out,
-                                 f32x16_t (&o)[4], RowState& st, float c, float cap) {
+__device__ inline bool phase_a1(const uint16_t* next_buf, int kbase, int lane, const u32x4_t (&qf)[8],
+                                const f32x16_t& s_in, f32x16_t& s_out, RowState& st, float c, float cap,
+                                u32x4_t (&p)[1][2]) {
   using M = Mma<DT>;
   const int lhalf = lane >> 5;
   const int krow_i = kbase + key_perm(lane & 31);
@@ -293,17 +292,20 @@ __device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_b
     pk[i] = M::pack2(e0, e1);
     __builtin_amdgcn_sched_barrier(0);
   }
-  u32x4_t p[1][2] = {{u32x4_t{pk[0], pk[1], pk[2], pk[3]}, u32x4_t{pk[4], pk[5], pk[6], pk[7]}}};
+  p[0][0] = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
+  p[0][1] = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
   const float acc = acc0 + acc1;
-  if (__ballot(!(acc <= RESCALE_SUM)) != 0) {
-    __asm__ volatile("" ::: "memory");
-    const uint32_t vis[1] = {0xFFFFu};
-    const f32x16_t s1[1] = {s_in};
-    weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, o);
-  } else {
-    st.lsum += acc;
-  }
-  // phase C: PV of the current tile (MFMA j: step kk = j/4, dim block mb = j%4)
+  if (__ballot(!(acc <= RESCALE_SUM)) != 0) return true;
+  st.lsum += acc;
+  return false;
+}
+
+// Phase C: the current tile's PV with its transposing reads two MFMAs ahead
+// (MFMA j: step kk = j/4, dim block mb = j%4).
+template <int DT>
+__device__ inline void phase_c1(const uint16_t* cur_buf, int kbase, int lane, const u32x4_t (&p)[1][2],
+                                f32x16_t (&o)[4]) {
+  using M = Mma<DT>;
   const int g = lane >> 4, sl = lane & 15;
   const uint16_t* vsrc = cur_buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
   auto vfrag = [&](int j) {
@@ -324,6 +326,22 @@ __device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_b
   }
 }
 
+// One pipelined step with the exact path in line (phase A; the exact weights
+// when phase A reports it; phase C).
+template <int DT, bool SOFTCAP>
+__device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_buf, int kbase, int lane,
+                                 const u32x4_t (&qf)[8], const f32x16_t& s_in, f32x16_t& s_out,
+                                 f32x16_t (&o)[4], RowState& st, float c, float cap) {
+  u32x4_t p[1][2];
+  if (phase_a1<DT, SOFTCAP>(next_buf, kbase, lane, qf, s_in, s_out, st, c, cap, p)) {
+    __asm__ volatile("" ::: "memory");
+    const uint32_t vis[1] = {0xFFFFu};
+    const f32x16_t s1[1] = {s_in};
+    weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, o);
+  }
+  phase_c1<DT>(cur_buf, kbase, lane, p, o);
+}
+
 // PREFILL: the varlen causal mode (gr_paged_attn_prefill).  The argument
 // block is read as: prefix_bt = block table, prefix_len = sequence length,
 // beam_start = query start per request, num_beams = query tokens, T = the
@@ -341,6 +359,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   __shared__ int suf_s0[4][32];          // per row group beam: first suffix position
   __shared__ int suf_blk[4][32][SB_STAGE];  // per row group beam: its first suffix block ids
   __shared__ int pbt_s[PBT_WIN];         // staged prefix block ids (-1 = invalid)
+  __shared__ int hot_flag;               // a tile of the fast loop needed the exact path
 
   // ---- XCD-aware tile placement: all m-tiles of a (request, KV head) land on
   // the same XCD (round-robin dispatch puts workgroup i on XCD i % 8)
@@ -518,6 +537,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       suf_cum[rg][33] = b_lo;  // first beam of the group
     }
   }
+  if (tid == 0) hot_flag = 0;
   __syncthreads();
 
   // loader roles: thread (lk, lc) moves keys 2*lk and 2*lk+1 (one block: the
@@ -654,15 +674,78 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       __syncthreads();
     }
   } else {
-    for (; it + 2 < n_st; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
-      prefix_step(it, s_cur, s_alt);
-      prefix_step(it + 1, s_alt, s_cur);
+    // Fully visible tiles but the last two run in a loop that never rescales
+    // O (a rescale in the loop makes the compiler copy the accumulators every
+    // step).  The workgroup's first tile (peeled: O is still zero) sets each
+    // row's reference; a later tile with a score more than RESCALE_THRESH
+    // above it -- never for ordinary inputs -- is only recorded, and the
+    // workgroup then recomputes its prefix range exactly.
+    bool hot_seen = false;
+    u32x4_t p[1][2];
+    auto fetch_ahead = [&](int t) {
+      if (t + 2 < n_st) {
+        load_prefix(kb + (t + 2) * ST_KEYS, pf_blk);
+        if (t + 3 < n_st) {
+          ensure_window(kb + (t + 3) * ST_KEYS);
+          pf_blk = read_blk(kb + (t + 3) * ST_KEYS);
+        }
+      }
+    };
+    auto finish_step = [&](int t) {
+      phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
+      if (t + 2 < n_st) store_tile(lds + ((t + 2) % NBUF) * BUF);
+      __syncthreads();
+    };
+    if (n_st >= 3) {
+      fetch_ahead(0);
+      phase_a1<DT, SOFTCAP>(lds + BUF, ks * 32, lane, qf, s_cur, s_alt, st, c, cap, p);
+      f32x16_t zo[4] = {};
+      const uint32_t vis[1] = {0xFFFFu};
+      const f32x16_t s1[1] = {s_cur};
+      weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, zo);
+      finish_step(0);
+      s_cur = s_alt;
+      it = 1;
     }
+    for (; it + 2 < n_st; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
+      fetch_ahead(it);
+      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_cur, s_alt, st, c,
+                                        cap, p);
+      finish_step(it);
+      fetch_ahead(it + 1);
+      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 2) % NBUF) * BUF, ks * 32, lane, qf, s_alt, s_cur, st, c,
+                                        cap, p);
+      finish_step(it + 1);
+    }
+    if (hot_seen && lane == 0) hot_flag = 1;
     if (it + 1 < n_st) {
       prefix_step(it, s_cur, s_alt);
       last_step(it + 1, s_alt);
     } else if (it < n_st) {
       last_step(it, s_cur);
+    }
+    __syncthreads();
+    if (hot_flag) {
+      // exact recomputation of the workgroup's prefix range, one tile at a
+      // time through buffer 0, every tile on the exact path
+      st = RowState{-INFINITY, 0.f};
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
+      for (int t = 0; t < n_st; ++t) {
+        ensure_window(kb + t * ST_KEYS);
+        load_prefix(kb + t * ST_KEYS, read_blk(kb + t * ST_KEYS));
+        store_tile(lds);
+        __syncthreads();
+        const int nk = t == n_st - 1 ? p_last : ST_KEYS;
+        uint32_t v = 0;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) v |= (ks * 32 + 16 * (rr >> 3) + 8 * lhalf + (rr & 7) < nk ? 1u : 0u) << rr;
+        const uint32_t vis[1] = {v};
+        const f32x16_t s1[1] = {qk_half<DT>(lds, ks * 32, lane, qf)};
+        weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, p, o);
+        pv<DT, 1>(lds, ks * 32, lane, p, o);
+        __syncthreads();
+      }
     }
   }
 
