@@ -550,11 +550,31 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const int key0 = k0 + 2 * lk;
     return key0 < P ? pbt_s[(key0 >> bsh) - win0] : -1;
   };
-  // Branch-free loads: keys outside the prefix or in an invalid block read a
-  // zero source, so every thread issues the same loads.
+  // zero source of the last tile's loads
   const S* zsrc = reinterpret_cast<const S*>(g_zero16);
+  // Element offset of this thread's first key in tile k0 (k0 is a multiple
+  // of 64): blk * block_stride + ((k0 & (bs-1)) + (2*lk & (bs-1))) * tok_stride
+  // + head + chunk; the first product is 32 x 32 bits (block strides below
+  // 2^32 elements: mfma_decode_supported), the second term is uniform.
+  const int64_t thr_off = (int64_t)((2 * lk) & (a.bs - 1)) * a.kv_tok_stride + head_off + lc * 8;
+  const uint32_t blk_stride = (uint32_t)a.kv_block_stride;
   auto load_prefix = [&](int k0, int blk) {
     const int key0 = k0 + 2 * lk;
+    if (k0 + ST_KEYS <= P) {
+      // whole tile inside the prefix: no per-key test; an invalid block
+      // (flagged when the window was staged) reads block 0
+      const uint64_t off = (uint64_t)(uint32_t)max(blk, 0) * blk_stride +
+                           (uint64_t)(thr_off + (int64_t)(k0 & (a.bs - 1)) * a.kv_tok_stride);
+      const S* kp = kc + off;
+      const S* vp = vc + off;
+      kreg[0] = *reinterpret_cast<const u32x4_t*>(kp);
+      kreg[1] = *reinterpret_cast<const u32x4_t*>(kp + a.kv_tok_stride);
+      vreg[0] = *reinterpret_cast<const u32x4_t*>(vp);
+      vreg[1] = *reinterpret_cast<const u32x4_t*>(vp + a.kv_tok_stride);
+      return;
+    }
+    // the last tile: keys past the prefix or in an invalid block read a zero
+    // source, so every thread issues the same loads
     const int64_t off = (int64_t)(blk < 0 ? 0 : blk) * a.kv_block_stride +
                         (int64_t)(key0 & (a.bs - 1)) * a.kv_tok_stride + head_off + lc * 8;
 #pragma unroll
@@ -756,14 +776,13 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
   for (int g = 0; g < 4; ++g) max_tot = max(max_tot, suf_cum[g][32]);
   const int n_sit = !SPLIT || split == nsplit - 1 ? (max_tot + 31) / 32 : 0;
-  for (int it = 0; it < n_sit; ++it) {
-    // loader: 4 row groups x 32 slots x 16 chunks; row group g's slots live in
-    // buffer g >> 1, rows / columns (g & 1) * 32 .. + 31
-    // all loads of the iteration are issued before the first LDS store
-    constexpr int SUF_PER_THREAD = 4 * 32 * 16 / MF_THREADS;
-    static_assert(4 * 32 * 16 % MF_THREADS == 0, "suffix loader split");
-    u32x4_t skv[SUF_PER_THREAD], svv[SUF_PER_THREAD];
-    int sinfo[SUF_PER_THREAD];
+  // loader: 4 row groups x 32 slots x 16 chunks per tile; row group g's slots
+  // live in buffer g >> 1, rows / columns (g & 1) * 32 .. + 31; all loads of a
+  // tile are issued before its first LDS store.
+  constexpr int SUF_PER_THREAD = 4 * 32 * 16 / MF_THREADS;
+  static_assert(4 * 32 * 16 % MF_THREADS == 0, "suffix loader split");
+  auto suf_gather = [&](int it, u32x4_t (&skv)[SUF_PER_THREAD], u32x4_t (&svv)[SUF_PER_THREAD],
+                        int (&sinfo)[SUF_PER_THREAD]) {
 #pragma unroll
     for (int i = 0; i < SUF_PER_THREAD; ++i) {
       const int e = tid + i * MF_THREADS;
@@ -797,6 +816,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         }
       }
     }
+  };
+  auto suf_tile = [&](const u32x4_t (&skv)[SUF_PER_THREAD], const u32x4_t (&svv)[SUF_PER_THREAD],
+                      const int (&sinfo)[SUF_PER_THREAD]) {
 #pragma unroll
     for (int i = 0; i < SUF_PER_THREAD; ++i) {
       const int e = tid + i * MF_THREADS;
@@ -828,6 +850,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       pv<DT, 1>(sbuf, (rg & 1) * 32, lane, pw, o);
     }
     __syncthreads();
+  };
+  for (int it = 0; it < n_sit; ++it) {
+    u32x4_t skv0[SUF_PER_THREAD], svv0[SUF_PER_THREAD];
+    int sinfo0[SUF_PER_THREAD];
+    suf_gather(it, skv0, svv0, sinfo0);
+    suf_tile(skv0, svv0, sinfo0);
   }
 
   // ---- merge the two key halves and write O, LSE --------------------------
@@ -954,6 +982,8 @@ bool mfma_decode_supported(const DecodeArgs& a) {
   if (a.q_tok_stride % 8 || a.out_tok_stride % 8 || a.kv_block_stride % 8 || a.kv_tok_stride % 8 ||
       a.kv_head_stride % 8)
     return false;
+  // tile loads multiply block ids by the block stride in 32 bits
+  if (a.kv_block_stride <= 0 || a.kv_block_stride > 0xFFFFFFFFll) return false;
   return true;
 }
 
