@@ -781,17 +781,23 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // tile are issued before its first LDS store.
   constexpr int SUF_PER_THREAD = 4 * 32 * 16 / MF_THREADS;
   static_assert(4 * 32 * 16 % MF_THREADS == 0, "suffix loader split");
-  auto suf_gather = [&](int it, u32x4_t (&skv)[SUF_PER_THREAD], u32x4_t (&svv)[SUF_PER_THREAD],
+  auto suf_gather = [&](int it, int t, u32x4_t (&skv)[SUF_PER_THREAD], u32x4_t (&svv)[SUF_PER_THREAD],
                         int (&sinfo)[SUF_PER_THREAD]) {
+    // Two passes: every address first, then all the loads back to back.  Any
+    // wait on a global or scratch read in the first pass then has no K/V
+    // load to wait for (the vector-memory counter retires in order).
+    // Empty slots and invalid blocks read the zero source.
+    const S* ksrc[SUF_PER_THREAD];
+    const S* vsrc[SUF_PER_THREAD];
 #pragma unroll
     for (int i = 0; i < SUF_PER_THREAD; ++i) {
-      const int e = tid + i * MF_THREADS;
+      const int e = t + i * MF_THREADS;
       const int grp = e >> 9;
       const int slot = (e >> 4) & 31;
       const int ch = e & 15;
       const int gs = it * 32 + slot;
-      skv[i] = u32x4_t{0, 0, 0, 0};
-      svv[i] = u32x4_t{0, 0, 0, 0};
+      ksrc[i] = zsrc;
+      vsrc[i] = zsrc;
       sinfo[i] = -1;
       if (gs < suf_cum[grp][32]) {
         int lo = 0, hi = 31;  // largest beam index i with cum[i] <= gs (skips empty beams)
@@ -803,25 +809,34 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         const int j = gs - suf_cum[grp][lo];
         const int n = nb0 + b;
         const int pos = suf_s0[grp][lo] + j;
-        const int bi = bsh >= 0 ? pos >> bsh : pos / a.bs;
-        const int blk = bi < SB_STAGE ? suf_blk[grp][lo][bi] : a.suffix_bt[(int64_t)n * a.suffix_bt_stride + bi];
+        const int bi = pos >> bsh;  // power-of-two block size on this path
+        int blk;  // staged ids from LDS, later ones (long suffixes) from HBM
+        if (bi < SB_STAGE) blk = suf_blk[grp][lo][bi];
+        else blk = a.suffix_bt[(int64_t)n * a.suffix_bt_stride + bi];
         if (blk >= 0 && blk < a.num_blocks) {
-          const int64_t base = (int64_t)blk * a.kv_block_stride + (int64_t)(pos % a.bs) * a.kv_tok_stride +
+          const int64_t base = (int64_t)blk * a.kv_block_stride + (int64_t)(pos & (a.bs - 1)) * a.kv_tok_stride +
                                head_off + ch * 8;
-          skv[i] = *reinterpret_cast<const u32x4_t*>(kc + base);
-          svv[i] = *reinterpret_cast<const u32x4_t*>(vc + base);
+          ksrc[i] = kc + base;
+          vsrc[i] = vc + base;
           sinfo[i] = (b << 16) | j;
         } else {
           flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
         }
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    using gvec = const __attribute__((address_space(1))) u32x4_t*;  // global loads, not flat
+#pragma unroll
+    for (int i = 0; i < SUF_PER_THREAD; ++i) {
+      skv[i] = *(gvec)(ksrc[i]);
+      svv[i] = *(gvec)(vsrc[i]);
+    }
   };
-  auto suf_tile = [&](const u32x4_t (&skv)[SUF_PER_THREAD], const u32x4_t (&svv)[SUF_PER_THREAD],
+  auto suf_tile = [&](int t, const u32x4_t (&skv)[SUF_PER_THREAD], const u32x4_t (&svv)[SUF_PER_THREAD],
                       const int (&sinfo)[SUF_PER_THREAD]) {
 #pragma unroll
     for (int i = 0; i < SUF_PER_THREAD; ++i) {
-      const int e = tid + i * MF_THREADS;
+      const int e = t + i * MF_THREADS;
       const int grp = e >> 9;
       const int slot = (e >> 4) & 31;
       const int ch = e & 15;
@@ -852,10 +867,15 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     __syncthreads();
   };
   for (int it = 0; it < n_sit; ++it) {
+    // a fresh copy of the thread index each trip: the slot addresses derived
+    // from it are recomputed in registers rather than hoisted out of the loop
+    // and spilled to scratch (whose reloads would wait on every load)
+    int t = tid;
+    __asm__ volatile("" : "+v"(t));
     u32x4_t skv0[SUF_PER_THREAD], svv0[SUF_PER_THREAD];
     int sinfo0[SUF_PER_THREAD];
-    suf_gather(it, skv0, svv0, sinfo0);
-    suf_tile(skv0, svv0, sinfo0);
+    suf_gather(it, t, skv0, svv0, sinfo0);
+    suf_tile(t, skv0, svv0, sinfo0);
   }
 
   // ---- merge the two key halves and write O, LSE --------------------------
