@@ -47,6 +47,7 @@ constexpr float RESCALE_THRESH = 60.0f;  // log2 units a key may exceed the refe
 constexpr float RESCALE_SUM = 1.152921504606846976e18f;  // 2^RESCALE_THRESH: a lane weight sum above it forces the exact path
 constexpr int PBT_WIN = 2048;  // prefix block-table entries staged in LDS
 constexpr int NBUF = 3;        // LDS tile buffers (V of tile t, K of tile t+1, fill of tile t+2)
+constexpr int NBUF_ALLOC = 4;  // buffers allocated: the suffix holds two tiles (two buffers each)
 constexpr int SB_STAGE = 2;    // suffix block ids staged in LDS per beam (more are read from HBM)
 
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
@@ -353,9 +354,9 @@ __device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_b
 // normalised partial O and LSE to the workspace; split_merge combines them.
 template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF_ALLOC * BUF];
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
-  __shared__ int suf_info[4][32];        // per row group slot: (beam << 16) | j, or -1
+  __shared__ int suf_info[2][4][32];     // per suffix tile and row group slot: (beam << 16) | j, or -1
   __shared__ int suf_s0[4][32];          // per row group beam: first suffix position
   __shared__ int suf_blk[4][32][SB_STAGE];  // per row group beam: its first suffix block ids
   __shared__ int pbt_s[PBT_WIN];         // staged prefix block ids (-1 = invalid)
@@ -832,50 +833,66 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       svv[i] = *(gvec)(vsrc[i]);
     }
   };
-  auto suf_tile = [&](int t, const u32x4_t (&skv)[SUF_PER_THREAD], const u32x4_t (&svv)[SUF_PER_THREAD],
-                      const int (&sinfo)[SUF_PER_THREAD]) {
+  // tile h (0 or 1) of a pair: row group g's slots in buffer 2h + (g >> 1),
+  // rows (g & 1) * 32 .. + 31
+  auto suf_store = [&](int t, int h, const u32x4_t (&skv)[SUF_PER_THREAD], const u32x4_t (&svv)[SUF_PER_THREAD],
+                       const int (&sinfo)[SUF_PER_THREAD]) {
 #pragma unroll
     for (int i = 0; i < SUF_PER_THREAD; ++i) {
       const int e = t + i * MF_THREADS;
       const int grp = e >> 9;
       const int slot = (e >> 4) & 31;
       const int ch = e & 15;
-      uint16_t* buf = lds + (grp >> 1) * BUF;
+      uint16_t* buf = lds + (2 * h + (grp >> 1)) * BUF;
       const int key = (grp & 1) * 32 + slot;
       *reinterpret_cast<u32x4_t*>(buf + key * KS_PITCH + kchunk(key, ch) * 8) = skv[i];
       *reinterpret_cast<u32x4_t*>(buf + K_TILE + key * VS_PITCH + ch * 8) = svv[i];
-      if (ch == 0) suf_info[grp][slot] = sinfo[i];
+      if (ch == 0) suf_info[h][grp][slot] = sinfo[i];
     }
-    __syncthreads();
-    if (ks == 0) {
-      // register r of this lane is slot 16*(r>>3) + 8*lhalf + (r&7) of the group's 32
-      const int lim = row_ok ? my_len - a.T + my_qi : -1;
-      uint32_t vis = 0;
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const int info = suf_info[rg][16 * (rr >> 3) + 8 * lhalf + (rr & 7)];
-        const bool ok = info >= 0 && (info >> 16) == my_b && (info & 0xFFFF) <= lim;
-        vis |= (ok ? 1u : 0u) << rr;
-      }
-      const uint16_t* sbuf = lds + (rg >> 1) * BUF;
-      const f32x16_t s1[1] = {qk_half<DT>(sbuf, (rg & 1) * 32, lane, qf)};
-      const uint32_t vis1[1] = {vis};
-      u32x4_t pw[1][2];
-      weights<DT, SOFTCAP, true, 1>(s1, vis1, st, c, cap, pw, o);
-      pv<DT, 1>(sbuf, (rg & 1) * 32, lane, pw, o);
-    }
-    __syncthreads();
   };
-  for (int it = 0; it < n_sit; ++it) {
+  // this wave's row group against tile h of the pair
+  auto suf_compute = [&](int h) {
+    // register r of this lane is slot 16*(r>>3) + 8*lhalf + (r&7) of the group's 32
+    const int lim = row_ok ? my_len - a.T + my_qi : -1;
+    uint32_t vis = 0;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const int info = suf_info[h][rg][16 * (rr >> 3) + 8 * lhalf + (rr & 7)];
+      const bool ok = info >= 0 && (info >> 16) == my_b && (info & 0xFFFF) <= lim;
+      vis |= (ok ? 1u : 0u) << rr;
+    }
+    const uint16_t* sbuf = lds + (2 * h + (rg >> 1)) * BUF;
+    const f32x16_t s1[1] = {qk_half<DT>(sbuf, (rg & 1) * 32, lane, qf)};
+    const uint32_t vis1[1] = {vis};
+    u32x4_t pw[1][2];
+    weights<DT, SOFTCAP, true, 1>(s1, vis1, st, c, cap, pw, o);
+    pv<DT, 1>(sbuf, (rg & 1) * 32, lane, pw, o);
+  };
+  // Tiles in pairs: the key-half-0 wave of each row group takes the first
+  // tile, the key-half-1 wave the second, at the same time (each adds to its
+  // own partial state; the halves merge below).
+  for (int it = 0; it < n_sit; it += 2) {
     // a fresh copy of the thread index each trip: the slot addresses derived
     // from it are recomputed in registers rather than hoisted out of the loop
     // and spilled to scratch (whose reloads would wait on every load)
     int t = tid;
     __asm__ volatile("" : "+v"(t));
-    u32x4_t skv0[SUF_PER_THREAD], svv0[SUF_PER_THREAD];
-    int sinfo0[SUF_PER_THREAD];
-    suf_gather(it, t, skv0, svv0, sinfo0);
-    suf_tile(t, skv0, svv0, sinfo0);
+    const bool two = it + 1 < n_sit;
+    {
+      u32x4_t skv0[SUF_PER_THREAD], svv0[SUF_PER_THREAD];
+      int sinfo0[SUF_PER_THREAD];
+      suf_gather(it, t, skv0, svv0, sinfo0);
+      suf_store(t, 0, skv0, svv0, sinfo0);
+    }
+    if (two) {
+      u32x4_t skv1[SUF_PER_THREAD], svv1[SUF_PER_THREAD];
+      int sinfo1[SUF_PER_THREAD];
+      suf_gather(it + 1, t, skv1, svv1, sinfo1);
+      suf_store(t, 1, skv1, svv1, sinfo1);
+    }
+    __syncthreads();
+    if (ks == 0 || two) suf_compute(ks);
+    __syncthreads();
   }
 
   // ---- merge the two key halves and write O, LSE --------------------------
