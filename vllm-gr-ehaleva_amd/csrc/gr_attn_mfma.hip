@@ -559,7 +559,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // 2^32 elements: mfma_decode_supported), the second term is uniform.
   const int64_t thr_off = (int64_t)((2 * lk) & (a.bs - 1)) * a.kv_tok_stride + head_off + lc * 8;
   const uint32_t blk_stride = (uint32_t)a.kv_block_stride;
-  auto load_prefix = [&](int k0, int blk) {
+  auto load_prefix_to = [&](int k0, int blk, u32x4_t (&kd)[2], u32x4_t (&vd)[2]) {
     const int key0 = k0 + 2 * lk;
     if (k0 + ST_KEYS <= P) {
       // whole tile inside the prefix: no per-key test; an invalid block
@@ -568,10 +568,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
                            (uint64_t)(thr_off + (int64_t)(k0 & (a.bs - 1)) * a.kv_tok_stride);
       const S* kp = kc + off;
       const S* vp = vc + off;
-      kreg[0] = *reinterpret_cast<const u32x4_t*>(kp);
-      kreg[1] = *reinterpret_cast<const u32x4_t*>(kp + a.kv_tok_stride);
-      vreg[0] = *reinterpret_cast<const u32x4_t*>(vp);
-      vreg[1] = *reinterpret_cast<const u32x4_t*>(vp + a.kv_tok_stride);
+      kd[0] = *reinterpret_cast<const u32x4_t*>(kp);
+      kd[1] = *reinterpret_cast<const u32x4_t*>(kp + a.kv_tok_stride);
+      vd[0] = *reinterpret_cast<const u32x4_t*>(vp);
+      vd[1] = *reinterpret_cast<const u32x4_t*>(vp + a.kv_tok_stride);
       return;
     }
     // the last tile: keys past the prefix or in an invalid block read a zero
@@ -581,10 +581,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const bool ok = blk >= 0 && key0 + j < P;
-      kreg[j] = *reinterpret_cast<const u32x4_t*>(ok ? kc + off + j * a.kv_tok_stride : zsrc);
-      vreg[j] = *reinterpret_cast<const u32x4_t*>(ok ? vc + off + j * a.kv_tok_stride : zsrc);
+      kd[j] = *reinterpret_cast<const u32x4_t*>(ok ? kc + off + j * a.kv_tok_stride : zsrc);
+      vd[j] = *reinterpret_cast<const u32x4_t*>(ok ? vc + off + j * a.kv_tok_stride : zsrc);
     }
   };
+  auto load_prefix = [&](int k0, int blk) { load_prefix_to(k0, blk, kreg, vreg); };
   // keep the window over [k0, k0 + 64); switching costs two barriers and
   // happens once per PBT_WIN blocks
   auto ensure_window = [&](int k0) {
@@ -596,27 +597,30 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       __syncthreads();
     }
   };
-  auto store_tile = [&](uint16_t* buf) {
+  auto store_tile_from = [&](uint16_t* buf, const u32x4_t (&kd)[2], const u32x4_t (&vd)[2]) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int row = 2 * lk + j;
-      *reinterpret_cast<u32x4_t*>(buf + row * KS_PITCH + kchunk(row, lc) * 8) = kreg[j];
-      *reinterpret_cast<u32x4_t*>(buf + K_TILE + row * VS_PITCH + lc * 8) = vreg[j];
+      *reinterpret_cast<u32x4_t*>(buf + row * KS_PITCH + kchunk(row, lc) * 8) = kd[j];
+      *reinterpret_cast<u32x4_t*>(buf + K_TILE + row * VS_PITCH + lc * 8) = vd[j];
     }
   };
+  auto store_tile = [&](uint16_t* buf) { store_tile_from(buf, kreg, vreg); };
   // Three LDS buffers: during step t the wave reads V of tile t, K of tile
   // t+1, while tile t+2 (loaded into registers at the start of the step) is
   // stored into the third buffer at its end.
+  // (the first two tiles' loads are both issued before either is stored)
+  u32x4_t k1reg[2], v1reg[2];
   if (n_st > 0) {
     ensure_window(kb);
     load_prefix(kb, read_blk(kb));
-    store_tile(lds);
   }
   if (n_st > 1) {
     ensure_window(kb + ST_KEYS);
-    load_prefix(kb + ST_KEYS, read_blk(kb + ST_KEYS));
-    store_tile(lds + BUF);
+    load_prefix_to(kb + ST_KEYS, read_blk(kb + ST_KEYS), k1reg, v1reg);
   }
+  if (n_st > 0) store_tile(lds);
+  if (n_st > 1) store_tile_from(lds + BUF, k1reg, v1reg);
   int pf_blk = -1;  // block id for the next tile to load (tile it+2 at step it)
   if (n_st > 2) {
     ensure_window(kb + 2 * ST_KEYS);
