@@ -661,21 +661,77 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   };
   f32x16_t s_alt;
   int it = 0;
+  // Fully visible tiles run in a loop that never rescales O (a rescale in
+  // the loop makes the compiler copy the accumulators every step).  The
+  // workgroup's first tile (peeled: O is still zero) sets each row's
+  // reference; a later tile with a score more than RESCALE_THRESH above it --
+  // never for ordinary inputs -- is only recorded, and the workgroup then
+  // recomputes its prefix range exactly (after the masked tiles).
+  bool hot_seen = false;
+  u32x4_t p[1][2];
+  auto fetch_ahead = [&](int t) {
+    if (t + 2 < n_st) {
+      load_prefix(kb + (t + 2) * ST_KEYS, pf_blk);
+      if (t + 3 < n_st) {
+        ensure_window(kb + (t + 3) * ST_KEYS);
+        pf_blk = read_blk(kb + (t + 3) * ST_KEYS);
+      }
+    }
+  };
+  auto finish_step = [&](int t) {
+    phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
+    if (t + 2 < n_st) store_tile(lds + ((t + 2) % NBUF) * BUF);
+    __syncthreads();
+  };
+  // tile 0 (and S^T of tile 1): exact weights, O still zero
+  auto peel = [&]() {
+    fetch_ahead(0);
+    phase_a1<DT, SOFTCAP>(lds + BUF, ks * 32, lane, qf, s_cur, s_alt, st, c, cap, p);
+    f32x16_t zo[4] = {};
+    const uint32_t vis[1] = {0xFFFFu};
+    const f32x16_t s1[1] = {s_cur};
+    weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, zo);
+    finish_step(0);
+    s_cur = s_alt;
+    it = 1;
+  };
+  // fast steps over tiles [it, t_end): S^T alternates between s_cur and s_alt
+  auto fast_steps = [&](int t_end) {
+    for (; it + 1 < t_end; it += 2) {
+      fetch_ahead(it);
+      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_cur, s_alt, st, c,
+                                        cap, p);
+      finish_step(it);
+      fetch_ahead(it + 1);
+      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 2) % NBUF) * BUF, ks * 32, lane, qf, s_alt, s_cur, st, c,
+                                        cap, p);
+      finish_step(it + 1);
+    }
+    if (it < t_end) {
+      fetch_ahead(it);
+      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_cur, s_alt, st, c,
+                                        cap, p);
+      finish_step(it);
+      s_cur = s_alt;
+      ++it;
+    }
+  };
+  // prefill: the last key this lane's row sees
+  const int lim = PREFILL ? (row_ok ? ctx + my_qi : -1) : 0;
   if constexpr (PREFILL) {
     // tiles below the workgroup's first query token's position are visible to
     // every row: pipelined steps; the rest (the causal edge, at most three
     // tiles for 128 rows) step one at a time with a per-row mask
     const int n_pipe = min((ctx + row_base / G + 1) / ST_KEYS, n_st - 1);
-    const int lim = row_ok ? ctx + my_qi : -1;  // last key this lane's row sees
-    for (; it + 2 <= n_pipe; it += 2) {
-      prefix_step(it, s_cur, s_alt);
-      prefix_step(it + 1, s_alt, s_cur);
-    }
-    if (it < n_pipe) {
-      prefix_step(it, s_cur, s_alt);
+    if (n_pipe >= 2) {
+      peel();
+      fast_steps(n_pipe);
+    } else if (n_pipe == 1) {
+      prefix_step(0, s_cur, s_alt);
       s_cur = s_alt;
-      ++it;
+      it = 1;
     }
+    if (hot_seen && lane == 0) hot_flag = 1;
     for (; it < n_st; ++it) {
       const bool fetch = it + 2 < n_st;
       if (fetch) {
@@ -699,39 +755,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       __syncthreads();
     }
   } else {
-    // Fully visible tiles but the last two run in a loop that never rescales
-    // O (a rescale in the loop makes the compiler copy the accumulators every
-    // step).  The workgroup's first tile (peeled: O is still zero) sets each
-    // row's reference; a later tile with a score more than RESCALE_THRESH
-    // above it -- never for ordinary inputs -- is only recorded, and the
-    // workgroup then recomputes its prefix range exactly.
-    bool hot_seen = false;
-    u32x4_t p[1][2];
-    auto fetch_ahead = [&](int t) {
-      if (t + 2 < n_st) {
-        load_prefix(kb + (t + 2) * ST_KEYS, pf_blk);
-        if (t + 3 < n_st) {
-          ensure_window(kb + (t + 3) * ST_KEYS);
-          pf_blk = read_blk(kb + (t + 3) * ST_KEYS);
-        }
-      }
-    };
-    auto finish_step = [&](int t) {
-      phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
-      if (t + 2 < n_st) store_tile(lds + ((t + 2) % NBUF) * BUF);
-      __syncthreads();
-    };
-    if (n_st >= 3) {
-      fetch_ahead(0);
-      phase_a1<DT, SOFTCAP>(lds + BUF, ks * 32, lane, qf, s_cur, s_alt, st, c, cap, p);
-      f32x16_t zo[4] = {};
-      const uint32_t vis[1] = {0xFFFFu};
-      const f32x16_t s1[1] = {s_cur};
-      weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, zo);
-      finish_step(0);
-      s_cur = s_alt;
-      it = 1;
-    }
+    // the last two tiles take the general step
+    if (n_st >= 3) peel();
     for (; it + 2 < n_st; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
       fetch_ahead(it);
       hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_cur, s_alt, st, c,
@@ -749,28 +774,31 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     } else if (it < n_st) {
       last_step(it, s_cur);
     }
-    __syncthreads();
-    if (hot_flag) {
-      // exact recomputation of the workgroup's prefix range, one tile at a
-      // time through buffer 0, every tile on the exact path
-      st = RowState{-INFINITY, 0.f};
+  }
+  __syncthreads();
+  if (hot_flag) {
+    // exact recomputation of the workgroup's prefix range, one tile at a time
+    // through buffer 0, every tile on the exact (masked) path
+    st = RowState{-INFINITY, 0.f};
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
-      for (int t = 0; t < n_st; ++t) {
-        ensure_window(kb + t * ST_KEYS);
-        load_prefix(kb + t * ST_KEYS, read_blk(kb + t * ST_KEYS));
-        store_tile(lds);
-        __syncthreads();
-        const int nk = t == n_st - 1 ? p_last : ST_KEYS;
-        uint32_t v = 0;
+    for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
+    for (int t = 0; t < n_st; ++t) {
+      ensure_window(kb + t * ST_KEYS);
+      load_prefix(kb + t * ST_KEYS, read_blk(kb + t * ST_KEYS));
+      store_tile(lds);
+      __syncthreads();
+      const int nk = t == n_st - 1 ? p_last : ST_KEYS;
+      uint32_t v = 0;
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) v |= (ks * 32 + 16 * (rr >> 3) + 8 * lhalf + (rr & 7) < nk ? 1u : 0u) << rr;
-        const uint32_t vis[1] = {v};
-        const f32x16_t s1[1] = {qk_half<DT>(lds, ks * 32, lane, qf)};
-        weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, p, o);
-        pv<DT, 1>(lds, ks * 32, lane, p, o);
-        __syncthreads();
+      for (int rr = 0; rr < 16; ++rr) {
+        const int kl = ks * 32 + 16 * (rr >> 3) + 8 * lhalf + (rr & 7);  // key within the tile
+        v |= (PREFILL ? t * ST_KEYS + kl <= lim : kl < nk) ? 1u << rr : 0u;
       }
+      const uint32_t vis[1] = {v};
+      const f32x16_t s1[1] = {qk_half<DT>(lds, ks * 32, lane, qf)};
+      weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, p, o);
+      pv<DT, 1>(lds, ks * 32, lane, p, o);
+      __syncthreads();
     }
   }
 
