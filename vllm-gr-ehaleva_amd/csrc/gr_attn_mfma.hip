@@ -45,6 +45,7 @@ constexpr int BUF = K_TILE + V_TILE;  // elements per buffer
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESH = 60.0f;  // log2 units a key may exceed the reference
 constexpr float RESCALE_SUM = 1.152921504606846976e18f;  // 2^RESCALE_THRESH: a lane weight sum above it forces the exact path
+static_assert(RESCALE_THRESH == 60.0f && RESCALE_SUM == (float)(1ull << 60), "RESCALE_SUM is 2^RESCALE_THRESH");
 constexpr int PBT_WIN = 2048;  // prefix block-table entries staged in LDS
 constexpr int NBUF = 3;        // LDS tile buffers (V of tile t, K of tile t+1, fill of tile t+2)
 constexpr int NBUF_ALLOC = 4;  // buffers allocated: the suffix holds two tiles (two buffers each)

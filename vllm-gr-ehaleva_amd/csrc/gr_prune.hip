@@ -164,11 +164,6 @@ __device__ inline float wave_max(float v) {
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
   return v;
 }
-__device__ inline int wave_sum_i(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
 
 // block-wide exclusive scan of one int per thread (NT threads); returns the total
 template <int NT = PR_THREADS>
@@ -1121,8 +1116,8 @@ __global__ __launch_bounds__(MG_LIST_THREADS) void prune_merge_lists(PruneArgs a
             const uint64_t km = lk[idx];
             const int64_t fm = lf[idx];
             const bool before = (km > ke) | ((km == ke) & (fm < fe));
-            lo[j] = open & before ? mid + 1 : lo[j];
-            hi[j] = open & !before ? mid : hi[j];
+            lo[j] = (open & before) ? mid + 1 : lo[j];
+            hi[j] = (open & !before) ? mid : hi[j];
           }
         }
       }
