@@ -11,7 +11,8 @@
 // the XCD under round-robin dispatch) so their prefix re-reads hit that
 // XCD's L2.  Each beam's short suffix is read from its own paged blocks into
 // masked 32-key tiles after the prefix, with the same online softmax; the two
-// key halves are merged in LDS at the end.  One launch, no gather/merge
+// waves of a row group (two partial states) are merged in LDS at the end.
+// One launch, no gather/merge
 // passes over HBM (contrast beam_attn.py:656-699).
 //
 // MFMA formulation (v_mfma_f32_32x32x16_{bf16,f16}, wave64):
@@ -47,8 +48,8 @@ constexpr float RESCALE_THRESH = 60.0f;  // log2 units a key may exceed the refe
 constexpr float RESCALE_SUM = 1.152921504606846976e18f;  // 2^RESCALE_THRESH: a lane weight sum above it forces the exact path
 static_assert(RESCALE_THRESH == 60.0f && RESCALE_SUM == (float)(1ull << 60), "RESCALE_SUM is 2^RESCALE_THRESH");
 constexpr int PBT_WIN = 2048;  // prefix block-table entries staged in LDS
-constexpr int NBUF = 3;        // LDS tile buffers (V of tile t, K of tile t+1, fill of tile t+2)
-constexpr int NBUF_ALLOC = 4;  // buffers allocated: the suffix holds two tiles (two buffers each)
+constexpr int NBUF = 3;        // prefix tile buffers (V of tile t, K of tile t+1, fill of tile t+2)
+constexpr int NBUF_ALLOC = 4;  // buffers allocated: a suffix tile pair takes four
 constexpr int SB_STAGE = 2;    // suffix block ids staged in LDS per beam (more are read from HBM)
 
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
@@ -607,10 +608,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     }
   };
   auto store_tile = [&](uint16_t* buf) { store_tile_from(buf, kreg, vreg); };
-  // Three LDS buffers: during step t the wave reads V of tile t, K of tile
+  // LDS tile buffers: during step t a wave reads V of tile t and K of tile
   // t+1, while tile t+2 (loaded into registers at the start of the step) is
-  // stored into the third buffer at its end.
-  // (the first two tiles' loads are both issued before either is stored)
+  // stored into its buffer at the end (tile t in buffer t % NBUF).  The
+  // first two tiles' loads are both issued before either is stored.
   u32x4_t k1reg[2], v1reg[2];
   if (n_st > 0) {
     ensure_window(kb);
@@ -804,8 +805,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   }
 
   // ---- suffix: each row group's beams' own tokens, masked 32-key tiles ----
-  // (computed by the key-half-0 wave of each row group; all threads load;
-  // the group's metadata was staged in the prologue)
+  // (all threads load; the two waves of a row group compute a pair of tiles
+  // side by side; the group's metadata was staged in the prologue)
   int max_tot = 0;
 #pragma unroll
   for (int g = 0; g < 4; ++g) max_tot = max(max_tot, suf_cum[g][32]);
