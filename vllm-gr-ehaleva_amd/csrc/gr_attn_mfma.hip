@@ -12,8 +12,7 @@
 // XCD's L2.  Each beam's short suffix is read from its own paged blocks into
 // masked 32-key tiles after the prefix, with the same online softmax; the two
 // waves of a row group (two partial states) are merged in LDS at the end.
-// One launch, no gather/merge
-// passes over HBM (contrast beam_attn.py:656-699).
+// One launch, no gather/merge passes over HBM (contrast beam_attn.py:656-699).
 //
 // MFMA formulation (v_mfma_f32_32x32x16_{bf16,f16}, wave64):
 //   S^T[key][row]  = K[key][:] . Q[row][:]    A = K tile, B = Q^T (registers)
