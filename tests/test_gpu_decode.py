@@ -270,3 +270,24 @@ def test_decode_dominant_key(device, split, pos):
     ref, ref_lse = run_oracle(wl)
     assert ref_lse[n, h] > 50.0
     _check(out, lse, ref, ref_lse, atol=2e-2)
+
+
+@pytest.mark.parametrize("dtype,softcap", [(torch.float16, 0.0), (torch.bfloat16, 30.0), (torch.float16, 30.0)])
+def test_decode_dominant_key_fp16_softcap(device, dtype, softcap):
+    """The exact recomputation in the fp16 and soft-capped instantiations: a
+    key in a pipelined tile dominates one row (with a soft cap of 30 the
+    score range is still 2 * 30 * log2(e) ~ 86 log2 units, above the 60 of
+    the lazy-rescale margin)."""
+    wl = workloads.make_decode(R=2, W=32, P=530, L=(1, 6), Hq=32, Hkv=8, D=128, dtype=dtype,
+                               input_scale=1.0, seed=43, softcap=softcap)
+    r, b, h = 0, 7, 1
+    n = int(wl.beam_start[r]) + b
+    q = wl.q[n, h].float()
+    pos = 200
+    blk = int(wl.prefix_bt[r, pos // wl.block_size])
+    wl.kv_cache[0, blk, pos % wl.block_size, 0] = (q / q.norm() * 60.0).to(dtype)
+    print(f"[decode] dominant key {dtype} softcap={softcap}", flush=True)
+    out, lse = run_gpu(wl, device, split=False)
+    ref, ref_lse = run_oracle(wl)
+    assert ref_lse[n, h] > (25.0 if softcap else 50.0)
+    _check(out, lse, ref, ref_lse, atol=2e-2)

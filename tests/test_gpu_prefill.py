@@ -142,19 +142,21 @@ def test_prefill_flags_inconsistent_request(device, kernel):
     assert np.all(out[int(qs[1]):int(qs[2])] == 7.0)
 
 
-@pytest.mark.parametrize("pos", [20, 300, 700, 1010, 1030])
-def test_prefill_dominant_key(device, pos):
+@pytest.mark.parametrize("pos,dtype", [(20, torch.bfloat16), (300, torch.bfloat16), (700, torch.bfloat16),
+                                       (1010, torch.bfloat16), (1030, torch.bfloat16), (300, torch.float16)])
+def test_prefill_dominant_key(device, pos, dtype):
     """A key planted to dominate one query row far beyond the lazy rescale
     margin: in the first tile, in the pipelined tiles (the workgroup's exact
     recomputation; 1010 is in the last of them for that row's workgroup) and
-    on the causal edge (1030, one of the request's own new tokens): every row
+    on the causal edge (1030, one of the request's own new tokens), and in
+    fp16, whose P operand bounds the lazy-rescale margin at 2^15: every row
     matches the oracle, the planted row's LSE included."""
     ctx, ql = 1000, 64
-    q, kv, bt, qs, seqs = _case([ql], [ctx], 16, 4, 128, torch.bfloat16, seed=23)
+    q, kv, bt, qs, seqs = _case([ql], [ctx], 16, 4, 128, dtype, seed=23)
     qi, h = 40, 5  # query token 40 (sees keys 0 .. ctx + 40), query head 5 (KV head 1)
     qv = q[qi, h].float()
     blk = int(bt[0, pos // BS])
-    kv[0, blk, pos % BS, h // 4] = (qv / qv.norm() * 60.0).to(torch.bfloat16)
+    kv[0, blk, pos % BS, h // 4] = (qv / qv.norm() * 60.0).to(dtype)
     out, lse, status = _run(device, q, kv, bt, qs, seqs, 128 ** -0.5)
     ops.check_status(status)
     ref, ref_lse = _oracle(q, kv, bt, qs, seqs, 128 ** -0.5)

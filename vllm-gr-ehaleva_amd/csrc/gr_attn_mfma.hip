@@ -43,9 +43,22 @@ constexpr int K_TILE = ST_KEYS * KS_PITCH;
 constexpr int V_TILE = ST_KEYS * VS_PITCH;
 constexpr int BUF = K_TILE + V_TILE;  // elements per buffer
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr float RESCALE_THRESH = 60.0f;  // log2 units a key may exceed the reference
-constexpr float RESCALE_SUM = 1.152921504606846976e18f;  // 2^RESCALE_THRESH: a lane weight sum above it forces the exact path
-static_assert(RESCALE_THRESH == 60.0f && RESCALE_SUM == (float)(1ull << 60), "RESCALE_SUM is 2^RESCALE_THRESH");
+// Lazy softmax reference: a key may exceed the row's reference by up to
+// Rescale::THRESH log2 units before the exact path moves the reference; a lane
+// weight sum above 2^Rescale::THRESH forces it.  The packed P operand bounds
+// the margin: 60 for bf16 (range to 2^127), 15 for fp16 (largest finite value
+// 65504 < 2^16).
+template <int DT> struct Rescale;
+template <> struct Rescale<GR_DTYPE_BF16> {
+  static constexpr float THRESH = 60.0f;
+  static constexpr float SUM = 1.152921504606846976e18f;  // 2^60
+};
+template <> struct Rescale<GR_DTYPE_F16> {
+  static constexpr float THRESH = 15.0f;
+  static constexpr float SUM = 32768.0f;  // 2^15
+};
+static_assert(Rescale<GR_DTYPE_BF16>::SUM == (float)(1ull << 60) && Rescale<GR_DTYPE_F16>::SUM == (float)(1 << 15),
+              "Rescale::SUM is 2^THRESH");
 constexpr int PBT_WIN = 2048;  // prefix block-table entries staged in LDS
 constexpr int NBUF = 3;        // prefix tile buffers (V of tile t, K of tile t+1, fill of tile t+2)
 constexpr int NBUF_ALLOC = 4;  // buffers allocated: a suffix tile pair takes four
@@ -137,8 +150,8 @@ __device__ inline float score_l2(float v, float c, float cap) {
 // mref (log2 domain), with no tile maximum: the branch-free common case.
 // Weights are packed pairwise as they are produced (p0: registers 0..7, p1:
 // 8..15).  Returns the lane's weight sum.  The caller sends the tile to
-// softmax_exact when any lane's sum exceeds 2^RESCALE_THRESH (some key is
-// more than RESCALE_THRESH above the reference) or is not finite (the row
+// softmax_exact when any lane's sum exceeds 2^Rescale::THRESH (some key is
+// more than Rescale::THRESH above the reference) or is not finite (the row
 // has no reference yet: mref = -inf makes every visible weight +inf).
 template <int DT, bool SOFTCAP, bool MASKED>
 __device__ inline float softmax_fast(const f32x16_t& s, uint32_t vis, float mref, float c, float cap,
@@ -211,7 +224,7 @@ __device__ inline void pv(const uint16_t* buf, int kbase, int lane, const u32x4_
 
 // Weights of NH half-tiles of the wave's rows (one row per lane pair): the
 // branch-free fast path against the row's reference, or -- when some weight
-// could exceed 2^RESCALE_THRESH or the row has no reference yet -- the exact
+// could exceed 2^Rescale::THRESH or the row has no reference yet -- the exact
 // path that moves the reference to the maximum over all NH halves and scales
 // O (skipped while the row has accumulated nothing).
 template <int DT, bool SOFTCAP, bool MASKED, int NH>
@@ -222,7 +235,7 @@ __device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
     const float a_h = softmax_fast<DT, SOFTCAP, MASKED>(s[h], vis[h], st.m, c, cap, p[h][0], p[h][1]);
-    hot |= !(a_h <= RESCALE_SUM);
+    hot |= !(a_h <= Rescale<DT>::SUM);
     acc += a_h;
   }
   if (__ballot(hot) == 0) {
@@ -230,7 +243,7 @@ __device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH
     return;
   }
   // exact path (wave-uniform; after a row's first tile it needs a score more
-  // than RESCALE_THRESH log2 units above everything before it).  The empty
+  // than Rescale::THRESH log2 units above everything before it).  The empty
   // volatile asm keeps the compiler from speculating this rare work into the
   // common path.
   __asm__ volatile("" ::: "memory");
@@ -265,7 +278,7 @@ __device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH
 // scores of the current tile against the row's reference.  s_in holds S^T of
 // the current tile, s_out receives that of the next tile (the caller
 // alternates two register sets: no copies).  Returns true when some weight
-// could exceed 2^RESCALE_THRESH or the row has no reference yet (the tile then
+// could exceed 2^Rescale::THRESH or the row has no reference yet (the tile then
 // needs the exact path); otherwise adds the weight sum to the row's state.
 template <int DT, bool SOFTCAP>
 __device__ inline bool phase_a1(const uint16_t* next_buf, int kbase, int lane, const u32x4_t (&qf)[8],
@@ -297,7 +310,7 @@ __device__ inline bool phase_a1(const uint16_t* next_buf, int kbase, int lane, c
   p[0][0] = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
   p[0][1] = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
   const float acc = acc0 + acc1;
-  if (__ballot(!(acc <= RESCALE_SUM)) != 0) return true;
+  if (__ballot(!(acc <= Rescale<DT>::SUM)) != 0) return true;
   st.lsum += acc;
   return false;
 }
@@ -665,7 +678,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // Fully visible tiles run in a loop that never rescales O (a rescale in
   // the loop makes the compiler copy the accumulators every step).  The
   // workgroup's first tile (peeled: O is still zero) sets each row's
-  // reference; a later tile with a score more than RESCALE_THRESH above it --
+  // reference; a later tile with a score more than Rescale::THRESH above it --
   // never for ordinary inputs -- is only recorded, and the workgroup then
   // recomputes its prefix range exactly (after the masked tiles).
   bool hot_seen = false;
