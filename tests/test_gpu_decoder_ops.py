@@ -55,13 +55,16 @@ def test_rms_norm(device, dtype, H, with_res):
     assert _rel_err(out, ref) <= TOL[dtype] * 1.01
 
 
-@pytest.mark.parametrize("dtype,D,heads", [(torch.bfloat16, 128, (16, 8)), (torch.float32, 32, (4, 2)),
-                                           (torch.float16, 256, (4, 4)), (torch.bfloat16, 64, (6, 2)),
-                                           (torch.bfloat16, 40, (3, 1))])  # 40: the scalar form
-def test_qk_norm_rope_cache(device, dtype, D, heads):
+@pytest.mark.parametrize("dtype,D,heads,T", [(torch.bfloat16, 128, (16, 8), 53), (torch.float32, 32, (4, 2), 53),
+                                             (torch.float16, 256, (4, 4), 53), (torch.bfloat16, 64, (6, 2), 53),
+                                             (torch.bfloat16, 40, (3, 1), 53),  # 40: the scalar form
+                                             # four tokens per workgroup, a partial last group
+                                             (torch.bfloat16, 128, (16, 8), 2051), (torch.float32, 64, (4, 1), 1025)])
+def test_qk_norm_rope_cache(device, dtype, D, heads, T):
     Hq, Hkv = heads
     g = torch.Generator().manual_seed(D + Hq)
-    T, NB, BS, maxpos = 53, 12, 16, 40000
+    BS, maxpos = 16, 40000
+    NB = T // BS + 9
     qkv = torch.randn(T, (Hq + 2 * Hkv) * D, generator=g).to(dtype)
     qn = (torch.rand(D, generator=g) + 0.5).to(dtype)
     kn = (torch.rand(D, generator=g) + 0.5).to(dtype)
@@ -73,7 +76,7 @@ def test_qk_norm_rope_cache(device, dtype, D, heads):
     rope = RotaryEmbedding(D, 1.0e6, maxpos, device)
     kv = kv0.to(device)
     status = ops.new_status(device)
-    print(f"[ops] qk_norm_rope_cache {dtype} D={D} heads={heads}", flush=True)
+    print(f"[ops] qk_norm_rope_cache {dtype} D={D} heads={heads} T={T}", flush=True)
     q = ops.qk_norm_rope_cache(qkv.to(device), pos.to(device), rope.cos, rope.sin, qn.to(device), kn.to(device),
                                kv[0], kv[1], slots.to(device), num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D,
                                eps=1e-6, status=status)

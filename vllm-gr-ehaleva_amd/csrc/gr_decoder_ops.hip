@@ -185,90 +185,108 @@ __global__ __launch_bounds__(EW_THREADS) void qk_norm_rope_k(RopeArgs a, int hgr
 // L = D / EPL lanes (a power of two, 2 .. 64), a wave covers 64 / L heads and
 // a workgroup 4 times that.  Lane j of a head holds elements
 // [EPL*j, EPL*j + EPL); the rotary partner of its elements is lane j ^ L/2.
-template <int DT>
-__global__ __launch_bounds__(EW_THREADS) void qk_norm_rope_vec_k(RopeArgs a, int hgroups, int L) {
+// A workgroup takes NT consecutive tokens and issues all their row, position
+// and slot loads before it computes any (one 16-byte load in flight per lane
+// leaves the chip's memory latency exposed on long prompts).
+template <typename S>
+struct alignas(16) Vec16 {
+  S e[16 / sizeof(S)];
+};
+
+template <int DT, int NT>
+__global__ __launch_bounds__(EW_THREADS) void qk_norm_rope_vec_k(RopeArgs a, int hgroups, int L, int num_tokens) {
   using E = Elem<DT>;
   using S = typename E::storage;
+  using Vec = Vec16<S>;
   constexpr int EPL = 16 / sizeof(S);
-  struct alignas(16) Vec { S e[EPL]; };
-  const int64_t t = blockIdx.x / hgroups;
+  const int64_t t0 = (int64_t)(blockIdx.x / hgroups) * NT;
   const int lane = threadIdx.x & 63;
   const int hpw = 64 / L;  // heads per wave
   const int h = ((blockIdx.x % hgroups) * (EW_THREADS / 64) + (threadIdx.x >> 6)) * hpw + lane / L;
   const int j = lane % L;  // lane within the head
   const int nheads = a.Hq + 2 * a.Hkv;
   const int D = a.D, half = D >> 1;
-  const int64_t pos = a.positions[t];
-  if (pos < 0 || pos >= a.table_len) {
-    if (h == 0 && j == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
-    return;
+  const bool valid = h < nheads;
+  const int hc = valid ? h : 0;  // clamped: every lane joins the shuffles
+  const bool is_v = hc >= a.Hq + a.Hkv, is_q = hc < a.Hq;
+  Vec xv[NT];
+  int64_t pos[NT], slot[NT];
+#pragma unroll
+  for (int u = 0; u < NT; ++u) {
+    const int64_t t = min(t0 + u, (int64_t)num_tokens - 1);  // clamped: loads stay in bounds
+    xv[u] = *reinterpret_cast<const Vec*>(static_cast<const S*>(a.qkv) + t * a.qkv_stride + (int64_t)hc * D +
+                                          j * EPL);
+    pos[u] = a.positions[t];
+    slot[u] = a.slot_mapping ? a.slot_mapping[t] : -1;
   }
-  int64_t kv_off = -1;
-  if (a.slot_mapping) {
-    const int64_t slot = a.slot_mapping[t];
-    if (slot >= 0) {
-      const int64_t blk = slot / a.bs;
+  const S* nw = static_cast<const S*>(is_q ? a.q_norm : a.k_norm);
+  const bool second = j >= (L >> 1);    // this lane holds the second half of its pairs
+  const int i0 = (j % (L >> 1)) * EPL;  // pair index of element 0
+  const int pj = j ^ (L >> 1);
+  Vec wv{}, pw{};
+  if (nw && valid && !is_v) {
+    wv = *reinterpret_cast<const Vec*>(nw + j * EPL);
+    pw = *reinterpret_cast<const Vec*>(nw + pj * EPL);
+  }
+  // one token; every branch before the shuffles is uniform over the workgroup
+  auto one = [&](int64_t t, const Vec& x_v, int64_t p_t, int64_t s_t) {
+    if (p_t < 0 || p_t >= a.table_len) {
+      if (h == 0 && j == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+      return;
+    }
+    int64_t kv_off = -1;
+    if (s_t >= 0) {
+      const int64_t blk = s_t / a.bs;
       if (blk < a.num_blocks) {
-        kv_off = blk * a.kv_block_stride + (slot % a.bs) * a.kv_tok_stride;
+        kv_off = blk * a.kv_block_stride + (s_t % a.bs) * a.kv_tok_stride;
       } else if (h == 0 && j == 0) {
         flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
       }
     }
-  }
-  const bool valid = h < nheads;
-  const int hc = valid ? h : 0;  // clamped: every lane joins the shuffles
-  const Vec xv = *reinterpret_cast<const Vec*>(static_cast<const S*>(a.qkv) + t * a.qkv_stride +
-                                               (int64_t)hc * D + j * EPL);
-  const bool is_v = hc >= a.Hq + a.Hkv, is_q = hc < a.Hq;
-  float x[EPL], p[EPL];
-  float ss = 0.f;
+    float x[EPL], p[EPL];
+    float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    x[e] = E::to_float(xv.e[e]);
-    ss += x[e] * x[e];
-  }
-  // partner elements (lane j ^ L/2) and the head's sum of squares
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) p[e] = __shfl_xor(x[e], L >> 1, 64);
-  for (int off = 1; off < L; off <<= 1) ss += __shfl_xor(ss, off, 64);
-  if (!valid) return;
-  if (is_v) {
-    if (kv_off >= 0)
-      *reinterpret_cast<Vec*>(static_cast<S*>(a.v_cache) + kv_off + (int64_t)(hc - a.Hq - a.Hkv) * a.kv_head_stride +
-                              j * EPL) = xv;
-    return;
-  }
-  S* dst;
-  if (is_q) {
-    dst = static_cast<S*>(a.q_out) + t * a.q_out_stride + (int64_t)hc * D;
-  } else {
-    if (kv_off < 0) return;
-    dst = static_cast<S*>(a.k_cache) + kv_off + (int64_t)(hc - a.Hq) * a.kv_head_stride;
-  }
-  const S* nw = static_cast<const S*>(is_q ? a.q_norm : a.k_norm);
-  const float inv = nw ? 1.0f / sqrtf(ss / (float)D + a.eps) : 1.f;
-  const bool second = j >= (L >> 1);  // this lane holds the second half of its pairs
-  const int i0 = (j % (L >> 1)) * EPL;  // pair index of element 0
-  const int pj = j ^ (L >> 1);
-  Vec wv{}, pw{};
-  if (nw) {
-    wv = *reinterpret_cast<const Vec*>(nw + j * EPL);
-    pw = *reinterpret_cast<const Vec*>(nw + pj * EPL);
-  }
-  const float* ct = a.cos_t + pos * half + i0;
-  const float* st = a.sin_t + pos * half + i0;
-  Vec ov;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    float y = x[e] * inv, q = p[e] * inv;
-    if (nw) {
-      y *= E::to_float(wv.e[e]);
-      q *= E::to_float(pw.e[e]);
+    for (int e = 0; e < EPL; ++e) {
+      x[e] = E::to_float(x_v.e[e]);
+      ss += x[e] * x[e];
     }
-    const float c = ct[e], sn = st[e];
-    ov.e[e] = E::from_float(second ? y * c + q * sn : y * c - q * sn);
-  }
-  *reinterpret_cast<Vec*>(dst + j * EPL) = ov;
+    // partner elements (lane j ^ L/2) and the head's sum of squares
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) p[e] = __shfl_xor(x[e], L >> 1, 64);
+    for (int off = 1; off < L; off <<= 1) ss += __shfl_xor(ss, off, 64);
+    if (!valid) return;
+    if (is_v) {
+      if (kv_off >= 0)
+        *reinterpret_cast<Vec*>(static_cast<S*>(a.v_cache) + kv_off +
+                                (int64_t)(hc - a.Hq - a.Hkv) * a.kv_head_stride + j * EPL) = x_v;
+      return;
+    }
+    S* dst;
+    if (is_q) {
+      dst = static_cast<S*>(a.q_out) + t * a.q_out_stride + (int64_t)hc * D;
+    } else {
+      if (kv_off < 0) return;
+      dst = static_cast<S*>(a.k_cache) + kv_off + (int64_t)(hc - a.Hq) * a.kv_head_stride;
+    }
+    const float inv = nw ? 1.0f / sqrtf(ss / (float)D + a.eps) : 1.f;
+    const float* ct = a.cos_t + p_t * half + i0;
+    const float* st = a.sin_t + p_t * half + i0;
+    Vec ov;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float y = x[e] * inv, q = p[e] * inv;
+      if (nw) {
+        y *= E::to_float(wv.e[e]);
+        q *= E::to_float(pw.e[e]);
+      }
+      const float c = ct[e], sn = st[e];
+      ov.e[e] = E::from_float(second ? y * c + q * sn : y * c - q * sn);
+    }
+    *reinterpret_cast<Vec*>(dst + j * EPL) = ov;
+  };
+#pragma unroll
+  for (int u = 0; u < NT; ++u)
+    if (t0 + u < num_tokens) one(t0 + u, xv[u], pos[u], slot[u]);
 }
 
 // ---- SiLU-gated product: out[t, i] = silu(x[t, i]) * x[t, F + i] -----------
@@ -292,6 +310,14 @@ __global__ __launch_bounds__(EW_THREADS) void silu_mul_k(void* out, int64_t out_
     o.e[j] = E::from_float(sg * E::to_float(u.e[j]));
   }
   *reinterpret_cast<Vec*>(static_cast<S*>(out) + t * out_stride + i) = o;
+}
+
+template <int DT>
+void launch_rope_vec(dim3 grid, hipStream_t stream, const RopeArgs& a, int hg, int L, int num_tokens, int nt) {
+  if (nt == 4)
+    hipLaunchKernelGGL((qk_norm_rope_vec_k<DT, 4>), grid, dim3(EW_THREADS), 0, stream, a, hg, L, num_tokens);
+  else
+    hipLaunchKernelGGL((qk_norm_rope_vec_k<DT, 1>), grid, dim3(EW_THREADS), 0, stream, a, hg, L, num_tokens);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -364,13 +390,15 @@ extern "C" gr_status_t gr_qk_norm_rope_cache(
   if (vec) {
     const int per_wg = (EW_THREADS / 64) * (64 / L);
     const int hg = (nheads + per_wg - 1) / per_wg;
-    const int64_t nwg = (int64_t)num_tokens * hg;
+    // four tokens per workgroup once there are enough tokens to fill the chip
+    const int nt = num_tokens >= 1024 ? 4 : 1;
+    const int64_t nwg = (int64_t)((num_tokens + nt - 1) / nt) * hg;
     if (nwg > 0x7fffffff) return GR_ERR_INVALID_ARG;
     dim3 grid((unsigned)nwg);
     switch (dtype) {
-      case GR_DTYPE_F32: hipLaunchKernelGGL(qk_norm_rope_vec_k<GR_DTYPE_F32>, grid, dim3(EW_THREADS), 0, stream, a, hg, L); break;
-      case GR_DTYPE_F16: hipLaunchKernelGGL(qk_norm_rope_vec_k<GR_DTYPE_F16>, grid, dim3(EW_THREADS), 0, stream, a, hg, L); break;
-      default: hipLaunchKernelGGL(qk_norm_rope_vec_k<GR_DTYPE_BF16>, grid, dim3(EW_THREADS), 0, stream, a, hg, L); break;
+      case GR_DTYPE_F32: launch_rope_vec<GR_DTYPE_F32>(grid, stream, a, hg, L, num_tokens, nt); break;
+      case GR_DTYPE_F16: launch_rope_vec<GR_DTYPE_F16>(grid, stream, a, hg, L, num_tokens, nt); break;
+      default: launch_rope_vec<GR_DTYPE_BF16>(grid, stream, a, hg, L, num_tokens, nt); break;
     }
     return launch_status();
   }
