@@ -32,7 +32,7 @@ def _rel_err(got, ref):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
-@pytest.mark.parametrize("H", [2048, 100])
+@pytest.mark.parametrize("H", [2048, 100, 1000, 5000])  # 1, 1 partial, 4 partial vectors per thread
 @pytest.mark.parametrize("with_res", [False, True])
 def test_rms_norm(device, dtype, H, with_res):
     g = torch.Generator().manual_seed(H + with_res)

@@ -102,6 +102,68 @@ struct RopeArgs {
   int32_t* dev_status;
 };
 
+// Register form of rms_norm_k for rows of at most 4 * EW_THREADS * V
+// elements: each thread keeps its NV vectors of y (and of the weight) in
+// registers from the first read, so the second pass re-reads nothing.  The
+// same roundings as rms_norm_k, so the same results bit for bit.
+template <int DT, int V, int NV>
+__global__ __launch_bounds__(EW_THREADS) void rms_norm_reg_k(RmsArgs a) {
+  using E = Elem<DT>;
+  using S = typename E::storage;
+  struct alignas(sizeof(S) * V) Vec { S e[V]; };
+  const int64_t t = blockIdx.x;
+  const S* x = static_cast<const S*>(a.x) + t * a.x_stride;
+  S* res = a.residual ? static_cast<S*>(a.residual) + t * a.res_stride : nullptr;
+  S* out = static_cast<S*>(a.out) + t * a.out_stride;
+  const S* w = static_cast<const S*>(a.weight);
+  const int H = a.hidden;
+  Vec yv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = (threadIdx.x + k * EW_THREADS) * V;
+    if (i < H) {
+      yv[k] = *reinterpret_cast<const Vec*>(x + i);
+      if (res) rv[k] = *reinterpret_cast<const Vec*>(res + i);
+      wv[k] = *reinterpret_cast<const Vec*>(w + i);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = (threadIdx.x + k * EW_THREADS) * V;
+    if (i < H) {
+      if (res) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) yv[k].e[j] = E::from_float(E::to_float(yv[k].e[j]) + E::to_float(rv[k].e[j]));
+        *reinterpret_cast<Vec*>(res + i) = yv[k];
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float y = E::to_float(yv[k].e[j]);
+        ss += y * y;
+      }
+    }
+  }
+  __shared__ float part[EW_THREADS / 64];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < EW_THREADS / 64; ++i) tot += part[i];
+  const float inv = 1.0f / sqrtf(tot / (float)H + a.eps);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = (threadIdx.x + k * EW_THREADS) * V;
+    if (i < H) {
+      Vec ov;
+#pragma unroll
+      for (int j = 0; j < V; ++j) ov.e[j] = E::from_float(E::to_float(yv[k].e[j]) * inv * E::to_float(wv[k].e[j]));
+      *reinterpret_cast<Vec*>(out + i) = ov;
+    }
+  }
+}
+
 // One wave per head: workgroup g covers heads 4*(g % hgroups) .. +3 of token
 // g / hgroups, over the token's Hq query, Hkv key and Hkv value heads (in
 // that order); lane l holds the rotary pairs (i, i + D/2), i = l, l + 64.
@@ -312,6 +374,17 @@ __global__ __launch_bounds__(EW_THREADS) void silu_mul_k(void* out, int64_t out_
   *reinterpret_cast<Vec*>(static_cast<S*>(out) + t * out_stride + i) = o;
 }
 
+// rms_norm launch: the register form when a row fits 4 vectors per thread
+template <int DT, int V>
+void launch_rms(dim3 grid, hipStream_t stream, const RmsArgs& a, bool vec) {
+  const int nv = vec ? (a.hidden + EW_THREADS * V - 1) / (EW_THREADS * V) : 0;
+  if (nv == 1) hipLaunchKernelGGL((rms_norm_reg_k<DT, V, 1>), grid, dim3(EW_THREADS), 0, stream, a);
+  else if (nv == 2) hipLaunchKernelGGL((rms_norm_reg_k<DT, V, 2>), grid, dim3(EW_THREADS), 0, stream, a);
+  else if (nv == 3 || nv == 4) hipLaunchKernelGGL((rms_norm_reg_k<DT, V, 4>), grid, dim3(EW_THREADS), 0, stream, a);
+  else if (vec) hipLaunchKernelGGL((rms_norm_k<DT, V>), grid, dim3(EW_THREADS), 0, stream, a);
+  else hipLaunchKernelGGL((rms_norm_k<DT, 1>), grid, dim3(EW_THREADS), 0, stream, a);
+}
+
 template <int DT>
 void launch_rope_vec(dim3 grid, hipStream_t stream, const RopeArgs& a, int hg, int L, int num_tokens, int nt) {
   if (nt == 4)
@@ -341,18 +414,9 @@ extern "C" gr_status_t gr_rms_norm(void* out, int64_t out_stride, const void* x,
                    (x_stride * es) % 16 == 0 && (!residual || (res_stride * es) % 16 == 0);
   dim3 grid((unsigned)num_tokens);
   switch (dtype) {
-    case GR_DTYPE_F32:
-      if (vec) hipLaunchKernelGGL((rms_norm_k<GR_DTYPE_F32, 4>), grid, dim3(EW_THREADS), 0, stream, a);
-      else hipLaunchKernelGGL((rms_norm_k<GR_DTYPE_F32, 1>), grid, dim3(EW_THREADS), 0, stream, a);
-      break;
-    case GR_DTYPE_F16:
-      if (vec) hipLaunchKernelGGL((rms_norm_k<GR_DTYPE_F16, 8>), grid, dim3(EW_THREADS), 0, stream, a);
-      else hipLaunchKernelGGL((rms_norm_k<GR_DTYPE_F16, 1>), grid, dim3(EW_THREADS), 0, stream, a);
-      break;
-    default:
-      if (vec) hipLaunchKernelGGL((rms_norm_k<GR_DTYPE_BF16, 8>), grid, dim3(EW_THREADS), 0, stream, a);
-      else hipLaunchKernelGGL((rms_norm_k<GR_DTYPE_BF16, 1>), grid, dim3(EW_THREADS), 0, stream, a);
-      break;
+    case GR_DTYPE_F32: launch_rms<GR_DTYPE_F32, 4>(grid, stream, a, vec); break;
+    case GR_DTYPE_F16: launch_rms<GR_DTYPE_F16, 8>(grid, stream, a, vec); break;
+    default: launch_rms<GR_DTYPE_BF16, 8>(grid, stream, a, vec); break;
   }
   return launch_status();
 }
