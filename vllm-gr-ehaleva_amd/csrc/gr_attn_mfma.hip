@@ -187,7 +187,8 @@ __device__ inline f32x16_t qk_half(const uint16_t* buf, int kbase, int lane, con
   const int lhalf = lane >> 5;
   f32x16_t s = {};
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) s = M::mma(lds_read16(krow + kchunk(krow_i, 2 * kk + lhalf) * 8), qf[kk], s);
+  for (int kk = 0; kk < 8; ++kk)
+    s = M::mma(lds_read16(krow + kchunk(krow_i, 2 * (kk & 3) + lhalf) * 8 + (kk >> 2) * 64), qf[kk], s);
   return s;
 }
 
@@ -288,7 +289,9 @@ __device__ inline bool phase_a1(const uint16_t* next_buf, int kbase, int lane, c
   const int lhalf = lane >> 5;
   const int krow_i = kbase + key_perm(lane & 31);
   const uint16_t* krow = next_buf + krow_i * KS_PITCH;
-  auto kfrag = [&](int kk) { return lds_read16(krow + kchunk(krow_i, 2 * kk + lhalf) * 8); };
+  // the swizzle leaves chunk bit 3 alone: fragments kk and kk + 4 sit 64
+  // elements apart, so four lane addresses serve all eight reads
+  auto kfrag = [&](int kk) { return lds_read16(krow + kchunk(krow_i, 2 * (kk & 3) + lhalf) * 8 + (kk >> 2) * 64); };
   const float mref = st.m;
   u32x4_t kf[8];
   kf[0] = kfrag(0);
