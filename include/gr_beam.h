@@ -269,6 +269,37 @@ gr_status_t gr_beam_prune_topk(
     int32_t* parent, int32_t* token, float* score, float* eos_score,
     void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * gr_beam_prune_topk / gr_beam_prune_topk_catalog with the beam scores
+ * carried in float64 between steps.
+ *
+ * The reference keeps each beam's cumulative logprob as a Python float
+ * (float64) from step to step and adds the new token's logprob to it in
+ * float64 (vllm_gr/entrypoints/openai/serving_engine.py:511, :538-539;
+ * offline twin vllm_gr/entrypoints/llm.py:231-245).  cum [R*W] float64 is
+ * used as is (c_b = cum[b] - lse[b]); score [R, k] and eos_score [R*W]
+ * receive the float64 scores themselves, not their float32 roundings, so a
+ * multi-step search never rounds a beam's score.  Selection, order, ties
+ * and workspace as in gr_beam_prune_topk.  beam_node == NULL: no catalog
+ * (the trie arguments and node_out are ignored); otherwise the catalog mode
+ * of gr_beam_prune_topk_catalog.
+ *
+ * cand_token / cand_logprob [R*W, k] (both NULL or both given) receive each
+ * beam's top-k by (logit desc, token asc) before EOS or the catalog take
+ * anything out, with logprob = float32(x - lse) -- the per-step lists the
+ * reference keeps for every beam and rebuilds along parent pointers
+ * (vllm_gr/logprobs.py:34-53 extract_and_dedup_flat_logprobs, :56-85
+ * reconstruct_beam_logprobs; vllm_gr/entrypoints/llm.py:203-220).
+ */
+gr_status_t gr_beam_prune_topk_f64(
+    const float* logits, int64_t logits_row_stride, const double* cum,
+    int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
+    const int32_t* beam_node, const int32_t* node_start, const int32_t* child_token,
+    const int32_t* child_node, int num_nodes, int num_edges,
+    int32_t* parent, int32_t* token, double* score, double* eos_score, int32_t* node_out,
+    int32_t* cand_token, float* cand_logprob,
+    void* workspace, size_t workspace_bytes, int32_t* dev_status, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

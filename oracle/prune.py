@@ -59,7 +59,7 @@ def _load():
         lib.oracle_prune_row_stats.argtypes = [P, P, ctypes.c_int, ctypes.c_int, P, P, P, P]
         lib.oracle_prune_topk.restype = ctypes.c_int
         lib.oracle_prune_topk.argtypes = [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                          ctypes.c_int, ctypes.c_int, P, P, P, P, P, P]
+                                          ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, P, P]
         _lib = lib
     return _lib
 
@@ -76,11 +76,17 @@ def log_f64(s: float) -> float:
     return float(_load().oracle_log_f64(float(s)))
 
 
+def _cum64(cum) -> np.ndarray:
+    """The cumulative scores as float64: a float32 array enters exactly."""
+    c = np.asarray(cum)
+    return c.astype(np.float64) if c.dtype != np.float64 else c
+
+
 def row_stats(logits: np.ndarray, cum: np.ndarray):
     """Per-row (max, fp32 exp-sum, lse, cum - lse) under the build contract."""
     x = np.ascontiguousarray(logits, dtype=np.float32)
     rows, V = x.reshape(-1, x.shape[-1]).shape
-    c_in = np.ascontiguousarray(np.broadcast_to(np.asarray(cum, np.float32).reshape(-1), (rows,)))
+    c_in = np.ascontiguousarray(np.broadcast_to(_cum64(cum).reshape(-1), (rows,)))
     m = np.empty(rows, np.float32)
     S = np.empty(rows, np.float32)
     lse = np.empty(rows, np.float64)
@@ -89,29 +95,42 @@ def row_stats(logits: np.ndarray, cum: np.ndarray):
     return m, S, lse, c
 
 
-def prune_topk(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id: int = -1, allowed=None):
-    """Bit-exact oracle.  ``logits [R, W, V]`` fp32, ``cum [R, W]`` fp32;
-    ``allowed [R, W, V]`` bool (optional): the catalog mask applied to each
-    beam's top-k candidates.
+def prune_topk(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id: int = -1, allowed=None,
+               candidates: bool = False):
+    """Bit-exact oracle.  ``logits [R, W, V]`` fp32, ``cum [R, W]`` fp32 or
+    fp64 (a float32 score enters as its exact float64 value); ``allowed [R,
+    W, V]`` bool (optional): the catalog mask applied to each beam's top-k
+    candidates.
 
     Returns dict with ``parent, token [R, k]`` int32, ``score [R, k]`` fp32,
-    ``score64 [R, k]`` fp64 and ``eos_score [R, W]`` fp32.
+    ``score64 [R, k]`` fp64, ``eos_score [R, W]`` fp32 and ``eos_score64``
+    fp64; with ``candidates``, also ``cand_token [R, W, k1]`` int32 and
+    ``cand_logprob [R, W, k1]`` fp32 (each beam's top-k1 before EOS/catalog
+    removal, logprob = x - lse).
     """
     x = np.ascontiguousarray(logits, dtype=np.float32)
     R, W, V = x.shape
-    cm = np.ascontiguousarray(cum, dtype=np.float32).reshape(R, W)
+    cm = np.ascontiguousarray(_cum64(cum).reshape(R, W))
+    k1 = min(k, V)
     parent = np.empty((R, k), np.int32)
     token = np.empty((R, k), np.int32)
     score = np.empty((R, k), np.float32)
     score64 = np.empty((R, k), np.float64)
-    eos_score = np.empty((R, W), np.float32)
+    eos_score64 = np.empty((R, W), np.float64)
+    ct = np.empty((R, W, k1), np.int32) if candidates else None
+    cl = np.empty((R, W, k1), np.float32) if candidates else None
     al = None if allowed is None else np.ascontiguousarray(allowed, dtype=np.uint8).reshape(R, W, V)
     rc = _load().oracle_prune_topk(_ptr(x), _ptr(cm), R, W, V, int(k), int(eos_token_id),
                                    _ptr(parent), _ptr(token), _ptr(score), _ptr(score64),
-                                   _ptr(eos_score), None if al is None else _ptr(al))
+                                   _ptr(eos_score64), None if al is None else _ptr(al),
+                                   None if ct is None else _ptr(ct), None if cl is None else _ptr(cl))
     if rc != 0:
         raise ValueError("oracle_prune_topk: bad arguments")
-    return dict(parent=parent, token=token, score=score, score64=score64, eos_score=eos_score)
+    out = dict(parent=parent, token=token, score=score, score64=score64,
+               eos_score=eos_score64.astype(np.float32), eos_score64=eos_score64)
+    if candidates:
+        out.update(cand_token=ct, cand_logprob=cl)
+    return out
 
 
 def prune_topk_float64(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id: int = -1, valid_sets=None):

@@ -123,7 +123,7 @@ static float row_stats(const float* x, int V, float* S_out, double* lse_out) {
   return m;
 }
 
-void oracle_prune_row_stats(const float* logits, const float* cum, int rows, int V,
+void oracle_prune_row_stats(const float* logits, const double* cum, int rows, int V,
                             float* m_out, float* S_out, double* lse_out, double* c_out) {
   for (int r = 0; r < rows; ++r) {
     float S;
@@ -132,7 +132,7 @@ void oracle_prune_row_stats(const float* logits, const float* cum, int rows, int
     if (m_out) m_out[r] = m;
     if (S_out) S_out[r] = S;
     if (lse_out) lse_out[r] = lse;
-    if (c_out) c_out[r] = (m == -INFINITY) ? -INFINITY : (double)cum[r] - lse;
+    if (c_out) c_out[r] = (m == -INFINITY) ? -INFINITY : cum[r] - lse;
   }
 }
 
@@ -196,19 +196,24 @@ static void topk_push(topk_t* t, cand_t c) {
 }
 
 /*
- * Full prune.  logits [R*W, V] row-major, cum [R*W].  Outputs [R, k]:
+ * Full prune.  logits [R*W, V] row-major, cum [R*W] float64 (a float32
+ * cumulative score enters exactly, as its float64 value).  Outputs [R, k]:
  * parent (beam within request), token, score (fp32 of the fp64 score),
- * score64 (nullable); eos_score [R*W] (nullable; -inf when the beam's top-k
- * holds no EOS).  Slots past the available candidates get -1/-1/-inf.
+ * score64 (nullable); eos_score [R*W] float64 (nullable; -inf when the
+ * beam's top-k holds no EOS).  Slots past the available candidates get
+ * -1/-1/-inf.  cand_token / cand_logprob [R*W, k1] (nullable): each row's
+ * top-k1 by (x desc, v asc) before EOS / catalog removal, with logprob =
+ * (float)((double)x - lse) (-inf for a row of -inf logits).
  * allowed [R*W, V] (nullable): the catalog mask -- a stage-1 candidate whose
  * token is not allowed for its beam leaves the pool (the reference sets its
  * logprob to -inf after the per-beam top-K, serving_engine.py:504-506); EOS
  * reports a score only when allowed.
  * Returns 0, or -1 on bad arguments.
  */
-int oracle_prune_topk(const float* logits, const float* cum, int R, int W, int V, int k,
+int oracle_prune_topk(const float* logits, const double* cum, int R, int W, int V, int k,
                       int eos, int32_t* parent, int32_t* token, float* score,
-                      double* score64, float* eos_score, const uint8_t* allowed) {
+                      double* score64, double* eos_score, const uint8_t* allowed,
+                      int32_t* cand_token, float* cand_logprob) {
   if (R < 0 || W <= 0 || V <= 0 || k <= 0) return -1;
   int k1 = k < V ? k : V;
   cand_t* row_heap = (cand_t*)malloc(sizeof(cand_t) * (size_t)k1);
@@ -220,12 +225,24 @@ int oracle_prune_topk(const float* logits, const float* cum, int R, int W, int V
       float S;
       double lse;
       float m = row_stats(x, V, &S, &lse);
-      double c = (m == -INFINITY) ? -INFINITY : (double)cum[r * W + b] - lse;
+      double c = (m == -INFINITY) ? -INFINITY : cum[r * W + b] - lse;
       /* stage 1: per-row top-k1 by (x desc, v asc) */
       topk_t row = {row_heap, 0, k1};
       for (int v = 0; v < V; ++v) {
         cand_t cd = {(double)x[v], v};
         topk_push(&row, cd);
+      }
+      if (cand_token) {
+        /* the row's list in order: a copy of the heap, sorted */
+        cand_t* sorted = (cand_t*)malloc(sizeof(cand_t) * (size_t)k1);
+        memcpy(sorted, row.h, sizeof(cand_t) * (size_t)row.n);
+        qsort(sorted, row.n, sizeof(cand_t), cmp_desc);
+        for (int i = 0; i < k1; ++i) {
+          size_t o = ((size_t)r * W + b) * k1 + i;
+          cand_token[o] = i < row.n ? (int32_t)sorted[i].idx : -1;
+          cand_logprob[o] = i < row.n ? (m == -INFINITY ? -INFINITY : (float)(sorted[i].key - lse)) : -INFINITY;
+        }
+        free(sorted);
       }
       if (eos_score) eos_score[r * W + b] = -INFINITY;
       for (int i = 0; i < row.n; ++i) {
@@ -233,7 +250,7 @@ int oracle_prune_topk(const float* logits, const float* cum, int R, int W, int V
         if (allowed && !allowed[((size_t)r * W + b) * V + v]) continue;
         double s = (m == -INFINITY) ? -INFINITY : (double)x[v] + c;
         if (v == eos) {
-          if (eos_score) eos_score[r * W + b] = (float)s;
+          if (eos_score) eos_score[r * W + b] = s;
           continue;
         }
         cand_t cd = {s, (int64_t)b * V + v};

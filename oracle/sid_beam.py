@@ -20,7 +20,10 @@ Two pieces, both float64 on the CPU:
   beams and the best ``beam_width`` of completed + live by vLLM's beam-search
   score (:273-292).  The reference's ``np.argpartition`` leaves the order of
   equal scores open; here ties go to the lower (beam, token), the order of
-  the flat index ``beam * vocab + token``.  Pinned against brute-force
+  the flat index ``beam * vocab + token``.  Each sequence also carries its
+  per-step logprob lists (llm.py:115-118, :203-220, :283-288): the begin
+  token, the parent's top ``beam_width`` (token, logprob) list of every
+  step, the end token.  Pinned against brute-force
   enumeration where the beam keeps every sequence, against a hand-computed
   planted case and against an EOS case (tests/test_oracle_sid.py).
 """
@@ -99,6 +102,10 @@ class Seq:
     tokens: list
     cum_logprob: float
     finish_reason: str | None = None
+    # per generated position: (token ids, logprobs) -- the begin token (0.0),
+    # each step's parent top-W list, the end token (0.0) on a non-EOS beam
+    # (vllm_gr/entrypoints/llm.py:115-118, :203-220, :283-288)
+    logprobs: list = field(default_factory=list)
 
 
 @dataclass
@@ -131,16 +138,19 @@ def beam_search(next_logprobs, prompts, beam_width: int, max_tokens: int, eos_to
     insts, plen = [], []
     for p in prompts:
         toks = list(p) + ([begin_token] if begin_token is not None else [])
-        insts.append(_Instance([Seq(toks, 0.0)]))
+        first = [([begin_token], [0.0])] if begin_token is not None else []
+        insts.append(_Instance([Seq(toks, 0.0, logprobs=first)]))
         plen.append(len(toks))
     pre_calc = (begin_token is not None) + (end_token is not None)
     for _ in range(max(0, max_tokens - pre_calc)):
         for ii, inst in enumerate(insts):
             cand = []  # (score, beam index, token)
+            step_lists = []  # per beam: its top-W (tokens, logprobs)
             for bi, beam in enumerate(inst.beams):
                 lp = np.asarray(next_logprobs(beam.tokens), dtype=np.float64)
                 V = lp.shape[0]
                 top = np.lexsort((np.arange(V), -lp))[:W]  # (logprob desc, token asc)
+                step_lists.append(([int(t) for t in top], [float(lp[t]) for t in top]))
                 ok = None if valid_fn is None else valid_fn(beam.tokens[plen[ii]:])
                 for t in top:
                     if ok is not None and int(t) not in ok:
@@ -149,18 +159,21 @@ def beam_search(next_logprobs, prompts, beam_width: int, max_tokens: int, eos_to
             keep = []
             for sc, bi, t in cand:
                 if eos_token_id is not None and t == eos_token_id:
-                    inst.completed.append(Seq(inst.beams[bi].tokens + [t], sc, "stop"))
+                    inst.completed.append(Seq(inst.beams[bi].tokens + [t], sc, "stop",
+                                              inst.beams[bi].logprobs + [step_lists[bi]]))
                 else:
                     keep.append((sc, bi, t))
             keep.sort(key=lambda c: (-c[0], c[1], c[2]))
             if trace is not None:
                 trace.append([c[0] for c in keep])
-            inst.beams = [Seq(inst.beams[bi].tokens + [t], sc) for sc, bi, t in keep[:W]]
+            inst.beams = [Seq(inst.beams[bi].tokens + [t], sc, None, inst.beams[bi].logprobs + [step_lists[bi]])
+                          for sc, bi, t in keep[:W]]
     out = []
     for inst in insts:
         if end_token is not None:
             for b in inst.beams:
                 b.tokens.append(end_token)
+                b.logprobs = b.logprobs + [([end_token], [0.0])]
         allseq = inst.completed + inst.beams
         key = lambda s: beam_score(s.tokens, s.cum_logprob, eos_token_id, length_penalty)
         allseq = sorted(allseq, key=key, reverse=True)

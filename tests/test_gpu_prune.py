@@ -121,3 +121,80 @@ def test_prune_catalog_matches_oracle(device):
         for j in range(k):
             p, t = int(want["parent"][r, j]), int(want["token"][r, j])
             assert no[r, j] == (cat.node_of(prefixes[r][p] + [t]) if p >= 0 else -1)
+
+
+def _assert_exact64(got, want, R, W):
+    p, t, s, e = got
+    assert np.array_equal(p, want["parent"]), "parent beams differ"
+    assert np.array_equal(t, want["token"]), "tokens differ"
+    assert np.array_equal(s.view(np.int64), want["score64"].view(np.int64)), "float64 scores differ (bits)"
+    assert np.array_equal(e.view(np.int64), want["eos_score64"].reshape(R, W).view(np.int64)), "eos scores differ"
+
+
+@pytest.mark.parametrize("R,W,V,k,eos", [(64, 128, 8192, 128, -1), (3, 16, 512, 16, 7), (2, 300, 256, 100, 3)])
+def test_prune_f64_matches_oracle(device, R, W, V, k, eos):
+    """gr_beam_prune_topk_f64: float64 cumulative scores in, float64 scores out
+    (the reference's Python-float beam scores, serving_engine.py:511, 538-539),
+    and every beam's top-k (token, logprob) list: all bit-exact against the C
+    oracle, at the full pruning workload and smaller shapes."""
+    wl = workloads.make_prune(R=R, W=W, V=V, k=k, seed=5 + R)
+    if eos >= 0:
+        wl.logits[:, :, eos] += 6.0
+    cum = torch.from_numpy(np.random.default_rng(R + W).uniform(-20, 0, (R, W)))  # float64, not float32 values
+    print(f"[prune] f64 R={R} W={W} V={V} k={k} eos={eos}", flush=True)
+    parent, token, score, eos_score, ct, cl = ops.beam_prune_topk(wl.logits.to(device), cum.to(device), k, eos,
+                                                                  candidates=True)
+    torch.cuda.synchronize()
+    assert score.dtype == torch.float64 and eos_score.dtype == torch.float64
+    want = op.prune_topk(wl.logits.numpy(), cum.numpy(), k, eos, candidates=True)
+    _assert_exact64((parent.cpu().numpy(), token.cpu().numpy(), score.cpu().numpy(), eos_score.cpu().numpy()),
+                    want, R, W)
+    assert np.array_equal(ct.cpu().numpy(), want["cand_token"])
+    assert np.array_equal(cl.cpu().numpy().view(np.int32), want["cand_logprob"].view(np.int32))
+
+
+def test_prune_f64_catalog(device):
+    """The float64 entry point in catalog mode equals the masked oracle."""
+    from vllm_gr_amd.entrypoints.catalog import Catalog
+    rng = np.random.default_rng(12)
+    R, W, V, k = 2, 16, 1024, 16
+    cat = Catalog()
+    seqs = [rng.integers(0, V, size=3).tolist() for _ in range(500)]
+    for s in seqs:
+        cat.add(s)
+    prefixes = [[[] if b % 3 == 0 else seqs[int(rng.integers(0, len(seqs)))][:1 + b % 2] for b in range(W)]
+                for _ in range(R)]
+    node = torch.tensor([[cat.node_of(p) for p in row] for row in prefixes], dtype=torch.int32)
+    allowed = np.zeros((R, W, V), bool)
+    for r in range(R):
+        for b in range(W):
+            allowed[r, b, list(cat.valid(prefixes[r][b]))] = True
+    logits = torch.from_numpy((rng.standard_normal((R, W, V)) * 3 + allowed * 6.0).astype(np.float32))
+    cum = torch.from_numpy(rng.uniform(-20, 0, (R, W)))
+    parent, token, score, eos_score, node_out = ops.beam_prune_topk(
+        logits.to(device), cum.to(device), k, -1, catalog=cat.to_device(device), beam_node=node.to(device))
+    torch.cuda.synchronize()
+    want = op.prune_topk(logits.numpy(), cum.numpy(), k, -1, allowed=allowed)
+    _assert_exact64((parent.cpu().numpy(), token.cpu().numpy(), score.cpu().numpy(), eos_score.cpu().numpy()),
+                    want, R, W)
+    no = node_out.cpu().numpy()
+    for r in range(R):
+        for j in range(k):
+            p, t = int(want["parent"][r, j]), int(want["token"][r, j])
+            assert no[r, j] == (cat.node_of(prefixes[r][p] + [t]) if p >= 0 else -1)
+
+
+def test_prune_f64_planted_flip(device):
+    """Identical logits rows, scores 2^-30 apart: the float64 path selects the
+    second beam, float32 carrying of the same scores ties them and selects the
+    first (lowest flat index) -- a selection that carrying scores in float32
+    between steps would flip."""
+    x = torch.linspace(-1, 1, 8, dtype=torch.float32).repeat(1, 2, 1).contiguous()
+    cum64 = torch.tensor([[-10.0, -10.0 + 2.0 ** -30]], dtype=torch.float64)
+    p64, t64, s64, _ = ops.beam_prune_topk(x.to(device), cum64.to(device), 1)
+    p32, t32, s32, _ = ops.beam_prune_topk(x.to(device), cum64.to(torch.float32).to(device), 1)
+    torch.cuda.synchronize()
+    assert (int(p64[0, 0]), int(t64[0, 0])) == (1, 7)
+    assert (int(p32[0, 0]), int(t32[0, 0])) == (0, 7)
+    want = op.prune_topk(x.numpy(), cum64.numpy(), 1)
+    assert float(s64[0, 0]) == float(want["score64"][0, 0])

@@ -25,6 +25,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import prune as op
 from oracle import sid_beam as so
 from vllm_gr_amd.entrypoints.beam_search import BeamSearchParams
 from vllm_gr_amd.entrypoints.llm import LLM
@@ -49,6 +50,21 @@ def _llm(cfg, w, R, P, W, steps, eos=None):
     print(f"[sid] cfg layers={cfg.num_layers} hidden={cfg.hidden} D={cfg.head_dim} dtype={cfg.dtype} "
           f"R={R} P<={P} W={W} steps={steps} blocks={nb}", flush=True)
     return LLM(cfg, weights={k: v.cuda() for k, v in w.items()}, num_blocks=nb, eos_token_id=eos)
+
+
+def _assert_logprobs(got_seqs, ref_seqs, tol):
+    """Every output beam's per-step logprob lists equal the oracle's: the same
+    tokens at each position and logprobs within ``tol``."""
+    ref = {tuple(s.tokens): s.logprobs for s in ref_seqs}
+    for s in got_seqs:
+        want = ref[tuple(s.tokens)]
+        assert len(s.logprobs) == len(want)
+        for i, (wt, wl) in enumerate(want):
+            run = s.logprobs.position(i)
+            assert dict(zip(wt, range(len(wt)))).keys() == {t for t, _, _ in run}
+            got = {t: lp for t, lp, _ in run}
+            for t, lp in zip(wt, wl):
+                assert abs(got[t] - lp) <= tol, (s.tokens, i, t, got[t], lp)
 
 
 def _min_margin(trace, W):
@@ -78,8 +94,50 @@ def test_sid_beam_search_f32_matches_oracle(seed, lens, W, max_tokens):
             assert abs(got[k] - exp[k]) < 1e-4, (k, got[k], exp[k])
         sc = [s.cum_logprob for s in o.sequences]
         assert sc == sorted(sc, reverse=True)
+        _assert_logprobs(o.sequences, r, 1e-4)
     t = llm.last_times
     assert t.prefill_ms > 0 and len(t.step_ms) == max_tokens - 1
+
+
+@pytest.mark.parametrize("seed,lens,W,max_tokens,eos", [(21, [19, 40], 8, 5, None), (22, [30, 7, 12], 16, 4, 3)])
+def test_sid_beam_search_replayed_logits_exact(seed, lens, W, max_tokens, eos):
+    """No tie-margin filter: the oracle's beam-search loop (the reference's
+    llm.py:118-292 restated) runs over the GPU's own logits of every step,
+    with the prune contract's log_softmax, so every selection -- near ties
+    included -- must come out the same.  Beams, EOS completions, float64
+    cumulative scores (to 1e-12: the two sides associate the float64 sum
+    differently) and per-step logprob lists (tokens exact, values to 1e-6)
+    agree."""
+    w = init_weights(F32, seed)
+    prompts = _prompts(seed, lens, F32.vocab)
+    llm = _llm(F32, w, len(lens), max(lens), W, max_tokens, eos=eos)
+    rec = []
+    llm.logits_hook = lambda step, logits, hist: rec.append((logits.clone(), hist.clone()))
+    out = llm.beam_search(prompts, BeamSearchParams(W, max_tokens))
+    rows = {}
+    for lg, h in rec:
+        lg, h = lg.cpu().numpy(), h.cpu().numpy()
+        for r in range(lg.shape[0]):
+            for b in range(lg.shape[1]):
+                rows[tuple(prompts[r] + h[r, b].tolist())] = lg[r, b]
+
+    def next_logprobs(tokens):
+        x = rows[tuple(tokens)]
+        _, _, lse, _ = op.row_stats(x[None], np.zeros(1))
+        return x.astype(np.float64) - lse[0]
+
+    ref = so.beam_search(next_logprobs, prompts, W, max_tokens, eos_token_id=eos)
+    for o, r in zip(out, ref):
+        assert [s.tokens for s in o.sequences] == [s.tokens for s in r]
+        for a, b in zip(o.sequences, r):
+            assert abs(a.cum_logprob - b.cum_logprob) <= 1e-12, (a.tokens, a.cum_logprob, b.cum_logprob)
+            assert (a.finish_reason == "stop") == (b.finish_reason == "stop")
+            for i, (wt, wl) in enumerate(b.logprobs):
+                run = a.logprobs.position(i)
+                assert [t for t, _, _ in run] == wt
+                assert max(abs(lp - v) for (_, lp, _), v in zip(run, wl)) <= 1e-6
+    if eos is not None:
+        assert any(s.finish_reason == "stop" for o in out for s in o.sequences)
 
 
 def test_sid_beam_search_f32_eos_begin_end():
@@ -102,6 +160,7 @@ def test_sid_beam_search_f32_eos_begin_end():
         assert set(got) == set(exp)
         for k in exp:
             assert abs(got[k][0] - exp[k][0]) < 1e-4 and (got[k][1] == "stop") == (exp[k][1] == "stop")
+        _assert_logprobs(o.sequences, r, 1e-4)
 
 
 def test_sid_beam_search_f32_catalog():

@@ -232,3 +232,66 @@ def test_reference_minheap_cross_check():
         pairs = [(idx // k, int(toks[idx])) for _, idx in sel]
         if np.all(np.abs(np.diff(ref64["score"][r])) > 1e-5):
             assert pairs == list(zip(got["parent"][r].tolist(), got["token"][r].tolist()))
+
+
+def test_candidate_lists_vs_log_softmax():
+    """Each beam's top-k list before EOS removal: the tokens of a stable
+    (logit desc, token asc) sort, their logprobs equal to scipy's float64
+    log_softmax within float32 rounding; EOS stays in the list."""
+    rng = np.random.default_rng(7)
+    R, W, V, k = 3, 5, 96, 6
+    x = (rng.standard_normal((R, W, V)) * 3).astype(np.float32)
+    x[0, 1, 10:20] = x[0, 1, 10]  # a run of ties inside the top-k
+    x[0, 1, 10] += 9.0
+    x[2, 3] = -np.inf  # a row without any finite logit
+    cum = rng.uniform(-20, 0, (R, W))
+    eos = int(np.argmax(x[1, 2]))  # the top candidate of one beam
+    got = op.prune_topk(x, cum, k, eos, candidates=True)
+    ls = scipy.special.log_softmax(x.astype(np.float64), axis=2)
+    for r in range(R):
+        for b in range(W):
+            order = np.lexsort((np.arange(V), -x[r, b].astype(np.float64)))[:k]
+            assert got["cand_token"][r, b].tolist() == order.tolist()
+            if r == 2 and b == 3:
+                assert np.all(np.isneginf(got["cand_logprob"][r, b]))
+                continue
+            np.testing.assert_allclose(got["cand_logprob"][r, b], ls[r, b, order], atol=2e-6, rtol=0)
+    assert eos == got["cand_token"][1, 2, 0]
+
+
+def test_float64_cum_matches_float64_restatement():
+    """float64 scores between steps: the selected sets equal the plain float64
+    restatement's wherever its gaps exceed 2e-6, the scores agree to 1e-6 (the
+    float32 exp-sum of the build contract bounds the difference), and
+    cumulative scores that are exact float32 values give the float32 path's
+    bits."""
+    rng = np.random.default_rng(8)
+    R, W, V, k = 4, 8, 200, 8
+    x = (rng.standard_normal((R, W, V)) * 3).astype(np.float32)
+    cum = rng.uniform(-20, 0, (R, W))  # not float32 values
+    got = op.prune_topk(x, cum, k)
+    want = op.prune_topk_float64(x, cum, k)
+    for r in range(R):
+        s = np.sort(want["score"][r])[::-1]
+        if np.all(np.abs(np.diff(s)) > 2e-6):
+            assert set(zip(got["parent"][r], got["token"][r])) == set(zip(want["parent"][r], want["token"][r]))
+    np.testing.assert_allclose(got["score64"], want["score"], atol=1e-6, rtol=0)
+    c32 = cum.astype(np.float32)
+    a, b = op.prune_topk(x, c32, k), op.prune_topk(x, c32.astype(np.float64), k)
+    assert np.array_equal(a["score64"].view(np.int64), b["score64"].view(np.int64))
+    assert np.array_equal(a["parent"], b["parent"]) and np.array_equal(a["token"], b["token"])
+
+
+def test_float64_cum_planted_flip():
+    """Two beams with identical logits whose scores differ by 2^-30: float64
+    carrying ranks the second beam first, the float32 rounding of the same
+    scores ties them and the lowest flat index (the first beam) wins."""
+    x = np.tile(np.linspace(-1, 1, 8, dtype=np.float32), (1, 2, 1))
+    c = -10.0 + 2.0 ** -30
+    cum64 = np.array([[-10.0, c]])
+    assert np.float32(c) == np.float32(-10.0)
+    got64 = op.prune_topk(x, cum64, 1)
+    got32 = op.prune_topk(x, cum64.astype(np.float32), 1)
+    assert (got64["parent"][0, 0], got64["token"][0, 0]) == (1, 7)
+    assert (got32["parent"][0, 0], got32["token"][0, 0]) == (0, 7)
+    assert got64["score64"][0, 0] - got32["score64"][0, 0] == 2.0 ** -30

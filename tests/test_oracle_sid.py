@@ -192,12 +192,26 @@ def test_outputs_assembly():
     hist = [[[1, 2], [3, 4], [0, 0]]]
     score = [[-1.0, -3.0, ninf]]
     finished = [([[-0.5]], [[[]]]), ([[ninf, -2.5, ninf]], [[[1], [3], [5]]])]
-    out = llm_mod.LLM._outputs(toks, hist, score, finished, 2, 9, 8, 1.0, 3)[0].sequences
+    # step 0: the prompt's top-3 list; step 1: each of the three beams' lists
+    parents = [[[0, 0, 0]], [[0, 1, -1]]]
+    c0 = ([[[1, 3, 5]]], [[[-0.1, -0.2, -0.3]]])
+    c1 = ([[[2, 9, 4], [4, 9, 6], [7, 8, 6]]], [[[-1.0, -1.1, -1.2], [-2.0, -2.1, -2.2], [-3.0, -3.1, -3.2]]])
+    out = llm_mod.LLM._outputs(toks, hist, score, finished, 2, 9, None, 8, 1.0, 3, parents, [c0, c1])[0].sequences
     # scores: [7,7,9] -0.5/2; [7,7,3,9] -2.5/3; [7,7,1,2,8] -1/5; [7,7,3,4,8] -3/5
     assert [s.tokens for s in out] == [[7, 7, 1, 2, 8], [7, 7, 9], [7, 7, 3, 4, 8]]
     assert [s.finish_reason for s in out] == ["length", "stop", "length"]
-    out0 = llm_mod.LLM._outputs(toks, [[[]]], [[0.0]], [], 0, None, None, 1.0, 2)[0].sequences
-    assert [s.tokens for s in out0] == [[7, 7]]
+    # logprob lists rebuilt along the parents (worked by hand): each step's
+    # entry is the parent's whole list, ranks 1..3; the end token closes the
+    # live beams, not the EOS one
+    pos = lambda s: [s.logprobs.position(i) for i in range(len(s.logprobs))]
+    l0 = [(1, -0.1, 1), (3, -0.2, 2), (5, -0.3, 3)]
+    end = [(8, 0.0, None)]
+    assert pos(out[0]) == [l0, [(2, -1.0, 1), (9, -1.1, 2), (4, -1.2, 3)], end]
+    assert pos(out[1]) == [l0]
+    assert pos(out[2]) == [l0, [(4, -2.0, 1), (9, -2.1, 2), (6, -2.2, 3)], end]
+    out0 = llm_mod.LLM._outputs(toks, [[[]]], [[0.0]], [], 0, None, 5, 6, 1.0, 2, [], [])[0].sequences
+    assert [s.tokens for s in out0] == [[7, 7, 6]]
+    assert pos(out0[0]) == [[(5, 0.0, None)], [(6, 0.0, None)]]
 
 
 def _mega_side(tables_of_reqs, W):

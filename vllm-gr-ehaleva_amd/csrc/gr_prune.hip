@@ -108,6 +108,7 @@ struct PruneArgs {
   const float* logits;
   int64_t row_stride;
   const float* cum;
+  const double* cum64;  // float64 cumulative scores (gr_beam_prune_topk_f64); overrides cum
   int R, W, V, k1, k, eos;
   float* cand_x;    // [R*W, k1] row top-k logits, sorted; EOS removed, tail padded
   int32_t* cand_v;  // [R*W, k1] tokens (-1 = empty)
@@ -116,6 +117,10 @@ struct PruneArgs {
   int32_t* token;
   float* score;
   float* eos_score;
+  double* score64;      // float64 outputs (gr_beam_prune_topk_f64); override score / eos_score
+  double* eos_score64;
+  int32_t* cand_token;   // nullable [R*W, k1]: each row's top-k1 tokens before EOS / catalog removal
+  float* cand_logprob;   // nullable [R*W, k1]: their logprobs x - lse
   uint64_t* part_key;  // [R, ng, k] stage-1 selections: score key (0 = empty) ...
   int64_t* part_flat;  // ... and flat index b * V + v
   int ng, gr;          // row groups per request, rows per group
@@ -129,6 +134,12 @@ struct PruneArgs {
   int num_nodes, num_edges;
   int32_t* dev_status;
 };
+
+// Output slot o of the selection: the float64 score, or its float32 rounding.
+__device__ inline void put_score(const PruneArgs& a, int64_t o, double v) {
+  if (a.score64) a.score64[o] = v;
+  else a.score[o] = (float)v;
+}
 
 // Position of token t among the children [c0, c1) of a trie node, or -1.
 __device__ inline int catalog_find(const int32_t* child_token, int c0, int c1, int t) {
@@ -428,6 +439,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 
   // ---- fixed-order exp-sum: thread partial in element order, xor butterfly, waves pairwise ----
   double c_row = -INFINITY;
+  double lse_row = INFINITY;  // a row of -inf logits has logprobs -inf
   if (m != -INFINITY) {
     float acc = 0.0f;
     PR_FOR_CHUNKS(c) {
@@ -446,7 +458,8 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     __syncthreads();
     const float S = (wred[0] + wred[1]) + (wred[2] + wred[3]);
     const double lse = (double)m + log_f64((double)S);
-    c_row = (double)a.cum[row] - lse;
+    c_row = (a.cum64 ? a.cum64[row] : (double)a.cum[row]) - lse;
+    lse_row = lse;
   }
 
   // ---- stage 1: row top-k1 by (logit desc, token asc) ----
@@ -569,6 +582,14 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 #undef PR_FOR_CHUNKS
   if (tid == 0) eos_pos = -1;
   __syncthreads();
+  if (a.cand_token) {
+    // the row's whole top-k1 list with its logprobs (the sampler's per-beam
+    // logprobs, before EOS or the catalog take anything out)
+    for (int i = tid; i < k1; i += PR_THREADS) {
+      a.cand_token[(int64_t)row * k1 + i] = ov[i];
+      a.cand_logprob[(int64_t)row * k1 + i] = (float)((double)ox[i] - lse_row);
+    }
+  }
   float* cx = a.cand_x + (int64_t)row * k1;
   int32_t* cv = a.cand_v + (int64_t)row * k1;
   if constexpr (CATALOG) {
@@ -620,11 +641,9 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   const int e = eos_pos;
   if (tid == 0) {
     a.row_c[row] = c_row;
-    if (a.eos_score) {
-      float es = -INFINITY;
-      if (e >= 0 && c_row != -INFINITY) es = (float)((double)ox[e] + c_row);
-      a.eos_score[row] = es;
-    }
+    const double es = e >= 0 && c_row != -INFINITY ? (double)ox[e] + c_row : -INFINITY;
+    if (a.eos_score64) a.eos_score64[row] = es;
+    else if (a.eos_score) a.eos_score[row] = (float)es;
   }
 }
 
@@ -801,13 +820,13 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
     const int b = (int)(fi / a.V);
     a.parent[o] = b;
     a.token[o] = (int32_t)(fi - (int64_t)b * a.V);
-    a.score[o] = (float)dval(ki);
+    put_score(a, o, dval(ki));
   }
   for (int i = nsel + tid; i < k; i += MG_THREADS) {
     const int64_t o = (int64_t)r * k + i;
     a.parent[o] = -1;
     a.token[o] = -1;
-    a.score[o] = -INFINITY;
+    put_score(a, o, -INFINITY);
   }
 }
 
@@ -1041,13 +1060,13 @@ __global__ __launch_bounds__(NT) void prune_merge_final(PruneArgs a) {
     const int b = (int)(fi / a.V);
     a.parent[o] = b;
     a.token[o] = (int32_t)(fi - (int64_t)b * a.V);
-    a.score[o] = (float)dval(ki);
+    put_score(a, o, dval(ki));
   }
   for (int i = nsel + tid; i < k; i += NT) {
     const int64_t o = (int64_t)r * k + i;
     a.parent[o] = -1;
     a.token[o] = -1;
-    a.score[o] = -INFINITY;
+    put_score(a, o, -INFINITY);
   }
 }
 
@@ -1129,7 +1148,7 @@ __global__ __launch_bounds__(MG_LIST_THREADS) void prune_merge_lists(PruneArgs a
       const int b = (int)(fe / a.V);
       a.parent[o] = b;
       a.token[o] = (int32_t)(fe - (int64_t)b * a.V);
-      a.score[o] = (float)dval(ke);
+      put_score(a, o, dval(ke));
       ++filled;
     }
   }
@@ -1139,7 +1158,7 @@ __global__ __launch_bounds__(MG_LIST_THREADS) void prune_merge_lists(PruneArgs a
     const int64_t o = (int64_t)r * k + i;
     a.parent[o] = -1;
     a.token[o] = -1;
-    a.score[o] = -INFINITY;
+    put_score(a, o, -INFINITY);
   }
 }
 
@@ -1186,15 +1205,17 @@ __global__ void catalog_advance(PruneArgs a, int32_t* node_out) {
   node_out[i] = node;
 }
 
-static gr_status_t prune_launch(PruneArgs& a, const float* logits, int64_t logits_row_stride, const float* cum,
+// a.cum / a.cum64, a.score / a.score64, a.eos_score / a.eos_score64 and the
+// catalog fields are set by the caller.
+static gr_status_t prune_launch(PruneArgs& a, const float* logits, int64_t logits_row_stride,
                                 int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
-                                int32_t* parent, int32_t* token, float* score, float* eos_score,
-                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                int32_t* parent, int32_t* token, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream) {
   if (num_reqs < 0 || beam_width < 1 || vocab < 4 || vocab % 4 != 0 || k < 1 || k > PR_MAXK || k > vocab ||
       beam_width > PR_MAXW || logits_row_stride < vocab || logits_row_stride % 4 != 0)
     return GR_ERR_INVALID_ARG;
   if (num_reqs == 0) return GR_OK;
-  if (!logits || !cum || !parent || !token || !score) return GR_ERR_INVALID_ARG;
+  if (!logits || !(a.cum || a.cum64) || !parent || !token || !(a.score || a.score64)) return GR_ERR_INVALID_ARG;
   if ((reinterpret_cast<uintptr_t>(logits) & 15) != 0) return GR_ERR_INVALID_ARG;
   const size_t need = gr_beam_prune_workspace_size(num_reqs, beam_width, vocab, k);
   if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
@@ -1203,7 +1224,6 @@ static gr_status_t prune_launch(PruneArgs& a, const float* logits, int64_t logit
   const size_t rows = (size_t)num_reqs * beam_width;
   a.logits = logits;
   a.row_stride = logits_row_stride;
-  a.cum = cum;
   a.R = num_reqs;
   a.W = beam_width;
   a.V = vocab;
@@ -1217,8 +1237,6 @@ static gr_status_t prune_launch(PruneArgs& a, const float* logits, int64_t logit
                                       align256(rows * k1 * sizeof(int32_t)));
   a.parent = parent;
   a.token = token;
-  a.score = score;
-  a.eos_score = eos_score;
   merge_groups(beam_width, k1, k, a.gr, a.ng);
   const size_t parts = (size_t)num_reqs * a.ng * k;
   uint8_t* part_base = ws + align256(rows * k1 * sizeof(float)) + align256(rows * k1 * sizeof(int32_t)) +
@@ -1253,13 +1271,39 @@ static gr_status_t prune_launch(PruneArgs& a, const float* logits, int64_t logit
   return launch_status();
 }
 
+// The catalog fields of the arguments; false on an inconsistent trie.
+static bool set_catalog(PruneArgs& a, const int32_t* beam_node, const int32_t* node_start,
+                        const int32_t* child_token, const int32_t* child_node, int num_nodes, int num_edges,
+                        const int32_t* node_out) {
+  if (num_nodes < 1 || num_edges < 0 || !beam_node || !node_start || !node_out ||
+      (num_edges > 0 && (!child_token || !child_node)))
+    return false;
+  a.beam_node = beam_node;
+  a.node_start = node_start;
+  a.child_token = child_token;
+  a.child_node = child_node;
+  a.num_nodes = num_nodes;
+  a.num_edges = num_edges;
+  return true;
+}
+
+static gr_status_t catalog_advance_launch(PruneArgs& a, int32_t* node_out, hipStream_t stream) {
+  const int n = a.R * a.k;
+  if (n == 0) return GR_OK;
+  hipLaunchKernelGGL(catalog_advance, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, node_out);
+  return launch_status();
+}
+
 extern "C" gr_status_t gr_beam_prune_topk(const float* logits, int64_t logits_row_stride, const float* cum,
                                           int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
                                           int32_t* parent, int32_t* token, float* score, float* eos_score,
                                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
   PruneArgs a = {};
-  return prune_launch(a, logits, logits_row_stride, cum, num_reqs, beam_width, vocab, k, eos_token_id, parent,
-                      token, score, eos_score, workspace, workspace_bytes, stream);
+  a.cum = cum;
+  a.score = score;
+  a.eos_score = eos_score;
+  return prune_launch(a, logits, logits_row_stride, num_reqs, beam_width, vocab, k, eos_token_id, parent, token,
+                      workspace, workspace_bytes, stream);
 }
 
 extern "C" gr_status_t gr_beam_prune_topk_catalog(
@@ -1269,21 +1313,40 @@ extern "C" gr_status_t gr_beam_prune_topk_catalog(
     const int32_t* child_node, int num_nodes, int num_edges,
     int32_t* parent, int32_t* token, float* score, float* eos_score, int32_t* node_out,
     void* workspace, size_t workspace_bytes, int32_t* dev_status, hipStream_t stream) {
-  if (num_nodes < 1 || num_edges < 0 || !beam_node || !node_start || !node_out ||
-      (num_edges > 0 && (!child_token || !child_node)))
-    return GR_ERR_INVALID_ARG;
   PruneArgs a = {};
-  a.beam_node = beam_node;
-  a.node_start = node_start;
-  a.child_token = child_token;
-  a.child_node = child_node;
-  a.num_nodes = num_nodes;
-  a.num_edges = num_edges;
+  if (!set_catalog(a, beam_node, node_start, child_token, child_node, num_nodes, num_edges, node_out))
+    return GR_ERR_INVALID_ARG;
+  a.cum = cum;
+  a.score = score;
+  a.eos_score = eos_score;
   a.dev_status = dev_status;
-  gr_status_t st = prune_launch(a, logits, logits_row_stride, cum, num_reqs, beam_width, vocab, k, eos_token_id,
-                                parent, token, score, eos_score, workspace, workspace_bytes, stream);
+  gr_status_t st = prune_launch(a, logits, logits_row_stride, num_reqs, beam_width, vocab, k, eos_token_id,
+                                parent, token, workspace, workspace_bytes, stream);
   if (st != GR_OK || num_reqs == 0) return st;
-  const int n = num_reqs * k;
-  hipLaunchKernelGGL(catalog_advance, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, node_out);
-  return launch_status();
+  return catalog_advance_launch(a, node_out, stream);
+}
+
+extern "C" gr_status_t gr_beam_prune_topk_f64(
+    const float* logits, int64_t logits_row_stride, const double* cum,
+    int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
+    const int32_t* beam_node, const int32_t* node_start, const int32_t* child_token,
+    const int32_t* child_node, int num_nodes, int num_edges,
+    int32_t* parent, int32_t* token, double* score, double* eos_score, int32_t* node_out,
+    int32_t* cand_token, float* cand_logprob,
+    void* workspace, size_t workspace_bytes, int32_t* dev_status, hipStream_t stream) {
+  PruneArgs a = {};
+  if (!cand_token != !cand_logprob) return GR_ERR_INVALID_ARG;
+  a.cand_token = cand_token;
+  a.cand_logprob = cand_logprob;
+  if (beam_node &&
+      !set_catalog(a, beam_node, node_start, child_token, child_node, num_nodes, num_edges, node_out))
+    return GR_ERR_INVALID_ARG;
+  a.cum64 = cum;
+  a.score64 = score;
+  a.eos_score64 = eos_score;
+  a.dev_status = dev_status;
+  gr_status_t st = prune_launch(a, logits, logits_row_stride, num_reqs, beam_width, vocab, k, eos_token_id,
+                                parent, token, workspace, workspace_bytes, stream);
+  if (st != GR_OK || num_reqs == 0 || !beam_node) return st;
+  return catalog_advance_launch(a, node_out, stream);
 }

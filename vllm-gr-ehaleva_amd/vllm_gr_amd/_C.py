@@ -97,6 +97,13 @@ SIGNATURES = {
     "gr_beam_prune_topk": (_I, [
         _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _SZ, _P,
     ]),
+    "gr_beam_prune_topk_f64": (_I, [
+        _P, _L, _P, _I, _I, _I, _I, _I,    # logits, stride, cum (float64), R, W, V, k, eos
+        _P, _P, _P, _P, _I, _I,            # beam_node (nullable), node_start, child_token, child_node, nodes, edges
+        _P, _P, _P, _P, _P,                # parent, token, score, eos_score (float64), node_out
+        _P, _P,                            # cand_token, cand_logprob (nullable)
+        _P, _SZ, _P, _P,                   # workspace, bytes, dev_status, stream
+    ]),
 }
 
 _lib = None

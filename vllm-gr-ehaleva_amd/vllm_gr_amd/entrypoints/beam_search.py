@@ -45,28 +45,37 @@ class BeamSearchParams:
 class PruneResult:
     parent: torch.Tensor     # [R, W] int32: beam (within the request) each new beam extends
     token: torch.Tensor      # [R, W] int32
-    score: torch.Tensor      # [R, W] float32: new cumulative logprob, descending per request
-    eos_score: torch.Tensor  # [R, W_old] float32: score of a beam's EOS candidate (-inf if none)
+    score: torch.Tensor      # [R, W] new cumulative logprob (cum's dtype), descending per request
+    eos_score: torch.Tensor  # [R, W_old] score of a beam's EOS candidate (-inf if none)
     node: torch.Tensor | None = None  # [R, W] int32: each new beam's catalog trie node (with a catalog)
+    # with candidates=True: each old beam's top-W list before EOS / catalog removal
+    cand_token: torch.Tensor | None = None    # [R, W_old, W] int32
+    cand_logprob: torch.Tensor | None = None  # [R, W_old, W] float32 (logit - lse)
 
 
 def prune_step(logits: torch.Tensor, cum_logprob: torch.Tensor, beam_width: int,
                eos_token_id: int | None = None, *, workspace: torch.Tensor | None = None,
-               catalog=None, beam_node: torch.Tensor | None = None) -> PruneResult:
+               catalog=None, beam_node: torch.Tensor | None = None, candidates: bool = False) -> PruneResult:
     """Fused log_softmax + cumulative logprob + top-``beam_width`` over
-    beams x vocab per request.  ``logits [R, W, V]`` float32, ``cum [R, W]``.
+    beams x vocab per request.  ``logits [R, W, V]`` float32, ``cum [R, W]``
+    float64 (the reference's Python-float scores, serving_engine.py:511,
+    :538-539; the result's scores are float64 too) or float32.
     With ``catalog`` (device trie) and ``beam_node [R, W]``, each beam's
     candidates outside its valid continuations leave the pool (the catalog
     mask of serving_engine.py:381-394, 504-506) and the result carries the
-    new beams' trie nodes."""
+    new beams' trie nodes.  ``candidates`` (float64 ``cum`` only) also
+    returns every old beam's top-``beam_width`` (token, logprob) list, the
+    per-step logprobs of the reference's beam search
+    (vllm_gr/entrypoints/llm.py:203-220)."""
     eos = -1 if eos_token_id is None else int(eos_token_id)
-    if catalog is None:
-        parent, token, score, eos_score = ops.beam_prune_topk(logits, cum_logprob, beam_width, eos,
-                                                               workspace=workspace)
-        return PruneResult(parent, token, score, eos_score)
-    parent, token, score, eos_score, node = ops.beam_prune_topk(
-        logits, cum_logprob, beam_width, eos, workspace=workspace, catalog=catalog, beam_node=beam_node)
-    return PruneResult(parent, token, score, eos_score, node)
+    out = list(ops.beam_prune_topk(logits, cum_logprob, beam_width, eos, workspace=workspace, catalog=catalog,
+                                   beam_node=beam_node, candidates=candidates))
+    ct = cl = None
+    if candidates:
+        ct, cl = out[-2], out[-1]
+        del out[-2:]
+    node = out[4] if catalog is not None else None
+    return PruneResult(out[0], out[1], out[2], out[3], node, ct, cl)
 
 
 def fork_info(res: PruneResult) -> list[list[tuple[int, int]]]:
@@ -89,17 +98,19 @@ def pruned_parents(res: PruneResult, beam_width: int) -> list[list[int]]:
 
 def beam_search_step(table, logits: torch.Tensor, cum_logprob: torch.Tensor, kv_caches,
                      eos_token_id: int | None = None, status: torch.Tensor | None = None, *,
-                     catalog=None, beam_node: torch.Tensor | None = None):
+                     catalog=None, beam_node: torch.Tensor | None = None, candidates: bool = False):
     """Prune the candidates of every beam and fork the beams' resident KV.
 
     ``table``: the batch's :class:`~vllm_gr_amd.v1.beam_kv.BeamKVTable`;
     ``logits [R, W, V]`` are the last decode step's logits rows (one per
     beam), ``cum_logprob [R, W]`` the beams' scores.  Returns the
     :class:`PruneResult`; its ``token`` are the next step's query tokens and
-    its ``score`` the new cumulative logprobs.  Unfilled slots (fewer live
+    its ``score`` the new cumulative logprobs (float64 when ``cum_logprob``
+    is).  Unfilled slots (fewer live
     candidates than beams) keep their parent's KV."""
     W = table.beam_width
-    res = prune_step(logits, cum_logprob, W, eos_token_id, catalog=catalog, beam_node=beam_node)
+    res = prune_step(logits, cum_logprob, W, eos_token_id, catalog=catalog, beam_node=beam_node,
+                     candidates=candidates)
     parent = torch.where(res.parent >= 0, res.parent,
                          torch.arange(W, device=res.parent.device, dtype=res.parent.dtype)[None])
     table.fork(parent, kv_caches, status=status)

@@ -29,6 +29,7 @@ from dataclasses import dataclass, field
 
 import torch
 
+from .. import logprobs as lpm
 from ..v1.beam_kv import BeamKVTable
 from ..v1.sid_decoder import SID_DECODER_1P7B, DecoderConfig, SidDecoder, init_weights
 from ..v1.sid_runner import SidModelRunner
@@ -46,6 +47,7 @@ class BeamSearchSequence:
     finish_reason: str | None = None
     stop_reason: int | None = None
     text: str | None = None
+    logprobs: lpm.FlatLogprobs | None = None
 
 
 @dataclass
@@ -92,7 +94,7 @@ class LLM:
     def __init__(self, cfg: DecoderConfig = SID_DECODER_1P7B, *, seed: int = 0, device="cuda",
                  num_blocks: int = 4096, block_size: int = 16, eos_token_id: int | None = None,
                  special_tokens: dict[str, int] | None = None, weights: dict | None = None,
-                 max_position: int = 32768, use_graphs: bool = True, catalog=None):
+                 max_position: int = 32768, use_graphs: bool = True, catalog=None, logprobs: bool = True):
         dev = torch.device(device)
         if dev.type != "cuda":
             raise ValueError("the beam path runs on a HIP device (torch 'cuda')")
@@ -108,6 +110,13 @@ class LLM:
         self._catalog_dev = None
         self.last_times = StepTimes()
         self._batch = 0
+        # rebuild every output beam's per-step logprob lists (the reference always does,
+        # vllm_gr/entrypoints/llm.py:283-288)
+        self.logprobs = logprobs
+        # observer of every step's logits: hook(step, logits [R, W, V] float32,
+        # the beams' generated tokens [R, W, step] int32), called on the
+        # stream before the step's pruning reads the logits
+        self.logits_hook = None
 
     def _token_id(self, tok, what: str) -> int | None:
         if tok is None:
@@ -156,8 +165,12 @@ class LLM:
                 self._catalog_dev = self.catalog.to_device(dev)
             cat = self._catalog_dev
         hist = torch.empty(R, W, 0, dtype=torch.int32, device=dev)
-        score = torch.zeros(R, W, dtype=torch.float32, device=dev)
+        # beam scores stay float64 from step to step (serving_engine.py:511, :538-539)
+        score = torch.zeros(R, W, dtype=torch.float64, device=dev)
         finished: list[tuple[torch.Tensor, torch.Tensor]] = []  # (eos_score [R, W_old], hist_old)
+        parents: list[torch.Tensor] = []  # per step: each new beam's parent [R, W]
+        cands: list[tuple[torch.Tensor, torch.Tensor]] = []  # per step: old beams' top-W lists
+        lp = self.logprobs
         blocks: list[int] = []
         try:
             if steps > 0:
@@ -173,9 +186,14 @@ class LLM:
                 ev[-1].record(stream)
                 # the prompt is the one beam of every request (llm.py:118-146), at the trie's root
                 node0 = None if cat is None else torch.zeros(R, 1, dtype=torch.int32, device=dev)
-                res = bsm.prune_step(logits[:, None], torch.zeros(R, 1, device=dev), W, eos, catalog=cat,
-                                     beam_node=node0)
+                if self.logits_hook is not None:
+                    self.logits_hook(0, logits[:, None], torch.empty(R, 1, 0, dtype=torch.int32, device=dev))
+                res = bsm.prune_step(logits[:, None], torch.zeros(R, 1, dtype=torch.float64, device=dev), W, eos,
+                                     catalog=cat, beam_node=node0, candidates=lp)
                 finished.append((res.eos_score, torch.empty(R, 1, 0, dtype=torch.int32, device=dev)))
+                parents.append(res.parent)
+                if lp:
+                    cands.append((res.cand_token, res.cand_logprob))
                 hist = res.token[..., None]
                 score = res.score
                 table = None if sbt is None else BeamKVTable(prefix_bt, prefix_len, W, sbt, block_size=bs)
@@ -183,13 +201,18 @@ class LLM:
                     tok = res.token.clamp(min=0).view(-1).to(torch.int64)
                     logits = self.runner.decode(table, tok, rids, lens, step=s - 1)
                     table.advance()
+                    if self.logits_hook is not None:
+                        self.logits_hook(s, logits, hist)
                     node = res.node
                     if s + 1 < steps:
                         res = bsm.beam_search_step(table, logits, score, self.runner.kv_caches, eos, catalog=cat,
-                                                   beam_node=node)
+                                                   beam_node=node, candidates=lp)
                     else:
-                        res = bsm.prune_step(logits, score, W, eos, catalog=cat, beam_node=node)
+                        res = bsm.prune_step(logits, score, W, eos, catalog=cat, beam_node=node, candidates=lp)
                     finished.append((res.eos_score, hist))
+                    parents.append(res.parent)
+                    if lp:
+                        cands.append((res.cand_token, res.cand_logprob))
                     par = res.parent.clamp(min=0).to(torch.int64)
                     hist = torch.cat((hist.gather(1, par[..., None].expand(-1, -1, hist.shape[2])),
                                       res.token[..., None]), dim=2)
@@ -198,6 +221,8 @@ class LLM:
                     ev[-1].record(stream)
             hist_h, score_h = hist.cpu().tolist(), score.cpu().tolist()
             fin_h = [(e.cpu().tolist(), h.cpu().tolist()) for e, h in finished]
+            par_h = [p.cpu().tolist() for p in parents]
+            cand_h = [lpm.step_lists(t, l) for t, l in cands] if lp else None
         finally:
             self.runner.pool.release(blocks)
         times.wall_ms = (time.perf_counter() - t_wall) * 1e3
@@ -206,30 +231,41 @@ class LLM:
             times.step_ms = [a.elapsed_time(b) for a, b in zip(ev[1:-1], ev[2:])]
             times.total_ms = ev[0].elapsed_time(ev[-1])
         self.last_times = times
-        return self._outputs(toks, hist_h, score_h, fin_h, steps, eos, end, params.length_penalty, W)
+        return self._outputs(toks, hist_h, score_h, fin_h, steps, eos, begin, end, params.length_penalty, W,
+                             par_h, cand_h)
 
     @staticmethod
-    def _outputs(toks, hist, score, finished, steps, eos, end, length_penalty, W):
+    def _outputs(toks, hist, score, finished, steps, eos, begin, end, length_penalty, W, parents, cands):
         outs = []
         for r, prompt in enumerate(toks):
+            # (sequence, parent at its last step, that step) per candidate output
             done = []
-            for eos_sc, hist_old in finished:
+            for s, (eos_sc, hist_old) in enumerate(finished):
                 for b, sc in enumerate(eos_sc[r]):
                     if sc != float("-inf"):
-                        done.append(BeamSearchSequence(prompt + hist_old[r][b] + [eos], sc,
-                                                       finish_reason="stop", stop_reason=eos))
+                        done.append((BeamSearchSequence(prompt + hist_old[r][b] + [eos], sc,
+                                                        finish_reason="stop", stop_reason=eos), b, s))
             live = []
             tail = [] if end is None else [end]
             if steps == 0:
-                live.append(BeamSearchSequence(prompt + tail, 0.0, finish_reason="length"))
+                live.append((BeamSearchSequence(prompt + tail, 0.0, finish_reason="length"), None, -1))
             else:
                 for b in range(W):
                     if score[r][b] == float("-inf"):
                         continue  # a slot no candidate filled
-                    live.append(BeamSearchSequence(prompt + hist[r][b] + tail, score[r][b],
-                                                   finish_reason="length"))
+                    live.append((BeamSearchSequence(prompt + hist[r][b] + tail, score[r][b],
+                                                    finish_reason="length"), parents[-1][r][b], steps - 1))
             allseq = done + live
-            allseq.sort(key=lambda x: beam_search_score(x.tokens, x.cum_logprob, eos, length_penalty),
+            allseq.sort(key=lambda x: beam_search_score(x[0].tokens, x[0].cum_logprob, eos, length_penalty),
                         reverse=True)
-            outs.append(BeamSearchOutput(allseq[:W]))
+            best = allseq[:W]
+            if cands is not None:
+                # the best beams' lists, rebuilt along the parent indices (llm.py:283-288)
+                for seq, p, s in best:
+                    if s < 0:
+                        seq.logprobs = lpm.rebuild(r, 0, -1, parents, cands, begin, end)
+                    else:
+                        stop = seq.finish_reason == "stop"
+                        seq.logprobs = lpm.rebuild(r, p, s, parents, cands, begin, None if stop else end)
+            outs.append(BeamSearchOutput([seq for seq, _, _ in best]))
         return outs

@@ -313,34 +313,76 @@ def prune_workspace_bytes(num_reqs: int, beam_width: int, vocab: int, k: int) ->
 def beam_prune_topk(logits: torch.Tensor, cum: torch.Tensor, k: int, eos_token_id: int = -1, *,
                     workspace: torch.Tensor | None = None, out=None, catalog=None,
                     beam_node: torch.Tensor | None = None, node_out: torch.Tensor | None = None,
-                    status: torch.Tensor | None = None):
+                    status: torch.Tensor | None = None, candidates: bool = False):
     """Fused log_softmax + cum + top-k over beams x vocab per request.
 
-    ``logits``: ``[R, W, V]`` float32 (vocab contiguous), ``cum``: ``[R, W]``.
-    Returns ``(parent [R,k] int32, token [R,k] int32, score [R,k] float32,
-    eos_score [R,W] float32)``.  With ``catalog`` (a
+    ``logits``: ``[R, W, V]`` float32 (vocab contiguous), ``cum``: ``[R, W]``
+    float32 or float64.  Returns ``(parent [R,k] int32, token [R,k] int32,
+    score [R,k], eos_score [R,W])``, the scores in ``cum``'s dtype: a float64
+    ``cum`` runs gr_beam_prune_topk_f64, which carries the beam scores in
+    float64 as the reference does between steps (serving_engine.py:511,
+    :538-539).  With ``catalog`` (a
     :class:`~vllm_gr_amd.entrypoints.catalog.CatalogTensors`) and ``beam_node
-    [R, W]`` int32, candidates outside each beam's trie node are dropped
-    (gr_beam_prune_topk_catalog) and a fifth value, ``node_out [R, k]``, is
-    returned."""
+    [R, W]`` int32, candidates outside each beam's trie node are dropped and
+    ``node_out [R, k]`` is appended to the result.  ``candidates=True``
+    (float64 ``cum`` only) appends each beam's top-k list before EOS/catalog
+    removal: ``cand_token [R, W, k]`` int32 and ``cand_logprob [R, W, k]``
+    float32 (logit - lse), the per-step logprob lists of the reference's
+    beam search (vllm_gr/logprobs.py:34-85)."""
     dev = _need_cuda(logits, cum, workspace, beam_node, node_out, status)
     if logits.dim() != 3 or logits.dtype != torch.float32 or logits.stride(2) != 1 \
             or logits.stride(0) != logits.shape[1] * logits.stride(1):
         raise ValueError("logits must be float32 [R, W, V] with rows at a uniform stride")
     R, W, V = logits.shape
-    if cum.shape != (R, W) or cum.dtype != torch.float32 or not cum.is_contiguous():
-        raise ValueError("cum must be a contiguous float32 [R, W] tensor")
+    f64 = cum.dtype == torch.float64
+    if cum.shape != (R, W) or cum.dtype not in (torch.float32, torch.float64) or not cum.is_contiguous():
+        raise ValueError("cum must be a contiguous float32 or float64 [R, W] tensor")
+    if candidates and not f64:
+        raise ValueError("candidates=True needs a float64 cum (gr_beam_prune_topk_f64)")
     need = prune_workspace_bytes(R, W, V, k)
     if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    sdt = cum.dtype
     if out is None:
         parent = torch.empty((R, k), dtype=torch.int32, device=dev)
         token = torch.empty((R, k), dtype=torch.int32, device=dev)
-        score = torch.empty((R, k), dtype=torch.float32, device=dev)
-        eos_score = torch.empty((R, W), dtype=torch.float32, device=dev)
+        score = torch.empty((R, k), dtype=sdt, device=dev)
+        eos_score = torch.empty((R, W), dtype=sdt, device=dev)
     else:
         parent, token, score, eos_score = out
+        if score.dtype != sdt or eos_score.dtype != sdt:
+            raise ValueError("score / eos_score must have cum's dtype")
     ws_bytes = workspace.numel() * workspace.element_size()
+    if catalog is not None:
+        _need_cuda(catalog.node_start, catalog.child_token, catalog.child_node)
+        for name, t in (("node_start", catalog.node_start), ("child_token", catalog.child_token),
+                        ("child_node", catalog.child_node)):
+            _need_i32(name, t)
+        if beam_node is None or beam_node.shape != (R, W):
+            raise ValueError("beam_node must be an int32 [R, W] tensor")
+        _need_i32("beam_node", beam_node)
+        if node_out is None:
+            node_out = torch.empty((R, k), dtype=torch.int32, device=dev)
+        if node_out.shape != (R, k):
+            raise ValueError("node_out must be [R, k]")
+        _need_i32("node_out", node_out)
+        trie = (beam_node.data_ptr(), catalog.node_start.data_ptr(),
+                _ptr(catalog.child_token if catalog.num_edges else None),
+                _ptr(catalog.child_node if catalog.num_edges else None), catalog.num_nodes, catalog.num_edges)
+    if f64:
+        cand_tok = cand_lp = None
+        if candidates:
+            cand_tok = torch.empty((R, W, k), dtype=torch.int32, device=dev)
+            cand_lp = torch.empty((R, W, k), dtype=torch.float32, device=dev)
+        if catalog is None:
+            trie = (None, None, None, None, 0, 0)
+        code = _C.lib().gr_beam_prune_topk_f64(
+            logits.data_ptr(), logits.stride(1), cum.data_ptr(), R, W, V, int(k), int(eos_token_id), *trie,
+            parent.data_ptr(), token.data_ptr(), score.data_ptr(), eos_score.data_ptr(), _ptr(node_out),
+            _ptr(cand_tok), _ptr(cand_lp), workspace.data_ptr(), ws_bytes, _ptr(status), _stream(dev))
+        _C.check("gr_beam_prune_topk_f64", code)
+        res = (parent, token, score, eos_score) + ((node_out,) if catalog is not None else ())
+        return res + ((cand_tok, cand_lp) if candidates else ())
     if catalog is None:
         code = _C.lib().gr_beam_prune_topk(
             logits.data_ptr(), logits.stride(1), cum.data_ptr(), R, W, V, int(k), int(eos_token_id),
@@ -348,22 +390,8 @@ def beam_prune_topk(logits: torch.Tensor, cum: torch.Tensor, k: int, eos_token_i
             workspace.data_ptr(), ws_bytes, _stream(dev))
         _C.check("gr_beam_prune_topk", code)
         return parent, token, score, eos_score
-    _need_cuda(catalog.node_start, catalog.child_token, catalog.child_node)
-    for name, t in (("node_start", catalog.node_start), ("child_token", catalog.child_token),
-                    ("child_node", catalog.child_node)):
-        _need_i32(name, t)
-    if beam_node is None or beam_node.shape != (R, W):
-        raise ValueError("beam_node must be an int32 [R, W] tensor")
-    _need_i32("beam_node", beam_node)
-    if node_out is None:
-        node_out = torch.empty((R, k), dtype=torch.int32, device=dev)
-    if node_out.shape != (R, k):
-        raise ValueError("node_out must be [R, k]")
-    _need_i32("node_out", node_out)
     code = _C.lib().gr_beam_prune_topk_catalog(
-        logits.data_ptr(), logits.stride(1), cum.data_ptr(), R, W, V, int(k), int(eos_token_id),
-        beam_node.data_ptr(), catalog.node_start.data_ptr(), _ptr(catalog.child_token if catalog.num_edges else None),
-        _ptr(catalog.child_node if catalog.num_edges else None), catalog.num_nodes, catalog.num_edges,
+        logits.data_ptr(), logits.stride(1), cum.data_ptr(), R, W, V, int(k), int(eos_token_id), *trie,
         parent.data_ptr(), token.data_ptr(), score.data_ptr(), eos_score.data_ptr(), node_out.data_ptr(),
         workspace.data_ptr(), ws_bytes, _ptr(status), _stream(dev))
     _C.check("gr_beam_prune_topk_catalog", code)
