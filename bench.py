@@ -33,18 +33,18 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "vllm-gr-ehaleva_amd")]
 
 METRIC = "BeamAttention decode µs/step + HBM GB/s (% peak) at 128 beams, 2K prefix"
 HBM_PEAK_GBPS = 8000.0
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_beam128_hbm_traffic.txt")
+PMC_SUMMARY = {w: os.path.join(ROOT, "profiles", f"{w}_beam128_hbm_traffic.txt") for w in ("decode", "fork", "prune")}
 
 
 def _log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def _traffic_from_profile():
+def _traffic_from_profile(workload: str = "decode"):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
     calibrated against a copy kernel), when that summary has been committed."""
     try:
-        with open(PMC_SUMMARY) as f:
+        with open(PMC_SUMMARY[workload]) as f:
             m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read())
         return float(m.group(1)) if m else None
     except OSError:
@@ -83,22 +83,43 @@ def cpu_baseline(wl, budget_s: float = 20.0):
                       f"(prefix pass + suffix pass + LSE merge)"}
 
 
-def _time_launches(step, steps: int, warmup: int) -> float:
+# Copies of a workload that one timed loop rotates over: their inputs total
+# well over the MI355X's 256 MB Infinity Cache (MALL), so a launch finds the
+# bytes the previous launches touched evicted and reads its own from HBM --
+# as a served decode step does, whose 28 layers each read distinct KV.
+COLD_COPIES = 5
+MALL_BYTES = 256 << 20
+
+
+def _time_launches(steps_fns, steps: int, warmup: int) -> float:
     """Average microseconds per launch over ``steps`` back-to-back launches on
-    the current stream (HIP events), after ``warmup`` untimed launches."""
+    the current stream (HIP events), after ``warmup`` untimed launches.
+    ``steps_fns``: one launch closure, or a list of them (one per workload
+    copy) taken in turn."""
     import torch
-    for _ in range(warmup):
-        step()
+    fns = steps_fns if isinstance(steps_fns, list) else [steps_fns]
+    for i in range(warmup):
+        fns[i % len(fns)]()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for _ in range(steps):
-        step()
+    for i in range(steps):
+        fns[i % len(fns)]()
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) * 1000.0 / steps
+
+
+def _device_copy(t, gen):
+    """A fresh device tensor shaped like ``t``: float tensors redrawn from
+    ``gen`` (N(0,1) scaled to t's std), integer tensors cloned."""
+    import torch
+    if t.is_floating_point():
+        std = float(t[:1].float().std()) if t.numel() > 1 else 1.0
+        return (torch.randn(t.shape, generator=gen, device=t.device, dtype=torch.float32) * std).to(t.dtype)
+    return t.clone()
 
 
 def bench_other(args) -> int:
@@ -110,16 +131,22 @@ def bench_other(args) -> int:
 
     dev = torch.device("cuda:0")
     n_cpu = len(os.sched_getaffinity(0))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
     if args.workload == "fork":
         host = workloads.fork_beam128(seed=0)
         wl = host.to(dev)
-        k_cache, v_cache = wl.kv_cache[0], wl.kv_cache[1]
         bt_out = torch.empty_like(wl.suffix_bt)
         len_out = torch.empty_like(wl.suffix_len)
 
-        def step():  # out-of-place tables; copies and appends rewrite the same bytes each time
-            ops.beam_kv_fork(wl.parent, wl.suffix_bt, wl.suffix_len, k_cache, v_cache, wl.k_new, wl.v_new,
-                             bt_out=bt_out, len_out=len_out)
+        def make_step(kv, k_new, v_new):
+            def step():  # out-of-place tables; copies and appends rewrite the same bytes each time
+                ops.beam_kv_fork(wl.parent, wl.suffix_bt, wl.suffix_len, kv[0], kv[1], k_new, v_new,
+                                 bt_out=bt_out, len_out=len_out)
+            return step
+        warm = make_step(wl.kv_cache, wl.k_new, wl.v_new)
+        cold = [warm] + [make_step(_device_copy(wl.kv_cache, gen), _device_copy(wl.k_new, gen),
+                                   _device_copy(wl.v_new, gen)) for _ in range(COLD_COPIES - 1)]
         nbytes = host.algorithmic_bytes()
         metric = "beam KV fork+append us/step + HBM GB/s at 16 requests x 128 beams"
         workload = "fork+append: 16 requests x 128 beams, old suffix U[1,15], 8 kv heads x 128, block 16, bf16"
@@ -133,15 +160,21 @@ def bench_other(args) -> int:
                 torch.empty((64, 128), dtype=torch.float32, device=dev),
                 torch.empty((64, 128), dtype=torch.float32, device=dev))
 
-        def step():
-            ops.beam_prune_topk(wl.logits, wl.cum, 128, -1, workspace=ws, out=outs)
+        def make_step(logits):
+            def step():
+                ops.beam_prune_topk(logits, wl.cum, 128, -1, workspace=ws, out=outs)
+            return step
+        warm = make_step(wl.logits)
+        cold = [warm, make_step(_device_copy(wl.logits, gen))]  # 2 x 256 MiB of logits
         nbytes = host.algorithmic_bytes()
         metric = "fused beam pruning us/step + HBM GB/s at 64 requests x 128 beams x vocab 8192"
         workload = "prune: log_softmax + cum + top-128 over 128 beams x 8192 vocab, 64 requests, fp32"
         dtype = "f32 (f64 scores)"
-    us = _time_launches(step, args.steps, args.warmup)
+    us = _time_launches(cold, args.steps, args.warmup)
+    us_warm = None if args.no_warm else _time_launches(warm, args.steps, args.warmup)
     gbps = nbytes / (us * 1e-6) / 1e9
-    _log(f"bench: {args.workload}: {us:.2f} us/step, {gbps:.1f} GB/s algorithmic ({nbytes} B/step)")
+    _log(f"bench: {args.workload}: cold {us:.2f} us/step, {gbps:.1f} GB/s algorithmic ({nbytes} B/step); "
+         f"warm {us_warm} us/step")
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
@@ -177,9 +210,14 @@ def bench_other(args) -> int:
             "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 5), "us_per_step": round(us, 3),
             "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded)",
-            "config": {"workload": workload, "algorithmic_bytes_per_step": nbytes},
+            "config": {"workload": workload, "algorithmic_bytes_per_step": nbytes,
+                       "inputs": f"{len(cold)} copies rotated per launch (cold: no reuse through the "
+                                 f"256 MB Infinity Cache)"},
+            "warm": None if us_warm is None else {
+                "us_per_step": round(us_warm, 3), "gbps": round(nbytes / (us_warm * 1e-6) / 1e9, 2),
+                "inputs": "one copy relaunched"},
             "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": _traffic_from_profile(args.workload)},
             "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
     return 0
@@ -287,6 +325,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-warm", action="store_true",
+                    help="skip the warm (one relaunched copy) timing; the cold rotation is the headline")
     ap.add_argument("--kernel", choices=["auto", "generic"], default="auto")
     ap.add_argument("--workload", choices=["decode", "fork", "prune", "e2e"], default="decode",
                     help="decode (the headline line), the fork+append / pruning kernels, or e2e "
@@ -323,30 +363,30 @@ def main() -> int:
     _log("bench: building decode_beam128 inputs (seed 0)")
     host_wl = workloads.decode_beam128(seed=0)
     wl = host_wl.to(dev)
-    out = torch.empty_like(wl.q)
     ops.set_decode_kernel(args.kernel)
 
-    def step():
-        ops.beam_attn_decode(wl.q, wl.k_cache, wl.v_cache, wl.prefix_bt, wl.prefix_len, wl.beam_start,
-                             wl.suffix_bt, wl.suffix_len, scale=wl.scale, max_beams_per_req=wl.max_beams,
-                             out=out)
+    def make_step(kv, q):
+        out = torch.empty_like(q)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(args.steps):
-        step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms_total = start.elapsed_time(end)
-    us_step = ms_total * 1000.0 / args.steps
+        def step():
+            ops.beam_attn_decode(q, kv[0], kv[1], wl.prefix_bt, wl.prefix_len, wl.beam_start,
+                                 wl.suffix_bt, wl.suffix_len, scale=wl.scale, max_beams_per_req=wl.max_beams,
+                                 out=out)
+        return step
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    warm = make_step(wl.kv_cache, wl.q)
+    # each copy: its own cache pool and queries (the same tables: tiny), drawn on the device
+    cold = [warm] + [make_step(_device_copy(wl.kv_cache, gen), _device_copy(wl.q, gen))
+                     for _ in range(COLD_COPIES - 1)]
     nbytes = host_wl.algorithmic_bytes()
+    assert (COLD_COPIES - 1) * nbytes > MALL_BYTES
+    us_step = _time_launches(cold, args.steps, args.warmup)
+    us_warm = None if args.no_warm else _time_launches(warm, args.steps, args.warmup)
     gbps = nbytes / (us_step * 1e-6) / 1e9
-    _log(f"bench: {us_step:.2f} us/step, {gbps:.1f} GB/s algorithmic ({nbytes} B/step)")
+    _log(f"bench: cold {us_step:.2f} us/step, {gbps:.1f} GB/s algorithmic ({nbytes} B/step); "
+         f"warm {us_warm} us/step")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -372,9 +412,14 @@ def main() -> int:
         "config": {"workload": "beam decode: 8 requests x 128 beams, shared prefix 2048, suffix U[1,8], "
                                "32 q / 8 kv heads, head_dim 128, block 16",
                    "requests": 8, "beams": 128, "prefix": 2048, "kernel": args.kernel,
-                   "algorithmic_bytes_per_step": nbytes, "flops_per_step": host_wl.flops()},
+                   "algorithmic_bytes_per_step": nbytes, "flops_per_step": host_wl.flops(),
+                   "inputs": f"{len(cold)} copies rotated per launch (cold: no reuse through the 256 MB "
+                             f"Infinity Cache)"},
+        "warm": None if us_warm is None else {
+            "us_per_step": round(us_warm, 3), "gbps": round(nbytes / (us_warm * 1e-6) / 1e9, 2),
+            "inputs": "one copy relaunched"},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": _traffic_from_profile()},
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": _traffic_from_profile("decode")},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
