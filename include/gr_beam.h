@@ -270,6 +270,27 @@ gr_status_t gr_beam_prune_topk(
     void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * gr_beam_prune_topk without a workspace argument: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ *
+ * Same arguments (minus workspace / workspace_bytes), kernels and results as
+ * gr_beam_prune_topk.  The workspace is a static device array of
+ * GR_PRUNE_SCRATCH_BYTES per GPU (held until the process ends; the device
+ * address is looked up on the first call on each device, which must be the
+ * current device, the stream's).  A call whose gr_beam_prune_workspace_size
+ * exceeds GR_PRUNE_SCRATCH_BYTES returns GR_ERR_WORKSPACE and launches
+ * nothing.  The call allocates nothing.  Every call on one GPU shares that
+ * array: calls that may overlap on one GPU (different streams, or host
+ * threads) race and must be serialised by the caller.
+ */
+#define GR_PRUNE_SCRATCH_BYTES ((size_t)16 << 20)
+gr_status_t gr_beam_prune_topk_noalloc(
+    const float* logits, int64_t logits_row_stride, const float* cum,
+    int num_reqs, int beam_width, int vocab, int k, int eos_token_id,
+    int32_t* parent, int32_t* token, float* score, float* eos_score, hipStream_t stream);
+
+/*
  * gr_beam_prune_topk / gr_beam_prune_topk_catalog with the beam scores
  * carried in float64 between steps.
  *

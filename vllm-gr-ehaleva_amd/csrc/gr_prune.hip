@@ -20,6 +20,7 @@
 // bit for bit.
 #include "gr_common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace gr {
@@ -1349,4 +1350,48 @@ extern "C" gr_status_t gr_beam_prune_topk_f64(
                                 parent, token, workspace, workspace_bytes, stream);
   if (st != GR_OK || num_reqs == 0 || !beam_node) return st;
   return catalog_advance_launch(a, node_out, stream);
+}
+
+// ---- the entry point that allocates nothing -----------------------------
+// Scratch of gr_beam_prune_topk_noalloc: the workspace of gr_beam_prune_topk
+// in a static device array.  Each device holds its own copy until the
+// process ends.  In host code `scratch` names a host-side stand-in, never the
+// device memory: the device address comes from hipGetSymbolAddress, taken
+// once per device with that device current, and only that address is passed
+// to kernels.
+static __device__ __attribute__((aligned(256))) uint8_t scratch[GR_PRUNE_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+// The current device's address of `scratch` (looked up on its first use).
+gr_status_t scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return GR_ERR_LAUNCH;
+  if (dev < 0 || dev >= kMaxDevices) return GR_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return GR_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GR_OK;
+}
+}  // namespace
+
+extern "C" gr_status_t gr_beam_prune_topk_noalloc(const float* logits, int64_t logits_row_stride,
+                                                  const float* cum, int num_reqs, int beam_width, int vocab,
+                                                  int k, int eos_token_id, int32_t* parent, int32_t* token,
+                                                  float* score, float* eos_score, hipStream_t stream) {
+  if (num_reqs < 0 || beam_width < 1 || vocab < 1 || k < 1) return GR_ERR_INVALID_ARG;
+  if (gr_beam_prune_workspace_size(num_reqs, beam_width, vocab, k) > GR_PRUNE_SCRATCH_BYTES)
+    return GR_ERR_WORKSPACE;
+  void* ws = nullptr;
+  const gr_status_t st = scratch_address(&ws);
+  if (st != GR_OK) return st;
+  return gr_beam_prune_topk(logits, logits_row_stride, cum, num_reqs, beam_width, vocab, k, eos_token_id, parent,
+                            token, score, eos_score, ws, GR_PRUNE_SCRATCH_BYTES, stream);
 }

@@ -26,6 +26,8 @@ GR_DEV_BAD_PARENT = 4
 GR_DEV_SUFFIX_FULL = 8
 GR_DEV_BAD_NODE = 16
 
+GR_PRUNE_SCRATCH_BYTES = 16 << 20  # static scratch of gr_beam_prune_topk_noalloc
+
 GR_DTYPE_F32 = 0
 GR_DTYPE_F16 = 1
 GR_DTYPE_BF16 = 2
@@ -96,6 +98,9 @@ SIGNATURES = {
     ]),
     "gr_beam_prune_topk": (_I, [
         _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _SZ, _P,
+    ]),
+    "gr_beam_prune_topk_noalloc": (_I, [
+        _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P,
     ]),
     "gr_beam_prune_topk_f64": (_I, [
         _P, _L, _P, _I, _I, _I, _I, _I,    # logits, stride, cum (float64), R, W, V, k, eos

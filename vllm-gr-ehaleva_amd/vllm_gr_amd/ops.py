@@ -398,6 +398,34 @@ def beam_prune_topk(logits: torch.Tensor, cum: torch.Tensor, k: int, eos_token_i
     return parent, token, score, eos_score, node_out
 
 
+def beam_prune_topk_noalloc(logits: torch.Tensor, cum: torch.Tensor, k: int, eos_token_id: int = -1, *,
+                            out):
+    """``beam_prune_topk`` (float32 scores, no catalog) through
+    gr_beam_prune_topk_noalloc: the library's static per-GPU scratch replaces
+    the workspace, so the call allocates nothing -- ``out`` = ``(parent [R,k]
+    int32, token [R,k] int32, score [R,k] float32, eos_score [R,W] float32)``
+    must be given.  Calls that may overlap on one GPU race on the scratch."""
+    dev = _need_cuda(logits, cum, *out)
+    if logits.dim() != 3 or logits.dtype != torch.float32 or logits.stride(2) != 1 \
+            or logits.stride(0) != logits.shape[1] * logits.stride(1):
+        raise ValueError("logits must be float32 [R, W, V] with rows at a uniform stride")
+    R, W, V = logits.shape
+    if cum.shape != (R, W) or cum.dtype != torch.float32 or not cum.is_contiguous():
+        raise ValueError("cum must be a contiguous float32 [R, W] tensor")
+    parent, token, score, eos_score = out
+    if parent.shape != (R, k) or token.shape != (R, k) or score.shape != (R, k) or eos_score.shape != (R, W):
+        raise ValueError("out must be (parent [R,k], token [R,k], score [R,k], eos_score [R,W])")
+    need = prune_workspace_bytes(R, W, V, k)
+    if need > _C.GR_PRUNE_SCRATCH_BYTES:
+        raise ValueError(f"gr_beam_prune_topk_noalloc: this call needs {need} bytes of scratch; the static "
+                         f"scratch holds {_C.GR_PRUNE_SCRATCH_BYTES} (use beam_prune_topk with a workspace)")
+    code = _C.lib().gr_beam_prune_topk_noalloc(
+        logits.data_ptr(), logits.stride(1), cum.data_ptr(), R, W, V, int(k), int(eos_token_id),
+        parent.data_ptr(), token.data_ptr(), score.data_ptr(), eos_score.data_ptr(), _stream(dev))
+    _C.check("gr_beam_prune_topk_noalloc", code)
+    return parent, token, score, eos_score
+
+
 # ---- fused decoder stages (include/gr_decoder.h) ---------------------------
 
 
