@@ -173,3 +173,65 @@ def test_fork_info_and_abort_set():
                            token=torch.zeros(1, 5, dtype=torch.int32), score=torch.zeros(1, 5),
                            eos_score=torch.zeros(1, 5))
     assert bsm.pruned_parents(res5, 5) == [[1, 3]]
+
+
+def _ref_build(q_lens, seq_lens, bt, mega, bs=16):
+    """Build with the reference's own mega dicts (no beam_kv)."""
+    m = _common(q_lens, seq_lens, bt, bs)
+    builder = ba.BeamAttentionMetadataBuilder(types.SimpleNamespace(block_size=bs), ["l0"], None, "cpu")
+    rids = [f"r{i}" for i in range(len(q_lens))]
+    tok = ba.MEGA_DATA_VAR.set({"req_ids": rids, "mega_data": {rids[i]: d for i, d in mega.items()}})
+    try:
+        return builder.build(0, m)
+    finally:
+        ba.MEGA_DATA_VAR.reset(tok)
+
+
+def _ref_mega(P, C, W, t):
+    return dict(is_mega_decode=True, mega_beam_width=W, mega_decode_steps=t, prefix_len=P, cache_len=C)
+
+
+def test_builder_reference_layout_complete_step():
+    """W=3, P=20, block 16, t=2, cache hit 16 (worked by hand): rows 0..5 are
+    beam 0 (the tail at positions 16..19 and its tokens at 20, 21) -> one
+    causal prefill row range over 22 keys; beams 1 and 2 (rows 6..7 and 8..9,
+    own tokens at positions 22.. and 24..) -> a decode group with the whole
+    20-token prompt as prefix and 2 query rows each."""
+    bt = torch.tensor([[5, 9, 4, 0]], dtype=torch.int32)
+    md = _ref_build([10], [26], bt, {0: _ref_mega(20, 16, 3, 2)})
+    p = md.prefill
+    assert p.token_index.tolist() == list(range(6)) and p.seq_len.tolist() == [22]
+    assert p.query_start.tolist() == [0, 6] and p.block_table.tolist() == bt.tolist()
+    (g,) = md.groups
+    assert g.q_per_beam == 2 and g.token_index.tolist() == [6, 7, 8, 9]
+    assert g.prefix_len.tolist() == [20] and g.beam_start.tolist() == [0, 2]
+    assert g.prefix_bt.tolist() == bt.tolist()
+    # positions 22 and 24 live in logical block 1 (physical 9) at offsets 6 and 8
+    assert g.suffix_bt.tolist() == [[9], [9]] and g.suffix_start.tolist() == [6, 8]
+    assert g.suffix_len.tolist() == [2, 2]
+    assert md.slot_mapping is not None and md.mega_req_idxs == [0]
+
+
+def test_builder_reference_layout_budget_and_standard_routing():
+    bt = torch.tensor([[5, 9, 4, 0], [1, 2, 3, 6]], dtype=torch.int32)
+    # request 0: 7 rows -> beam 0 takes 6, beam 1 only 1 of its 2, beam 2 none;
+    # request 1: P=40 with nothing cached -> rows 0..39 standard over 40 keys,
+    # beam 0's 1 token continues that prefill, beam 1 decodes at position 41
+    mega = {0: _ref_mega(20, 16, 3, 2), 1: _ref_mega(40, 0, 2, 1)}
+    md = _ref_build([7, 42], [26, 42], bt, mega)
+    assert mega[1]["cache_len"] == 40  # written back (beam_attn.py:280)
+    p = md.prefill
+    assert p.token_index.tolist() == list(range(6)) + list(range(7, 48))
+    assert p.query_start.tolist() == [0, 6, 47] and p.seq_len.tolist() == [22, 41]
+    assert p.block_table.tolist() == bt.tolist()
+    (g,) = md.groups  # both decode beams have one row: one group
+    assert g.q_per_beam == 1 and g.token_index.tolist() == [6, 48]
+    assert g.prefix_len.tolist() == [20, 40] and g.beam_start.tolist() == [0, 1, 2]
+    assert g.suffix_start.tolist() == [22 % 16, 41 % 16] and g.suffix_bt[:, 0].tolist() == [9, 3]
+    # a full beam and a budget-cut one make two groups (2 rows, 1 row)
+    md = _ref_build([9], [26], bt[:1], {0: _ref_mega(20, 16, 3, 2)})
+    assert [g.q_per_beam for g in md.groups] == [2, 1]
+    assert md.groups[0].token_index.tolist() == [6, 7] and md.groups[1].token_index.tolist() == [8]
+    # the reference's assertion for a cache hit past the prefix
+    with pytest.raises(AssertionError, match="prefix_len: 20, cache_len: 24"):
+        _ref_build([6], [26], bt[:1], {0: _ref_mega(20, 24, 3, 2)})

@@ -23,13 +23,34 @@ Kept from the reference (same names, argument meaning and error behaviour):
   NHD/HND stride orders, head size %8 and <= 256, ``supports_combination``
   returning a reason string or None.
 
-What differs, by design: a mega-decode request's beams attend their resident
-suffix (one new query token per beam) instead of recomputing W*t tokens, and
-the mega requests of a batch are one ``gr_beam_attn_decode`` launch (no
-prefix/suffix/merge passes, beam_attn.py:656-701).  The standard requests
-(prefill chunks, plain decodes) are one ``gr_paged_attn_prefill`` launch:
-varlen causal attention over their block-table rows, the
-``flash_attn_varlen_func`` call of the standard path (:643-654).
+Two mega-request layouts are accepted:
+
+* the reference's own (``MEGA_DATA_VAR`` exactly as engine_core_patch.py:258-271
+  emits it): ``prefill ++ concat(beam tokens)`` scheduled as one request
+  (core.py:108-112), row k at logical position ``cache_len + k`` of its
+  block-table row.  The builder applies the reference's routing
+  (beam_attn.py:255-413): an uncached prefix of at least two blocks goes to
+  the standard path (and ``cache_len`` is written back, :280), beam 0
+  computes the uncached prefix tail every other beam's suffix shares, and the
+  chunk budget leaves later beams partially run or skipped.  It maps that
+  routing onto the kernels by position: the standard rows and beam 0's rows
+  continue one causal prefill of the request (``gr_paged_attn_prefill``: a
+  row at position p sees keys 0..p, which is the cascade's cached prefix +
+  causal suffix), and every other beam is a decode beam whose prefix is the
+  whole shared prompt (cached part + the tail written this step) and whose
+  suffix is its own tokens at positions ``prefix_len + b * t + j``
+  (``gr_beam_attn_decode`` with ``q_per_beam`` = its row count, bottom-right
+  causal);
+* the resident layout of this build (the request's dict carries
+  ``beam_kv``, its :class:`~vllm_gr_amd.v1.beam_kv.BeamKVTable`): each beam
+  attends its resident suffix with one new query token, and the mega
+  requests of a batch are one ``gr_beam_attn_decode`` launch instead of
+  recomputing W*t tokens (no prefix/suffix/merge passes, :656-701).
+
+The standard requests (prefill chunks, plain decodes) are one
+``gr_paged_attn_prefill`` launch: varlen causal attention over their
+block-table rows, the ``flash_attn_varlen_func`` call of the standard path
+(:643-654).
 """
 
 from __future__ import annotations
@@ -146,11 +167,16 @@ class BeamAttentionMetadataBuilder:
         dev = self.device
         slot_mapping = m.slot_mapping
 
-        mega, std = [], []
+        mega, ref_mega, std = [], [], []
         for i in range(m.num_reqs):
             rid = req_ids[i] if i < len(req_ids) else None
             md = mega_data.get(rid, {}) if rid is not None else {}
-            (mega if md.get("is_mega_decode", False) else std).append((i, md))
+            if not md.get("is_mega_decode", False):
+                std.append((i, md))
+            elif "beam_kv" in md:
+                mega.append((i, md))
+            else:
+                ref_mega.append((i, md))
 
         groups: list[DecodeGroup] = []
         # ---- mega-decode requests: one query token per beam over the resident suffix.
@@ -207,20 +233,26 @@ class BeamAttentionMetadataBuilder:
                 groups.append(self._group(rows, m.num_actual_tokens, pbt, plen, widths, sbt, slen, None, 1))
                 groups[-1].max_prefix_len = max_prefix
 
-        # ---- standard requests: one varlen causal launch over their own rows
+        # ---- the reference's mega layout: causal prefill rows + decode beams
+        causal = [(q_starts[i], q_starts[i + 1], i, seq_lens[i]) for i, _ in std]
+        if ref_mega:
+            causal += self._route_reference_mega(ref_mega, q_starts, m, groups)
+
+        # ---- standard requests (and beam-0 / standard-routed mega rows): one
+        # varlen causal launch over their own rows
         prefill = None
-        reqs = [i for i, _ in std if q_starts[i + 1] > q_starts[i]]
-        if reqs:
-            rows = [(q_starts[i], q_starts[i + 1]) for i in reqs]
+        causal = [c for c in causal if c[1] > c[0]]
+        if causal:
+            rows = [(q0, q1) for q0, q1, _, _ in causal]
             qlens = [q1 - q0 for q0, q1 in rows]
-            every = reqs == list(range(m.num_reqs))
-            if every:  # the batch's own tensors serve as they are
+            reqs = [i for _, _, i, _ in causal]
+            if not ref_mega and reqs == list(range(m.num_reqs)):  # the batch's own tensors serve as they are
                 bt, qs, sl = m.block_table_tensor, m.query_start_loc, m.seq_lens
             else:
                 idx = torch.tensor(reqs, dtype=torch.int64).to(dev)
                 bt = m.block_table_tensor.index_select(0, idx)
                 qs = torch.tensor([0] + qlens, dtype=torch.int64).cumsum(0).to(torch.int32).to(dev)
-                sl = m.seq_lens_cpu.index_select(0, torch.tensor(reqs)).to(torch.int32).to(dev)
+                sl = torch.tensor([c[3] for c in causal], dtype=torch.int32).to(dev)
             prefill = PrefillGroup(
                 token_index=self._token_index(rows, m.num_actual_tokens),
                 block_table=bt.to(torch.int32).contiguous(), query_start=qs.to(torch.int32).contiguous(),
@@ -229,7 +261,82 @@ class BeamAttentionMetadataBuilder:
             num_actual_tokens=m.num_actual_tokens, max_query_len=m.max_query_len,
             query_start_loc=m.query_start_loc, max_seq_len=m.max_seq_len, seq_lens=m.seq_lens,
             block_table=m.block_table_tensor, slot_mapping=slot_mapping, causal=m.causal,
-            groups=groups, prefill=prefill, mega_req_idxs=[i for i, _ in mega], std_req_idxs=[i for i, _ in std])
+            groups=groups, prefill=prefill, mega_req_idxs=sorted(i for i, _ in mega + ref_mega),
+            std_req_idxs=[i for i, _ in std])
+
+    def _route_reference_mega(self, reqs, q_starts, m, groups) -> list[tuple[int, int, int, int]]:
+        """Route the reference-layout mega requests (beam_attn.py:255-413):
+        returns their causal-prefill row ranges ``(q0, q1, request, seq_len)``
+        and appends their decode beams to ``groups``, one group per query
+        count (full beams take ``mega_decode_steps`` rows; the chunk budget
+        leaves at most one partial beam per request)."""
+        bs, dev = self.block_size, self.device
+        causal = []
+        beams: dict[int, list[tuple[int, int, int, int]]] = {}  # rows -> [(request, prefix, pos0, row0)]
+        for i, md in reqs:
+            P, C = int(md["prefix_len"]), int(md["cache_len"])
+            W, t = int(md["mega_beam_width"]), int(md["mega_decode_steps"])
+            q0, q1 = q_starts[i], q_starts[i + 1]
+            # an uncached prefix of two blocks or more: the standard path over
+            # its rows (:273-282); the reference writes the new hit back
+            std_q = 0
+            if P - C > 0 and P - C >= 2 * bs:
+                std_q = min(P - C, q1 - q0)
+                C += std_q
+                md["cache_len"] = C
+            start = q0 + std_q
+            budget = q1 - start
+            b0 = 0
+            if W > 0 and t > 0 and budget > 0:
+                tail = P - C
+                assert tail >= 0, f"prefix_len: {P}, cache_len: {C}"
+                # beam 0: the shared tail and its own tokens, continuing the
+                # causal prefill at position C (:368-372)
+                b0 = min(budget, tail + t)
+                budget -= b0
+                row = start + b0
+                for b in range(1, W):
+                    if budget <= 0:
+                        break
+                    n = min(budget, t)  # the last beam may be cut by the chunk budget (:351-366)
+                    beams.setdefault(n, []).append((i, P, P + b * t, row))
+                    row += n
+                    budget -= n
+            if std_q + b0 > 0:
+                causal.append((q0, start + b0, i, C + b0))
+        for n, members in sorted(beams.items(), reverse=True):
+            groups.append(self._reference_beam_group(members, n, m, bs, dev))
+        return causal
+
+    def _reference_beam_group(self, members, n, m, bs, dev) -> DecodeGroup:
+        """Decode beams of the reference layout with ``n`` query rows each:
+        prefix = the request's first ``prefix_len`` tokens; suffix = the
+        beam's own ``n`` tokens at logical positions ``pos0 ..`` of the same
+        block-table row, given to the kernel as a window of that row."""
+        reqs = []
+        for i, P, _, _ in members:
+            if not reqs or reqs[-1][0] != i:
+                reqs.append((i, P))
+        widths = [sum(1 for mi in members if mi[0] == i) for i, _ in reqs]
+        req_of_beam = torch.tensor([mi[0] for mi in members], dtype=torch.int64)
+        pos0 = torch.tensor([mi[2] for mi in members], dtype=torch.int64)
+        first = pos0 // bs
+        cap = int(((pos0 % bs + n + bs - 1) // bs).max())
+        nb = m.block_table_tensor.shape[1]
+        win = (first[:, None] + torch.arange(cap)[None]).clamp(max=nb - 1)
+        bt = m.block_table_tensor
+        suffix_bt = bt[req_of_beam.to(dev)[:, None], win.to(dev)].to(torch.int32).contiguous()
+        rows = [(r0, r0 + n) for _, _, _, r0 in members]
+        idx = torch.tensor([i for i, _ in reqs], dtype=torch.int64).to(dev)
+        return DecodeGroup(
+            token_index=self._token_index(rows, m.num_actual_tokens),
+            prefix_bt=bt.index_select(0, idx).to(torch.int32).contiguous(),
+            prefix_len=torch.tensor([P for _, P in reqs], dtype=torch.int32).to(dev),
+            beam_start=torch.tensor([0] + widths, dtype=torch.int64).cumsum(0).to(torch.int32).to(dev),
+            suffix_bt=suffix_bt,
+            suffix_len=torch.full((len(members),), n, dtype=torch.int32).to(dev),
+            suffix_start=(pos0 % bs).to(torch.int32).to(dev), q_per_beam=n, max_beams=max(widths),
+            max_prefix_len=max(P for _, P in reqs))
 
     def _token_index(self, rows, ntok) -> torch.Tensor | None:
         """Batch positions of token ranges ``(q0, q1)``; None when they are
