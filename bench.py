@@ -327,7 +327,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-warm", action="store_true",
                     help="skip the warm (one relaunched copy) timing; the cold rotation is the headline")
-    ap.add_argument("--kernel", choices=["auto", "generic"], default="auto")
+    ap.add_argument("--kernel", choices=["auto", "generic", "mfma16"], default="auto")
     ap.add_argument("--workload", choices=["decode", "fork", "prune", "e2e"], default="decode",
                     help="decode (the headline line), the fork+append / pruning kernels, or e2e "
                          "(whole semantic-ID beam decode through a 28-layer decoder; a step is one batch)")

@@ -50,8 +50,10 @@ const char* gr_status_string(gr_status_t status);
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
 int gr_version(void);
 /* Decode kernel selection for tests and measurement (no reference
- * counterpart): 0 = automatic (matrix-core kernel where supported),
- * 1 = always the generic kernel.  Process-wide. */
+ * counterpart): 0 = automatic (the 32-row matrix-core kernel where
+ * supported, else the generic one), 1 = always the generic kernel, 2 = the
+ * 64-row matrix-core kernel where it applies (head_dim 128, block size 16 ..
+ * 256), else as 0.  Process-wide. */
 gr_status_t gr_set_decode_kernel(int which);
 
 /*

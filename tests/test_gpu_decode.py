@@ -70,7 +70,7 @@ def test_decode_small_fp32(device):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("kernel", ["auto", "generic"])
+@pytest.mark.parametrize("kernel", ["auto", "mfma16", "generic"])
 def test_decode_unscaled_tail_tile(device, dtype, kernel):
     """Prefix not a multiple of the 64-key tile, ragged suffixes, N(0,1) inputs."""
     wl = workloads.make_decode(R=2, W=16, P=300, L=(1, 8), Hq=32, Hkv=8, D=128, dtype=dtype,
@@ -213,7 +213,7 @@ def test_decode_prefix_beyond_staged_window(device):
     _check(out, lse, ref, ref_lse, atol=2e-2, rel=5e-2)
 
 
-@pytest.mark.parametrize("kernel", ["auto", "generic"])
+@pytest.mark.parametrize("kernel", ["auto", "mfma16", "generic"])
 def test_decode_long_suffix(device, kernel):
     """Suffixes spanning several blocks (37 and 60 tokens at block size 16):
     block ids past the ones staged per beam are read from the table."""
@@ -294,7 +294,7 @@ def test_decode_dominant_key_fp16_softcap(device, dtype, softcap):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("kernel,split", [("auto", False), ("auto", True), ("generic", False)])
+@pytest.mark.parametrize("kernel,split", [("auto", False), ("auto", True), ("mfma16", False), ("generic", False)])
 def test_decode_large_scores(device, dtype, kernel, split):
     """Q/K/V ~ N(0, 16): scores spread over tens of log2 units, so many rows
     leave the lazy softmax reference in the prefix loop, the last tiles and

@@ -330,7 +330,8 @@ extern "C" gr_status_t gr_beam_attn_decode(
   bool empty;
   const gr_status_t st = decode_args(a, empty, GR_DECODE_ARG_NAMES);
   if (st != GR_OK || empty) return st;
-  if (g_decode_kernel_override == 0 && mfma_decode_supported(a)) return launch_mfma_decode(a, stream);
+  if (g_decode_kernel_override == 2 && d16_decode_supported(a)) return launch_d16_decode(a, stream);
+  if (g_decode_kernel_override != 1 && mfma_decode_supported(a)) return launch_mfma_decode(a, stream);
   return launch_generic<false>(a, stream);
 }
 
@@ -375,11 +376,14 @@ extern "C" gr_status_t gr_beam_attn_decode_ws(
   const gr_status_t st = decode_args(a, empty, GR_DECODE_ARG_NAMES);
   if (st != GR_OK || empty) return st;
   if (max_prefix_len < 0) return GR_ERR_INVALID_ARG;
-  if (g_decode_kernel_override != 0 || !mfma_decode_supported(a)) return launch_generic<false>(a, stream);
+  if (g_decode_kernel_override == 1 || !mfma_decode_supported(a)) return launch_generic<false>(a, stream);
   int tiles, nsplit;
   mfma_decode_plan(num_reqs, max_beams_per_req, q_per_beam, num_q_heads, num_kv_heads, max_prefix_len, &tiles,
                    &nsplit);
-  if (nsplit <= 1) return launch_mfma_decode(a, stream);
+  if (nsplit <= 1) {
+    if (g_decode_kernel_override == 2 && d16_decode_supported(a)) return launch_d16_decode(a, stream);
+    return launch_mfma_decode(a, stream);
+  }
   const SplitLayout l = split_layout(tiles, nsplit);
   if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || workspace_bytes < l.total)
     return GR_ERR_WORKSPACE;
@@ -421,12 +425,12 @@ extern "C" gr_status_t gr_paged_attn_prefill(
   a.Hq = num_q_heads; a.Hkv = num_kv_heads; a.D = head_dim; a.bs = block_size; a.dtype = dtype;
   a.scale = scale; a.softcap = softcap; a.lse_out = lse_out; a.dev_status = dev_status;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
-  if (g_decode_kernel_override == 0 && mfma_decode_supported(a)) return launch_mfma_prefill(a, stream);
+  if (g_decode_kernel_override != 1 && mfma_decode_supported(a)) return launch_mfma_prefill(a, stream);
   return launch_generic<true>(a, stream);
 }
 
 extern "C" int gr_set_decode_kernel(int which) {
-  if (which < 0 || which > 1) return GR_ERR_INVALID_ARG;
+  if (which < 0 || which > 2) return GR_ERR_INVALID_ARG;
   g_decode_kernel_override = which;
   return GR_OK;
 }

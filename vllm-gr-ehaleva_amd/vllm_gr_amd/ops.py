@@ -88,8 +88,9 @@ def check_status(status: torch.Tensor) -> None:
 
 
 def set_decode_kernel(which: str) -> None:
-    """'auto' (matrix-core kernel where supported) or 'generic'."""
-    code = {"auto": 0, "generic": 1}[which]
+    """'auto' (the 32-row matrix-core kernel where supported), 'generic', or
+    'mfma16' (the 64-row matrix-core kernel where it applies)."""
+    code = {"auto": 0, "generic": 1, "mfma16": 2}[which]
     _C.check("gr_set_decode_kernel", _C.lib().gr_set_decode_kernel(code))
 
 
