@@ -2,15 +2,19 @@
 //
 // All three kernels move K/V rows of head_dim elements in 16-byte vectors;
 // they are pure HBM copy work (no arithmetic), so the design goal is wide
-// coalesced accesses and no serialisation:
-//  * beam_fork: one workgroup per child.  Every workgroup recomputes its
-//    request's row assignment from the read-only input tables (LDS atomics
-//    for each parent's lowest child and child count, wave ballots for the
-//    ranks), so there is no inter-workgroup dependency and no atomics on the
-//    tables; the new tables are written out of place.  Copy-on-write
-//    destinations are rows of childless parents, which nobody reads, and
-//    in-place appends write positions past every copied range, so the single
-//    launch is race-free.  Copies issue a batch of loads before the stores.
+// coalesced accesses, balanced work and no serialisation:
+//  * beam_fork: one workgroup per child (W per request).  Every workgroup
+//    works out its request's whole plan in LDS from the read-only input
+//    tables: each parent's lowest child (kept in place), the copying children
+//    and their ranks, the childless parents they take over (the owners), and
+//    the prefix sums of the copy lengths.  The request's copy-on-write tokens,
+//    concatenated, are then split evenly over its W workgroups, so the copy
+//    work is spread over every workgroup whichever children copy.  Copy
+//    destinations are rows of childless parents, which nobody reads; sources
+//    are rows of parents with children, which nobody writes below their
+//    length; each child's own append goes to a position past every copied
+//    range of its row; the new tables are written out of place -- so the
+//    single launch is race-free with no inter-workgroup dependency.
 //  * beam_append / reshape_and_cache: one wave per beam / token.
 #include "gr_common.h"
 
@@ -21,9 +25,17 @@ typedef uint32_t u32x4_t __attribute__((__vector_size__(4 * sizeof(uint32_t))));
 
 constexpr int FORK_THREADS = 256;
 constexpr int FORK_MAX_W = 1024;
-constexpr int FORK_STAGE_BT = 1024;  // a request's whole block table is staged in LDS up to this many entries
-constexpr int FORK_STAGE_S = 256;    // else the two rows a child uses, up to this many blocks each
-constexpr int FORK_BATCH = 4;        // 16-byte K and V vectors per thread in flight
+constexpr int FORK_STAGE_BT = 2048;  // a request's whole block table is staged in LDS up to this many entries
+
+// the fork kernel's LDS, sized by the request width W (ints; the 64-bit masks
+// first): cow and free masks, group bases, par, first (later the copy
+// lengths), cnt, lens, owner_of, cpre (W + 1), the scan scratch, the staged
+// block table
+__host__ __device__ inline int fork_lds_ints(int W, int S) {
+  const int ng = (W + 63) >> 6;
+  return 4 * ng + 2 * (ng + 1) + 6 * W + 1 + 8 + 1 + (W * S <= FORK_STAGE_BT ? W * S : 0);
+}
+constexpr int FORK_BATCH = 2;        // 16-byte K and V vectors per thread in flight
 
 struct KvGeom {
   void* k_cache;
@@ -37,16 +49,60 @@ __device__ inline int64_t kv_byte_off(const KvGeom& g, int64_t blk, int off, int
   return (blk * g.block_stride + (int64_t)off * g.tok_stride + (int64_t)h * g.head_stride) * g.esize;
 }
 
-__global__ __launch_bounds__(FORK_THREADS) void beam_fork(
+// exclusive prefix sum of v[0 .. n) into out[0 .. n] (out[n] = total) by a
+// 256-thread workgroup, n <= FORK_MAX_W; tmp: 8 ints
+__device__ inline void block_scan(const int* v, int* out, int n, int* tmp) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int PER = FORK_MAX_W / FORK_THREADS;
+  int x[PER], s = 0;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {  // thread tid owns entries PER*tid .. PER*tid + PER-1
+    const int i = PER * tid + u;
+    x[u] = i < n ? v[i] : 0;
+    s += x[u];
+  }
+  int incl = s;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) tmp[wave] = incl;
+  __syncthreads();
+  int base = incl - s;
+  for (int w = 0; w < wave; ++w) base += tmp[w];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = PER * tid + u;
+    if (i < n) out[i] = base;
+    base += x[u];
+  }
+  if (tid == FORK_THREADS - 1) out[n] = base;
+  __syncthreads();
+}
+
+// 8 waves per SIMD: every workgroup of a 2048-child batch resident at once
+__global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
     const int32_t* __restrict__ parent, int R, int W, const int32_t* __restrict__ bt_in,
     const int32_t* __restrict__ len_in, int32_t* __restrict__ bt_out, int32_t* __restrict__ len_out,
     int S, KvGeom g, const uint8_t* k_new, const uint8_t* v_new, int64_t new_tok_stride,
     int32_t* dev_status) {
-  __shared__ int par[FORK_MAX_W], first[FORK_MAX_W], cnt[FORK_MAX_W], lens[FORK_MAX_W];
-  __shared__ uint64_t cow_mask[FORK_MAX_W / 64], free_mask[FORK_MAX_W / 64];
-  __shared__ int bts[FORK_STAGE_BT];
-  __shared__ int src_row[FORK_STAGE_S], dst_row[FORK_STAGE_S];
-  __shared__ int bad;
+  extern __shared__ __attribute__((aligned(8))) int fork_lds[];
+  const int ngroups = (W + 63) >> 6;
+  uint64_t* cow_mask = reinterpret_cast<uint64_t*>(fork_lds);
+  uint64_t* free_mask = cow_mask + ngroups;
+  int* cow_base = fork_lds + 4 * ngroups;
+  int* free_base = cow_base + ngroups + 1;
+  int* par = free_base + ngroups + 1;
+  int* first = par + W;
+  int* cnt = first + W;
+  int* lens = cnt + W;
+  int* owner_of = lens + W;
+  int* cpre = owner_of + W;
+  int* scan_tmp = cpre + W + 1;
+  int& bad = scan_tmp[8];
+  int* bts = scan_tmp + 9;
+  int* cplen = first;  // once the masks are built
   const int r = blockIdx.x / W;
   const int c = blockIdx.x - r * W;  // this workgroup's child
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -98,7 +154,12 @@ __global__ __launch_bounds__(FORK_THREADS) void beam_fork(
   }
   __syncthreads();
   const bool req_bad = bad != 0;
-  if (req_bad && c == 0 && tid == 0) flag_status(dev_status, GR_DEV_BAD_PARENT);
+  if (req_bad) {  // a request with a bad parent keeps its tables
+    if (c == 0 && tid == 0) flag_status(dev_status, GR_DEV_BAD_PARENT);
+    for (int j = tid; j < S; j += FORK_THREADS) bt_out[n_c * S + j] = bt_in[n_c * S + j];
+    if (tid == 0) len_out[n_c] = lens[c];
+    return;
+  }
   // per 64-entry group: the children that copy (not their parent's lowest
   // child) and the parents without children
   for (int base = 0; base < W; base += FORK_THREADS) {
@@ -114,110 +175,66 @@ __global__ __launch_bounds__(FORK_THREADS) void beam_fork(
     }
   }
   __syncthreads();
-  const int p = par[c];
-  const bool cow = !req_bad && first[p] != c;
-  int owner = req_bad ? c : p;  // beam whose old row child c receives
-  if (cow) {
-    // k = rank of c among the copying children; owner = the k-th childless
-    // parent (both ascending; the two counts are equal)
-    const int gc = c >> 6;
-    int k = __builtin_popcountll(cow_mask[gc] & ((1ull << (c & 63)) - 1));
-    for (int gi = 0; gi < gc; ++gi) k += __builtin_popcountll(cow_mask[gi]);
-    const int ngroups = (W + 63) >> 6;
-    int gi = 0;
-    uint64_t m = free_mask[0];
-    while (gi + 1 < ngroups && k >= __builtin_popcountll(m)) {
-      k -= __builtin_popcountll(m);
-      m = free_mask[++gi];
-    }
-    for (; k > 0 && m != 0; --k) m &= m - 1;
-    owner = m != 0 ? gi * 64 + __builtin_ctzll(m) : c;
-  }
-  const int64_t n_p = (int64_t)r * W + p, n_o = (int64_t)r * W + owner;
-  const bool staged = !all_staged && S <= FORK_STAGE_S;
-  for (int j = tid; j < S; j += FORK_THREADS) {
-    const int b = all_staged ? bts[owner * S + j] : bt_in[n_o * S + j];
-    bt_out[n_c * S + j] = b;
-    if (staged) {
-      dst_row[j] = b;
-      if (cow) src_row[j] = bt_in[n_p * S + j];
+  if (tid == 0) {  // group bases of the two rank sequences (at most 16 groups)
+    int cb = 0, fb = 0;
+    for (int gi = 0; gi < ngroups; ++gi) {
+      cow_base[gi] = cb;
+      free_base[gi] = fb;
+      cb += __builtin_popcountll(cow_mask[gi]);
+      fb += __builtin_popcountll(free_mask[gi]);
     }
   }
-  if (req_bad) {  // a request with a bad parent keeps its tables
-    if (tid == 0) len_out[n_c] = lens[c];
-    return;
+  __syncthreads();
+  // the k-th childless parent (ascending) goes to the k-th copying child
+  // (ascending): the two counts are equal; owner_of temporarily holds the
+  // list of childless parents by rank
+  for (int i = tid; i < W; i += FORK_THREADS) {
+    const uint64_t fm = free_mask[i >> 6];
+    if ((fm >> (i & 63)) & 1)
+      owner_of[free_base[i >> 6] + __builtin_popcountll(fm & ((1ull << (i & 63)) - 1))] = i;
   }
+  __syncthreads();
   const int cap = S * g.bs;
+  int own_i[FORK_MAX_W / FORK_THREADS];
+#pragma unroll
+  for (int u = 0; u < FORK_MAX_W / FORK_THREADS; ++u) {
+    const int i = tid + u * FORK_THREADS;
+    own_i[u] = 0;
+    if (i < W) {
+      const uint64_t cm = cow_mask[i >> 6];
+      const bool cw = (cm >> (i & 63)) & 1;
+      own_i[u] = cw ? owner_of[cow_base[i >> 6] + __builtin_popcountll(cm & ((1ull << (i & 63)) - 1))] : par[i];
+      const int len = lens[par[i]];
+      cplen[i] = cw ? (len < 0 ? 0 : len > cap ? cap : len) : 0;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < FORK_MAX_W / FORK_THREADS; ++u) {
+    const int i = tid + u * FORK_THREADS;
+    if (i < W) owner_of[i] = own_i[u];
+  }
+  block_scan(cplen, cpre, W, scan_tmp);  // (its barriers publish owner_of too)
+  const int p = par[c];
+  const int owner = owner_of[c];  // beam whose old row child c receives
+  const int64_t n_o = (int64_t)r * W + owner;
+  for (int j = tid; j < S; j += FORK_THREADS) bt_out[n_c * S + j] = all_staged ? bts[owner * S + j] : bt_in[n_o * S + j];
   int len = lens[p];
   if (len < 0 || len > cap) {
     if (tid == 0) flag_status(dev_status, GR_DEV_BAD_LENGTH);
     len = len < 0 ? 0 : cap;
   }
-  if (staged) __syncthreads();  // staged rows visible
-  auto src_blk = [&](int i) {
-    return all_staged ? bts[p * S + i] : staged ? src_row[i] : bt_in[n_p * S + i];
-  };
-  auto dst_blk = [&](int i) {
-    return all_staged ? bts[owner * S + i] : staged ? dst_row[i] : bt_in[n_o * S + i];
+  auto row_blk = [&](int row, int bi) -> int {
+    return all_staged ? bts[row * S + bi] : bt_in[((int64_t)r * W + row) * S + bi];
   };
   uint8_t* kc = static_cast<uint8_t*>(g.k_cache);
   uint8_t* vc = static_cast<uint8_t*>(g.v_cache);
-  if (cow) {
-    // copy tokens [0, len) of the parent's row into the owner's row
-    if (FORK_THREADS % tv == 0 && g.num_blocks > 0) {
-      // a token's vectors divide the workgroup: each thread keeps one (head,
-      // vector) and steps over tokens with FORK_BATCH loads in flight; lanes
-      // past the end or on a bad block load an in-range row and skip the store
-      const int tpp = FORK_THREADS / tv;  // tokens per pass
-      const int h = (tid % tv) / row_vecs, vec = (tid % tv) % row_vecs;
-#pragma unroll 1
-      for (int p0 = tid / tv; p0 < len; p0 += tpp * FORK_BATCH) {
-        u32x4_t kb[FORK_BATCH], vb[FORK_BATCH];
-        int64_t dof[FORK_BATCH];
-        bool ok[FORK_BATCH];
-#pragma unroll
-        for (int u = 0; u < FORK_BATCH; ++u) {
-          const int pos = min(p0 + u * tpp, len - 1);
-          const int bi = pos / g.bs, off = pos - bi * g.bs;
-          const int bsrc = src_blk(bi), bdst = dst_blk(bi);
-          const bool valid = bsrc >= 0 && bsrc < g.num_blocks && bdst >= 0 && bdst < g.num_blocks;
-          ok[u] = valid && p0 + u * tpp < len;
-          if (!valid) flag_status(dev_status, GR_DEV_BAD_BLOCK);
-          const int64_t so = kv_byte_off(g, valid ? bsrc : 0, off, h) + vec * 16;
-          dof[u] = kv_byte_off(g, valid ? bdst : 0, off, h) + vec * 16;
-          kb[u] = *reinterpret_cast<const u32x4_t*>(kc + so);
-          vb[u] = *reinterpret_cast<const u32x4_t*>(vc + so);
-        }
-#pragma unroll
-        for (int u = 0; u < FORK_BATCH; ++u) {
-          if (ok[u]) {
-            *reinterpret_cast<u32x4_t*>(kc + dof[u]) = kb[u];
-            *reinterpret_cast<u32x4_t*>(vc + dof[u]) = vb[u];
-          }
-        }
-      }
-    } else {
-#pragma unroll 1
-      for (int e = tid; e < len * tv; e += FORK_THREADS) {
-        const int pos = e / tv, rem = e - pos * tv;
-        const int h = rem / row_vecs, vec = rem - h * row_vecs;
-        const int bi = pos / g.bs, off = pos - bi * g.bs;
-        const int bsrc = src_blk(bi), bdst = dst_blk(bi);
-        if (bsrc < 0 || bsrc >= g.num_blocks || bdst < 0 || bdst >= g.num_blocks) {
-          flag_status(dev_status, GR_DEV_BAD_BLOCK);
-          continue;
-        }
-        const int64_t so = kv_byte_off(g, bsrc, off, h) + vec * 16;
-        const int64_t dst = kv_byte_off(g, bdst, off, h) + vec * 16;
-        *reinterpret_cast<u32x4_t*>(kc + dst) = *reinterpret_cast<const u32x4_t*>(kc + so);
-        *reinterpret_cast<u32x4_t*>(vc + dst) = *reinterpret_cast<const u32x4_t*>(vc + so);
-      }
-    }
-  }
+  // ---- this child's appended token, at its row's length (before the copies:
+  // its position lies past every copied range of the row)
   int new_len = len;
   if (k_new) {
     if (len < cap) {
-      const int bdst = dst_blk(len / g.bs);
+      const int bdst = row_blk(owner, len / g.bs);
       if (bdst >= 0 && bdst < g.num_blocks) {
         if (tv <= FORK_THREADS) {
           if (pre_new) {
@@ -240,6 +257,49 @@ __global__ __launch_bounds__(FORK_THREADS) void beam_fork(
       }
     } else if (tid == 0) {
       flag_status(dev_status, GR_DEV_SUFFIX_FULL);
+    }
+  }
+  // ---- this workgroup's share of the request's copy-on-write tokens
+  const int total = cpre[W];
+  const int e0 = (int)((int64_t)total * c / W), e1 = (int)((int64_t)total * (c + 1) / W);
+  const int items = (e1 - e0) * tv;
+  if (items > 0 && g.num_blocks > 0) {
+#pragma unroll 1
+    for (int i0 = tid; i0 < items; i0 += FORK_THREADS * FORK_BATCH) {
+      u32x4_t kb[FORK_BATCH], vb[FORK_BATCH];
+      int64_t dof[FORK_BATCH];
+      bool ok[FORK_BATCH];
+#pragma unroll
+      for (int u = 0; u < FORK_BATCH; ++u) {
+        const int it = i0 + u * FORK_THREADS;
+        ok[u] = false;
+        dof[u] = 0;
+        if (it >= items) continue;
+        const int e = e0 + it / tv, rem = it - (it / tv) * tv;
+        const int h = rem / row_vecs, vec = rem - h * row_vecs;
+        int lo = 0, hi = W - 1;  // the copying child whose range holds e (skips empty ranges)
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (cpre[mid] <= e) lo = mid; else hi = mid - 1;
+        }
+        const int pos = e - cpre[lo];
+        const int bi = pos / g.bs, off = pos - bi * g.bs;
+        const int bsrc = row_blk(par[lo], bi), bdst = row_blk(owner_of[lo], bi);
+        const bool valid = bsrc >= 0 && bsrc < g.num_blocks && bdst >= 0 && bdst < g.num_blocks;
+        ok[u] = valid;
+        if (!valid) flag_status(dev_status, GR_DEV_BAD_BLOCK);
+        const int64_t so = kv_byte_off(g, valid ? bsrc : 0, off, h) + vec * 16;
+        dof[u] = kv_byte_off(g, valid ? bdst : 0, off, h) + vec * 16;
+        kb[u] = *reinterpret_cast<const u32x4_t*>(kc + so);
+        vb[u] = *reinterpret_cast<const u32x4_t*>(vc + so);
+      }
+#pragma unroll
+      for (int u = 0; u < FORK_BATCH; ++u) {
+        if (ok[u]) {
+          *reinterpret_cast<u32x4_t*>(kc + dof[u]) = kb[u];
+          *reinterpret_cast<u32x4_t*>(vc + dof[u]) = vb[u];
+        }
+      }
     }
   }
   if (tid == 0) len_out[n_c] = new_len;
@@ -358,7 +418,8 @@ extern "C" gr_status_t gr_beam_kv_fork(const int32_t* parent, int num_reqs, int 
                 new_tok_stride < (int64_t)num_kv_heads * head_dim))
     return GR_ERR_INVALID_ARG;
   if ((int64_t)num_reqs * beam_width > INT32_MAX) return GR_ERR_INVALID_ARG;
-  hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * beam_width)), dim3(FORK_THREADS), 0, stream, parent,
+  const size_t lds = sizeof(int) * (size_t)fork_lds_ints(beam_width, bt_stride);
+  hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * beam_width)), dim3(FORK_THREADS), lds, stream, parent,
                      num_reqs, beam_width, bt_in, len_in, bt_out, len_out, bt_stride, g,
                      static_cast<const uint8_t*>(k_new), static_cast<const uint8_t*>(v_new), new_tok_stride,
                      dev_status);
