@@ -465,33 +465,35 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 
   // ---- stage 1: row top-k1 by (logit desc, token asc) ----
   // Lower bound t0 of the k1-th largest key: per wave, the ceil(k1/4)-th
-  // largest thread maximum (bisection over the key range with wave ballots),
-  // least over the waves.  Every wave then has that many threads holding a
+  // largest thread maximum rounded down to its top 16 bits (bisection over
+  // that range with wave ballots), least over the waves.  Every wave then has that many threads holding a
   // key >= t0: at least k1 keys in all.  Only keys >= t0 can be selected; with
   // few of them they are ranked directly.
   uint32_t t0 = 0;
   if (k1 <= PR_THREADS) {
     const int kw = (k1 + 3) >> 2;
-    const uint32_t a0 = fkey(tm);
+    const uint32_t a0 = fkey(tm) >> 16;  // the top 16 bits of the key suffice for a bound
     // invariant: at least kw lanes have a0 >= lo; the answer is <= hi (bounds
     // are wave-uniform, kept in scalar registers)
-    uint32_t lo = 0, hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)fkey(m));
+    uint32_t lo = 0, hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(fkey(m) >> 16));
     while (lo < hi) {
       const uint32_t mid = lo + ((hi - lo + 1) >> 1);
       const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(a0 >= mid));
       if (c >= kw) lo = mid;
       else hi = mid - 1;
     }
-    if (lane == 0) wkey[wave] = lo;
+    if (lane == 0) wkey[wave] = lo << 16;
     __syncthreads();
     t0 = wkey[0];
 #pragma unroll
     for (int w = 1; w < PR_THREADS / 64; ++w) t0 = min(t0, wkey[w]);
+    // a bound at or below -inf (a wave of padding, rounded down into the NaN
+    // patterns 0 .. fkey(-inf)) admits every key
+    if (t0 <= fkey(-INFINITY)) t0 = 0;
   }
-  // the same bound on the logits (t0 = 0 admits every key; keys 0 .. fkey(-inf)
-  // are NaN patterns)
+  // the same bound on the logits (t0 = 0 admits every key)
   const float t0f = t0 == 0 ? -INFINITY : fval(t0);
-  // survivors -> LDS in any order (an LDS counter hands out each thread's slots)
+  // survivors -> LDS in thread order (a block scan hands out each thread's slots)
   int ns = 0;
   PR_FOR_CHUNKS(c) {
     if (live(c)) {
@@ -499,8 +501,10 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
       for (int j = 0; j < PR_VEC; ++j) ns += get(c, j) >= t0f;
     }
   }
+  int pos;
+  const int n_surv = block_scan(ns, pos, itmp);
+  if (tid == 0) scnt = n_surv;
   if (ns > 0) {
-    int pos = atomicAdd(&scnt, ns);
     PR_FOR_CHUNKS(c) {
       if (live(c)) {
 #pragma unroll
@@ -518,28 +522,19 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   __syncthreads();
   const int S = scnt;
   if (S <= PR_SURV && k1 <= PR_THREADS) {
-    // each thread's survivors (slots tid, tid + 256) as row keys: distinct
-    const bool ha = tid < S, hb = tid + PR_THREADS < S;
+    // the survivors as row keys (all distinct: the token is part of the key)
     auto to_key = [](uint64_t raw) { return row_key(fkey(__builtin_bit_cast(float, (uint32_t)(raw >> 32))), (int)(uint32_t)raw); };
-    const uint64_t ka = ha ? to_key(sk[tid]) : 0, kb = hb ? to_key(sk[tid + PR_THREADS]) : 0;
-    // the k1-th largest survivor key: all keys are distinct, so the selection
-    // ends with the boundary bin holding exactly the keys still needed
-    const RadixSel<uint64_t> rs = radix_select<PR_THREADS, uint64_t>(
-        [&](auto&& f) {
-          if (ha) f(ka);
-          if (hb) f(kb);
-        },
-        k1, (uint64_t)t0 << 32, ((uint64_t)fkey(m) << 32) | 0xffffffffu, hist, itmp, sel);
-    const bool sa = ha && (ka & rs.mask) >= rs.prefix, sb = hb && (kb & rs.mask) >= rs.prefix;
-    int off;
-    block_scan((int)sa + (int)sb, off, itmp);  // k1 in total; its barriers end all reads of sk above
-    if (sa) sk[off++] = ka;
-    if (sb) sk[off] = kb;
+#pragma unroll
+    for (int h = 0; h < PR_SURV / PR_THREADS; ++h) {
+      const int i = tid + h * PR_THREADS;
+      if (i < S) sk[i] = to_key(sk[i]);
+    }
     __syncthreads();
-    // rank of selected key i = number of selected keys greater than it.  Wave
-    // w counts over the keys [w*Q, (w+1)*Q) for every target; lane l holds the
-    // targets l, l + 64, ...; the four partial counts are summed in LDS.
-    const int Q = (k1 + 3) >> 2, q0 = wave * Q, q1 = min(k1, q0 + Q);
+    // rank of survivor i = number of survivors with a greater key; the k1 of
+    // rank < k1 are the row's top-k1, in order.  Wave w counts over the
+    // survivors [w*Q, (w+1)*Q) for every target; lane l holds the targets l,
+    // l + 64, ...; the four partial counts are summed in LDS.
+    const int Q = (S + 3) >> 2, q0 = wave * Q, q1 = min(S, q0 + Q);
     auto partial = [&](auto tg_c) {
       constexpr int TG = decltype(tg_c)::value;
       uint64_t kt[TG];
@@ -547,7 +542,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 #pragma unroll
       for (int mi = 0; mi < TG; ++mi) {
         const int i = lane + 64 * mi;
-        kt[mi] = i < k1 ? sk[i] : ~0ull;
+        kt[mi] = i < S ? sk[i] : ~0ull;
         rk[mi] = 0;
       }
 #pragma unroll 4
@@ -559,22 +554,25 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 #pragma unroll
       for (int mi = 0; mi < TG; ++mi) {
         const int i = lane + 64 * mi;
-        if (i < k1) part[wave * PR_SURV + i] = rk[mi];
+        if (i < S) part[wave * PR_SURV + i] = rk[mi];
       }
     };
-    if (k1 <= 128) partial(std::integral_constant<int, 2>{});
-    else partial(std::integral_constant<int, 4>{});
+    if (S <= 128) partial(std::integral_constant<int, 2>{});
+    else if (S <= 256) partial(std::integral_constant<int, 4>{});
+    else partial(std::integral_constant<int, 8>{});
     __syncthreads();
 #pragma unroll
     for (int h = 0; h < PR_SURV / PR_THREADS; ++h) {
       const int i = tid + h * PR_THREADS;
-      if (i < k1) {
+      if (i < S) {
         int rank = 0;
 #pragma unroll
         for (int w = 0; w < PR_THREADS / 64; ++w) rank += part[w * PR_SURV + i];
-        const uint64_t ki = sk[i];
-        ox[rank] = fval((uint32_t)(ki >> 32));
-        ov[rank] = (int)~(uint32_t)ki;
+        if (rank < k1) {
+          const uint64_t ki = sk[i];
+          ox[rank] = fval((uint32_t)(ki >> 32));
+          ov[rank] = (int)~(uint32_t)ki;
+        }
       }
     }
   } else {
