@@ -154,6 +154,63 @@ gr_status_t gr_paged_attn_prefill(
     float scale, float softcap, float* lse_out, int32_t* dev_status, hipStream_t stream);
 
 /*
+ * Optional attention features: the sliding window, attention sinks and ALiBi
+ * slopes BeamAttentionImpl takes (vllm_gr/v1/attention/backends/beam_attn.py:
+ * 597-625) and hands to every flash_attn_varlen_func call of the cascade
+ * (window_size, alibi_slopes, s_aux: :643-695), and the non-causal standard
+ * path of the encoder attention types (causal flag, :648; ENCODER,
+ * ENCODER_ONLY, ENCODER_DECODER accepted at :771-773).
+ *
+ * Positions are indices into a row's key sequence: a request's prefix
+ * (decode: shared prefix then the beam's own suffix), a query sitting at its
+ * own token's position.  A key at kpos is visible to a query at qpos when
+ * qpos - window_left <= kpos (window_left >= 0) and kpos <= qpos +
+ * window_right (window_right >= 0, non-causal prefill only); -1 = unbounded.
+ * The reference's sliding_window w maps to window_left = w - 1 (decoder: right
+ * 0) or left = right = w - 1 (ENCODER_ONLY).  alibi_slopes[h] adds
+ * -slope * |qpos - kpos| to the (soft-capped) score; sinks[h] joins head h's
+ * softmax as one more logit without a value (natural-log units).  causal = 0
+ * (prefill only) lets every query see all of its sequence's keys.  Passing
+ * NULL options is the same as the functions without _opt.
+ */
+typedef struct gr_attn_options {
+  int window_left;            /* -1: no left bound */
+  int window_right;           /* -1: no right bound (non-causal prefill only) */
+  int causal;                 /* 1: causal (required for decode); 0: prefill over every key */
+  const float* sinks;         /* [num_q_heads] or NULL */
+  const float* alibi_slopes;  /* [num_q_heads] or NULL */
+} gr_attn_options;
+
+/* gr_beam_attn_decode_ws with options (the optional features run on the
+ * generic kernel). */
+gr_status_t gr_beam_attn_decode_opt(
+    void* out, int64_t out_tok_stride,
+    const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* prefix_bt, int prefix_bt_stride, const int32_t* prefix_len,
+    const int32_t* beam_start,
+    const int32_t* suffix_bt, int suffix_bt_stride, const int32_t* suffix_len,
+    const int32_t* suffix_start,
+    int num_reqs, int max_beams_per_req, int num_beams, int q_per_beam,
+    int num_q_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
+    float scale, float softcap, float* lse_out, int32_t* dev_status,
+    int max_prefix_len, void* workspace, size_t workspace_bytes,
+    const gr_attn_options* options, hipStream_t stream);
+
+/* gr_paged_attn_prefill with options. */
+gr_status_t gr_paged_attn_prefill_opt(
+    void* out, int64_t out_tok_stride,
+    const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* block_table, int bt_stride, const int32_t* query_start,
+    const int32_t* seq_len, int num_reqs, int num_tokens, int max_query_len,
+    int num_q_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
+    float scale, float softcap, float* lse_out, int32_t* dev_status,
+    const gr_attn_options* options, hipStream_t stream);
+
+/*
  * Scatter new K/V tokens into the paged cache by flat slot
  * (slot = block * block_size + offset; slot < 0 is skipped).
  *

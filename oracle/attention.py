@@ -35,6 +35,15 @@ Functions and how each is pinned (tests/test_oracle_attention.py):
 * ``gather_tokens`` -- paged gather, restating the index arithmetic of
   ``paged_kv_to_contig_suffix_kernel`` (``beam_attn.py:62-92``).  Pinned by
   a block-permutation test.
+* The optional features of ``beam_attention_dense`` (``window``, ``causal``,
+  ``sinks``, ``alibi_slopes``: the ``window_size`` / ``causal`` /
+  ``s_aux`` / ``alibi_slopes`` arguments the reference hands to
+  flash_attn_varlen_func, ``beam_attn.py:597-625``, ``:643-695``).  A key or
+  query position is its index in the row's ``[prefix ; suffix]`` sequence,
+  a query sitting at its own token's.  Pinned by a brute-force scalar loop,
+  by the window = the unwindowed oracle over the truncated key set, and by
+  the sink closed forms ``lse' = logaddexp(lse, sink)`` and
+  ``out' = out * exp(lse - lse')``.
 """
 
 from __future__ import annotations
@@ -94,20 +103,38 @@ def _softmax_rows(s: np.ndarray, visible: np.ndarray, V: np.ndarray):
 
 
 def _attend_group(qg: np.ndarray, K: np.ndarray, V: np.ndarray, visible: np.ndarray,
-                  scale: float, softcap: float):
-    """Query rows ``qg [rows, D]`` of one KV head against ``K, V [S, D]``."""
+                  scale: float, softcap: float, bias: np.ndarray | None = None,
+                  sink: np.ndarray | None = None):
+    """Query rows ``qg [rows, D]`` of one KV head against ``K, V [S, D]``;
+    ``bias [rows, S]`` is added after the soft cap, ``sink [rows]`` joins
+    each row's softmax as a logit without a value."""
     s = _softcap(scale * (qg @ K.T), softcap)
-    return _softmax_rows(s, visible, V)
+    if bias is not None:
+        s = s + bias
+    out, lse = _softmax_rows(s, visible, V)
+    if sink is not None:
+        new = np.logaddexp(lse, sink)
+        out = out * np.exp(lse - new)[:, None]
+        lse = new
+    return out, lse
 
 
 def beam_attention_dense(q, k_cache, v_cache, prefix_bt, prefix_len, beam_start,
                          suffix_bt, suffix_len, suffix_start=None, *, q_per_beam=1,
-                         scale, softcap=0.0, block_size):
+                         scale, softcap=0.0, block_size, window=(-1, -1), causal=True,
+                         sinks=None, alibi_slopes=None):
     """Dense per-beam attention in float64.
 
     Mirrors ``run_reference_attention`` (``test_cascade_beam_flash_attn.py:191-319``):
     each beam's ``[prefix ; suffix]`` KV is materialised (``:281-282``) and the
     beam's query tokens attend causally, bottom-right aligned (``:301-315``).
+    Options (flash_attn_varlen_func's, ``beam_attn.py:643-695``): key kpos is
+    visible to query qpos only if ``qpos - window[0] <= kpos`` (window[0] >=
+    0) and ``kpos <= qpos + window[1]`` (window[1] >= 0); ``causal=False``
+    lets every query see all ``P + L`` keys (the one-beam prefill form of
+    the encoder types); ``alibi_slopes[h]`` adds ``-slope * |qpos - kpos|``
+    after the soft cap; ``sinks[h]`` joins head h's softmax as a logit
+    without a value.
 
     ``q``: ``[N*T, Hq, D]``.  Returns ``(out [N*T, Hq, D] float64, lse [N*T, Hq])``.
     """
@@ -129,10 +156,24 @@ def beam_attention_dense(q, k_cache, v_cache, prefix_bt, prefix_len, beam_start,
             vis_t = np.concatenate(
                 [np.ones((T, P), bool), np.arange(L)[None, :] <= (L - T + np.arange(T))[:, None]],
                 axis=1)
+            if not causal:
+                vis_t = np.ones((T, P + L), bool)
+            qpos = P + L - T + np.arange(T)  # query token i sits at its own token's position
+            kpos = np.arange(P + L)
+            if window[0] >= 0:
+                vis_t &= kpos[None, :] >= (qpos - window[0])[:, None]
+            if window[1] >= 0:
+                vis_t &= kpos[None, :] <= (qpos + window[1])[:, None]
+            dist = np.abs(qpos[:, None] - kpos[None, :]).astype(np.float64)  # [T, P+L]
             for hk in range(Hkv):
                 qg = q[n * T:(n + 1) * T, hk * G:(hk + 1) * G].reshape(T * G, D)
                 vis = np.repeat(vis_t, G, axis=0)
-                o, l = _attend_group(qg, K[:, hk], V[:, hk], vis, scale, softcap)
+                heads = np.tile(np.arange(hk * G, (hk + 1) * G), T)  # row (i, g) -> head hk*G + g
+                bias = None
+                if alibi_slopes is not None:
+                    bias = -np.asarray(alibi_slopes, np.float64)[heads][:, None] * np.repeat(dist, G, axis=0)
+                sink = None if sinks is None else np.asarray(sinks, np.float64)[heads]
+                o, l = _attend_group(qg, K[:, hk], V[:, hk], vis, scale, softcap, bias, sink)
                 out[n * T:(n + 1) * T, hk * G:(hk + 1) * G] = o.reshape(T, G, D)
                 lse[n * T:(n + 1) * T, hk * G:(hk + 1) * G] = l.reshape(T, G)
     return out, lse

@@ -37,13 +37,18 @@ def test_backend_static_contract():
         assert B.supports_head_size(hs) is ok
 
 
+def test_supports_combination_sinks_accepted():
+    args = dict(head_size=128, dtype=torch.bfloat16, kv_cache_dtype="auto", block_size=16, use_mla=False,
+                has_sink=True, use_sparse=False, device_capability="gfx950:sramecc+:xnack-")
+    assert B.supports_sink() and B.supports_combination(**args) is None
+
+
 @pytest.mark.parametrize("kw,reason", [
     (dict(dtype=torch.float32), "Unsupported dtype"),
     (dict(head_size=264), "Unsupported head_size"),
     (dict(kv_cache_dtype="fp8"), "Unsupported kv_cache_dtype"),
     (dict(block_size=8), "not multiple of 16"),
     (dict(device_capability="gfx942"), "gfx950"),
-    (dict(has_sink=True), "sink"),
     (dict(use_mla=True), "MLA"),
     (dict(use_sparse=True), "sparse"),
 ])
@@ -61,10 +66,19 @@ def test_impl_rejects_unsupported_features():
                                                       kv_cache_dtype="auto"), **kw})
     impl = mk()
     assert impl.num_queries_per_kv == 4 and impl.logits_soft_cap == 0.0
-    for kw in (dict(alibi_slopes=[0.1] * 32), dict(sliding_window=128), dict(kv_cache_dtype="fp8"),
-               dict(running_sinks=torch.zeros(32))):
-        with pytest.raises(NotImplementedError):
-            mk(**kw)
+    with pytest.raises(NotImplementedError):
+        mk(kv_cache_dtype="fp8")
+    with pytest.raises(AssertionError, match="Sinks must have the same number of heads"):
+        mk(running_sinks=torch.zeros(31))
+    # the reference's window convention (beam_attn.py:600-605)
+    assert mk(sliding_window=128).sliding_window == (127, 0)
+    assert mk(sliding_window=128, attn_type=ba.AttentionType.ENCODER_ONLY).sliding_window == (127, 127)
+    assert mk().sliding_window == (-1, -1)
+    assert mk(alibi_slopes=[0.1] * 32).alibi_slopes.dtype == torch.float32
+    assert mk(running_sinks=torch.zeros(32)).sinks.shape == (32,)
+    for t in ba.AttentionType:
+        assert ba.BeamAttentionBackend.supports_attn_type(t)
+    assert not ba.BeamAttentionBackend.supports_attn_type("mamba")
     q = torch.zeros(4, 32, 128)
     kv = torch.zeros(2, 4, 16, 8, 128)
     with pytest.raises(AssertionError):

@@ -32,7 +32,18 @@ struct DecodeArgs {
   int nsplit;
   float* ws_o;    // [tiles * nsplit][128 rows][128] float32
   float* ws_lse;  // [tiles * nsplit][128 rows] float32 (natural log)
+  // optional features (gr_attn_options); positions are indices into the
+  // row's [prefix ; suffix] sequence, a query row sitting at its own token's
+  int win_left, win_right;   // keys before / after the query's position it sees; -1 = unbounded
+  int causal;                // prefill: 0 = every key of the sequence (decode is always causal)
+  const float* sinks;        // [Hq] sink logits (natural log units) or null
+  const float* alibi;        // [Hq] ALiBi slopes or null
 };
+
+// any of the optional features set (only the generic kernel implements them)
+inline bool has_options(const DecodeArgs& a) {
+  return a.win_left >= 0 || a.win_right >= 0 || !a.causal || a.sinks || a.alibi;
+}
 
 // MFMA path (gr_attn_mfma.hip): bf16/fp16, head_dim 128, 16-byte aligned rows.
 bool mfma_decode_supported(const DecodeArgs& a);
@@ -46,13 +57,14 @@ gr_status_t launch_mfma_decode_split(const DecodeArgs& a, hipStream_t stream);
 void mfma_decode_plan(int num_reqs, int max_beams, int q_per_beam, int Hq, int Hkv, int max_prefix_len,
                       int* tiles, int* nsplit);
 
-// 64-row-per-wave MFMA decode (gr_attn_mfma16.hip): the default decode
-// kernel where supported (the unsplit decode mode only).
+// 64-row-per-wave MFMA decode (gr_attn_mfma16.hip): selected by
+// gr_set_decode_kernel(2) where supported (the unsplit decode mode only).
 bool d16_decode_supported(const DecodeArgs& a);
 gr_status_t launch_d16_decode(const DecodeArgs& a, hipStream_t stream);
 
-// 0 = choose automatically, 1 = always the generic kernel, 2 = the 32-row
-// MFMA decode kernel instead of the 64-row one (testing and measurement hook).
+// 0 = choose automatically (the 32-row MFMA kernel where supported), 1 =
+// always the generic kernel, 2 = the 64-row MFMA kernel where supported
+// (testing and measurement hook).
 extern int g_decode_kernel_override;
 
 }  // namespace gr

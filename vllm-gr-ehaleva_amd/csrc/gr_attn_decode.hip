@@ -30,10 +30,17 @@ __device__ inline int find_request(const int32_t* beam_start, int num_reqs, int 
   return lo;
 }
 
-// PREFILL: the varlen causal mode (gr_paged_attn_prefill): blockIdx.x / chunks
-// is the request, prefix_bt / prefix_len its block table and sequence length,
+// PREFILL: the varlen mode (gr_paged_attn_prefill): blockIdx.x / chunks is
+// the request, prefix_bt / prefix_len its block table and sequence length,
 // beam_start its query start, T the largest query count; query i of a request
-// with ql queries sees keys 0 .. seq - ql + i, and there is no suffix.
+// with ql queries sees keys 0 .. seq - ql + i (causal) or all seq keys, and
+// there is no suffix.
+// Options (gr_attn_options): a key or query position is its index in the
+// row's [prefix ; suffix] sequence (a query sits at its own token's); a
+// window keeps keys with qpos - win_left <= kpos <= qpos + win_right; ALiBi
+// adds -slope * |qpos - kpos| after the soft cap; a sink adds exp(sink) to
+// the softmax denominator (beam_attn.py:597-625, flash_attn_varlen_func's
+// window_size / alibi_slopes / s_aux).
 template <int DT, bool PREFILL = false>
 __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   using E = Elem<DT>;
@@ -71,8 +78,8 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
     if (row0 >= G * ql) return;
     nrows = min(GEN_ROWS, G * ql - row0);
     ctx = seq - ql;
-    // keys up to the chunk's last query token
-    P = Pc = ctx + (row0 + nrows - 1) / G + 1;
+    // keys up to the chunk's last query token (all of them when non-causal)
+    P = Pc = a.causal ? ctx + (row0 + nrows - 1) / G + 1 : seq;
     L = Lc = s0 = 0;
     tok0 = q0;
   } else {
@@ -111,7 +118,11 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   for (int i = 0; i < GEN_ACC; ++i) acc[i] = 0.f;
 
   const int total = Pc + Lc;
-  for (int k0 = 0; k0 < total; k0 += GEN_TK) {
+  // position of the query token of chunk row `row`
+  auto qpos_of = [&](int row) { return PREFILL ? ctx + (row0 + row) / G : Pc + Lc - a.T + (row0 + row) / G; };
+  // a left window: the tiles before the chunk's first row's window hold no visible key
+  const int k_start = a.win_left >= 0 ? max(0, qpos_of(0) - a.win_left) / GEN_TK * GEN_TK : 0;
+  for (int k0 = k_start; k0 < total; k0 += GEN_TK) {
     __syncthreads();
     if (t < GEN_TK) {
       int kk = k0 + t;
@@ -156,12 +167,16 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
         for (int d = 0; d < D; ++d) s += q_s[row * D + d] * k_s[key * (D + 1) + d];
         s *= a.scale;
         if (a.softcap > 0.f) s = a.softcap * tanhf(s / a.softcap);
+        const int qpos = qpos_of(row);
+        if (a.alibi) s -= a.alibi[hk * G + (row0 + row) % G] * (float)abs(qpos - kk);
         bool vis = row < nrows && kk < total && kv_ok[key];
-        if (PREFILL) vis = vis && kk <= ctx + (row0 + row) / G;
+        if (PREFILL && a.causal) vis = vis && kk <= qpos;
         if (!PREFILL && vis && kk >= Pc) {
           int qi = (row0 + row) / G;
           vis = (kk - Pc) <= Lc - a.T + qi;
         }
+        if (a.win_left >= 0) vis = vis && kk >= qpos - a.win_left;
+        if (a.win_right >= 0) vis = vis && kk <= qpos + a.win_right;
         p_s[row * (GEN_TK + 1) + key] = vis ? s : -INFINITY;
       }
     }
@@ -200,6 +215,17 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
     }
   }
   __syncthreads();
+  if (a.sinks && t < GEN_ROWS) {
+    // the sink joins the row's softmax: max over it too, exp(sink) in the
+    // denominator; a_s carries the rescaling of the accumulated output
+    const float sk = a.sinks[hk * G + (row0 + t) % G];
+    const float m = m_s[t], mn = fmaxf(m, sk);
+    const float al = m == -INFINITY ? 0.f : expf(m - mn);
+    l_s[t] = l_s[t] * al + expf(sk - mn);
+    m_s[t] = mn;
+    a_s[t] = al;
+  }
+  __syncthreads();
   S* out = static_cast<S*>(a.out);
 #pragma unroll
   for (int i = 0; i < GEN_ACC; ++i) {
@@ -210,7 +236,7 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
         int rho = row0 + row;
         int qi = rho / G, g = rho % G;
         float l = l_s[row];
-        float o = l > 0.f ? acc[i] / l : 0.f;
+        float o = l > 0.f ? (a.sinks ? acc[i] * a_s[row] : acc[i]) / l : 0.f;
         out[(tok0 + qi) * a.out_tok_stride + (int64_t)(hk * G + g) * D + d] = E::from_float(o);
       }
     }
@@ -307,6 +333,24 @@ static gr_status_t decode_args(
   a.scale = scale; a.softcap = softcap; a.lse_out = lse_out; a.dev_status = dev_status;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.nsplit = 1;
+  a.win_left = a.win_right = -1;
+  a.causal = 1;
+  return GR_OK;
+}
+
+// Copies the optional features into the argument block.  Decode attention is
+// causal over the beam's own tokens: a non-causal option is invalid there,
+// and a right window is a no-op.
+static gr_status_t apply_options(DecodeArgs& a, const gr_attn_options* opt, bool prefill) {
+  if (!opt) return GR_OK;
+  if (opt->window_left < -1 || opt->window_right < -1 || (opt->causal != 0 && opt->causal != 1))
+    return GR_ERR_INVALID_ARG;
+  if (!prefill && !opt->causal) return GR_ERR_INVALID_ARG;
+  a.win_left = opt->window_left;
+  a.win_right = prefill && !opt->causal ? opt->window_right : -1;
+  a.causal = opt->causal;
+  a.sinks = opt->sinks;
+  a.alibi = opt->alibi_slopes;
   return GR_OK;
 }
 
@@ -361,7 +405,7 @@ extern "C" size_t gr_beam_attn_decode_workspace_size(int num_reqs, int max_beams
   return nsplit > 1 ? split_layout(tiles, nsplit).total : 0;
 }
 
-extern "C" gr_status_t gr_beam_attn_decode_ws(
+static gr_status_t decode_ws_impl(
     void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
     const void* k_cache, const void* v_cache, int64_t num_blocks,
     int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
@@ -370,10 +414,13 @@ extern "C" gr_status_t gr_beam_attn_decode_ws(
     const int32_t* suffix_len, const int32_t* suffix_start, int num_reqs, int max_beams_per_req,
     int num_beams, int q_per_beam, int num_q_heads, int num_kv_heads, int head_dim,
     int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
-    int max_prefix_len, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    int max_prefix_len, void* workspace, size_t workspace_bytes, const gr_attn_options* opt,
+    hipStream_t stream) {
   DecodeArgs a;
   bool empty;
-  const gr_status_t st = decode_args(a, empty, GR_DECODE_ARG_NAMES);
+  gr_status_t st = decode_args(a, empty, GR_DECODE_ARG_NAMES);
+  if (st != GR_OK) return st;
+  st = apply_options(a, opt, false);
   if (st != GR_OK || empty) return st;
   if (max_prefix_len < 0) return GR_ERR_INVALID_ARG;
   if (g_decode_kernel_override == 1 || !mfma_decode_supported(a)) return launch_generic<false>(a, stream);
@@ -394,14 +441,43 @@ extern "C" gr_status_t gr_beam_attn_decode_ws(
   return launch_mfma_decode_split(a, stream);
 }
 
-extern "C" gr_status_t gr_paged_attn_prefill(
+#define GR_DECODE_WS_NAMES GR_DECODE_ARG_NAMES, max_prefix_len, workspace, workspace_bytes
+
+extern "C" gr_status_t gr_beam_attn_decode_ws(
+    void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* prefix_bt, int prefix_bt_stride, const int32_t* prefix_len,
+    const int32_t* beam_start, const int32_t* suffix_bt, int suffix_bt_stride,
+    const int32_t* suffix_len, const int32_t* suffix_start, int num_reqs, int max_beams_per_req,
+    int num_beams, int q_per_beam, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
+    int max_prefix_len, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return decode_ws_impl(GR_DECODE_WS_NAMES, nullptr, stream);
+}
+
+extern "C" gr_status_t gr_beam_attn_decode_opt(
+    void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* prefix_bt, int prefix_bt_stride, const int32_t* prefix_len,
+    const int32_t* beam_start, const int32_t* suffix_bt, int suffix_bt_stride,
+    const int32_t* suffix_len, const int32_t* suffix_start, int num_reqs, int max_beams_per_req,
+    int num_beams, int q_per_beam, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
+    int max_prefix_len, void* workspace, size_t workspace_bytes, const gr_attn_options* options,
+    hipStream_t stream) {
+  return decode_ws_impl(GR_DECODE_WS_NAMES, options, stream);
+}
+
+static gr_status_t prefill_impl(
     void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
     const void* k_cache, const void* v_cache, int64_t num_blocks,
     int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
     const int32_t* block_table, int bt_stride, const int32_t* query_start, const int32_t* seq_len,
     int num_reqs, int num_tokens, int max_query_len, int num_q_heads, int num_kv_heads, int head_dim,
     int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
-    hipStream_t stream) {
+    const gr_attn_options* opt, hipStream_t stream) {
   if (num_reqs < 0 || num_tokens < 0 || max_query_len < 0 || num_q_heads < 1 || num_kv_heads < 1 ||
       num_q_heads % num_kv_heads != 0 || block_size < 1 || head_dim < 8 || head_dim % 8 != 0 ||
       num_blocks < 0 || bt_stride < 0 || !dtype_valid(dtype) || !(softcap >= 0.f))
@@ -425,9 +501,42 @@ extern "C" gr_status_t gr_paged_attn_prefill(
   a.Hq = num_q_heads; a.Hkv = num_kv_heads; a.D = head_dim; a.bs = block_size; a.dtype = dtype;
   a.scale = scale; a.softcap = softcap; a.lse_out = lse_out; a.dev_status = dev_status;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  a.win_left = a.win_right = -1;
+  a.causal = 1;
+  const gr_status_t st = apply_options(a, opt, true);
+  if (st != GR_OK) return st;
   if (g_decode_kernel_override != 1 && mfma_decode_supported(a)) return launch_mfma_prefill(a, stream);
   return launch_generic<true>(a, stream);
 }
+
+#define GR_PREFILL_ARG_NAMES                                                                             \
+  out, out_tok_stride, q, q_tok_stride, k_cache, v_cache, num_blocks, kv_block_stride, kv_tok_stride,     \
+      kv_head_stride, block_table, bt_stride, query_start, seq_len, num_reqs, num_tokens, max_query_len, \
+      num_q_heads, num_kv_heads, head_dim, block_size, dtype, scale, softcap, lse_out, dev_status
+
+extern "C" gr_status_t gr_paged_attn_prefill(
+    void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* block_table, int bt_stride, const int32_t* query_start, const int32_t* seq_len,
+    int num_reqs, int num_tokens, int max_query_len, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
+    hipStream_t stream) {
+  return prefill_impl(GR_PREFILL_ARG_NAMES, nullptr, stream);
+}
+
+extern "C" gr_status_t gr_paged_attn_prefill_opt(
+    void* out, int64_t out_tok_stride, const void* q, int64_t q_tok_stride,
+    const void* k_cache, const void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int32_t* block_table, int bt_stride, const int32_t* query_start, const int32_t* seq_len,
+    int num_reqs, int num_tokens, int max_query_len, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int dtype, float scale, float softcap, float* lse_out, int32_t* dev_status,
+    const gr_attn_options* options, hipStream_t stream) {
+  return prefill_impl(GR_PREFILL_ARG_NAMES, options, stream);
+}
+
+
 
 extern "C" int gr_set_decode_kernel(int which) {
   if (which < 0 || which > 2) return GR_ERR_INVALID_ARG;

@@ -1059,6 +1059,7 @@ __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
 
 bool mfma_decode_supported(const DecodeArgs& a) {
   if (a.D != HD || (a.dtype != GR_DTYPE_BF16 && a.dtype != GR_DTYPE_F16)) return false;
+  if (has_options(a)) return false;  // windows, sinks, ALiBi, non-causal: the generic kernel
   if (a.bs_shift < 2) return false;  // power-of-two block size >= 4
   // the suffix tiles tag each key with its 16-bit index within the beam's suffix
   if ((int64_t)a.suffix_bt_stride * a.bs > 0xFFFF) return false;

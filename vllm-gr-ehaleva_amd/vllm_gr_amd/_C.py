@@ -38,6 +38,13 @@ _L = ctypes.c_int64
 _F = ctypes.c_float
 _SZ = ctypes.c_size_t
 
+
+class AttnOptions(ctypes.Structure):
+    """gr_attn_options (include/gr_beam.h)."""
+    _fields_ = [("window_left", ctypes.c_int), ("window_right", ctypes.c_int), ("causal", ctypes.c_int),
+                ("sinks", ctypes.c_void_p), ("alibi_slopes", ctypes.c_void_p)]
+
+
 # name -> (restype, argtypes); mirrors include/gr_beam.h and include/gr_decoder.h one to one
 SIGNATURES = {
     "gr_status_string": (ctypes.c_char_p, [_I]),
@@ -59,6 +66,17 @@ SIGNATURES = {
         _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _P, _P, _P, _I, _P, _P,
         _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _P,
         _I, _P, _SZ, _P,                # max_prefix_len, workspace, workspace_bytes, stream
+    ]),
+    "gr_beam_attn_decode_opt": (_I, [
+        _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _P, _P, _P, _I, _P, _P,
+        _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _P,
+        _I, _P, _SZ,                    # max_prefix_len, workspace, workspace_bytes
+        _P, _P,                         # options (gr_attn_options*), stream
+    ]),
+    "gr_paged_attn_prefill_opt": (_I, [
+        _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _P, _P, _I, _I, _I,
+        _I, _I, _I, _I, _I, _F, _F, _P, _P,
+        _P, _P,                         # options (gr_attn_options*), stream
     ]),
     "gr_paged_attn_prefill": (_I, [
         _P, _L, _P, _L,                 # out, out_tok_stride, q, q_tok_stride

@@ -9,6 +9,8 @@ the HIP library every call raises.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _C
@@ -101,8 +103,12 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                      scale: float, softcap: float = 0.0, max_beams_per_req: int | None = None,
                      out: torch.Tensor | None = None, lse: torch.Tensor | None = None,
                      status: torch.Tensor | None = None, max_prefix_len: int | None = None,
-                     split: bool = True) -> torch.Tensor:
-    """BeamAttention decode step; see ``gr_beam_attn_decode`` / ``_ws`` in gr_beam.h.
+                     split: bool = True, window: tuple[int, int] | None = None,
+                     sinks: torch.Tensor | None = None,
+                     alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
+    """BeamAttention decode step; see ``gr_beam_attn_decode`` / ``_ws`` / ``_opt``
+    in gr_beam.h.  ``window`` (left, right), ``sinks`` and ``alibi_slopes``
+    are the optional features of ``gr_attn_options``.
 
     ``q``: ``[num_beams*q_per_beam, Hq, D]`` (token stride free, heads and dims
     contiguous).  Returns ``out`` (same shape/dtype as ``q``).  With ``split``
@@ -148,6 +154,11 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
             R, max_beams_per_req, N, q_per_beam, Hq, Hkv, D, bs, _dtype_code(q),
             float(scale), float(softcap or 0.0), _ptr(lse), _ptr(status))
     hint = int(max_prefix_len or 0)
+    opt = _attn_options(dev, Hq, window, True, sinks, alibi_slopes)
+    if opt is not None:
+        code = _C.lib().gr_beam_attn_decode_opt(*args, hint, None, 0, ctypes.byref(opt), _stream(dev))
+        _C.check("gr_beam_attn_decode_opt", code)
+        return out
     ws_bytes = (_C.lib().gr_beam_attn_decode_workspace_size(R, max_beams_per_req, q_per_beam, Hq, Hkv, D, hint)
                 if split and R else 0)
     if ws_bytes:
@@ -158,6 +169,22 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
         code = _C.lib().gr_beam_attn_decode(*args, _stream(dev))
         _C.check("gr_beam_attn_decode", code)
     return out
+
+
+def _attn_options(dev, Hq: int, window, causal: bool, sinks, alibi_slopes):
+    """The gr_attn_options struct for the optional features, or None when
+    none is set.  ``window`` = (left, right), -1 = unbounded; ``sinks`` /
+    ``alibi_slopes``: float32 [Hq] device tensors."""
+    left, right = (-1, -1) if window is None else (int(window[0]), int(window[1]))
+    if left < -1 or right < -1:
+        raise ValueError("window bounds must be >= -1")
+    for name, t in (("sinks", sinks), ("alibi_slopes", alibi_slopes)):
+        if t is not None and (t.device != dev or t.dtype != torch.float32 or t.shape != (Hq,)
+                              or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous float32 [Hq] tensor on the query's device")
+    if left < 0 and right < 0 and causal and sinks is None and alibi_slopes is None:
+        return None
+    return _C.AttnOptions(left, right, 1 if causal else 0, _ptr(sinks), _ptr(alibi_slopes))
 
 
 _SPLIT_WS: dict = {}
@@ -181,9 +208,12 @@ def paged_attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
                        block_table: torch.Tensor, query_start: torch.Tensor, seq_len: torch.Tensor, *,
                        max_query_len: int, scale: float, softcap: float = 0.0,
                        out: torch.Tensor | None = None, lse: torch.Tensor | None = None,
-                       status: torch.Tensor | None = None) -> torch.Tensor:
-    """Varlen causal attention of standard requests over the paged cache; see
-    ``gr_paged_attn_prefill`` in gr_beam.h.  ``q``: ``[num_tokens, Hq, D]``,
+                       status: torch.Tensor | None = None, causal: bool = True,
+                       window: tuple[int, int] | None = None, sinks: torch.Tensor | None = None,
+                       alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
+    """Varlen attention of standard requests over the paged cache (causal, or
+    over every key of the sequence with ``causal=False``); see
+    ``gr_paged_attn_prefill`` / ``_opt`` in gr_beam.h.  ``q``: ``[num_tokens, Hq, D]``,
     ``block_table [R, blocks]``, ``query_start [R+1]``, ``seq_len [R]`` int32.
     ``max_query_len`` must bound every request's query count (it sizes the
     grid; a request above it is flagged and skipped)."""
@@ -208,13 +238,18 @@ def paged_attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
         raise ValueError("out must match q's shape/dtype with heads and dims contiguous")
     if lse is not None and (lse.shape != (NT, Hq) or lse.dtype != torch.float32 or not lse.is_contiguous()):
         raise ValueError("lse must be a contiguous float32 [tokens, Hq] tensor")
-    code = _C.lib().gr_paged_attn_prefill(
-        out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0),
-        k_cache.data_ptr(), v_cache.data_ptr(), NB, bstr, tstr, hstr,
-        block_table.data_ptr(), block_table.shape[1], query_start.data_ptr(), seq_len.data_ptr(),
-        R, NT, int(max_query_len), Hq, Hkv, D, bs, _dtype_code(q), float(scale), float(softcap or 0.0),
-        _ptr(lse), _ptr(status), _stream(dev))
-    _C.check("gr_paged_attn_prefill", code)
+    args = (out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0),
+            k_cache.data_ptr(), v_cache.data_ptr(), NB, bstr, tstr, hstr,
+            block_table.data_ptr(), block_table.shape[1], query_start.data_ptr(), seq_len.data_ptr(),
+            R, NT, int(max_query_len), Hq, Hkv, D, bs, _dtype_code(q), float(scale), float(softcap or 0.0),
+            _ptr(lse), _ptr(status))
+    opt = _attn_options(dev, Hq, window, causal, sinks, alibi_slopes)
+    if opt is not None:
+        code = _C.lib().gr_paged_attn_prefill_opt(*args, ctypes.byref(opt), _stream(dev))
+        _C.check("gr_paged_attn_prefill_opt", code)
+    else:
+        code = _C.lib().gr_paged_attn_prefill(*args, _stream(dev))
+        _C.check("gr_paged_attn_prefill", code)
     return out
 
 

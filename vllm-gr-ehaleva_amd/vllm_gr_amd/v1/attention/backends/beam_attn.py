@@ -21,7 +21,12 @@ Kept from the reference (same names, argument meaning and error behaviour):
 * ``BeamAttentionBackend`` static surface (:758-846): name ``CUSTOM``,
   fp16/bf16, block size a multiple of 16, KV shape ``(2, NB, bs, Hkv, D)``,
   NHD/HND stride orders, head size %8 and <= 256, ``supports_combination``
-  returning a reason string or None.
+  returning a reason string or None; the four attention types (:771-773).
+* the optional features of ``BeamAttentionImpl`` (:597-625): ALiBi slopes,
+  the sliding window ((w-1, 0), or (w-1, w-1) for ENCODER_ONLY) and the
+  sinks reach every kernel launch (``gr_attn_options``), and a non-causal
+  batch (the encoder types) runs its standard rows over every key of their
+  sequence.  fp8 KV caches are rejected.
 
 Two mega-request layouts are accepted:
 
@@ -388,18 +393,40 @@ class BeamAttentionImpl:
         if num_heads % num_kv_heads != 0:
             raise ValueError("num_heads must be a multiple of num_kv_heads")
         self.num_queries_per_kv = num_heads // num_kv_heads
-        if alibi_slopes is not None:
-            raise NotImplementedError("BeamAttention does not support ALiBi slopes.")
-        if sliding_window is not None:
-            raise NotImplementedError("BeamAttention does not support sliding windows.")
+        # ALiBi slopes, the sliding window as (left, right) and the sinks as the
+        # reference keeps them (beam_attn.py:597-625); they reach every kernel
+        # launch through gr_attn_options
+        self.alibi_slopes = None if alibi_slopes is None else torch.tensor(alibi_slopes, dtype=torch.float32)
+        if sliding_window is None:
+            self.sliding_window = (-1, -1)
+        elif attn_type == AttentionType.ENCODER_ONLY:
+            self.sliding_window = (sliding_window - 1, sliding_window - 1)
+        else:
+            self.sliding_window = (sliding_window - 1, 0)
         if kv_cache_dtype not in ("auto", None):
             raise NotImplementedError(f"BeamAttention does not support kv_cache_dtype={kv_cache_dtype}.")
-        if running_sinks is not None:
-            raise NotImplementedError("BeamAttention does not support attention sinks.")
+        self.sinks = running_sinks
+        if self.sinks is not None:
+            assert self.sinks.shape[0] == num_heads, (
+                "Sinks must have the same number of heads as the number of heads in the layer")
+        self._dev_opts: dict = {}
         self.kv_cache_dtype = kv_cache_dtype
         self.logits_soft_cap = float(logits_soft_cap or 0.0)
         self.attn_type = attn_type
         self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
+
+    def _options(self, device) -> dict:
+        """The optional features as kernel arguments on ``device`` (float32
+        copies of the sinks and slopes, made once per device)."""
+        opts = self._dev_opts.get(device)
+        if opts is None:
+            left, right = self.sliding_window
+            opts = dict(window=(left, right) if left >= 0 or right >= 0 else None,
+                        sinks=None if self.sinks is None else
+                        self.sinks.detach().to(device=device, dtype=torch.float32).contiguous(),
+                        alibi_slopes=None if self.alibi_slopes is None else self.alibi_slopes.to(device))
+            self._dev_opts[device] = opts
+        return opts
 
     def forward(self, layer, query: torch.Tensor, key: torch.Tensor | None, value: torch.Tensor | None,
                 kv_cache: torch.Tensor, attn_metadata: BeamAttentionMetadata | None,
@@ -414,22 +441,31 @@ class BeamAttentionImpl:
         n = attn_metadata.num_actual_tokens
         if self.kv_sharing_target_layer_name is None and key is not None and value is not None:
             ops.reshape_and_cache(key[:n], value[:n], k_cache, v_cache, attn_metadata.slot_mapping)
+        opts = self._options(query.device)
+        # decode attention is causal over the beam's own tokens: its window has no right bound
+        dec_window = None if opts["window"] is None else (opts["window"][0], -1)
         for g in attn_metadata.groups:
             q = query[:n] if g.token_index is None else query.index_select(0, g.token_index)
             out = output[:n] if g.token_index is None else None
             res = ops.beam_attn_decode(q, k_cache, v_cache, g.prefix_bt, g.prefix_len, g.beam_start,
                                        g.suffix_bt, g.suffix_len, g.suffix_start, q_per_beam=g.q_per_beam,
                                        scale=self.scale, softcap=self.logits_soft_cap,
-                                       max_beams_per_req=g.max_beams, out=out, max_prefix_len=g.max_prefix_len)
+                                       max_beams_per_req=g.max_beams, out=out, max_prefix_len=g.max_prefix_len,
+                                       window=dec_window, sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"])
             if g.token_index is not None:
                 output.index_copy_(0, g.token_index, res)
         p = attn_metadata.prefill
         if p is not None:
             q = query[:n] if p.token_index is None else query.index_select(0, p.token_index)
             out = output[:n] if p.token_index is None else None
+            causal = attn_metadata.causal
+            win = opts["window"]
+            if win is not None and causal:
+                win = (win[0], -1)
             res = ops.paged_attn_prefill(q, k_cache, v_cache, p.block_table, p.query_start, p.seq_len,
                                          max_query_len=p.max_query_len, scale=self.scale,
-                                         softcap=self.logits_soft_cap, out=out)
+                                         softcap=self.logits_soft_cap, out=out, causal=causal, window=win,
+                                         sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"])
             if p.token_index is not None:
                 output.index_copy_(0, p.token_index, res)
         return output
@@ -451,7 +487,8 @@ class BeamAttentionBackend:
 
     @classmethod
     def supports_attn_type(cls, attn_type: str) -> bool:
-        return attn_type == AttentionType.DECODER
+        return attn_type in (AttentionType.DECODER, AttentionType.ENCODER, AttentionType.ENCODER_ONLY,
+                             AttentionType.ENCODER_DECODER)
 
     @staticmethod
     def get_impl_cls() -> type[BeamAttentionImpl]:
@@ -485,7 +522,7 @@ class BeamAttentionBackend:
 
     @classmethod
     def supports_sink(cls) -> bool:
-        return False
+        return True  # the sinks run on the generic kernels (gr_attn_options)
 
     @classmethod
     def supports_compute_capability(cls, capability) -> bool:
