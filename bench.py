@@ -177,32 +177,27 @@ def bench_other(args) -> int:
          f"warm {us_warm} us/step")
     cpu = None
     if not args.no_cpu_baseline:
-        t0 = time.perf_counter()
+        from oracle import cpu_baseline as cb
+        torch.set_num_threads(n_cpu)
         if args.workload == "fork":
-            from oracle import fork as of
-            bits = lambda t: t.contiguous().view(torch.int16).numpy()
-            par = host.parent[:1].numpy()  # one request of 16 per timing (bounded sample)
-            W = par.shape[1]
-            runs = 0
-            while runs < 3 or time.perf_counter() - t0 < 10.0:
-                of.fork_append(par, host.suffix_bt[:W].numpy(), host.suffix_len[:W].numpy(),
-                               bits(host.kv_cache[0]), bits(host.kv_cache[1]), bits(host.k_new[:W]),
-                               bits(host.v_new[:W]), block_size=host.block_size)
-                runs += 1
-            us_cpu = (time.perf_counter() - t0) / runs * 16 * 1e6
-            sample = f"1 of 16 requests per run, {runs} runs, scaled x16; numpy fork+append restatement"
-            cores = 1
+            kc, vc = host.kv_cache[0].clone(), host.kv_cache[1].clone()
+            run = lambda: cb.fork_append_torch(host.parent, host.suffix_bt, host.suffix_len, kc, vc,
+                                               host.k_new, host.v_new, block_size=host.block_size)
+            what = "torch index ops (owner / copy-on-write tables, slot gather-scatter, append)"
         else:
-            from oracle import prune as op
-            x = host.logits[:4].numpy()
-            c = host.cum[:4].numpy()
-            runs = 0
-            while runs < 3 or time.perf_counter() - t0 < 10.0:
-                op.prune_topk(x, c, 128)
-                runs += 1
-            us_cpu = (time.perf_counter() - t0) / runs * 16 * 1e6
-            sample = f"4 of 64 requests per run, {runs} runs, scaled x16; scalar C restatement"
-            cores = 1
+            run = lambda: cb.prune_topk_torch(host.logits, host.cum, 128)
+            what = "torch float32 log_softmax + per-beam top-128, then per-request top-128 of cum + logprob"
+        run()  # warm-up
+        times = []
+        t_end = time.perf_counter() + 10.0
+        while len(times) < 3 or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        us_cpu = times[len(times) // 2] * 1e6
+        sample = f"the full step, median of {len(times)} runs after a warm-up; {what}"
+        cores = n_cpu
         cpu = {"value": round(nbytes / (us_cpu * 1e-6) / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
                "us_per_step": round(us_cpu, 1), "sample": sample}
         _log(f"bench: cpu {cpu} (host has {n_cpu} cores)")

@@ -66,3 +66,59 @@ def cascade_decode_fp32(q, k_cache, v_cache, prefix_bt, prefix_len, beam_start, 
         o = (wa[..., None] * o_p + wb[..., None] * o_s) / (wa + wb)[..., None]
         out[n0:n1] = o.reshape(Hkv, Wr, G, D).permute(1, 0, 2, 3).reshape(Wr, Hq, D)
     return out
+
+
+def fork_append_torch(parent, suffix_bt, suffix_len, k_cache, v_cache, k_new, v_new, *, block_size):
+    """Beam KV fork + append as torch index operations on the host cores (the
+    CPU baseline of the device fork).  Same contract as ``oracle.fork``'s
+    ``fork_append`` (the reference's content rule, child suffix = parent
+    suffix ++ new token, ``vllm_gr/entrypoints/openai/serving_engine.py:113-120``),
+    vectorised: the owner / copy-on-write assignment as tensor ops, then one
+    gather-scatter of every copy-on-write token's K and V rows by slot and one
+    scatter of the appended tokens.  Updates the caches in place and returns
+    ``(new_bt, new_len)``."""
+    parent = parent.long()
+    R, W = parent.shape
+    NB, bs = k_cache.shape[0], block_size
+    cols = torch.arange(W).expand(R, W)
+    first = torch.full((R, W), W, dtype=torch.long).scatter_reduce(1, parent, cols, "amin")
+    owner = first.gather(1, parent) == cols                           # child inherits the row in place
+    free = first == W                                                 # childless parents
+    # k-th copy-on-write child <- k-th childless parent (stable sorts put them first, in order)
+    cow_c = torch.argsort((owner).to(torch.int8), dim=1, stable=True)
+    free_p = torch.argsort((~free).to(torch.int8), dim=1, stable=True)
+    src_row = torch.where(owner, parent, torch.zeros_like(parent))
+    src_row.scatter_(1, cow_c, torch.where(~owner.gather(1, cow_c), free_p, src_row.gather(1, cow_c)))
+    base = (torch.arange(R) * W)[:, None]
+    new_bt = suffix_bt[(base + src_row).reshape(-1)]
+    par_flat = (base + parent).reshape(-1)
+    new_len = suffix_len[par_flat].clone()
+    # copy-on-write tokens: slots of the parent's row -> slots of the child's new row
+    cow = (~owner).reshape(-1).nonzero().squeeze(1)
+    n_tok = new_len[cow].long()
+    child = torch.repeat_interleave(cow, n_tok)
+    pos = torch.arange(int(n_tok.sum())) - torch.repeat_interleave(torch.cumsum(n_tok, 0) - n_tok, n_tok)
+    src_slot = suffix_bt[par_flat[child], pos // bs].long() * bs + pos % bs
+    dst_slot = new_bt[child, pos // bs].long() * bs + pos % bs
+    for cache, new in ((k_cache, k_new), (v_cache, v_new)):
+        flat = cache.view(NB * bs, -1)
+        flat[dst_slot] = flat[src_slot]
+        L = new_len.long()
+        app = new_bt[torch.arange(R * W), L // bs].long() * bs + L % bs
+        flat[app] = new.reshape(R * W, -1)
+    return new_bt, new_len + 1
+
+
+def prune_topk_torch(logits, cum, k):
+    """Beam pruning in the reference's formulation on the host cores (the CPU
+    baseline of the fused prune): the sampler's float32 ``log_softmax`` and
+    per-beam top-k logprobs (``serving_engine.py:300-308``), then per request
+    the top-k of ``cum + logprob`` over all beams' candidates
+    (``serving_engine.py:511-567``).  Returns ``(parent, token, score)``
+    ``[R, k]`` for ``logits [R, W, V]`` and ``cum [R, W]``; ties are left in
+    torch's order."""
+    R, W, V = logits.shape
+    lp, tok = torch.log_softmax(logits, dim=-1).topk(k, dim=-1)          # [R, W, k]
+    score = (cum.double().reshape(R, W, 1) + lp.double()).reshape(R, W * k)
+    best, idx = score.topk(k, dim=-1)
+    return idx // k, tok.reshape(R, W * k).gather(1, idx), best
