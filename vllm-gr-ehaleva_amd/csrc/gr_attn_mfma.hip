@@ -376,6 +376,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   __shared__ int suf_info[2][4][32];     // per suffix tile and row group slot: (beam << 16) | j, or -1
   __shared__ int suf_s0[4][32];          // per row group beam: first suffix position
   __shared__ int suf_blk[4][32][SB_STAGE];  // per row group beam: its first suffix block ids
+  __shared__ int64_t suf_off[4][64];     // per row group: element offset of its first 64 suffix slots (-1: none)
+  __shared__ int suf_tab_bad[4];         // per row group: its slot table is not built (unstaged block ids)
   __shared__ int pbt_s[PBT_WIN];         // staged prefix block ids (-1 = invalid)
   __shared__ int hot_flag;               // a tile of the fast loop needed the exact path
 
@@ -534,6 +536,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     }
     pbt_s[tid + i * MF_THREADS] = blk;
   }
+  int suf_len = 0, suf_incl = 0;  // this meta lane's validated suffix length, inclusive prefix sum
   if (ks == 0) {
     int len = 0;
     if (meta_lane) {
@@ -550,6 +553,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       if ((lane & 31) >= off) incl += y;
     }
     if (lane < 32) suf_cum[rg][lane + 1] = incl;
+    suf_len = len;
+    suf_incl = incl;
     if (lane == 0) {
       suf_cum[rg][0] = 0;
       suf_cum[rg][33] = b_lo;  // first beam of the group
@@ -635,6 +640,38 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   if (n_st > 1) {
     ensure_window(kb + ST_KEYS);
     load_prefix_to(kb + ST_KEYS, read_blk(kb + ST_KEYS), k1reg, v1reg);
+  }
+  // Slot table of each row group's first suffix tile pair (64 slots), built
+  // while the first tiles' loads are in flight: the element offset of the
+  // slot's token row (-1: empty or invalid block) and its tag (beam << 16 | j)
+  // for the masks, so the suffix gathers need one LDS read per slot.  Only
+  // the staged block ids are used (no memory reads here: a wait would also
+  // wait for the tile loads); a group that needs others is flagged, and its
+  // workgroup gathers the first pair the general way.
+  if (!PREFILL && ks == 0) {
+    const int tot = __shfl(suf_incl, 31, 64);
+    const int c0 = suf_incl - suf_len;
+    const int n_in = meta_lane && c0 < 64 ? min(suf_len, 64 - c0) : 0;
+    const bool bad = __ballot(n_in > 0 && ((sS0 + n_in - 1) >> bsh) >= SB_STAGE) != 0;
+    if (lane == 0) suf_tab_bad[rg] = bad ? 1 : 0;
+    if (!bad && lane >= tot) {
+      suf_off[rg][lane] = -1;
+      suf_info[lane >> 5][rg][lane & 31] = -1;
+    }
+    if (!bad) {
+      for (int j = 0; j < n_in; ++j) {
+        const int pos = sS0 + j;
+        const int bi = pos >> bsh;
+        int blk = -1;
+#pragma unroll
+        for (int q = 0; q < SB_STAGE; ++q) blk = bi == q ? sBlk[q] : blk;
+        const bool ok = blk >= 0 && blk < a.num_blocks;
+        if (!ok) flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
+        const int slot = c0 + j;
+        suf_off[rg][slot] = ok ? (int64_t)blk * a.kv_block_stride + (int64_t)(pos & (a.bs - 1)) * a.kv_tok_stride + head_off : -1;
+        suf_info[slot >> 5][rg][slot & 31] = ok ? ((b_lo + lane) << 16) | j : -1;
+      }
+    }
   }
   if (n_st > 0) store_tile(lds);
   if (n_st > 1) store_tile_from(lds + BUF, k1reg, v1reg);
@@ -884,8 +921,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   };
   // tile h (0 or 1) of a pair: row group g's slots in buffer 2h + (g >> 1),
   // rows (g & 1) * 32 .. + 31
-  auto suf_store = [&](int t, int h, const u32x4_t (&skv)[SUF_PER_THREAD], const u32x4_t (&svv)[SUF_PER_THREAD],
-                       const int (&sinfo)[SUF_PER_THREAD]) {
+  auto suf_store = [&](int t, int h, const u32x4_t (&skv)[SUF_PER_THREAD], const u32x4_t (&svv)[SUF_PER_THREAD]) {
 #pragma unroll
     for (int i = 0; i < SUF_PER_THREAD; ++i) {
       const int e = t + i * MF_THREADS;
@@ -896,7 +932,34 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       const int key = (grp & 1) * 32 + slot;
       *reinterpret_cast<u32x4_t*>(buf + key * KS_PITCH + kchunk(key, ch) * 8) = skv[i];
       *reinterpret_cast<u32x4_t*>(buf + K_TILE + key * VS_PITCH + ch * 8) = svv[i];
-      if (ch == 0) suf_info[h][grp][slot] = sinfo[i];
+    }
+  };
+  auto suf_tag = [&](int t, int h, const int (&sinfo)[SUF_PER_THREAD]) {
+#pragma unroll
+    for (int i = 0; i < SUF_PER_THREAD; ++i) {
+      const int e = t + i * MF_THREADS;
+      if ((e & 15) == 0) suf_info[h][e >> 9][(e >> 4) & 31] = sinfo[i];
+    }
+  };
+  // the first pair's slots come from the prologue's slot table (tags already
+  // in suf_info): one LDS read per slot, then the loads
+  auto suf_gather_tab = [&](int h, int t, u32x4_t (&skv)[SUF_PER_THREAD], u32x4_t (&svv)[SUF_PER_THREAD]) {
+    const S* ksrc[SUF_PER_THREAD];
+    const S* vsrc[SUF_PER_THREAD];
+#pragma unroll
+    for (int i = 0; i < SUF_PER_THREAD; ++i) {
+      const int e = t + i * MF_THREADS;
+      const int64_t off = suf_off[e >> 9][h * 32 + ((e >> 4) & 31)];
+      const int ch = e & 15;
+      ksrc[i] = off < 0 ? zsrc : kc + off + ch * 8;
+      vsrc[i] = off < 0 ? zsrc : vc + off + ch * 8;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    using gvec = const __attribute__((address_space(1))) u32x4_t*;  // global loads, not flat
+#pragma unroll
+    for (int i = 0; i < SUF_PER_THREAD; ++i) {
+      skv[i] = *(gvec)(ksrc[i]);
+      svv[i] = *(gvec)(vsrc[i]);
     }
   };
   // this wave's row group against tile h of the pair
@@ -920,6 +983,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // Tiles in pairs: the key-half-0 wave of each row group takes the first
   // tile, the key-half-1 wave the second, at the same time (each adds to its
   // own partial state; the halves merge below).
+  const bool tab_ok = !(suf_tab_bad[0] | suf_tab_bad[1] | suf_tab_bad[2] | suf_tab_bad[3]);
   for (int it = 0; it < n_sit; it += 2) {
     // a fresh copy of the thread index each trip: the slot addresses derived
     // from it are recomputed in registers rather than hoisted out of the loop
@@ -927,17 +991,29 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     int t = tid;
     __asm__ volatile("" : "+v"(t));
     const bool two = it + 1 < n_sit;
-    {
-      u32x4_t skv0[SUF_PER_THREAD], svv0[SUF_PER_THREAD];
-      int sinfo0[SUF_PER_THREAD];
-      suf_gather(it, t, skv0, svv0, sinfo0);
-      suf_store(t, 0, skv0, svv0, sinfo0);
-    }
-    if (two) {
-      u32x4_t skv1[SUF_PER_THREAD], svv1[SUF_PER_THREAD];
-      int sinfo1[SUF_PER_THREAD];
-      suf_gather(it + 1, t, skv1, svv1, sinfo1);
-      suf_store(t, 1, skv1, svv1, sinfo1);
+    if (it == 0 && tab_ok) {
+      // both tiles' loads in flight at once (a missing second tile's slots are
+      // empty and read the zero source)
+      u32x4_t skv0[SUF_PER_THREAD], svv0[SUF_PER_THREAD], skv1[SUF_PER_THREAD], svv1[SUF_PER_THREAD];
+      suf_gather_tab(0, t, skv0, svv0);
+      suf_gather_tab(1, t, skv1, svv1);
+      suf_store(t, 0, skv0, svv0);
+      suf_store(t, 1, skv1, svv1);
+    } else {
+      {
+        u32x4_t skv0[SUF_PER_THREAD], svv0[SUF_PER_THREAD];
+        int sinfo0[SUF_PER_THREAD];
+        suf_gather(it, t, skv0, svv0, sinfo0);
+        suf_store(t, 0, skv0, svv0);
+        suf_tag(t, 0, sinfo0);
+      }
+      if (two) {
+        u32x4_t skv1[SUF_PER_THREAD], svv1[SUF_PER_THREAD];
+        int sinfo1[SUF_PER_THREAD];
+        suf_gather(it + 1, t, skv1, svv1, sinfo1);
+        suf_store(t, 1, skv1, svv1);
+        suf_tag(t, 1, sinfo1);
+      }
     }
     __syncthreads();
     if (ks == 0 || two) suf_compute(ks);
