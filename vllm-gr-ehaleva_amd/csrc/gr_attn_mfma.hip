@@ -397,6 +397,25 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   if (unit >= units) return;
   const int r = unit / a.Hkv, hk = unit % a.Hkv;
   const int G = a.Hq / a.Hkv;
+  const int tid = threadIdx.x;
+  // ---- prologue, two memory round trips.  First the reads that need only the
+  // arguments -- the request's beam range, its prefix length and the first
+  // window of its prefix block table; then, with the window staged in LDS, the
+  // suffix metadata, Q and the first two prefix tiles, all in flight together.
+  const int32_t* pbt = a.prefix_bt + (int64_t)r * a.prefix_bt_stride;
+  constexpr int WIN_PER_THREAD = PBT_WIN / MF_THREADS;
+  static_assert(PBT_WIN % MF_THREADS == 0, "window split");
+  // (prologue loads are branch-free -- an unused lane reads a zero source --
+  // so the compiler's wait counts stay exact and later loads stay in flight)
+  const int* zint = reinterpret_cast<const int*>(g_zero16);
+  int raw_blk[WIN_PER_THREAD];
+#pragma unroll
+  for (int i = 0; i < WIN_PER_THREAD; ++i) {
+    const int bi = tid + i * MF_THREADS;
+    raw_blk[i] = *(bi < a.prefix_bt_stride ? pbt + bi : zint);
+  }
+  const int P_arg = PREFILL ? 0 : a.prefix_len[r];
+  __asm__ volatile("" ::"s"(P_arg));  // read with the beam range, not after its checks
   const int nb0 = a.beam_start[r];  // prefill: first query token of the request
   int W, TG, rows_r, ctx = 0;
   if constexpr (PREFILL) {
@@ -423,7 +442,6 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   const int row_base = mt * MF_ROWS;
   if (row_base >= rows_r) return;
 
-  const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int rg = wave >> 1, ks = wave & 1;  // row group (32 rows), key half
   const int lrow = lane & 31, lhalf = lane >> 5;
@@ -440,12 +458,6 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   const int my_qi = PREFILL ? my_rho / G : (my_rho / G) % a.T, my_g = my_rho % G;
   const int64_t my_tok = PREFILL ? (int64_t)(nb0 + my_qi) : (int64_t)((nb0 + my_b) * a.T + my_qi);
   u32x4_t qf[8];
-  {
-    const S* src = qp + my_tok * a.q_tok_stride + (int64_t)(hk * G + my_g) * HD + lhalf * 8;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      qf[kk] = row_ok ? *reinterpret_cast<const u32x4_t*>(src + kk * 16) : u32x4_t{0, 0, 0, 0};
-  }
   const float c = SOFTCAP ? a.scale / a.softcap : a.scale * LOG2E;
   const float cap = a.softcap;
 
@@ -454,46 +466,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
   RowState st = {-INFINITY, 0.f};
 
-  // ---- prologue: every read that depends only on the arguments is issued
-  // before the first wait -- the prefix length, the first window of the
-  // prefix block table, and this row group's suffix metadata (lengths, start
-  // positions, first block ids) -- so the set-up costs one memory round trip.
   const int pre_cap = a.prefix_bt_stride * a.bs;
-  const int32_t* pbt = a.prefix_bt + (int64_t)r * a.prefix_bt_stride;
   // prefill: the workgroup reads keys up to its last query token's
-  int P = PREFILL ? ctx + (min(row_base + MF_ROWS, rows_r) - 1) / G + 1 : a.prefix_len[r];
-  constexpr int WIN_PER_THREAD = PBT_WIN / MF_THREADS;
-  static_assert(PBT_WIN % MF_THREADS == 0, "window split");
-  int raw_blk[WIN_PER_THREAD];
-#pragma unroll
-  for (int i = 0; i < WIN_PER_THREAD; ++i) {
-    const int bi = tid + i * MF_THREADS;
-    raw_blk[i] = bi < a.prefix_bt_stride ? pbt[bi] : -1;
-  }
-  // suffix metadata: lane l < nbeams of the key-half-0 wave of row group rg
-  // owns beam b_lo + l of the group
-  const int suf_cap = a.suffix_bt_stride * a.bs;
-  const int rlo = row_base + rg * 32;
-  const int b_lo = rlo / TG;
-  const int nbeams = !PREFILL && rlo < rows_r ? min((rlo + 31) / TG, W - 1) - b_lo + 1 : 0;  // <= 32
-  const bool meta_lane = ks == 0 && lane < nbeams;
-  int sL = 0, sS0 = 0, sBlk[SB_STAGE];
-  {
-    const int n = nb0 + b_lo + lane;
-    if (meta_lane) {
-      sL = a.suffix_len[n];
-      sS0 = a.suffix_start ? a.suffix_start[n] : 0;
-    }
-#pragma unroll
-    for (int j = 0; j < SB_STAGE; ++j)
-      sBlk[j] = meta_lane && j < a.suffix_bt_stride ? a.suffix_bt[(int64_t)n * a.suffix_bt_stride + j] : -1;
-  }
-  const int my_len = !PREFILL && row_ok ? a.suffix_len[nb0 + my_b] : 0;  // this lane's beam (causal limit)
-  // Retire every prologue load (Q included) here: the main loop's first read
-  // of qf is otherwise preceded by a full vector-memory wait in every
-  // iteration, which also waits for the tile prefetch issued at its top.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-
+  int P = PREFILL ? ctx + (min(row_base + MF_ROWS, rows_r) - 1) / G + 1 : P_arg;
   if (P < 0 || P > pre_cap) {
     if (tid == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
     P = P < 0 ? 0 : pre_cap;
@@ -528,37 +503,13 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const int bi = tid + i * MF_THREADS;
     int blk = -1;
     if (bi < nblk) {
-      blk = raw_blk[i];
+      blk = tid + i * MF_THREADS < a.prefix_bt_stride ? raw_blk[i] : -1;
       if (blk < 0 || blk >= a.num_blocks) {
         flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
         blk = -1;
       }
     }
     pbt_s[tid + i * MF_THREADS] = blk;
-  }
-  int suf_len = 0, suf_incl = 0;  // this meta lane's validated suffix length, inclusive prefix sum
-  if (ks == 0) {
-    int len = 0;
-    if (meta_lane) {
-      len = (sL < 0 || sS0 < 0 || sS0 + sL > suf_cap) ? 0 : sL;
-      if (len != sL) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
-      suf_s0[rg][lane] = sS0;
-#pragma unroll
-      for (int j = 0; j < SB_STAGE; ++j) suf_blk[rg][lane][j] = sBlk[j];
-    }
-    int incl = len;  // inclusive scan over the first 32 lanes
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) {
-      const int y = __shfl_up(incl, off, 64);
-      if ((lane & 31) >= off) incl += y;
-    }
-    if (lane < 32) suf_cum[rg][lane + 1] = incl;
-    suf_len = len;
-    suf_incl = incl;
-    if (lane == 0) {
-      suf_cum[rg][0] = 0;
-      suf_cum[rg][33] = b_lo;  // first beam of the group
-    }
   }
   if (tid == 0) hot_flag = 0;
   __syncthreads();
@@ -633,13 +584,76 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // stored into its buffer at the end (tile t in buffer t % NBUF).  The
   // first two tiles' loads are both issued before either is stored.
   u32x4_t k1reg[2], v1reg[2];
-  if (n_st > 0) {
-    ensure_window(kb);
-    load_prefix(kb, read_blk(kb));
+  // the first two tiles' block ids (a window move, if any, happens here, before
+  // the loads below)
+  ensure_window(kb);
+  const int blk0 = read_blk(kb);
+  ensure_window(kb + ST_KEYS);
+  const int blk1 = read_blk(kb + ST_KEYS);
+  // branch-free form of the first tiles' loads: keys past the prefix or in an
+  // invalid block read the zero source
+  auto load_first = [&](int k0, int blk, u32x4_t (&kd)[2], u32x4_t (&vd)[2]) {
+    const int key0 = k0 + 2 * lk;
+    const int64_t off = (int64_t)max(blk, 0) * a.kv_block_stride + (int64_t)(key0 & (a.bs - 1)) * a.kv_tok_stride +
+                        head_off + lc * 8;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const bool ok = blk >= 0 && key0 + j < P;
+      kd[j] = *reinterpret_cast<const u32x4_t*>(ok ? kc + off + j * a.kv_tok_stride : zsrc);
+      vd[j] = *reinterpret_cast<const u32x4_t*>(ok ? vc + off + j * a.kv_tok_stride : zsrc);
+    }
+  };
+  // second round trip: suffix metadata (needed first, by the slot table), Q,
+  // then the first two tiles.  Suffix metadata: lane l < nbeams of the
+  // key-half-0 wave of row group rg owns beam b_lo + l of the group.
+  const int suf_cap = a.suffix_bt_stride * a.bs;
+  const int rlo = row_base + rg * 32;
+  const int b_lo = rlo / TG;
+  const int nbeams = !PREFILL && rlo < rows_r ? min((rlo + 31) / TG, W - 1) - b_lo + 1 : 0;  // <= 32
+  const bool meta_lane = ks == 0 && lane < nbeams;
+  int sL, sS0, sBlk[SB_STAGE];
+  {
+    const int n = nb0 + b_lo + lane;
+    sL = *(meta_lane ? a.suffix_len + n : zint);
+    sS0 = *(meta_lane && a.suffix_start ? a.suffix_start + n : zint);
+#pragma unroll
+    for (int j = 0; j < SB_STAGE; ++j)
+      sBlk[j] = *(meta_lane && j < a.suffix_bt_stride ? a.suffix_bt + (int64_t)n * a.suffix_bt_stride + j : zint);
   }
-  if (n_st > 1) {
-    ensure_window(kb + ST_KEYS);
-    load_prefix_to(kb + ST_KEYS, read_blk(kb + ST_KEYS), k1reg, v1reg);
+  const int my_len = *(!PREFILL && row_ok ? a.suffix_len + nb0 + my_b : zint);  // this lane's beam (causal limit)
+  __builtin_amdgcn_sched_barrier(0);  // the metadata loads stay first: the slot table waits only for them
+  {
+    const S* src = qp + my_tok * a.q_tok_stride + (int64_t)(hk * G + my_g) * HD + lhalf * 8;
+    const S* zq = reinterpret_cast<const S*>(g_zero16);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = *reinterpret_cast<const u32x4_t*>(row_ok ? src + kk * 16 : zq);
+  }
+
+  load_first(kb, blk0, kreg, vreg);
+  load_first(kb + ST_KEYS, blk1, k1reg, v1reg);
+  int suf_len = 0, suf_incl = 0;  // this meta lane's validated suffix length, inclusive prefix sum
+  if (ks == 0) {
+    int len = 0;
+    if (meta_lane) {
+      len = (sL < 0 || sS0 < 0 || sS0 + sL > suf_cap) ? 0 : sL;
+      if (len != sL) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+      suf_s0[rg][lane] = sS0;
+#pragma unroll
+      for (int j = 0; j < SB_STAGE; ++j) suf_blk[rg][lane][j] = j < a.suffix_bt_stride ? sBlk[j] : -1;
+    }
+    int incl = len;  // inclusive scan over the first 32 lanes
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if ((lane & 31) >= off) incl += y;
+    }
+    if (lane < 32) suf_cum[rg][lane + 1] = incl;
+    suf_len = len;
+    suf_incl = incl;
+    if (lane == 0) {
+      suf_cum[rg][0] = 0;
+      suf_cum[rg][33] = b_lo;  // first beam of the group
+    }
   }
   // Slot table of each row group's first suffix tile pair (64 slots), built
   // while the first tiles' loads are in flight: the element offset of the
@@ -659,18 +673,21 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       suf_info[lane >> 5][rg][lane & 31] = -1;
     }
     if (!bad) {
+      bool bad_blk = false;  // reported after the loop: a memory operation inside it makes the
+                             // compiler wait for every load in flight before entering it
       for (int j = 0; j < n_in; ++j) {
         const int pos = sS0 + j;
         const int bi = pos >> bsh;
         int blk = -1;
 #pragma unroll
-        for (int q = 0; q < SB_STAGE; ++q) blk = bi == q ? sBlk[q] : blk;
+        for (int q = 0; q < SB_STAGE; ++q) blk = bi == q && q < a.suffix_bt_stride ? sBlk[q] : blk;
         const bool ok = blk >= 0 && blk < a.num_blocks;
-        if (!ok) flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
+        bad_blk |= !ok;
         const int slot = c0 + j;
         suf_off[rg][slot] = ok ? (int64_t)blk * a.kv_block_stride + (int64_t)(pos & (a.bs - 1)) * a.kv_tok_stride + head_off : -1;
         suf_info[slot >> 5][rg][slot & 31] = ok ? ((b_lo + lane) << 16) | j : -1;
       }
+      if (bad_blk) flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
     }
   }
   if (n_st > 0) store_tile(lds);
@@ -680,6 +697,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     ensure_window(kb + 2 * ST_KEYS);
     pf_blk = read_blk(kb + 2 * ST_KEYS);
   }
+  // Retire every prologue load (Q included) here: the main loop's first read
+  // of qf is otherwise preceded by a full vector-memory wait in every
+  // iteration, which also waits for the tile prefetch issued at its top.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
   f32x16_t s_cur = qk_half<DT>(lds, ks * 32, lane, qf);  // (stale LDS when n_st == 0: never used)
   // One step over a fully visible tile `it` (not the last): consumes its S^T
