@@ -183,3 +183,38 @@ def test_beam_search_loop_keeps_lineage(device):
             assert torch.equal(kvh[1, blk, j % BS].view(torch.int16), hist_v[n][j].view(torch.int16))
     # every beam owns distinct blocks
     assert len(set(sbt[:, 0].tolist())) == W
+
+
+def test_forward_reports_bad_block_through_metadata_status(device):
+    """The builder's status word reaches every launch of the forward: a block
+    id past the cache in a request's table leaves the result finite (the
+    kernels read that block as zeros) and is reported by ops.check_status;
+    a clean batch leaves the word at zero."""
+    from vllm_gr_amd import ops
+    g = torch.Generator().manual_seed(2)
+    Hq, Hkv, D = 8, 2, 128
+    NB = 16
+    kv = torch.randn((2, NB, BS, Hkv, D), generator=g).to(torch.bfloat16).to(device)
+    bt = torch.tensor([[3, 7, 1, 0], [9, 2, 12, 5]], dtype=torch.int32)
+    seq, q_lens = [40, 45], [1, 5]
+    n = sum(q_lens)
+    slots = torch.tensor([int(bt[r, p // BS]) * BS + p % BS for r, (S, ql) in enumerate(zip(seq, q_lens))
+                          for p in range(S - ql, S)], dtype=torch.int64)
+    q = torch.randn((n, Hq, D), generator=g).to(torch.bfloat16).to(device)
+    k_new = torch.randn((n, Hkv, D), generator=g).to(torch.bfloat16).to(device)
+    v_new = torch.randn((n, Hkv, D), generator=g).to(torch.bfloat16).to(device)
+    builder = ba.BeamAttentionMetadataBuilder(types.SimpleNamespace(block_size=BS), ["l0"], None, device)
+    out = torch.empty((n, Hq, D), dtype=torch.bfloat16, device=device)
+    md = _build(builder, None, _common(q_lens, seq, bt, device, slots))
+    assert md.status is builder.status
+    _impl(Hq, Hkv, D).forward(None, q, k_new, v_new, kv, md, output=out)
+    ops.check_status(md.status)  # clean batch: no bits
+    bad = bt.clone()
+    bad[0, 1] = NB + 5  # request 0's cached positions 16..31 (no new token is written there)
+    md = _build(builder, None, _common(q_lens, seq, bad, device, slots))
+    _impl(Hq, Hkv, D).forward(None, q, k_new, v_new, kv, md, output=out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    with pytest.raises(ValueError, match="block id out of range"):
+        ops.check_status(md.status)
+    builder.status.zero_()

@@ -55,7 +55,8 @@ class PruneResult:
 
 def prune_step(logits: torch.Tensor, cum_logprob: torch.Tensor, beam_width: int,
                eos_token_id: int | None = None, *, workspace: torch.Tensor | None = None,
-               catalog=None, beam_node: torch.Tensor | None = None, candidates: bool = False) -> PruneResult:
+               catalog=None, beam_node: torch.Tensor | None = None, candidates: bool = False,
+               status: torch.Tensor | None = None) -> PruneResult:
     """Fused log_softmax + cumulative logprob + top-``beam_width`` over
     beams x vocab per request.  ``logits [R, W, V]`` float32, ``cum [R, W]``
     float64 (the reference's Python-float scores, serving_engine.py:511,
@@ -66,10 +67,11 @@ def prune_step(logits: torch.Tensor, cum_logprob: torch.Tensor, beam_width: int,
     new beams' trie nodes.  ``candidates`` (float64 ``cum`` only) also
     returns every old beam's top-``beam_width`` (token, logprob) list, the
     per-step logprobs of the reference's beam search
-    (vllm_gr/entrypoints/llm.py:203-220)."""
+    (vllm_gr/entrypoints/llm.py:203-220).  ``status``: a device status
+    word (``ops.new_status``) the kernels OR table errors into."""
     eos = -1 if eos_token_id is None else int(eos_token_id)
     out = list(ops.beam_prune_topk(logits, cum_logprob, beam_width, eos, workspace=workspace, catalog=catalog,
-                                   beam_node=beam_node, candidates=candidates))
+                                   beam_node=beam_node, candidates=candidates, status=status))
     ct = cl = None
     if candidates:
         ct, cl = out[-2], out[-1]
@@ -110,7 +112,7 @@ def beam_search_step(table, logits: torch.Tensor, cum_logprob: torch.Tensor, kv_
     candidates than beams) keep their parent's KV."""
     W = table.beam_width
     res = prune_step(logits, cum_logprob, W, eos_token_id, catalog=catalog, beam_node=beam_node,
-                     candidates=candidates)
+                     candidates=candidates, status=status)
     parent = torch.where(res.parent >= 0, res.parent,
                          torch.arange(W, device=res.parent.device, dtype=res.parent.dtype)[None])
     table.fork(parent, kv_caches, status=status)

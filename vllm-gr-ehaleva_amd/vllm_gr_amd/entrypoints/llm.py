@@ -30,6 +30,7 @@ from dataclasses import dataclass, field
 import torch
 
 from .. import logprobs as lpm
+from .. import ops
 from ..v1.beam_kv import BeamKVTable
 from ..v1.sid_decoder import SID_DECODER_1P7B, DecoderConfig, SidDecoder, init_weights
 from ..v1.sid_runner import SidModelRunner
@@ -171,6 +172,10 @@ class LLM:
         parents: list[torch.Tensor] = []  # per step: each new beam's parent [R, W]
         cands: list[tuple[torch.Tensor, torch.Tensor]] = []  # per step: old beams' top-W lists
         lp = self.logprobs
+        # one device status word for the batch's launches (the builder's, which the
+        # attention and cache-write kernels already use), checked at the batch's sync
+        status = self.runner.builder.status
+        status.zero_()
         blocks: list[int] = []
         try:
             if steps > 0:
@@ -189,7 +194,7 @@ class LLM:
                 if self.logits_hook is not None:
                     self.logits_hook(0, logits[:, None], torch.empty(R, 1, 0, dtype=torch.int32, device=dev))
                 res = bsm.prune_step(logits[:, None], torch.zeros(R, 1, dtype=torch.float64, device=dev), W, eos,
-                                     catalog=cat, beam_node=node0, candidates=lp)
+                                     catalog=cat, beam_node=node0, candidates=lp, status=status)
                 finished.append((res.eos_score, torch.empty(R, 1, 0, dtype=torch.int32, device=dev)))
                 parents.append(res.parent)
                 if lp:
@@ -205,10 +210,11 @@ class LLM:
                         self.logits_hook(s, logits, hist)
                     node = res.node
                     if s + 1 < steps:
-                        res = bsm.beam_search_step(table, logits, score, self.runner.kv_caches, eos, catalog=cat,
-                                                   beam_node=node, candidates=lp)
+                        res = bsm.beam_search_step(table, logits, score, self.runner.kv_caches, eos, status,
+                                                   catalog=cat, beam_node=node, candidates=lp)
                     else:
-                        res = bsm.prune_step(logits, score, W, eos, catalog=cat, beam_node=node, candidates=lp)
+                        res = bsm.prune_step(logits, score, W, eos, catalog=cat, beam_node=node, candidates=lp,
+                                             status=status)
                     finished.append((res.eos_score, hist))
                     parents.append(res.parent)
                     if lp:
@@ -223,6 +229,7 @@ class LLM:
             fin_h = [(e.cpu().tolist(), h.cpu().tolist()) for e, h in finished]
             par_h = [p.cpu().tolist() for p in parents]
             cand_h = [lpm.step_lists(t, l) for t, l in cands] if lp else None
+            ops.check_status(status)  # the copies above synchronised: raises on a flagged table entry
         finally:
             self.runner.pool.release(blocks)
         times.wall_ms = (time.perf_counter() - t_wall) * 1e3

@@ -146,6 +146,9 @@ class BeamAttentionMetadata:
     prefill: PrefillGroup | None = None
     mega_req_idxs: list[int] = field(default_factory=list)
     std_req_idxs: list[int] = field(default_factory=list)
+    # the builder's device status word: every launch of the forward ORs the
+    # error bits of out-of-range table entries into it (ops.check_status reads it)
+    status: torch.Tensor | None = None
 
 
 class BeamAttentionMetadataBuilder:
@@ -159,6 +162,9 @@ class BeamAttentionMetadataBuilder:
         self.vllm_config = vllm_config
         self.device = torch.device(device)
         self.block_size = int(kv_cache_spec.block_size)
+        # one status word for every batch this builder routes: sticky until
+        # the caller clears it (ops.check_status after a synchronisation)
+        self.status = ops.new_status(self.device)
 
     def build(self, common_prefix_len: int, common_attn_metadata: CommonAttentionMetadata,
               fast_build: bool = False) -> BeamAttentionMetadata:
@@ -267,7 +273,7 @@ class BeamAttentionMetadataBuilder:
             query_start_loc=m.query_start_loc, max_seq_len=m.max_seq_len, seq_lens=m.seq_lens,
             block_table=m.block_table_tensor, slot_mapping=slot_mapping, causal=m.causal,
             groups=groups, prefill=prefill, mega_req_idxs=sorted(i for i, _ in mega + ref_mega),
-            std_req_idxs=[i for i, _ in std])
+            std_req_idxs=[i for i, _ in std], status=self.status)
 
     def _route_reference_mega(self, reqs, q_starts, m, groups) -> list[tuple[int, int, int, int]]:
         """Route the reference-layout mega requests (beam_attn.py:255-413):
@@ -440,7 +446,8 @@ class BeamAttentionImpl:
         k_cache, v_cache = ops.split_kv_cache(kv_cache)
         n = attn_metadata.num_actual_tokens
         if self.kv_sharing_target_layer_name is None and key is not None and value is not None:
-            ops.reshape_and_cache(key[:n], value[:n], k_cache, v_cache, attn_metadata.slot_mapping)
+            ops.reshape_and_cache(key[:n], value[:n], k_cache, v_cache, attn_metadata.slot_mapping,
+                                  status=attn_metadata.status)
         opts = self._options(query.device)
         # decode attention is causal over the beam's own tokens: its window has no right bound
         dec_window = None if opts["window"] is None else (opts["window"][0], -1)
@@ -451,7 +458,8 @@ class BeamAttentionImpl:
                                        g.suffix_bt, g.suffix_len, g.suffix_start, q_per_beam=g.q_per_beam,
                                        scale=self.scale, softcap=self.logits_soft_cap,
                                        max_beams_per_req=g.max_beams, out=out, max_prefix_len=g.max_prefix_len,
-                                       window=dec_window, sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"])
+                                       window=dec_window, sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"],
+                                       status=attn_metadata.status)
             if g.token_index is not None:
                 output.index_copy_(0, g.token_index, res)
         p = attn_metadata.prefill
@@ -465,7 +473,8 @@ class BeamAttentionImpl:
             res = ops.paged_attn_prefill(q, k_cache, v_cache, p.block_table, p.query_start, p.seq_len,
                                          max_query_len=p.max_query_len, scale=self.scale,
                                          softcap=self.logits_soft_cap, out=out, causal=causal, window=win,
-                                         sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"])
+                                         sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"],
+                                         status=attn_metadata.status)
             if p.token_index is not None:
                 output.index_copy_(0, p.token_index, res)
         return output

@@ -148,6 +148,7 @@ class SidDecoder:
         cfg, w, eps = self.cfg, self.w, self.cfg.rms_eps
         T = input_ids.shape[0]
         slots = attn_metadata.slot_mapping if attn_metadata is not None else None
+        status = attn_metadata.status if attn_metadata is not None else None
         h = w["embed"][input_ids]  # the residual stream
         x = ops.rms_norm(h, w["layers.0.input_norm"], eps)
         mlp = None
@@ -159,7 +160,8 @@ class SidDecoder:
             k_cache, v_cache = ops.split_kv_cache(kv_caches[i])
             q = ops.qk_norm_rope_cache(qkv, positions, self.rope.cos, self.rope.sin, w[p + "q_norm"],
                                        w[p + "k_norm"], k_cache, v_cache, slots, num_q_heads=cfg.num_heads,
-                                       num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, eps=eps)
+                                       num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, eps=eps,
+                                       status=status)
             attn = torch.empty_like(q)
             self.attn[i].forward(None, q, None, None, kv_caches[i], attn_metadata, output=attn)
             x = ops.rms_norm(F.linear(attn.view(T, cfg.q_size), w[p + "o"]), w[p + "post_norm"], eps,
