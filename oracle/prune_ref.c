@@ -15,7 +15,7 @@
  * Build contract restated here (the reference leaves tie order unspecified
  * and composes the score in float64 on the host, :538-539):
  *   m     = max_v x[v]                                   (fp32, exact)
- *   e_v   = exp2_neg((x[v] - m) * LOG2E_F)               (fp32, see below)
+ *   e_v   = exp2_neg(fmaf(x[v], LOG2E_F, -(m * LOG2E_F))) (fp32, see below)
  *   S     = fp32 sum of e_v in the fixed order below
  *   lse   = (double)m + log_f64((double)S)               (fp64, see below)
  *   c_b   = (double)cum[b] - lse                         (fp64)
@@ -31,8 +31,9 @@
  *   a[l] = a[l] + a[l ^ mask]; finally S = (w0 + w1) + (w2 + w3).
  *
  * exp2_neg(t), t <= 0: 0 if t < -125; else k = rint(t), f = t - k (exact),
- *   p = Horner in f with fmaf over c_j = fp32((ln 2)^j / j!), j = 7..0
- *   (Taylor series of e^(f ln 2)), result = ldexpf(p, k).
+ *   p = Horner in f with fmaf over the degree-5 coefficients EXP2_C (a
+ *   relative-error fit of 2^f on [-1/2, 1/2] with p(0) = 1, within 2.1 ulp), result =
+ *   ldexpf(p, k).
  * log_f64(s), s >= 1: s = mant * 2^e with mant in [sqrt(1/2), sqrt(2));
  *   z = (mant - 1) / (mant + 1); w = z*z;
  *   q = Horner in w with fma over 1/(2j+1), j = 11..0 (atanh series,
@@ -52,9 +53,8 @@
 #define PRUNE_VEC 4
 
 static const float LOG2E_F = 0x1.715476p+0f;
-static const float EXP2_C[8] = {
-    0x1.000000p+0f, 0x1.62e430p-1f, 0x1.ebfbe0p-3f, 0x1.c6b08ep-5f,
-    0x1.3b2ab6p-7f, 0x1.5d87fep-10f, 0x1.430912p-13f, 0x1.ffcbfcp-17f};
+static const float EXP2_C[6] = {
+    0x1.000000p+0f, 0x1.62e42ap-1f, 0x1.ebf9bcp-3f, 0x1.c6b746p-5f, 0x1.3cea88p-7f, 0x1.5bbea6p-10f};
 static const double LN2_HI = 0x1.62e42p-1;
 static const double LN2_LO = 0x1.fdf473de6af28p-22;
 static const double SQRT_HALF = 0x1.6a09e667f3bcdp-1;
@@ -63,8 +63,8 @@ float oracle_exp2_neg(float t) {
   if (!(t >= -125.0f)) return 0.0f;
   float k = rintf(t);
   float f = t - k;
-  float p = EXP2_C[7];
-  for (int j = 6; j >= 0; --j) p = fmaf(p, f, EXP2_C[j]);
+  float p = EXP2_C[5];
+  for (int j = 4; j >= 0; --j) p = fmaf(p, f, EXP2_C[j]);
   return ldexpf(p, (int)k);
 }
 
@@ -92,6 +92,7 @@ static float row_stats(const float* x, int V, float* S_out, double* lse_out) {
     *lse_out = -INFINITY;
     return m;
   }
+  const float ml = m * LOG2E_F;
   float part[PRUNE_THREADS];
   for (int t = 0; t < PRUNE_THREADS; ++t) {
     float acc = 0.0f;
@@ -99,8 +100,7 @@ static float row_stats(const float* x, int V, float* S_out, double* lse_out) {
       for (int j = 0; j < PRUNE_VEC; ++j) {
         int v = base + PRUNE_VEC * t + j;
         if (v < V) {
-          float d = x[v] - m;
-          float tt = d * LOG2E_F;
+          float tt = fmaf(x[v], LOG2E_F, -ml);
           acc = acc + oracle_exp2_neg(tt);
         }
       }

@@ -39,20 +39,19 @@ constexpr int MG_THREADS = 1024;               // merge workgroup
 typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 
 // ---- bit-exact numerics ------------------------------------------------------
-// exp2 of t <= 0: Taylor series of e^(f ln2) (degree 7, Horner with fma) on the
-// fractional part f = t - rint(t), scaled by 2^rint(t).
+// exp2 of t <= 0: a degree-5 polynomial (Horner with fma; a relative-error fit
+// of 2^f on [-1/2, 1/2] with p(0) = 1, within 2.1 ulp) on the fractional part f = t - rint(t),
+// scaled by 2^rint(t).
 __device__ inline float exp2_neg(float t) {
   const bool zero = !(t >= -125.0f);  // a select, not a branch: the 32 chains interleave
   t = zero ? 0.0f : t;
   const float k = __builtin_rintf(t);
   const float f = t - k;
-  float p = 0x1.ffcbfcp-17f;
-  p = __builtin_fmaf(p, f, 0x1.430912p-13f);
-  p = __builtin_fmaf(p, f, 0x1.5d87fep-10f);
-  p = __builtin_fmaf(p, f, 0x1.3b2ab6p-7f);
-  p = __builtin_fmaf(p, f, 0x1.c6b08ep-5f);
-  p = __builtin_fmaf(p, f, 0x1.ebfbe0p-3f);
-  p = __builtin_fmaf(p, f, 0x1.62e430p-1f);
+  float p = 0x1.5bbea6p-10f;
+  p = __builtin_fmaf(p, f, 0x1.3cea88p-7f);
+  p = __builtin_fmaf(p, f, 0x1.c6b746p-5f);
+  p = __builtin_fmaf(p, f, 0x1.ebf9bcp-3f);
+  p = __builtin_fmaf(p, f, 0x1.62e42ap-1f);
   p = __builtin_fmaf(p, f, 0x1.000000p+0f);
   const float e = __builtin_amdgcn_ldexpf(p, (int)k);
   return zero ? 0.0f : e;
@@ -422,12 +421,14 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 #define PR_FOR_CHUNKS(c) \
   _Pragma("unroll") for (int c = 0; c < (MAXC > 0 ? MAXC : nch); ++c) if (c < nch)
 
-  // ---- row max ----
-  float tm = -INFINITY;
+  // ---- row max; also the thread's second-largest chunk maximum (an element
+  // other than the thread maximum: it tightens the selection bound below) ----
+  float tm = -INFINITY, t2 = -INFINITY;
   PR_FOR_CHUNKS(c) {
     if (live(c)) {
-#pragma unroll
-      for (int j = 0; j < PR_VEC; ++j) tm = fmaxf(tm, get(c, j));
+      const float cm = fmaxf(fmaxf(get(c, 0), get(c, 1)), fmaxf(get(c, 2), get(c, 3)));
+      t2 = fmaxf(t2, cm >= tm ? tm : cm);  // NaN chunk maxima (all four NaN) are skipped
+      tm = fmaxf(tm, cm);
     }
   }
   const float wm = wave_max(tm);
@@ -443,12 +444,12 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   double lse_row = INFINITY;  // a row of -inf logits has logprobs -inf
   if (m != -INFINITY) {
     float acc = 0.0f;
+    const float ml = m * 0x1.715476p+0f;
     PR_FOR_CHUNKS(c) {
       if (live(c)) {
 #pragma unroll
         for (int j = 0; j < PR_VEC; ++j) {
-          const float d = get(c, j) - m;
-          const float t = d * 0x1.715476p+0f;
+          const float t = __builtin_fmaf(get(c, j), 0x1.715476p+0f, -ml);
           acc = acc + exp2_neg(t);
         }
       }
@@ -465,20 +466,24 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
 
   // ---- stage 1: row top-k1 by (logit desc, token asc) ----
   // Lower bound t0 of the k1-th largest key: per wave, the ceil(k1/4)-th
-  // largest thread maximum rounded down to its top 16 bits (bisection over
-  // that range with wave ballots), least over the waves.  Every wave then has that many threads holding a
-  // key >= t0: at least k1 keys in all.  Only keys >= t0 can be selected; with
-  // few of them they are ranked directly.
+  // largest of the threads' maxima and second-largest chunk maxima (two
+  // distinct elements per thread) rounded down to its top 16 bits (bisection
+  // over that range with wave ballots), least over the waves.  Every wave then
+  // holds that many distinct elements with a key >= t0: at least k1 keys in
+  // all.  Only keys >= t0 can be selected; with few of them they are ranked
+  // directly.
   uint32_t t0 = 0;
   if (k1 <= PR_THREADS) {
     const int kw = (k1 + 3) >> 2;
     const uint32_t a0 = fkey(tm) >> 16;  // the top 16 bits of the key suffice for a bound
-    // invariant: at least kw lanes have a0 >= lo; the answer is <= hi (bounds
+    const uint32_t a1 = fkey(t2) >> 16;
+    // invariant: at least kw of the lanes' a0, a1 are >= lo; the answer is <= hi (bounds
     // are wave-uniform, kept in scalar registers)
     uint32_t lo = 0, hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(fkey(m) >> 16));
     while (lo < hi) {
       const uint32_t mid = lo + ((hi - lo + 1) >> 1);
-      const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(a0 >= mid));
+      const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(a0 >= mid)) +
+                    __builtin_popcountll(__builtin_amdgcn_ballot_w64(a1 >= mid));
       if (c >= kw) lo = mid;
       else hi = mid - 1;
     }
