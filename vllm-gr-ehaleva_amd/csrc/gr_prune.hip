@@ -480,11 +480,17 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     // invariant: at least kw of the lanes' a0, a1 are >= lo; the answer is <= hi (bounds
     // are wave-uniform, kept in scalar registers)
     uint32_t lo = 0, hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(fkey(m) >> 16));
+    auto count_ge = [&](uint32_t v) {
+      return __builtin_popcountll(__builtin_amdgcn_ballot_w64(a0 >= v)) +
+             __builtin_popcountll(__builtin_amdgcn_ballot_w64(a1 >= v));
+    };
+    // first one trial 256 units of the 16-bit key below the maximum (two
+    // binades of the 7 mantissa bits it keeps): where it holds, the bisection
+    // needs 8 steps instead of 16
+    if (hi > 256 && count_ge(hi - 256) >= kw) lo = hi - 256;
     while (lo < hi) {
       const uint32_t mid = lo + ((hi - lo + 1) >> 1);
-      const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(a0 >= mid)) +
-                    __builtin_popcountll(__builtin_amdgcn_ballot_w64(a1 >= mid));
-      if (c >= kw) lo = mid;
+      if (count_ge(mid) >= kw) lo = mid;
       else hi = mid - 1;
     }
     if (lane == 0) wkey[wave] = lo << 16;
