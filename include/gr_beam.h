@@ -43,7 +43,12 @@ enum {
   GR_DEV_BAD_NODE = 16    /* catalog node id or child range outside the trie */
 };
 
-enum { GR_DTYPE_F32 = 0, GR_DTYPE_F16 = 1, GR_DTYPE_BF16 = 2 };
+enum { GR_DTYPE_F32 = 0, GR_DTYPE_F16 = 1, GR_DTYPE_BF16 = 2,
+       /* KV-cache element type only: OCP fp8 e4m3 (float8_e4m3fn: 1 sign, 4
+        * exponent bits with bias 7, 3 mantissa bits, no infinities, 0x7F/0xFF
+        * NaN, largest finite 448) -- the reference's fp8 / fp8_e4m3 cache
+        * (beam_attn.py:617-618, :734-737, :801-804) */
+       GR_DTYPE_FP8_E4M3 = 3 };
 
 /* Human-readable name of a status code (static storage). */
 const char* gr_status_string(gr_status_t status);
@@ -179,6 +184,12 @@ typedef struct gr_attn_options {
   int causal;                 /* 1: causal (required for decode); 0: prefill over every key */
   const float* sinks;         /* [num_q_heads] or NULL */
   const float* alibi_slopes;  /* [num_q_heads] or NULL */
+  /* GR_DTYPE_FP8_E4M3: the caches hold fp8 e4m3 elements, read as
+   * fp8_value * k_scale[0] (K) and * v_scale[0] (V); any other value: the
+   * caches hold elements of `dtype`, like q */
+  int kv_dtype;
+  const float* k_scale;       /* [1] device float, or NULL for 1.0 */
+  const float* v_scale;       /* [1] device float, or NULL for 1.0 */
 } gr_attn_options;
 
 /* gr_beam_attn_decode_ws with options (the optional features run on the
@@ -226,6 +237,22 @@ gr_status_t gr_reshape_and_cache(
     int block_size, int dtype, int32_t* dev_status, hipStream_t stream);
 
 /*
+ * gr_reshape_and_cache into an fp8 e4m3 cache: each element is stored as
+ * e4m3(clamp(x / scale, -448, 448)), rounded to nearest even (x of `dtype`,
+ * scale = k_scale[0] / v_scale[0], NULL for 1.0) -- reshape_and_cache_flash
+ * with the layer's _k_scale / _v_scale and an fp8 kv_cache_dtype
+ * (beam_attn.py:727-732).  Strides count elements of their own tensors;
+ * head_dim a multiple of 4.
+ */
+gr_status_t gr_reshape_and_cache_fp8(
+    const void* key, int64_t key_tok_stride, const void* value, int64_t value_tok_stride,
+    void* k_cache, void* v_cache, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    const int64_t* slot_mapping, int num_tokens, int num_kv_heads, int head_dim,
+    int block_size, int dtype, const float* k_scale, const float* v_scale, int32_t* dev_status,
+    hipStream_t stream);
+
+/*
  * Beam KV fork, optionally fused with the append of one new token per beam.
  *
  * Replaces the reference's per-step suffix rebuild: _mega_request_step
@@ -243,6 +270,8 @@ gr_status_t gr_reshape_and_cache(
  * bt_out/len_out must not alias bt_in/len_in.  When k_new/v_new
  * ([num_reqs*beam_width, num_kv_heads, head_dim]) are given, each child's
  * token is appended at position len_out[c] and len_out[c] is incremented.
+ * dtype may be GR_DTYPE_FP8_E4M3 (the copies move bytes; k_new/v_new then
+ * hold e4m3 elements; the same holds for gr_beam_kv_append).
  */
 gr_status_t gr_beam_kv_fork(
     const int32_t* parent, int num_reqs, int beam_width,

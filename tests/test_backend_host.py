@@ -46,7 +46,7 @@ def test_supports_combination_sinks_accepted():
 @pytest.mark.parametrize("kw,reason", [
     (dict(dtype=torch.float32), "Unsupported dtype"),
     (dict(head_size=264), "Unsupported head_size"),
-    (dict(kv_cache_dtype="fp8"), "Unsupported kv_cache_dtype"),
+    (dict(kv_cache_dtype="fp8_e5m2"), "Unsupported kv_cache_dtype"),
     (dict(block_size=8), "not multiple of 16"),
     (dict(device_capability="gfx942"), "gfx950"),
     (dict(use_mla=True), "MLA"),
@@ -66,8 +66,13 @@ def test_impl_rejects_unsupported_features():
                                                       kv_cache_dtype="auto"), **kw})
     impl = mk()
     assert impl.num_queries_per_kv == 4 and impl.logits_soft_cap == 0.0
+    # fp8 e4m3 caches are accepted (beam_attn.py:617-618, :801-804); e5m2 is
+    # not (the reference's get_fp8_dtype_for_flashattn knows only e4m3)
+    assert mk(kv_cache_dtype="fp8").kv_fp8 and mk(kv_cache_dtype="fp8_e4m3").kv_fp8 and not impl.kv_fp8
+    assert B.supports_kv_cache_dtype("fp8") and B.supports_kv_cache_dtype("fp8_e4m3")
+    assert not B.supports_kv_cache_dtype("fp8_e5m2")
     with pytest.raises(NotImplementedError):
-        mk(kv_cache_dtype="fp8")
+        mk(kv_cache_dtype="fp8_e5m2")
     with pytest.raises(AssertionError, match="Sinks must have the same number of heads"):
         mk(running_sinks=torch.zeros(31))
     # the reference's window convention (beam_attn.py:600-605)

@@ -38,11 +38,14 @@ struct DecodeArgs {
   int causal;                // prefill: 0 = every key of the sequence (decode is always causal)
   const float* sinks;        // [Hq] sink logits (natural log units) or null
   const float* alibi;        // [Hq] ALiBi slopes or null
+  int kv8;                   // the caches hold fp8 e4m3 elements (dequantised by k_scale / v_scale)
+  const float* k_scale;      // [1] or null (1.0)
+  const float* v_scale;      // [1] or null (1.0)
 };
 
 // any of the optional features set (only the generic kernel implements them)
 inline bool has_options(const DecodeArgs& a) {
-  return a.win_left >= 0 || a.win_right >= 0 || !a.causal || a.sinks || a.alibi;
+  return a.win_left >= 0 || a.win_right >= 0 || !a.causal || a.sinks || a.alibi || a.kv8;
 }
 
 // MFMA path (gr_attn_mfma.hip): bf16/fp16, head_dim 128, 16-byte aligned rows.

@@ -41,7 +41,9 @@ __device__ inline int find_request(const int32_t* beam_start, int num_reqs, int 
 // adds -slope * |qpos - kpos| after the soft cap; a sink adds exp(sink) to
 // the softmax denominator (beam_attn.py:597-625, flash_attn_varlen_func's
 // window_size / alibi_slopes / s_aux).
-template <int DT, bool PREFILL = false>
+// KV8: the caches hold fp8 e4m3 elements, dequantised on load by the
+// per-tensor scales (value = e4m3 * scale).
+template <int DT, bool PREFILL = false, bool KV8 = false>
 __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   using E = Elem<DT>;
   using S = typename E::storage;
@@ -98,6 +100,9 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   const S* q = static_cast<const S*>(a.q);
   const S* kc = static_cast<const S*>(a.k_cache);
   const S* vc = static_cast<const S*>(a.v_cache);
+  const uint8_t* kc8 = static_cast<const uint8_t*>(a.k_cache);
+  const uint8_t* vc8 = static_cast<const uint8_t*>(a.v_cache);
+  const float k_sc = KV8 && a.k_scale ? a.k_scale[0] : 1.f, v_sc = KV8 && a.v_scale ? a.v_scale[0] : 1.f;
 
   for (int e = t; e < GEN_ROWS * D; e += GEN_THREADS) {
     int row = e / D, d = e % D;
@@ -152,8 +157,13 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
         }
         int64_t o = (int64_t)blk * a.kv_block_stride + (int64_t)off * a.kv_tok_stride +
                     (int64_t)hk * a.kv_head_stride + d;
-        kv = E::to_float(kc[o]);
-        vv = E::to_float(vc[o]);
+        if constexpr (KV8) {
+          kv = fp8e4m3_to_float(kc8[o]) * k_sc;
+          vv = fp8e4m3_to_float(vc8[o]) * v_sc;
+        } else {
+          kv = E::to_float(kc[o]);
+          vv = E::to_float(vc[o]);
+        }
       }
       k_s[key * (D + 1) + d] = kv;
       v_s[key * D + d] = vv;
@@ -256,6 +266,30 @@ static size_t generic_smem_bytes(int D) {
 
 int g_decode_kernel_override = 0;
 
+template <bool PREFILL, bool KV8>
+static gr_status_t launch_generic_kv(const DecodeArgs& a, dim3 grid, size_t smem, hipStream_t stream) {
+  static bool attr_done[3] = {};
+  const void* fn = a.dtype == GR_DTYPE_F32 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F32, PREFILL, KV8>)
+                   : a.dtype == GR_DTYPE_F16 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F16, PREFILL, KV8>)
+                                             : reinterpret_cast<const void*>(decode_generic<GR_DTYPE_BF16, PREFILL, KV8>);
+  if (!attr_done[a.dtype]) {  // head_dim 256 needs more than the default 64 KB
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)generic_smem_bytes(256));
+    attr_done[a.dtype] = true;
+  }
+  switch (a.dtype) {
+    case GR_DTYPE_F32:
+      hipLaunchKernelGGL((decode_generic<GR_DTYPE_F32, PREFILL, KV8>), grid, dim3(GEN_THREADS), smem, stream, a);
+      break;
+    case GR_DTYPE_F16:
+      hipLaunchKernelGGL((decode_generic<GR_DTYPE_F16, PREFILL, KV8>), grid, dim3(GEN_THREADS), smem, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_generic<GR_DTYPE_BF16, PREFILL, KV8>), grid, dim3(GEN_THREADS), smem, stream, a);
+      break;
+  }
+  return launch_status();
+}
+
 template <bool PREFILL>
 static gr_status_t launch_generic(const DecodeArgs& a, hipStream_t stream) {
   const int G = a.Hq / a.Hkv;
@@ -264,27 +298,9 @@ static gr_status_t launch_generic(const DecodeArgs& a, hipStream_t stream) {
   if (gx == 0) return GR_OK;
   if (gx > 0x7fffffff || a.Hkv > 65535) return GR_ERR_INVALID_ARG;
   dim3 grid((unsigned)gx, (unsigned)a.Hkv);
-  size_t smem = generic_smem_bytes(a.D);
-  static bool attr_done[2][3] = {};
-  if (!attr_done[PREFILL][a.dtype]) {  // head_dim 256 needs more than the default 64 KB
-    const void* fn = a.dtype == GR_DTYPE_F32 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F32, PREFILL>)
-                     : a.dtype == GR_DTYPE_F16 ? reinterpret_cast<const void*>(decode_generic<GR_DTYPE_F16, PREFILL>)
-                                               : reinterpret_cast<const void*>(decode_generic<GR_DTYPE_BF16, PREFILL>);
-    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)generic_smem_bytes(256));
-    attr_done[PREFILL][a.dtype] = true;
-  }
-  switch (a.dtype) {
-    case GR_DTYPE_F32:
-      hipLaunchKernelGGL((decode_generic<GR_DTYPE_F32, PREFILL>), grid, dim3(GEN_THREADS), smem, stream, a);
-      break;
-    case GR_DTYPE_F16:
-      hipLaunchKernelGGL((decode_generic<GR_DTYPE_F16, PREFILL>), grid, dim3(GEN_THREADS), smem, stream, a);
-      break;
-    default:
-      hipLaunchKernelGGL((decode_generic<GR_DTYPE_BF16, PREFILL>), grid, dim3(GEN_THREADS), smem, stream, a);
-      break;
-  }
-  return launch_status();
+  const size_t smem = generic_smem_bytes(a.D);
+  return a.kv8 ? launch_generic_kv<PREFILL, true>(a, grid, smem, stream)
+               : launch_generic_kv<PREFILL, false>(a, grid, smem, stream);
 }
 
 }  // namespace gr
@@ -351,6 +367,9 @@ static gr_status_t apply_options(DecodeArgs& a, const gr_attn_options* opt, bool
   a.causal = opt->causal;
   a.sinks = opt->sinks;
   a.alibi = opt->alibi_slopes;
+  a.kv8 = opt->kv_dtype == GR_DTYPE_FP8_E4M3;
+  a.k_scale = a.kv8 ? opt->k_scale : nullptr;
+  a.v_scale = a.kv8 ? opt->v_scale : nullptr;
   return GR_OK;
 }
 

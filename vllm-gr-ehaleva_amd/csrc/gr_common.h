@@ -38,9 +38,34 @@ template <> struct Elem<GR_DTYPE_F16> {
   }
 };
 
-inline int dtype_size(int dtype) { return dtype == GR_DTYPE_F32 ? 4 : 2; }
+inline int dtype_size(int dtype) { return dtype == GR_DTYPE_F32 ? 4 : dtype == GR_DTYPE_FP8_E4M3 ? 1 : 2; }
 inline bool dtype_valid(int dtype) {
   return dtype == GR_DTYPE_F32 || dtype == GR_DTYPE_F16 || dtype == GR_DTYPE_BF16;
+}
+// element types a KV cache may hold (the byte-moving kernels: fork, append)
+inline bool cache_dtype_valid(int dtype) { return dtype_valid(dtype) || dtype == GR_DTYPE_FP8_E4M3; }
+
+// ---- OCP fp8 e4m3 (float8_e4m3fn) -------------------------------------------
+// Value of a byte: sign, 4 exponent bits e (bias 7), 3 mantissa bits m:
+// 2^(e-7) (1 + m/8); e = 0: 2^-6 m/8; e = 15, m = 7: NaN (no infinities).
+__device__ inline float fp8e4m3_to_float(uint32_t b) {
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  float v = e == 0 ? (float)m * 0x1p-9f : __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+  v = (e == 15 && m == 7) ? __builtin_bit_cast(float, 0x7FC00000u) : v;  // quiet NaN
+  return (b & 0x80u) ? -v : v;
+}
+// The e4m3 byte nearest to clamp(x, -448, 448), ties to even; NaN -> 0x7F.
+// With e' = max(floor(log2 |x|), -6) the quantum is 2^(e' - 3), q = rint(|x| /
+// quantum) (exact scaling) and the code is ((e' + 7) << 3) + q - 8: a q of 16
+// carries into the next exponent, and e' = -6 covers the subnormals.
+__device__ inline uint32_t float_to_fp8e4m3(float x) {
+  if (x != x) return 0x7Fu;
+  const uint32_t sign = (__builtin_bit_cast(uint32_t, x) >> 24) & 0x80u;
+  const float a = fminf(fabsf(x), 448.0f);
+  const int fe = (int)((__builtin_bit_cast(uint32_t, a) >> 23) & 0xFFu) - 127;
+  const int e = fe < -6 ? -6 : fe;
+  const int q = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(a, 3 - e));
+  return a == 0.0f ? sign : sign | (uint32_t)(((e + 7) << 3) + q - 8);
 }
 
 // One 16-byte chunk per lane from global memory straight into LDS: lane i's

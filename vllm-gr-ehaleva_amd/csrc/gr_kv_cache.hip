@@ -363,6 +363,46 @@ __global__ __launch_bounds__(64) void reshape_and_cache_k(const uint8_t* key, in
   }
 }
 
+// Quantising scatter into an fp8 e4m3 cache: one workgroup per token, four
+// elements (one 32-bit word of the cache) per thread and step.
+template <int DT>
+__global__ __launch_bounds__(256) void reshape_and_cache_fp8_k(const void* key, int64_t key_stride, const void* value,
+                                                               int64_t value_stride, KvGeom g,
+                                                               const int64_t* __restrict__ slots, int T,
+                                                               const float* k_scale, const float* v_scale,
+                                                               int32_t* dev_status) {
+  using E = Elem<DT>;
+  using S = typename E::storage;
+  const int t = blockIdx.x;
+  if (t >= T) return;
+  const int64_t slot = slots[t];
+  if (slot < 0) return;
+  const int64_t blk = slot / g.bs;
+  const int off = (int)(slot % g.bs);
+  if (blk >= g.num_blocks) {
+    if (threadIdx.x == 0) flag_status(dev_status, GR_DEV_BAD_BLOCK);
+    return;
+  }
+  const float ks = k_scale ? k_scale[0] : 1.0f, vs = v_scale ? v_scale[0] : 1.0f;
+  const int words = g.D / 4;
+  uint8_t* kc = static_cast<uint8_t*>(g.k_cache);
+  uint8_t* vc = static_cast<uint8_t*>(g.v_cache);
+  for (int e = threadIdx.x; e < g.Hkv * words; e += 256) {
+    const int h = e / words, d0 = (e - h * words) * 4;
+    const S* kp = static_cast<const S*>(key) + (int64_t)t * key_stride + (int64_t)h * g.D + d0;
+    const S* vp = static_cast<const S*>(value) + (int64_t)t * value_stride + (int64_t)h * g.D + d0;
+    uint32_t kw = 0, vw = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kw |= float_to_fp8e4m3(E::to_float(kp[j]) / ks) << (8 * j);
+      vw |= float_to_fp8e4m3(E::to_float(vp[j]) / vs) << (8 * j);
+    }
+    const int64_t dof = kv_byte_off(g, blk, off, h) + d0;
+    *reinterpret_cast<uint32_t*>(kc + dof) = kw;
+    *reinterpret_cast<uint32_t*>(vc + dof) = vw;
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // 16-byte vector moves need every row start 16-byte aligned.
@@ -404,7 +444,7 @@ extern "C" gr_status_t gr_beam_kv_fork(const int32_t* parent, int num_reqs, int 
                                        int64_t kv_head_stride, const void* k_new, const void* v_new,
                                        int64_t new_tok_stride, int num_kv_heads, int head_dim,
                                        int block_size, int dtype, int32_t* dev_status, hipStream_t stream) {
-  if (!dtype_valid(dtype) || num_reqs < 0 || beam_width < 1 || bt_stride < 1) return GR_ERR_INVALID_ARG;
+  if (!cache_dtype_valid(dtype) || num_reqs < 0 || beam_width < 1 || bt_stride < 1) return GR_ERR_INVALID_ARG;
   if (beam_width > FORK_MAX_W) return GR_ERR_UNSUPPORTED;
   if (num_reqs == 0) return GR_OK;
   if (!parent || !bt_in || !len_in || !bt_out || !len_out) return GR_ERR_INVALID_ARG;
@@ -432,7 +472,7 @@ extern "C" gr_status_t gr_beam_kv_append(const void* k_new, const void* v_new, i
                                          const int32_t* suffix_bt, int bt_stride, int32_t* suffix_len,
                                          int num_beams, int num_kv_heads, int head_dim, int block_size, int dtype,
                                          int32_t* dev_status, hipStream_t stream) {
-  if (!dtype_valid(dtype) || num_beams < 0 || bt_stride < 1) return GR_ERR_INVALID_ARG;
+  if (!cache_dtype_valid(dtype) || num_beams < 0 || bt_stride < 1) return GR_ERR_INVALID_ARG;
   if (num_beams == 0) return GR_OK;
   if (!k_new || !v_new || !suffix_bt || !suffix_len) return GR_ERR_INVALID_ARG;
   KvGeom g = make_geom(k_cache, v_cache, num_blocks, kv_block_stride, kv_tok_stride, kv_head_stride,
@@ -468,6 +508,42 @@ extern "C" gr_status_t gr_reshape_and_cache(const void* key, int64_t key_tok_str
   hipLaunchKernelGGL(reshape_and_cache_k, dim3((unsigned)num_tokens), dim3(64), 0, stream,
                      static_cast<const uint8_t*>(key), key_tok_stride, static_cast<const uint8_t*>(value),
                      value_tok_stride, g, slot_mapping, num_tokens, dev_status);
+  return launch_status();
+}
+
+extern "C" gr_status_t gr_reshape_and_cache_fp8(const void* key, int64_t key_tok_stride, const void* value,
+                                                int64_t value_tok_stride, void* k_cache, void* v_cache,
+                                                int64_t num_blocks, int64_t kv_block_stride, int64_t kv_tok_stride,
+                                                int64_t kv_head_stride, const int64_t* slot_mapping,
+                                                int num_tokens, int num_kv_heads, int head_dim, int block_size,
+                                                int dtype, const float* k_scale, const float* v_scale,
+                                                int32_t* dev_status, hipStream_t stream) {
+  if (!dtype_valid(dtype) || num_tokens < 0) return GR_ERR_INVALID_ARG;
+  if (num_tokens == 0) return GR_OK;
+  if (!key || !value || !slot_mapping) return GR_ERR_INVALID_ARG;
+  KvGeom g = make_geom(k_cache, v_cache, num_blocks, kv_block_stride, kv_tok_stride, kv_head_stride,
+                       num_kv_heads, head_dim, block_size, GR_DTYPE_FP8_E4M3);
+  gr_status_t st = check_geom(g);  // cache rows 16-byte aligned: head_dim a multiple of 16
+  if (st != GR_OK) return st;
+  if (key_tok_stride < (int64_t)num_kv_heads * head_dim || value_tok_stride < (int64_t)num_kv_heads * head_dim)
+    return GR_ERR_INVALID_ARG;
+  switch (dtype) {
+    case GR_DTYPE_F32:
+      hipLaunchKernelGGL((reshape_and_cache_fp8_k<GR_DTYPE_F32>), dim3((unsigned)num_tokens), dim3(256), 0, stream,
+                         key, key_tok_stride, value, value_tok_stride, g, slot_mapping, num_tokens, k_scale,
+                         v_scale, dev_status);
+      break;
+    case GR_DTYPE_F16:
+      hipLaunchKernelGGL((reshape_and_cache_fp8_k<GR_DTYPE_F16>), dim3((unsigned)num_tokens), dim3(256), 0, stream,
+                         key, key_tok_stride, value, value_tok_stride, g, slot_mapping, num_tokens, k_scale,
+                         v_scale, dev_status);
+      break;
+    default:
+      hipLaunchKernelGGL((reshape_and_cache_fp8_k<GR_DTYPE_BF16>), dim3((unsigned)num_tokens), dim3(256), 0, stream,
+                         key, key_tok_stride, value, value_tok_stride, g, slot_mapping, num_tokens, k_scale,
+                         v_scale, dev_status);
+      break;
+  }
   return launch_status();
 }
 

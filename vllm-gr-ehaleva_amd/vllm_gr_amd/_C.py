@@ -31,6 +31,7 @@ GR_PRUNE_SCRATCH_BYTES = 16 << 20  # static scratch of gr_beam_prune_topk_noallo
 GR_DTYPE_F32 = 0
 GR_DTYPE_F16 = 1
 GR_DTYPE_BF16 = 2
+GR_DTYPE_FP8_E4M3 = 3  # KV-cache element type only
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -42,7 +43,8 @@ _SZ = ctypes.c_size_t
 class AttnOptions(ctypes.Structure):
     """gr_attn_options (include/gr_beam.h)."""
     _fields_ = [("window_left", ctypes.c_int), ("window_right", ctypes.c_int), ("causal", ctypes.c_int),
-                ("sinks", ctypes.c_void_p), ("alibi_slopes", ctypes.c_void_p)]
+                ("sinks", ctypes.c_void_p), ("alibi_slopes", ctypes.c_void_p),
+                ("kv_dtype", ctypes.c_int), ("k_scale", ctypes.c_void_p), ("v_scale", ctypes.c_void_p)]
 
 
 # name -> (restype, argtypes); mirrors include/gr_beam.h and include/gr_decoder.h one to one
@@ -98,6 +100,9 @@ SIGNATURES = {
     "gr_silu_mul": (_I, [_P, _L, _P, _L, _I, _I, _I, _P]),
     "gr_reshape_and_cache": (_I, [
         _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _I, _I, _I, _I, _P, _P,
+    ]),
+    "gr_reshape_and_cache_fp8": (_I, [
+        _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P,
     ]),
     "gr_beam_kv_fork": (_I, [
         _P, _I, _I, _P, _P, _P, _P, _I,

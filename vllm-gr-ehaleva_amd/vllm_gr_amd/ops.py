@@ -17,6 +17,23 @@ from . import _C
 
 _DTYPES = {torch.float32: _C.GR_DTYPE_F32, torch.float16: _C.GR_DTYPE_F16,
            torch.bfloat16: _C.GR_DTYPE_BF16}
+# KV-cache element types: an fp8 e4m3 cache as float8_e4m3fn, or as the raw
+# bytes (uint8) the engine allocates it as
+_FP8_CACHE = (torch.float8_e4m3fn, torch.uint8)
+
+
+def is_fp8_cache(t: torch.Tensor) -> bool:
+    return t.dtype in _FP8_CACHE
+
+
+def _cache_dtype_code(t: torch.Tensor) -> int:
+    return _C.GR_DTYPE_FP8_E4M3 if is_fp8_cache(t) else _dtype_code(t)
+
+
+def _scale_arg(name: str, t: torch.Tensor | None, dev) -> int | None:
+    if t is not None and (t.device != dev or t.dtype != torch.float32 or t.numel() != 1):
+        raise ValueError(f"{name} must be a one-element float32 tensor on the cache's device")
+    return _ptr(t)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -105,10 +122,13 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                      status: torch.Tensor | None = None, max_prefix_len: int | None = None,
                      split: bool = True, window: tuple[int, int] | None = None,
                      sinks: torch.Tensor | None = None,
-                     alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
+                     alibi_slopes: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
+                     v_scale: torch.Tensor | None = None) -> torch.Tensor:
     """BeamAttention decode step; see ``gr_beam_attn_decode`` / ``_ws`` / ``_opt``
     in gr_beam.h.  ``window`` (left, right), ``sinks`` and ``alibi_slopes``
-    are the optional features of ``gr_attn_options``.
+    are the optional features of ``gr_attn_options``; an fp8 e4m3 cache
+    (float8_e4m3fn or uint8) is read as ``e4m3 * k_scale`` / ``* v_scale``
+    (one-element float32 device tensors, None for 1.0).
 
     ``q``: ``[num_beams*q_per_beam, Hq, D]`` (token stride free, heads and dims
     contiguous).  Returns ``out`` (same shape/dtype as ``q``).  With ``split``
@@ -124,7 +144,8 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
         _need_i32(name, t)
     if suffix_start is not None:
         _need_i32("suffix_start", suffix_start)
-    if q.dtype != k_cache.dtype:
+    kv8 = is_fp8_cache(k_cache)
+    if q.dtype != k_cache.dtype and not kv8:
         raise ValueError("q and KV cache dtype must match")
     NT, Hq, D = q.shape
     NB, bs, Hkv, Dk = k_cache.shape
@@ -154,7 +175,7 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
             R, max_beams_per_req, N, q_per_beam, Hq, Hkv, D, bs, _dtype_code(q),
             float(scale), float(softcap or 0.0), _ptr(lse), _ptr(status))
     hint = int(max_prefix_len or 0)
-    opt = _attn_options(dev, Hq, window, True, sinks, alibi_slopes)
+    opt = _attn_options(dev, Hq, window, True, sinks, alibi_slopes, kv8, k_scale, v_scale)
     if opt is not None:
         code = _C.lib().gr_beam_attn_decode_opt(*args, hint, None, 0, ctypes.byref(opt), _stream(dev))
         _C.check("gr_beam_attn_decode_opt", code)
@@ -171,10 +192,12 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return out
 
 
-def _attn_options(dev, Hq: int, window, causal: bool, sinks, alibi_slopes):
+def _attn_options(dev, Hq: int, window, causal: bool, sinks, alibi_slopes, kv8: bool = False, k_scale=None,
+                  v_scale=None):
     """The gr_attn_options struct for the optional features, or None when
     none is set.  ``window`` = (left, right), -1 = unbounded; ``sinks`` /
-    ``alibi_slopes``: float32 [Hq] device tensors."""
+    ``alibi_slopes``: float32 [Hq] device tensors; ``kv8``: an fp8 e4m3
+    cache with its scales."""
     left, right = (-1, -1) if window is None else (int(window[0]), int(window[1]))
     if left < -1 or right < -1:
         raise ValueError("window bounds must be >= -1")
@@ -182,9 +205,11 @@ def _attn_options(dev, Hq: int, window, causal: bool, sinks, alibi_slopes):
         if t is not None and (t.device != dev or t.dtype != torch.float32 or t.shape != (Hq,)
                               or not t.is_contiguous()):
             raise ValueError(f"{name} must be a contiguous float32 [Hq] tensor on the query's device")
-    if left < 0 and right < 0 and causal and sinks is None and alibi_slopes is None:
+    ks, vs = _scale_arg("k_scale", k_scale, dev), _scale_arg("v_scale", v_scale, dev)
+    if left < 0 and right < 0 and causal and sinks is None and alibi_slopes is None and not kv8:
         return None
-    return _C.AttnOptions(left, right, 1 if causal else 0, _ptr(sinks), _ptr(alibi_slopes))
+    return _C.AttnOptions(left, right, 1 if causal else 0, _ptr(sinks), _ptr(alibi_slopes),
+                          _C.GR_DTYPE_FP8_E4M3 if kv8 else -1, ks if kv8 else None, vs if kv8 else None)
 
 
 _SPLIT_WS: dict = {}
@@ -210,7 +235,8 @@ def paged_attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
                        out: torch.Tensor | None = None, lse: torch.Tensor | None = None,
                        status: torch.Tensor | None = None, causal: bool = True,
                        window: tuple[int, int] | None = None, sinks: torch.Tensor | None = None,
-                       alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
+                       alibi_slopes: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
+                       v_scale: torch.Tensor | None = None) -> torch.Tensor:
     """Varlen attention of standard requests over the paged cache (causal, or
     over every key of the sequence with ``causal=False``); see
     ``gr_paged_attn_prefill`` / ``_opt`` in gr_beam.h.  ``q``: ``[num_tokens, Hq, D]``,
@@ -222,7 +248,8 @@ def paged_attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
         raise ValueError("q must be [tokens, Hq, D] with heads and dims contiguous")
     for name, t in (("block_table", block_table), ("query_start", query_start), ("seq_len", seq_len)):
         _need_i32(name, t)
-    if q.dtype != k_cache.dtype:
+    kv8 = is_fp8_cache(k_cache)
+    if q.dtype != k_cache.dtype and not kv8:
         raise ValueError("q and KV cache dtype must match")
     NT, Hq, D = q.shape
     NB, bs, Hkv, Dk = k_cache.shape
@@ -243,7 +270,7 @@ def paged_attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
             block_table.data_ptr(), block_table.shape[1], query_start.data_ptr(), seq_len.data_ptr(),
             R, NT, int(max_query_len), Hq, Hkv, D, bs, _dtype_code(q), float(scale), float(softcap or 0.0),
             _ptr(lse), _ptr(status))
-    opt = _attn_options(dev, Hq, window, causal, sinks, alibi_slopes)
+    opt = _attn_options(dev, Hq, window, causal, sinks, alibi_slopes, kv8, k_scale, v_scale)
     if opt is not None:
         code = _C.lib().gr_paged_attn_prefill_opt(*args, ctypes.byref(opt), _stream(dev))
         _C.check("gr_paged_attn_prefill_opt", code)
@@ -255,9 +282,12 @@ def paged_attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
 
 def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
                       v_cache: torch.Tensor, slot_mapping: torch.Tensor,
-                      status: torch.Tensor | None = None) -> None:
+                      status: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
+                      v_scale: torch.Tensor | None = None) -> None:
     """Scatter ``key/value [T, Hkv, D]`` into the paged cache by slot (the
-    ``reshape_and_cache_flash`` role, ``beam_attn.py:727-732``)."""
+    ``reshape_and_cache_flash`` role, ``beam_attn.py:727-732``).  Into an fp8
+    e4m3 cache each element is stored as e4m3(clamp(x / scale, -448, 448))
+    (``k_scale`` / ``v_scale``: one-element float32 tensors, None for 1.0)."""
     dev = _need_cuda(key, value, k_cache, v_cache, slot_mapping, status)
     if slot_mapping.dtype != torch.int64 or not slot_mapping.is_contiguous():
         raise ValueError("slot_mapping must be a contiguous int64 tensor")
@@ -268,9 +298,18 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
     if slot_mapping.numel() < T:
         raise ValueError("slot_mapping shorter than the number of tokens")
     NB, bs, Hk, Dk = k_cache.shape
-    if (Hk, Dk) != (Hkv, D) or key.dtype != k_cache.dtype or value.dtype != k_cache.dtype:
+    kv8 = is_fp8_cache(k_cache)
+    if (Hk, Dk) != (Hkv, D) or value.dtype != key.dtype or (key.dtype != k_cache.dtype and not kv8):
         raise ValueError("key/value do not match the KV cache")
     bstr, tstr, hstr = _cache_strides(k_cache, v_cache)
+    if kv8:
+        code = _C.lib().gr_reshape_and_cache_fp8(
+            key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0), k_cache.data_ptr(),
+            v_cache.data_ptr(), NB, bstr, tstr, hstr, slot_mapping.data_ptr(), T, Hkv, D, bs,
+            _dtype_code(key), _scale_arg("k_scale", k_scale, dev), _scale_arg("v_scale", v_scale, dev),
+            _ptr(status), _stream(dev))
+        _C.check("gr_reshape_and_cache_fp8", code)
+        return
     code = _C.lib().gr_reshape_and_cache(
         key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0), k_cache.data_ptr(),
         v_cache.data_ptr(), NB, bstr, tstr, hstr, slot_mapping.data_ptr(), T, Hkv, D, bs,
@@ -315,7 +354,7 @@ def beam_kv_fork(parent: torch.Tensor, bt_in: torch.Tensor, len_in: torch.Tensor
     code = _C.lib().gr_beam_kv_fork(
         parent.data_ptr(), R, W, bt_in.data_ptr(), len_in.data_ptr(), bt_out.data_ptr(),
         len_out.data_ptr(), bt_in.shape[1], k_cache.data_ptr(), v_cache.data_ptr(), NB, bstr, tstr,
-        hstr, _ptr(k_new), _ptr(v_new), new_stride, Hkv, D, bs, _dtype_code(k_cache), _ptr(status),
+        hstr, _ptr(k_new), _ptr(v_new), new_stride, Hkv, D, bs, _cache_dtype_code(k_cache), _ptr(status),
         _stream(dev))
     _C.check("gr_beam_kv_fork", code)
     return bt_out, len_out
@@ -338,7 +377,7 @@ def beam_kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tens
     code = _C.lib().gr_beam_kv_append(
         k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
         NB, bstr, tstr, hstr, suffix_bt.data_ptr(), suffix_bt.shape[1], suffix_len.data_ptr(), N,
-        Hkv, D, bs, _dtype_code(k_cache), _ptr(status), _stream(dev))
+        Hkv, D, bs, _cache_dtype_code(k_cache), _ptr(status), _stream(dev))
     _C.check("gr_beam_kv_append", code)
 
 

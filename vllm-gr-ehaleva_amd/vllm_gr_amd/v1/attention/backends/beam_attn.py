@@ -26,7 +26,9 @@ Kept from the reference (same names, argument meaning and error behaviour):
   the sliding window ((w-1, 0), or (w-1, w-1) for ENCODER_ONLY) and the
   sinks reach every kernel launch (``gr_attn_options``), and a non-causal
   batch (the encoder types) runs its standard rows over every key of their
-  sequence.  fp8 KV caches are rejected.
+  sequence.  An fp8 cache (``kv_cache_dtype`` "fp8" / "fp8_e4m3", stored as
+  float8_e4m3fn, :734-737, :801-804) is written as e4m3(x / scale) with the
+  layer's ``_k_scale`` / ``_v_scale`` and read as e4m3 * scale.
 
 Two mega-request layouts are accepted:
 
@@ -70,6 +72,9 @@ import torch
 from vllm_gr_amd import ops
 
 MEGA_DATA_VAR = contextvars.ContextVar("mega_data", default=None)
+
+
+FP8_KV_DTYPES = ("fp8", "fp8_e4m3")
 
 
 class AttentionType(str, Enum):
@@ -409,8 +414,13 @@ class BeamAttentionImpl:
             self.sliding_window = (sliding_window - 1, sliding_window - 1)
         else:
             self.sliding_window = (sliding_window - 1, 0)
-        if kv_cache_dtype not in ("auto", None):
+        if kv_cache_dtype not in ("auto", None) + FP8_KV_DTYPES:
             raise NotImplementedError(f"BeamAttention does not support kv_cache_dtype={kv_cache_dtype}.")
+        # an fp8 e4m3 cache (beam_attn.py:734-737): written with the layer's
+        # _k_scale / _v_scale (reshape_and_cache_flash, :727-732), read back
+        # scaled by them
+        self.kv_fp8 = kv_cache_dtype in FP8_KV_DTYPES
+        self._scales: dict = {}
         self.sinks = running_sinks
         if self.sinks is not None:
             assert self.sinks.shape[0] == num_heads, (
@@ -420,6 +430,26 @@ class BeamAttentionImpl:
         self.logits_soft_cap = float(logits_soft_cap or 0.0)
         self.attn_type = attn_type
         self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
+
+    def _kv_scales(self, layer, device):
+        """The layer's (_k_scale, _v_scale) as one-element float32 device
+        tensors (vLLM keeps them as tensors; floats and a missing layer are
+        accepted, 1.0 by default); None for a cache that is not fp8."""
+        if not self.kv_fp8:
+            return None, None
+        out = []
+        for name in ("_k_scale", "_v_scale"):
+            v = getattr(layer, name, None) if layer is not None else None
+            if isinstance(v, torch.Tensor) and v.device == device and v.dtype == torch.float32 and v.numel() == 1:
+                out.append(v.reshape(1))
+                continue
+            val = 1.0 if v is None else float(v)
+            key = (name, device, val)
+            t = self._scales.get(key)
+            if t is None:
+                t = self._scales[key] = torch.tensor([val], dtype=torch.float32, device=device)
+            out.append(t)
+        return out[0], out[1]
 
     def _options(self, device) -> dict:
         """The optional features as kernel arguments on ``device`` (float32
@@ -445,9 +475,10 @@ class BeamAttentionImpl:
             return output.fill_(0)
         k_cache, v_cache = ops.split_kv_cache(kv_cache)
         n = attn_metadata.num_actual_tokens
+        k_sc, v_sc = self._kv_scales(layer, query.device)
         if self.kv_sharing_target_layer_name is None and key is not None and value is not None:
             ops.reshape_and_cache(key[:n], value[:n], k_cache, v_cache, attn_metadata.slot_mapping,
-                                  status=attn_metadata.status)
+                                  status=attn_metadata.status, k_scale=k_sc, v_scale=v_sc)
         opts = self._options(query.device)
         # decode attention is causal over the beam's own tokens: its window has no right bound
         dec_window = None if opts["window"] is None else (opts["window"][0], -1)
@@ -459,7 +490,7 @@ class BeamAttentionImpl:
                                        scale=self.scale, softcap=self.logits_soft_cap,
                                        max_beams_per_req=g.max_beams, out=out, max_prefix_len=g.max_prefix_len,
                                        window=dec_window, sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"],
-                                       status=attn_metadata.status)
+                                       status=attn_metadata.status, k_scale=k_sc, v_scale=v_sc)
             if g.token_index is not None:
                 output.index_copy_(0, g.token_index, res)
         p = attn_metadata.prefill
@@ -474,7 +505,7 @@ class BeamAttentionImpl:
                                          max_query_len=p.max_query_len, scale=self.scale,
                                          softcap=self.logits_soft_cap, out=out, causal=causal, window=win,
                                          sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"],
-                                         status=attn_metadata.status)
+                                         status=attn_metadata.status, k_scale=k_sc, v_scale=v_sc)
             if p.token_index is not None:
                 output.index_copy_(0, p.token_index, res)
         return output
@@ -527,7 +558,7 @@ class BeamAttentionBackend:
 
     @classmethod
     def supports_kv_cache_dtype(cls, kv_cache_dtype: str | None) -> bool:
-        return kv_cache_dtype is None or kv_cache_dtype == "auto"
+        return kv_cache_dtype is None or kv_cache_dtype == "auto" or kv_cache_dtype in FP8_KV_DTYPES
 
     @classmethod
     def supports_sink(cls) -> bool:
