@@ -71,6 +71,28 @@ def test_prune_masked_logits(device):
     _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), 8))
 
 
+def test_prune_dead_rows(device):
+    """-inf cumulative scores (slots no candidate filled): every score of such
+    a row ties at -inf, so its candidate list (logit order) is not in flat
+    order.  Groups of 32 rows holding one are selected by radix select and
+    counting, the others by merging sorted lists, in the same launch."""
+    wl = workloads.make_prune(R=4, W=128, V=1024, k=128, seed=7)
+    wl.cum[1, 40:] = float("-inf")  # three of request 1's four row groups
+    wl.cum[2, 1:] = float("-inf")   # one live row: exactly k finite candidates
+    wl.cum[3, :] = float("-inf")    # none finite: the lowest flat indices win
+    _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), 128))
+
+
+def test_prune_rounding_collapse(device):
+    """Cumulative scores near -1e15 (float64 ulp 0.125): c + x rounds distinct
+    logits of a row to one score, whose ties go by token, not by the row's
+    logit order -- every group takes the radix-select path, with many ties."""
+    wl = workloads.make_prune(R=2, W=128, V=1024, k=128, seed=8)
+    g = torch.Generator().manual_seed(8)
+    wl.cum.copy_(torch.full_like(wl.cum, -1e15) - torch.randint(0, 4, wl.cum.shape, generator=g).float() * 2.0 ** 27)
+    _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), 128))
+
+
 def test_prune_catalog_matches_oracle(device):
     """Catalog-constrained pruning: each beam's top-k candidates outside its
     trie node's children leave the pool (serving_engine.py:504-506), bit for

@@ -850,7 +850,13 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
 // selects again (prune_merge_final).  A candidate of
 // the request's top-k is within its group's top-k under the same order, so
 // both stages together select what a single pass over all candidates does;
-// the work of stage 1 is spread over every request's groups.
+// the work of stage 1 is spread over every request's groups.  The rows' lists
+// arrive sorted, so stage 1 bounds the group's k-th score from below by the
+// k-th score of the MG_TOP_ROWS rows with the highest k-th entries (their
+// lists merged by a small tournament) and merges the few other entries at or
+// above it into that list by search; groups whose lists are out of flat
+// order, or with more rows or such entries than the tables hold, select by
+// radix select and counting.
 constexpr int MG_PART_PER_THREAD = 4;
 constexpr int MG_GROUP_CAND = MG_PART_PER_THREAD * MG_THREADS;
 
@@ -927,47 +933,261 @@ __device__ int merge_select(const uint64_t (&ck)[MPT], const int64_t (&cf)[MPT],
   return M < k ? M : k;
 }
 
+// floor(i / d) for 0 <= i < 2^20 and d >= 1: the float estimate is off by at
+// most one either way, which the two corrections remove.
+__device__ inline int div_small(int i, int d, float rcp) {
+  int q = (int)((float)i * rcp);
+  q += (q + 1) * d <= i;
+  q -= q * d > i;
+  return q;
+}
+
+// Entries of a list sorted by (key desc, position asc) that come before
+// (ke, ie): list entry j has key lk[j] and position li[j] (li null: position
+// j).  Branch-free lower bound; positions are read only at equal keys.
+__device__ inline int count_before(const uint64_t* lk, const unsigned short* li, int n, uint64_t ke, int ie) {
+  int b = 0;
+  while (n > 1) {
+    const int h = n >> 1;
+    const uint64_t kj = lk[b + h - 1];
+    bool bf = kj > ke;
+    if (kj == ke) bf = (li ? (int)li[b + h - 1] : b + h - 1) < ie;
+    b = bf ? b + h : b;
+    n -= h;
+  }
+  if (n == 1) {
+    const uint64_t kj = lk[b];
+    bool bf = kj > ke;
+    if (kj == ke) bf = (li ? (int)li[b] : b) < ie;
+    b += bf;
+  }
+  return b;
+}
+
+constexpr int MG_TOP_ROWS = 8;    // rows whose merged top-k bounds the group's k-th score
+constexpr int MG_MAX_ROWS = 128;  // rows a group may hold on the bounded path
+constexpr int MG_MAX_EXTRA = 64;  // other rows' entries at or above the bound, merged one by one
+
 __global__ __launch_bounds__(MG_THREADS) void prune_merge_part(PruneArgs a) {
-  __shared__ double cs[PR_MAXW];
+  __shared__ uint64_t mk[2][MG_GROUP_CAND];        // [0]: the group's keys by position; then merge lists
+  __shared__ unsigned short mi[2][MG_GROUP_CAND];  // position in the group of each merge-list entry
+  __shared__ int mtok[MG_GROUP_CAND];              // token of the group's candidate i
+  __shared__ uint64_t rowk[MG_MAX_ROWS];           // key of each row's k-th entry
+  __shared__ int top_row[MG_TOP_ROWS];
+  __shared__ unsigned char is_top[MG_MAX_ROWS];
+  __shared__ uint64_t xk[MG_MAX_EXTRA];
+  __shared__ int xi[MG_MAX_EXTRA];
   __shared__ int hist[PR_BINS];
   __shared__ uint64_t fkeys[PR_MAXK];
   __shared__ int64_t ffl[PR_MAXK];
   __shared__ int itmp[MG_THREADS / 64];
   __shared__ uint64_t kred[MG_THREADS / 64][2];
   __shared__ int sel[3];
+  __shared__ int unsorted, n_extra;
   constexpr int MPT = MG_PART_PER_THREAD;
   const int r = blockIdx.x / a.ng, g = blockIdx.x - r * a.ng;
   const int tid = threadIdx.x;
-  const int k1 = a.k1;
-  const int b0 = g * a.gr, b1 = min(a.W, b0 + a.gr);
-  const int n = (b1 - b0) * k1;  // <= MG_GROUP_CAND
+  const int k1 = a.k1, k = a.k;
+  const float rk1 = 1.0f / (float)k1;
+  const int b0 = g * a.gr, b1 = min(a.W, b0 + a.gr), nl = b1 - b0;
+  const int n = nl * k1;  // <= MG_GROUP_CAND
   const int64_t row0 = (int64_t)r * a.W + b0;
   const float* gx = a.cand_x + row0 * k1;
   const int32_t* gv = a.cand_v + row0 * k1;
-  for (int b = tid; b < b1 - b0; b += MG_THREADS) cs[b] = a.row_c[row0 + b];
-  __syncthreads();
-  // thread t: candidates i = MPT t .. MPT t + MPT - 1 of the group (row i / k1)
-  uint64_t ck[MPT];
-  int64_t cf[MPT];
-  const int i0 = MPT * tid;
+  // the bounded path: the k-th entry of a row exists and the rows fit the tables
+  const bool bounded = k <= k1 && nl <= MG_MAX_ROWS;
+  if (tid == 0) {
+    unsorted = 0;
+    n_extra = 0;
+  }
+  // thread t: candidates i = t + q NT of the group (row i / k1); every load
+  // is issued at a clamped index before any is used
+  int vq[MPT], bq[MPT];
+  float xq[MPT];
+  double cq[MPT];
 #pragma unroll
   for (int q = 0; q < MPT; ++q) {
-    const int i = i0 + q;
-    ck[q] = 0;
-    cf[q] = 0;
+    const int i = min(tid + q * MG_THREADS, n - 1);
+    bq[q] = div_small(i, k1, rk1);
+    vq[q] = gv[i];
+    xq[q] = gx[i];
+    cq[q] = a.row_c[row0 + bq[q]];
+  }
+  // pin every load ahead of the first use (else the compiler sinks the
+  // logit and row loads under the validity test: a second round trip)
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) __asm__ volatile("" ::"v"(xq[q]), "v"(cq[q]));
+  uint64_t ck[MPT];
+  int64_t cf[MPT];
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) {
+    const int i = tid + q * MG_THREADS;
+    const bool ok = i < n && vq[q] >= 0;
+    const double c = cq[q];
+    ck[q] = ok ? dkey(c == -INFINITY ? -INFINITY : ((double)xq[q] + c) + 0.0) : 0;  // -0 -> +0
+    cf[q] = ok ? (int64_t)(b0 + bq[q]) * a.V + vq[q] : 0;
     if (i < n) {
-      const int v = gv[i];
-      if (v >= 0) {
-        const int bl = i / k1;
-        const double c = cs[bl];
-        ck[q] = dkey(c == -INFINITY ? -INFINITY : ((double)gx[i] + c) + 0.0);  // -0 -> +0
-        cf[q] = (int64_t)(b0 + bl) * a.V + v;
+      mk[0][i] = ck[q];
+      mtok[i] = vq[q];
+      if (bounded && i - bq[q] * k1 == k - 1) rowk[bq[q]] = ck[q];
+    }
+  }
+  __syncthreads();
+  // The rows' lists are ranked by (logit desc, token asc), so with c + x
+  // monotone in x each is sorted by (score desc, flat asc) -- unless the
+  // float64 sum rounds two logits of a row to one score, or the row's score
+  // is -inf (all ties): then the order by flat is not the list order.  Check
+  // every adjacent pair of a row; empty entries (key 0) are at the tail.
+  // Meanwhile each row is ranked by its k-th key (ties: lower row first; one
+  // wave per row, a ballot per 64 rows) and the MG_TOP_ROWS best are marked.
+  const int T = min(MG_TOP_ROWS, nl);
+  {
+    bool bad = false;
+#pragma unroll
+    for (int q = 0; q < MPT; ++q) {
+      const int i = tid + q * MG_THREADS;
+      if (i + 1 < n && i + 1 != (bq[q] + 1) * k1) {
+        const uint64_t kb = mk[0][i + 1];
+        if (kb != 0 && (ck[q] < kb || (ck[q] == kb && vq[q] >= mtok[i + 1]))) bad = true;
+      }
+    }
+    if (bad) unsorted = 1;
+    if (bounded) {
+      const int wave = tid >> 6, lane = tid & 63;
+      for (int j = wave; j < nl; j += MG_THREADS / 64) {
+        const uint64_t bj = rowk[j];
+        int rank = 0;
+        for (int h = 0; h < nl; h += 64) {
+          const int jj = h + lane;
+          const uint64_t bo = jj < nl ? rowk[jj] : 0;
+          rank += __popcll(__ballot(jj < nl && (bo > bj || (bo == bj && jj < j))));
+        }
+        if (lane == 0) {
+          is_top[j] = rank < T;
+          if (rank < T) top_row[rank] = j;
+        }
       }
     }
   }
+  __syncthreads();
+  const int64_t o = ((int64_t)r * a.ng + g) * k;
+  if (bounded && unsorted == 0) {
+    // (1) the top-k of the MG_TOP_ROWS rows' union by a tournament of sorted
+    // lists: each level merges lists 2j and 2j+1, keeping the first k of each
+    // merge; entry e of list l goes to (its position in l) + (the entries of
+    // l's partner ordered before it, by binary search).  Ties of score go by
+    // group position, which is flat order in sorted rows.  The lists of a
+    // level have length L but the last (len_last).  Level 0 reads the top
+    // rows where they lie (positions implicit); with one top row it copies
+    // that row's first k.
+    int nt = T, L = k1, len_last = k1, cur = 1;
+    {
+      const int L2 = min(2 * k1, k);
+      for (int e = tid; e < T * k1; e += MG_THREADS) {
+        const int t = div_small(e, k1, rk1), p = e - t * k1, src = top_row[t] * k1 + p;
+        const uint64_t ke = mk[0][src];
+        int cnt = 0;
+        if ((t ^ 1) < T) {
+          const int pb = top_row[t ^ 1] * k1;
+          cnt = count_before(mk[0] + pb, nullptr, k1, ke, src - pb);
+        }
+        if (p + cnt < L2) {
+          mk[1][(t >> 1) * L2 + p + cnt] = ke;
+          mi[1][(t >> 1) * L2 + p + cnt] = (unsigned short)src;
+        }
+      }
+      len_last = (nt & 1) ? min(k1, k) : L2;
+      L = L2;
+      nt = (nt + 1) >> 1;
+      __syncthreads();
+    }
+    while (nt > 1) {
+      const int E = (nt - 1) * L + len_last, L2 = min(2 * L, k);
+      const float rL = 1.0f / (float)L;
+      const uint64_t* sk = mk[cur];
+      const unsigned short* si = mi[cur];
+      uint64_t* dk = mk[cur ^ 1];
+      unsigned short* di = mi[cur ^ 1];
+      for (int e = tid; e < E; e += MG_THREADS) {
+        const int l = div_small(e, L, rL), p = e - l * L, pl = l ^ 1;
+        const uint64_t ke = sk[e];
+        const int ie = si[e];
+        int cnt = 0;
+        if (pl < nt) {
+          const int pb = pl * L;
+          cnt = count_before(sk + pb, si + pb, pl == nt - 1 ? len_last : L, ke, ie);
+        }
+        if (p + cnt < L2) {
+          dk[(l >> 1) * L2 + p + cnt] = ke;
+          di[(l >> 1) * L2 + p + cnt] = (unsigned short)ie;
+        }
+      }
+      len_last = (nt & 1) ? min(len_last, k) : min(L + len_last, k);
+      L = L2;
+      nt = (nt + 1) >> 1;
+      cur ^= 1;
+      __syncthreads();
+    }
+    const int fl = min(len_last, k);  // entries of the merged list F
+    const uint64_t* fk = mk[cur];
+    const unsigned short* fi = mi[cur];
+    // (2) bound: F's k-th key is at most the group's k-th; the group's top-k
+    // is F plus the other rows' entries at or above it (the extras)
+    const uint64_t B = fl == k ? fk[k - 1] : 0;
+    {
+      int c = 0;
+#pragma unroll
+      for (int q = 0; q < MPT; ++q) c += ck[q] != 0 && ck[q] >= B && !is_top[bq[q]];
+      if (c > 0) {
+        int off = atomicAdd(&n_extra, c);
+#pragma unroll
+        for (int q = 0; q < MPT; ++q) {
+          if (ck[q] != 0 && ck[q] >= B && !is_top[bq[q]]) {
+            if (off < MG_MAX_EXTRA) {
+              xk[off] = ck[q];
+              xi[off] = tid + q * MG_THREADS;
+            }
+            ++off;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int nx = n_extra;
+    if (nx <= MG_MAX_EXTRA) {
+      // (3) ranks in F + extras: an F entry's position plus the extras before
+      // it; an extra's count of F entries before it (binary search) plus the
+      // extras before it
+      auto out = [&](int rank, uint64_t key, int pos) {
+        if (rank < k) {
+          a.part_key[o + rank] = key;
+          if (key != 0) a.part_flat[o + rank] = (int64_t)(b0 + div_small(pos, k1, rk1)) * a.V + mtok[pos];
+        }
+      };
+      if (tid < fl) {
+        const uint64_t ke = fk[tid];
+        const int ie = fi[tid];
+        int rank = tid;
+        for (int j = 0; j < nx; ++j) rank += xk[j] > ke || (xk[j] == ke && xi[j] < ie);
+        out(rank, ke, ie);
+      }
+      if (tid >= MG_THREADS - 64 && tid - (MG_THREADS - 64) < nx) {
+        const int x = tid - (MG_THREADS - 64);
+        const uint64_t ke = xk[x];
+        const int ie = xi[x];
+        int rank = count_before(fk, fi, fl, ke, ie);
+        for (int j = 0; j < nx; ++j) rank += xk[j] > ke || (xk[j] == ke && xi[j] < ie);
+        out(rank, ke, ie);
+      }
+      for (int i = fl + nx + tid; i < k; i += MG_THREADS) a.part_key[o + i] = 0;
+      return;
+    }
+  }
+  // rows out of flat order, too many rows or extras: radix select of the
+  // group's top-k, then ranking by counting
   bool take[MPT];
   int off;
-  const int nsel = merge_select<MG_THREADS, MPT>(ck, cf, a.k, (int64_t)a.W * a.V, take, off, hist, itmp, sel, kred);
+  const int nsel = merge_select<MG_THREADS, MPT>(ck, cf, k, (int64_t)a.W * a.V, take, off, hist, itmp, sel, kred);
 #pragma unroll
   for (int q = 0; q < MPT; ++q) {
     if (take[q]) {
@@ -981,7 +1201,6 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge_part(PruneArgs a) {
   // have key 0, below every score.  Rank of entry i = entries ordered before
   // it: wave w counts over the entries [w*Q, (w+1)*Q) for every target, lane
   // l holding targets l, l + 64, ...; the partial counts meet in LDS.
-  const int64_t o = ((int64_t)r * a.ng + g) * a.k;
   const int wave = tid >> 6, lane = tid & 63;
   for (int i = tid; i < nsel; i += MG_THREADS) hist[i] = 0;  // the histogram is dead: rank counters
   __syncthreads();
