@@ -6,7 +6,9 @@
 // it runs on MFMA.  A workgroup owns 128 of those rows (8 waves: 4 row groups
 // of 32 rows x 2 key halves, two waves per SIMD so one wave's matrix work
 // overlaps the other's softmax and loads) and streams the request's prefix
-// K/V through LDS in 64-key super-tiles, each loaded once for all 128 rows.
+// K/V through LDS in 64-key super-tiles, each loaded once for all 128 rows,
+// straight from global memory into LDS (global_load_lds_dwordx4: no register
+// staging, no LDS store instructions) two tiles ahead of the one computed.
 // Workgroups that share (r, h) are placed on the same XCD (blockIdx % 8 is
 // the XCD under round-robin dispatch) so their prefix re-reads hit that
 // XCD's L2.  Each beam's short suffix is read from its own paged blocks into
@@ -22,7 +24,8 @@
 // max/sum.  K rows are fed to the A operand through the permutation PI that
 // swaps bits 2 and 3 of the row index; with it the S^T accumulator registers
 // of each lane hold keys in exactly the order the PV B operand needs.  V stays
-// in its natural [key][d] layout in LDS and the V^T operand is assembled with
+// in its natural [key][d] layout in LDS (64-byte segments XOR-swizzled per
+// row, see vchunk) and the V^T operand is assembled with
 // gfx950's transposing LDS read (ds_read_b64_tr_b16): in each 16-lane group,
 // source lane s addresses V[k0 + s/4][d0 + 4*(s%4) .. +3] and lane i receives
 // V[k0 .. k0+3][d0 + i].
@@ -38,10 +41,10 @@ constexpr int MF_ROWS = 128;   // query rows per workgroup
 constexpr int ST_KEYS = 64;    // keys per super-tile (two 32-key halves)
 constexpr int HD = 128;        // head dim
 constexpr int KS_PITCH = 128;  // K tile row pitch in elements (256 B); 16-byte chunks XOR-swizzled
-constexpr int VS_PITCH = 160;  // V tile row pitch in elements (320 B): rows alternate 64-byte bank halves
+constexpr int VS_PITCH = 128;  // V tile row pitch in elements (256 B); 64-byte segments XOR-swizzled
 constexpr int K_TILE = ST_KEYS * KS_PITCH;
 constexpr int V_TILE = ST_KEYS * VS_PITCH;
-constexpr int BUF = K_TILE + V_TILE;  // elements per buffer
+constexpr int BUF = K_TILE + V_TILE;  // elements per buffer (32 KB)
 constexpr float LOG2E = 1.4426950408889634f;
 // Lazy softmax reference: a key may exceed the row's reference by up to
 // Rescale::THRESH log2 units before the exact path moves the reference; a lane
@@ -60,8 +63,9 @@ template <> struct Rescale<GR_DTYPE_F16> {
 static_assert(Rescale<GR_DTYPE_BF16>::SUM == (float)(1ull << 60) && Rescale<GR_DTYPE_F16>::SUM == (float)(1 << 15),
               "Rescale::SUM is 2^THRESH");
 constexpr int PBT_WIN = 2048;  // prefix block-table entries staged in LDS
-constexpr int NBUF = 3;        // prefix tile buffers (V of tile t, K of tile t+1, fill of tile t+2)
-constexpr int NBUF_ALLOC = 4;  // buffers allocated: a suffix tile pair takes four
+constexpr int NBUF = 4;        // tile buffers: prefix tile t in buffer t % 4 (V of t and K of t+1 read during
+                               // step t while tiles t+2 and t+3 land); a suffix tile pair takes all four
+constexpr int LOADS_PER_TILE = 4;  // direct-to-LDS loads each wave issues per prefix tile
 constexpr int SB_STAGE = 2;    // suffix block ids staged in LDS per beam (more are read from HBM)
 
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
@@ -104,6 +108,11 @@ __device__ inline int key_perm(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i
 // operand reads rows PI(0..7) = {0..3, 8..11} (and +4, +16) in one 8-lane
 // group; the XOR spreads those rows over 8 distinct 16-byte bank groups.
 __device__ inline int kchunk(int row, int c) { return c ^ ((row & 3) | (((row >> 3) & 1) << 2)); }
+// Physical 16-byte chunk of logical chunk c in V tile row `row`: the 64-byte
+// segment c >> 2 (32 dims) sits at segment (c >> 2) ^ (row & 3), so the four
+// rows that one half-wave of a transposing read touches (keys k0 .. k0 + 3,
+// 64 bytes each) cover all 64 banks.
+__device__ inline int vchunk(int row, int c) { return (((c >> 2) ^ (row & 3)) << 2) | (c & 3); }
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 // 4 keys x 1 dim per lane via the transposing LDS read (see the header comment)
@@ -207,6 +216,7 @@ template <int DT, int NH>
 __device__ inline void pv(const uint16_t* buf, int kbase, int lane, const u32x4_t (&p)[NH][2], f32x16_t (&o)[4]) {
   using M = Mma<DT>;
   const int g = lane >> 4, sl = lane & 15;
+  // every row this lane reads has row & 3 == sl >> 2: dim block mb sits in segment mb ^ (sl >> 2)
   const uint16_t* vsrc = buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
@@ -214,7 +224,7 @@ __device__ inline void pv(const uint16_t* buf, int kbase, int lane, const u32x4_
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        const uint16_t* vp = vsrc + (32 * h + 16 * kk) * VS_PITCH + 32 * mb;
+        const uint16_t* vp = vsrc + (32 * h + 16 * kk) * VS_PITCH + 32 * (mb ^ (sl >> 2));
         const uint2 lo = lds_read_tr(vp);
         const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
         o[mb] = M::mma(u32x4_t{lo.x, lo.y, hi.x, hi.y}, p[h][kk], o[mb]);
@@ -327,7 +337,7 @@ __device__ inline void phase_c1(const uint16_t* cur_buf, int kbase, int lane, co
   const int g = lane >> 4, sl = lane & 15;
   const uint16_t* vsrc = cur_buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
   auto vfrag = [&](int j) {
-    const uint16_t* vp = vsrc + (16 * (j >> 2)) * VS_PITCH + 32 * (j & 3);
+    const uint16_t* vp = vsrc + (16 * (j >> 2)) * VS_PITCH + 32 * ((j & 3) ^ (sl >> 2));
     const uint2 lo = lds_read_tr(vp);
     const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
     return u32x4_t{lo.x, lo.y, hi.x, hi.y};
@@ -342,6 +352,16 @@ __device__ inline void phase_c1(const uint16_t* cur_buf, int kbase, int lane, co
     o[j & 3] = M::mma(vf[j], p[0][j >> 2], o[j & 3]);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// Workgroup barrier once this wave's LDS reads are done and all but its newest
+// INFLIGHT direct-to-LDS tile loads have landed (the compiler does not see
+// those loads: the count is explicit).
+template <int INFLIGHT>
+__device__ inline void tile_barrier() {
+  static_assert(INFLIGHT == 0 || INFLIGHT == LOADS_PER_TILE, "one tile in flight at most");
+  if constexpr (INFLIGHT == LOADS_PER_TILE) __asm__ volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // One pipelined step with the exact path in line (phase A; the exact weights
@@ -371,7 +391,7 @@ __device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_b
 // normalised partial O and LSE to the workspace; split_merge combines them.
 template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF_ALLOC * BUF];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[NBUF * BUF];
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
   __shared__ int suf_info[2][4][32];     // per suffix tile and row group slot: (beam << 16) | j, or -1
   __shared__ int suf_s0[4][32];          // per row group beam: first suffix position
@@ -514,51 +534,6 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   if (tid == 0) hot_flag = 0;
   __syncthreads();
 
-  // loader roles: thread (lk, lc) moves keys 2*lk and 2*lk+1 (one block: the
-  // block size is a power of two >= 4), 16-byte chunk lc of K and of V.
-  const int lk = tid >> 4, lc = tid & 15;
-  u32x4_t kreg[2], vreg[2];
-  // block id of this thread's keys in the tile at k0 (read a step before the
-  // loads that use it, so the LDS latency hides behind a step's compute)
-  auto read_blk = [&](int k0) {
-    const int key0 = k0 + 2 * lk;
-    return key0 < P ? pbt_s[(key0 >> bsh) - win0] : -1;
-  };
-  // zero source of the last tile's loads
-  const S* zsrc = reinterpret_cast<const S*>(g_zero16);
-  // Element offset of this thread's first key in tile k0 (k0 is a multiple
-  // of 64): blk * block_stride + ((k0 & (bs-1)) + (2*lk & (bs-1))) * tok_stride
-  // + head + chunk; the first product is 32 x 32 bits (block strides below
-  // 2^32 elements: mfma_decode_supported), the second term is uniform.
-  const int64_t thr_off = (int64_t)((2 * lk) & (a.bs - 1)) * a.kv_tok_stride + head_off + lc * 8;
-  const uint32_t blk_stride = (uint32_t)a.kv_block_stride;
-  auto load_prefix_to = [&](int k0, int blk, u32x4_t (&kd)[2], u32x4_t (&vd)[2]) {
-    const int key0 = k0 + 2 * lk;
-    if (k0 + ST_KEYS <= P) {
-      // whole tile inside the prefix: no per-key test; an invalid block
-      // (flagged when the window was staged) reads block 0
-      const uint64_t off = (uint64_t)(uint32_t)max(blk, 0) * blk_stride +
-                           (uint64_t)(thr_off + (int64_t)(k0 & (a.bs - 1)) * a.kv_tok_stride);
-      const S* kp = kc + off;
-      const S* vp = vc + off;
-      kd[0] = *reinterpret_cast<const u32x4_t*>(kp);
-      kd[1] = *reinterpret_cast<const u32x4_t*>(kp + a.kv_tok_stride);
-      vd[0] = *reinterpret_cast<const u32x4_t*>(vp);
-      vd[1] = *reinterpret_cast<const u32x4_t*>(vp + a.kv_tok_stride);
-      return;
-    }
-    // the last tile: keys past the prefix or in an invalid block read a zero
-    // source, so every thread issues the same loads
-    const int64_t off = (int64_t)(blk < 0 ? 0 : blk) * a.kv_block_stride +
-                        (int64_t)(key0 & (a.bs - 1)) * a.kv_tok_stride + head_off + lc * 8;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const bool ok = blk >= 0 && key0 + j < P;
-      kd[j] = *reinterpret_cast<const u32x4_t*>(ok ? kc + off + j * a.kv_tok_stride : zsrc);
-      vd[j] = *reinterpret_cast<const u32x4_t*>(ok ? vc + off + j * a.kv_tok_stride : zsrc);
-    }
-  };
-  auto load_prefix = [&](int k0, int blk) { load_prefix_to(k0, blk, kreg, vreg); };
   // keep the window over [k0, k0 + 64); switching costs two barriers and
   // happens once per PBT_WIN blocks
   auto ensure_window = [&](int k0) {
@@ -570,38 +545,67 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       __syncthreads();
     }
   };
-  auto store_tile_from = [&](uint16_t* buf, const u32x4_t (&kd)[2], const u32x4_t (&vd)[2]) {
+  // zero source of loads past the prefix or the suffix
+  const S* zsrc = reinterpret_cast<const S*>(g_zero16);
+  // ---- prefix tile loads, straight from global memory into LDS
+  // (global_load_lds_dwordx4: no registers, no LDS store instructions).  Wave
+  // wv moves rows 8 wv .. 8 wv + 7 of a tile's K and of its V, four rows (1 KB
+  // of LDS) per instruction: lane i lands on row 8 wv + 4 j + (i >> 4),
+  // physical chunk i & 15, and fetches the logical chunk the swizzles put
+  // there.  Four rows never straddle a block (power-of-two block size >= 4),
+  // so each instruction has one wave-uniform base address.  Every wave issues
+  // exactly LOADS_PER_TILE loads per tile, tiles in order: the waits count on it.
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, pch = lane & 15;
+  const int ck = pch ^ (q4 | ((wv & 1) << 2));          // kchunk of rows 8 wv + 4 j + q4
+  const int cv = (((pch >> 2) ^ q4) << 2) | (pch & 3);  // vchunk of the same rows
+  const int64_t tok = a.kv_tok_stride;
+  const uint32_t vo_k = (uint32_t)((q4 * tok + ck * 8) * 2);
+  const uint32_t vo_v = (uint32_t)((q4 * tok + cv * 8) * 2);
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(lds);
+  const uint32_t blk_stride = (uint32_t)a.kv_block_stride;
+  // Prefix tile t of this workgroup's range into buffer buf: the wave-uniform
+  // addresses of its four loads (prep_tile, which may move the block-table
+  // window), then the loads one at a time (issue_load n: K of rows 8 wv + 4 j,
+  // then their V, j = n >> 1).  An invalid block (flagged when the window was
+  // staged) reads block 0 in a whole tile; rows past the prefix read the zero
+  // source.
+  struct TileLoads {
+    int64_t el[2];  // element offset of rows 8 wv + 4 j in the K and V caches
+    int key[2], blk[2];
+    uint32_t dst;  // LDS byte address of the wave's first K row
+  };
+  auto prep_tile = [&](int t, int buf) {
+    const int k0 = kb + t * ST_KEYS;
+    ensure_window(k0);
+    TileLoads L;
+    L.dst = lds0 + (uint32_t)(buf * BUF * 2) + (uint32_t)(wv * 8 * KS_PITCH * 2);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int row = 2 * lk + j;
-      *reinterpret_cast<u32x4_t*>(buf + row * KS_PITCH + kchunk(row, lc) * 8) = kd[j];
-      *reinterpret_cast<u32x4_t*>(buf + K_TILE + row * VS_PITCH + lc * 8) = vd[j];
+      const int key = k0 + 8 * wv + 4 * j;
+      const int blk = __builtin_amdgcn_readfirstlane(key < P ? pbt_s[(key >> bsh) - win0] : -1);
+      L.key[j] = key;
+      L.blk[j] = blk;
+      L.el[j] = (int64_t)((uint64_t)(uint32_t)max(blk, 0) * blk_stride) + (int64_t)(key & (a.bs - 1)) * tok + head_off;
+    }
+    return L;
+  };
+  auto issue_load = [&](const TileLoads& L, int n) {
+    const int j = n >> 1;
+    const bool isv = n & 1;
+    const uint32_t d = L.dst + (isv ? K_TILE * 2 : 0) + j * 1024;
+    const S* base = (isv ? vc : kc) + L.el[j];
+    if (L.key[j] + 4 <= P) {
+      dma_s(d, base, isv ? vo_v : vo_k);
+    } else {
+      const bool ok = L.blk[j] >= 0 && L.key[j] + q4 < P;
+      dma_v(d, ok ? base + q4 * tok + (isv ? cv : ck) * 8 : zsrc);
     }
   };
-  auto store_tile = [&](uint16_t* buf) { store_tile_from(buf, kreg, vreg); };
-  // LDS tile buffers: during step t a wave reads V of tile t and K of tile
-  // t+1, while tile t+2 (loaded into registers at the start of the step) is
-  // stored into its buffer at the end (tile t in buffer t % NBUF).  The
-  // first two tiles' loads are both issued before either is stored.
-  u32x4_t k1reg[2], v1reg[2];
-  // the first two tiles' block ids (a window move, if any, happens here, before
-  // the loads below)
-  ensure_window(kb);
-  const int blk0 = read_blk(kb);
-  ensure_window(kb + ST_KEYS);
-  const int blk1 = read_blk(kb + ST_KEYS);
-  // branch-free form of the first tiles' loads: keys past the prefix or in an
-  // invalid block read the zero source
-  auto load_first = [&](int k0, int blk, u32x4_t (&kd)[2], u32x4_t (&vd)[2]) {
-    const int key0 = k0 + 2 * lk;
-    const int64_t off = (int64_t)max(blk, 0) * a.kv_block_stride + (int64_t)(key0 & (a.bs - 1)) * a.kv_tok_stride +
-                        head_off + lc * 8;
+  auto issue_tile = [&](int t, int buf) {
+    const TileLoads L = prep_tile(t, buf);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const bool ok = blk >= 0 && key0 + j < P;
-      kd[j] = *reinterpret_cast<const u32x4_t*>(ok ? kc + off + j * a.kv_tok_stride : zsrc);
-      vd[j] = *reinterpret_cast<const u32x4_t*>(ok ? vc + off + j * a.kv_tok_stride : zsrc);
-    }
+    for (int n = 0; n < LOADS_PER_TILE; ++n) issue_load(L, n);
   };
   // second round trip: suffix metadata (needed first, by the slot table), Q,
   // then the first two tiles.  Suffix metadata: lane l < nbeams of the
@@ -629,8 +633,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     for (int kk = 0; kk < 8; ++kk) qf[kk] = *reinterpret_cast<const u32x4_t*>(row_ok ? src + kk * 16 : zq);
   }
 
-  load_first(kb, blk0, kreg, vreg);
-  load_first(kb + ST_KEYS, blk1, k1reg, v1reg);
+  // the first two tiles, into buffers 0 and 1
+  if (n_st > 0) issue_tile(0, 0);
+  if (n_st > 1) issue_tile(1, 1);
   int suf_len = 0, suf_incl = 0;  // this meta lane's validated suffix length, inclusive prefix sum
   if (ks == 0) {
     int len = 0;
@@ -690,35 +695,33 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       if (bad_blk) flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
     }
   }
-  if (n_st > 0) store_tile(lds);
-  if (n_st > 1) store_tile_from(lds + BUF, k1reg, v1reg);
-  int pf_blk = -1;  // block id for the next tile to load (tile it+2 at step it)
-  if (n_st > 2) {
-    ensure_window(kb + 2 * ST_KEYS);
-    pf_blk = read_blk(kb + 2 * ST_KEYS);
-  }
-  // Retire every prologue load (Q included) here: the main loop's first read
-  // of qf is otherwise preceded by a full vector-memory wait in every
-  // iteration, which also waits for the tile prefetch issued at its top.
+  // Retire every prologue load (Q and the first two tiles) here, with a wait
+  // the compiler sees: its own wait before the first read of qf would
+  // otherwise be a full vector-memory wait placed after the next tile load.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
+  if (n_st > 2) issue_tile(2, 2);
   f32x16_t s_cur = qk_half<DT>(lds, ks * 32, lane, qf);  // (stale LDS when n_st == 0: never used)
   // One step over a fully visible tile `it` (not the last): consumes its S^T
   // from s_in, leaves that of tile it+1 in s_out.  Keys of an invalid block
   // read as zero rows (the block was flagged when the window was staged).
+  // Tile t+3 goes out at the top of step t, into buffer (t+3) % 4: its
+  // previous tile, t-1, was last read in step t-1, before the barrier that
+  // ended it.
+  auto fetch_ahead = [&](int t) {
+    if (t + 3 < n_st) issue_tile(t + 3, (t + 3) % NBUF);
+  };
+  // The end of step t: tile t+2 (read from the next step on) has landed; tile
+  // t+3 may still be in flight.
+  auto step_barrier = [&](int t) {
+    if (t + 3 < n_st) tile_barrier<LOADS_PER_TILE>();
+    else tile_barrier<0>();
+  };
   auto prefix_step = [&](int it, const f32x16_t& s_in, f32x16_t& s_out) {
-    const int cur = it % NBUF, nxt = (it + 1) % NBUF, fill = (it + 2) % NBUF;
-    const bool fetch = it + 2 < n_st;
-    if (fetch) {
-      load_prefix(kb + (it + 2) * ST_KEYS, pf_blk);
-      if (it + 3 < n_st) {
-        ensure_window(kb + (it + 3) * ST_KEYS);
-        pf_blk = read_blk(kb + (it + 3) * ST_KEYS);
-      }
-    }
-    pipe_step<DT, SOFTCAP>(lds + cur * BUF, lds + nxt * BUF, ks * 32, lane, qf, s_in, s_out, o, st, c, cap);
-    if (fetch) store_tile(lds + fill * BUF);
-    __syncthreads();
+    fetch_ahead(it);
+    pipe_step<DT, SOFTCAP>(lds + (it % NBUF) * BUF, lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out,
+                           o, st, c, cap);
+    step_barrier(it);
   };
   // The last tile: no next tile; masked when only p_last of its keys exist.
   const int p_last = min(ST_KEYS, P - kb - (n_st - 1) * ST_KEYS);  // keys in the last tile (1 .. 64)
@@ -744,19 +747,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // recomputes its prefix range exactly (after the masked tiles).
   bool hot_seen = false;
   u32x4_t p[1][2];
-  auto fetch_ahead = [&](int t) {
-    if (t + 2 < n_st) {
-      load_prefix(kb + (t + 2) * ST_KEYS, pf_blk);
-      if (t + 3 < n_st) {
-        ensure_window(kb + (t + 3) * ST_KEYS);
-        pf_blk = read_blk(kb + (t + 3) * ST_KEYS);
-      }
-    }
-  };
   auto finish_step = [&](int t) {
     phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
-    if (t + 2 < n_st) store_tile(lds + ((t + 2) % NBUF) * BUF);
-    __syncthreads();
+    step_barrier(t);
   };
   // tile 0 (and S^T of tile 1): exact weights, O still zero
   auto peel = [&]() {
@@ -770,23 +763,22 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     s_cur = s_alt;
     it = 1;
   };
+  // One fast step over tile t (not the last): consumes its S^T from s_in and
+  // leaves that of tile t+1 in s_out.
+  auto fast_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
+    fetch_ahead(t);
+    hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((t + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p);
+    phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
+    step_barrier(t);
+  };
   // fast steps over tiles [it, t_end): S^T alternates between s_cur and s_alt
   auto fast_steps = [&](int t_end) {
     for (; it + 1 < t_end; it += 2) {
-      fetch_ahead(it);
-      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_cur, s_alt, st, c,
-                                        cap, p);
-      finish_step(it);
-      fetch_ahead(it + 1);
-      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 2) % NBUF) * BUF, ks * 32, lane, qf, s_alt, s_cur, st, c,
-                                        cap, p);
-      finish_step(it + 1);
+      fast_step(it, s_cur, s_alt);
+      fast_step(it + 1, s_alt, s_cur);
     }
     if (it < t_end) {
-      fetch_ahead(it);
-      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_cur, s_alt, st, c,
-                                        cap, p);
-      finish_step(it);
+      fast_step(it, s_cur, s_alt);
       s_cur = s_alt;
       ++it;
     }
@@ -808,14 +800,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     }
     if (hot_seen && lane == 0) hot_flag = 1;
     for (; it < n_st; ++it) {
-      const bool fetch = it + 2 < n_st;
-      if (fetch) {
-        load_prefix((it + 2) * ST_KEYS, pf_blk);
-        if (it + 3 < n_st) {
-          ensure_window((it + 3) * ST_KEYS);
-          pf_blk = read_blk((it + 3) * ST_KEYS);
-        }
-      }
+      fetch_ahead(it);
       uint32_t v = 0;
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr)
@@ -826,21 +811,14 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o);
       pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
       if (it + 1 < n_st) s_cur = qk_half<DT>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf);
-      if (fetch) store_tile(lds + ((it + 2) % NBUF) * BUF);
-      __syncthreads();
+      step_barrier(it);
     }
   } else {
     // the last two tiles take the general step
     if (n_st >= 3) peel();
     for (; it + 2 < n_st; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
-      fetch_ahead(it);
-      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_cur, s_alt, st, c,
-                                        cap, p);
-      finish_step(it);
-      fetch_ahead(it + 1);
-      hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((it + 2) % NBUF) * BUF, ks * 32, lane, qf, s_alt, s_cur, st, c,
-                                        cap, p);
-      finish_step(it + 1);
+      fast_step(it, s_cur, s_alt);
+      fast_step(it + 1, s_alt, s_cur);
     }
     if (hot_seen && lane == 0) hot_flag = 1;
     if (it + 1 < n_st) {
@@ -858,10 +836,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
     for (int t = 0; t < n_st; ++t) {
-      ensure_window(kb + t * ST_KEYS);
-      load_prefix(kb + t * ST_KEYS, read_blk(kb + t * ST_KEYS));
-      store_tile(lds);
-      __syncthreads();
+      issue_tile(t, 0);
+      tile_barrier<0>();
       const int nk = t == n_st - 1 ? p_last : ST_KEYS;
       uint32_t v = 0;
 #pragma unroll
@@ -952,7 +928,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       uint16_t* buf = lds + (2 * h + (grp >> 1)) * BUF;
       const int key = (grp & 1) * 32 + slot;
       *reinterpret_cast<u32x4_t*>(buf + key * KS_PITCH + kchunk(key, ch) * 8) = skv[i];
-      *reinterpret_cast<u32x4_t*>(buf + K_TILE + key * VS_PITCH + ch * 8) = svv[i];
+      *reinterpret_cast<u32x4_t*>(buf + K_TILE + key * VS_PITCH + vchunk(key, ch) * 8) = svv[i];
     }
   };
   auto suf_tag = [&](int t, int h, const int (&sinfo)[SUF_PER_THREAD]) {
