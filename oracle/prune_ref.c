@@ -30,7 +30,8 @@
  *   order; within each wave of 64 lanes, for mask = 32,16,8,4,2,1:
  *   a[l] = a[l] + a[l ^ mask]; finally S = (w0 + w1) + (w2 + w3).
  *
- * exp2_neg(t), t <= 0: 0 if t < -125; else k = rint(t), f = t - k (exact),
+ * exp2_neg(t), t <= 0: t = fmaxf(t, -126) (so -inf and NaN give 2^-126, a
+ *   normal float); k = rint(t), f = t - k (exact),
  *   p = Horner in f with fmaf over the degree-5 coefficients EXP2_C (a
  *   relative-error fit of 2^f on [-1/2, 1/2] with p(0) = 1, within 2.1 ulp), result =
  *   ldexpf(p, k).
@@ -60,7 +61,7 @@ static const double LN2_LO = 0x1.fdf473de6af28p-22;
 static const double SQRT_HALF = 0x1.6a09e667f3bcdp-1;
 
 float oracle_exp2_neg(float t) {
-  if (!(t >= -125.0f)) return 0.0f;
+  t = fmaxf(t, -126.0f);
   float k = rintf(t);
   float f = t - k;
   float p = EXP2_C[5];

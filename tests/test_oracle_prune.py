@@ -39,15 +39,17 @@ def _ulp32(x):
 
 
 def test_exp2_neg_accuracy():
-    ts = np.concatenate([np.linspace(-125, 0, 20001), -np.random.default_rng(0).random(5000) * 125,
-                         [0.0, -0.5, -1.0, -1e-7, -124.999]]).astype(np.float32)
+    ts = np.concatenate([np.linspace(-126, 0, 20001), -np.random.default_rng(0).random(5000) * 126,
+                         [0.0, -0.5, -1.0, -1e-7, -124.999, -125.5, -126.0]]).astype(np.float32)
     worst = 0.0
     for t in ts:
         got = op.exp2_neg(float(t))
         want = 2.0 ** float(t)
         worst = max(worst, abs(got - want) / float(_ulp32(want)))
     assert worst <= 4.0, worst
-    assert op.exp2_neg(-125.5) == 0.0 and op.exp2_neg(-1e30) == 0.0
+    # below -126 the argument is raised to -126: the result stays normal, 2^-126
+    assert op.exp2_neg(-1e30) == 2.0 ** -126 and op.exp2_neg(float("-inf")) == 2.0 ** -126
+    assert op.exp2_neg(-126.5) == 2.0 ** -126 and op.exp2_neg(float("nan")) == 2.0 ** -126
     assert op.exp2_neg(0.0) == 1.0
 
 

@@ -39,12 +39,13 @@ constexpr int MG_THREADS = 1024;               // merge workgroup
 typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 
 // ---- bit-exact numerics ------------------------------------------------------
-// exp2 of t <= 0: a degree-5 polynomial (Horner with fma; a relative-error fit
-// of 2^f on [-1/2, 1/2] with p(0) = 1, within 2.1 ulp) on the fractional part f = t - rint(t),
-// scaled by 2^rint(t).
+// exp2 of t <= 0: t is first raised to -126 (-inf and NaN included), so
+// k = rint(t) >= -126 and the result is a normal float (2^-126 at the floor,
+// invisible in a row sum >= 1); then a degree-5 polynomial (Horner with fma; a
+// relative-error fit of 2^f on [-1/2, 1/2] with p(0) = 1, within 2.1 ulp) on
+// the fractional part f = t - k, scaled by 2^k.
 __device__ inline float exp2_neg(float t) {
-  const bool zero = !(t >= -125.0f);  // a select, not a branch: the 32 chains interleave
-  t = zero ? 0.0f : t;
+  t = fmaxf(t, -126.0f);
   const float k = __builtin_rintf(t);
   const float f = t - k;
   float p = 0x1.5bbea6p-10f;
@@ -53,8 +54,7 @@ __device__ inline float exp2_neg(float t) {
   p = __builtin_fmaf(p, f, 0x1.ebf9bcp-3f);
   p = __builtin_fmaf(p, f, 0x1.62e42ap-1f);
   p = __builtin_fmaf(p, f, 0x1.000000p+0f);
-  const float e = __builtin_amdgcn_ldexpf(p, (int)k);
-  return zero ? 0.0f : e;
+  return __builtin_amdgcn_ldexpf(p, (int)k);
 }
 
 // natural log of s >= 1 in float64: s = mant * 2^e, mant in [sqrt(1/2), sqrt(2)),
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
       f32x4_t v = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
       if (c < nch && idx < V) v = *reinterpret_cast<const f32x4_t*>(xg + idx);
 #pragma unroll
-      for (int j = 0; j < PR_VEC; ++j) xr[c][j] = v[j] + 0.0f;  // -0 -> +0
+      for (int j = 0; j < PR_VEC; ++j) xr[c][j] = v[j];  // (-0 stays: only survivor keys are made canonical)
     }
   }
   auto valid = [&](int c) { return c * PR_CHUNK + PR_VEC * tid < V; };
@@ -534,7 +534,9 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   const int S = scnt;
   if (S <= PR_SURV && k1 <= PR_THREADS) {
     // the survivors as row keys (all distinct: the token is part of the key)
-    auto to_key = [](uint64_t raw) { return row_key(fkey(__builtin_bit_cast(float, (uint32_t)(raw >> 32))), (int)(uint32_t)raw); };
+    auto to_key = [](uint64_t raw) {  // (+ 0.0f: -0 orders as +0)
+      return row_key(fkey(__builtin_bit_cast(float, (uint32_t)(raw >> 32)) + 0.0f), (int)(uint32_t)raw);
+    };
 #pragma unroll
     for (int h = 0; h < PR_SURV / PR_THREADS; ++h) {
       const int i = tid + h * PR_THREADS;
@@ -569,6 +571,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
       }
     };
     if (S <= 128) partial(std::integral_constant<int, 2>{});
+    else if (S <= 192) partial(std::integral_constant<int, 3>{});
     else if (S <= 256) partial(std::integral_constant<int, 4>{});
     else partial(std::integral_constant<int, 8>{});
     __syncthreads();
