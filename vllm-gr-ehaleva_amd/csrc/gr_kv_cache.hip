@@ -3,13 +3,14 @@
 // All three kernels move K/V rows of head_dim elements in 16-byte vectors;
 // they are pure HBM copy work (no arithmetic), so the design goal is wide
 // coalesced accesses, balanced work and no serialisation:
-//  * beam_fork: one workgroup per child (W per request).  Every workgroup
-//    works out its request's whole plan in LDS from the read-only input
-//    tables: each parent's lowest child (kept in place), the copying children
-//    and their ranks, the childless parents they take over (the owners), and
-//    the prefix sums of the copy lengths.  The request's copy-on-write tokens,
-//    concatenated, are then split evenly over its W workgroups, so the copy
-//    work is spread over every workgroup whichever children copy.  Copy
+//  * beam_fork: one workgroup per two children (W/2 per request; one per
+//    child when W is odd).  Every workgroup works out its request's whole plan
+//    in LDS from the read-only input tables: each parent's lowest child (kept
+//    in place), the copying children and their ranks, the childless parents
+//    they take over (the owners), and the prefix sums of the copy lengths.
+//    The request's copy-on-write tokens, concatenated, are then split evenly
+//    over its workgroups, so the copy work is spread over every workgroup
+//    whichever children copy; each token's rows are resolved once.  Copy
 //    destinations are rows of childless parents, which nobody reads; sources
 //    are rows of parents with children, which nobody writes below their
 //    length; each child's own append goes to a position past every copied
@@ -27,13 +28,18 @@ constexpr int FORK_THREADS = 256;
 constexpr int FORK_MAX_W = 1024;
 constexpr int FORK_STAGE_BT = 2048;  // a request's whole block table is staged in LDS up to this many entries
 
-// the fork kernel's LDS, sized by the request width W (ints; the 64-bit masks
-// first): cow and free masks, group bases, par, first (later the copy
-// lengths), cnt, lens, owner_of, cpre (W + 1), the scan scratch, the staged
-// block table
+// Copy-on-write tokens a workgroup resolves per round: each token's source
+// and destination row offsets are worked out once (one search of the copy
+// prefix sums per token, not per vector) and staged in LDS.
+constexpr int FORK_TOK_CHUNK = 64;
+
+// the fork kernel's LDS, sized by the request width W (ints; the 64-bit words
+// first): cow and free masks, the staged token offsets, group bases, par,
+// first (later the copy lengths), cnt, lens, owner_of, cpre (W + 1), the scan
+// scratch, the staged block table
 __host__ __device__ inline int fork_lds_ints(int W, int S) {
   const int ng = (W + 63) >> 6;
-  return 4 * ng + 2 * (ng + 1) + 6 * W + 1 + 8 + 1 + (W * S <= FORK_STAGE_BT ? W * S : 0);
+  return 4 * ng + 4 * FORK_TOK_CHUNK + 2 * (ng + 1) + 6 * W + 1 + 8 + 1 + (W * S <= FORK_STAGE_BT ? W * S : 0);
 }
 constexpr int FORK_BATCH = 2;        // 16-byte K and V vectors per thread in flight
 
@@ -81,9 +87,10 @@ __device__ inline void block_scan(const int* v, int* out, int n, int* tmp) {
   __syncthreads();
 }
 
-// 8 waves per SIMD: every workgroup of a 2048-child batch resident at once
+// 8 waves per SIMD: every workgroup of a 2048-child batch resident at once.
+// Workgroup cg of request r owns children cg*cpw .. cg*cpw + cpw-1.
 __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
-    const int32_t* __restrict__ parent, int R, int W, const int32_t* __restrict__ bt_in,
+    const int32_t* __restrict__ parent, int R, int W, int cpw, const int32_t* __restrict__ bt_in,
     const int32_t* __restrict__ len_in, int32_t* __restrict__ bt_out, int32_t* __restrict__ len_out,
     int S, KvGeom g, const uint8_t* k_new, const uint8_t* v_new, int64_t new_tok_stride,
     int32_t* dev_status) {
@@ -91,7 +98,9 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
   const int ngroups = (W + 63) >> 6;
   uint64_t* cow_mask = reinterpret_cast<uint64_t*>(fork_lds);
   uint64_t* free_mask = cow_mask + ngroups;
-  int* cow_base = fork_lds + 4 * ngroups;
+  int64_t* tok_src = reinterpret_cast<int64_t*>(free_mask + ngroups);  // byte offset of a token's head-0 row, -1: skip
+  int64_t* tok_dst = tok_src + FORK_TOK_CHUNK;
+  int* cow_base = reinterpret_cast<int*>(tok_dst + FORK_TOK_CHUNK);
   int* free_base = cow_base + ngroups + 1;
   int* par = free_base + ngroups + 1;
   int* first = par + W;
@@ -103,19 +112,39 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
   int& bad = scan_tmp[8];
   int* bts = scan_tmp + 9;
   int* cplen = first;  // once the masks are built
-  const int r = blockIdx.x / W;
-  const int c = blockIdx.x - r * W;  // this workgroup's child
+  const int wpr = W / cpw;  // workgroups per request
+  const int r = blockIdx.x / wpr;
+  const int cg = blockIdx.x - r * wpr;  // this workgroup's group of children
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (r >= R) return;
-  const int64_t n_c = (int64_t)r * W + c;
   const int row_vecs = g.D * g.esize / 16;  // 16-byte vectors per (token, head) row
   const int tv = g.Hkv * row_vecs;          // 16-byte vectors per token, all heads
-  // the appended token's vectors, loaded before the tables are worked out
-  const bool pre_new = k_new && tv <= FORK_THREADS && tid < tv;
+  // the request's parents, lengths and (when small) block table first, then
+  // the appended tokens' vectors: the tables' wait does not include those
+  constexpr int PER = FORK_MAX_W / FORK_THREADS;
+  constexpr int BT_PER = FORK_STAGE_BT / FORK_THREADS;
+  const bool all_staged = W * S <= FORK_STAGE_BT;
+  int pv[PER], lv[PER], bv[BT_PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = tid + u * FORK_THREADS;
+    pv[u] = i < W ? parent[(int64_t)r * W + i] : 0;
+    lv[u] = i < W ? len_in[(int64_t)r * W + i] : 0;
+  }
+#pragma unroll
+  for (int u = 0; u < BT_PER; ++u) {
+    const int j = tid + u * FORK_THREADS;
+    bv[u] = all_staged && j < W * S ? bt_in[(int64_t)r * W * S + j] : 0;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // thread tid appends vector tid % tv of child cg*cpw + tid / tv (when the
+  // group's appended tokens fit one vector per thread)
+  const bool pre_new = k_new && tv * cpw <= FORK_THREADS && tid < tv * cpw;
+  const int aq = tid / tv, ae = tid - (tid / tv) * tv;
+  const int nh = ae / row_vecs, nvec = ae - (ae / row_vecs) * row_vecs;
   u32x4_t knew{}, vnew{};
-  const int nh = tid / row_vecs, nvec = tid - (tid / row_vecs) * row_vecs;
   if (pre_new) {
-    const int64_t src = (n_c * new_tok_stride + (int64_t)nh * g.D) * g.esize + nvec * 16;
+    const int64_t src = (((int64_t)r * W + cg * cpw + aq) * new_tok_stride + (int64_t)nh * g.D) * g.esize + nvec * 16;
     knew = *reinterpret_cast<const u32x4_t*>(k_new + src);
     vnew = *reinterpret_cast<const u32x4_t*>(v_new + src);
   }
@@ -124,22 +153,21 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
     first[i] = W;
     cnt[i] = 0;
   }
-  // the request's parents, lengths and (when small) block table in one round trip
-  const bool all_staged = W * S <= FORK_STAGE_BT;
-  int pv[FORK_MAX_W / FORK_THREADS];
 #pragma unroll
-  for (int u = 0; u < FORK_MAX_W / FORK_THREADS; ++u) {
+  for (int u = 0; u < PER; ++u) {
     const int i = tid + u * FORK_THREADS;
-    if (i < W) {
-      pv[u] = parent[(int64_t)r * W + i];
-      lens[i] = len_in[(int64_t)r * W + i];
+    if (i < W) lens[i] = lv[u];
+  }
+  if (all_staged) {
+#pragma unroll
+    for (int u = 0; u < BT_PER; ++u) {
+      const int j = tid + u * FORK_THREADS;
+      if (j < W * S) bts[j] = bv[u];
     }
   }
-  if (all_staged)
-    for (int j = tid; j < W * S; j += FORK_THREADS) bts[j] = bt_in[(int64_t)r * W * S + j];
   __syncthreads();
 #pragma unroll
-  for (int u = 0; u < FORK_MAX_W / FORK_THREADS; ++u) {
+  for (int u = 0; u < PER; ++u) {
     const int i = tid + u * FORK_THREADS;
     if (i < W) {
       int p = pv[u];
@@ -155,9 +183,12 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
   __syncthreads();
   const bool req_bad = bad != 0;
   if (req_bad) {  // a request with a bad parent keeps its tables
-    if (c == 0 && tid == 0) flag_status(dev_status, GR_DEV_BAD_PARENT);
-    for (int j = tid; j < S; j += FORK_THREADS) bt_out[n_c * S + j] = bt_in[n_c * S + j];
-    if (tid == 0) len_out[n_c] = lens[c];
+    if (cg == 0 && tid == 0) flag_status(dev_status, GR_DEV_BAD_PARENT);
+    for (int q = 0; q < cpw; ++q) {
+      const int64_t n_c = (int64_t)r * W + cg * cpw + q;
+      for (int j = tid; j < S; j += FORK_THREADS) bt_out[n_c * S + j] = bt_in[n_c * S + j];
+      if (tid == 0) len_out[n_c] = lens[cg * cpw + q];
+    }
     return;
   }
   // per 64-entry group: the children that copy (not their parent's lowest
@@ -195,9 +226,9 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
   }
   __syncthreads();
   const int cap = S * g.bs;
-  int own_i[FORK_MAX_W / FORK_THREADS];
+  int own_i[PER];
 #pragma unroll
-  for (int u = 0; u < FORK_MAX_W / FORK_THREADS; ++u) {
+  for (int u = 0; u < PER; ++u) {
     const int i = tid + u * FORK_THREADS;
     own_i[u] = 0;
     if (i < W) {
@@ -210,73 +241,71 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
   }
   __syncthreads();
 #pragma unroll
-  for (int u = 0; u < FORK_MAX_W / FORK_THREADS; ++u) {
+  for (int u = 0; u < PER; ++u) {
     const int i = tid + u * FORK_THREADS;
     if (i < W) owner_of[i] = own_i[u];
   }
   block_scan(cplen, cpre, W, scan_tmp);  // (its barriers publish owner_of too)
-  const int p = par[c];
-  const int owner = owner_of[c];  // beam whose old row child c receives
-  const int64_t n_o = (int64_t)r * W + owner;
-  for (int j = tid; j < S; j += FORK_THREADS) bt_out[n_c * S + j] = all_staged ? bts[owner * S + j] : bt_in[n_o * S + j];
-  int len = lens[p];
-  if (len < 0 || len > cap) {
-    if (tid == 0) flag_status(dev_status, GR_DEV_BAD_LENGTH);
-    len = len < 0 ? 0 : cap;
-  }
   auto row_blk = [&](int row, int bi) -> int {
     return all_staged ? bts[row * S + bi] : bt_in[((int64_t)r * W + row) * S + bi];
   };
   uint8_t* kc = static_cast<uint8_t*>(g.k_cache);
   uint8_t* vc = static_cast<uint8_t*>(g.v_cache);
-  // ---- this child's appended token, at its row's length (before the copies:
-  // its position lies past every copied range of the row)
-  int new_len = len;
-  if (k_new) {
-    if (len < cap) {
-      const int bdst = row_blk(owner, len / g.bs);
-      if (bdst >= 0 && bdst < g.num_blocks) {
-        if (tv <= FORK_THREADS) {
-          if (pre_new) {
-            const int64_t dof = kv_byte_off(g, bdst, len % g.bs, nh) + nvec * 16;
-            *reinterpret_cast<u32x4_t*>(kc + dof) = knew;
-            *reinterpret_cast<u32x4_t*>(vc + dof) = vnew;
-          }
-        } else {
-          for (int e = tid; e < tv; e += FORK_THREADS) {
-            const int h = e / row_vecs, vec = e - h * row_vecs;
-            const int64_t src = (n_c * new_tok_stride + (int64_t)h * g.D) * g.esize + vec * 16;
-            const int64_t dof = kv_byte_off(g, bdst, len % g.bs, h) + vec * 16;
-            *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(k_new + src);
-            *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(v_new + src);
-          }
-        }
-        new_len = len + 1;
-      } else if (tid == 0) {
-        flag_status(dev_status, GR_DEV_BAD_BLOCK);
-      }
-    } else if (tid == 0) {
-      flag_status(dev_status, GR_DEV_SUFFIX_FULL);
+  // ---- each child of the group: its new table row, its appended token at
+  // its row's length (past every copied range of the row), its new length
+  for (int q = 0; q < cpw; ++q) {
+    const int c = cg * cpw + q;
+    const int64_t n_c = (int64_t)r * W + c;
+    const int owner = owner_of[c];  // beam whose old row child c receives
+    const int64_t n_o = (int64_t)r * W + owner;
+    for (int j = tid; j < S; j += FORK_THREADS) bt_out[n_c * S + j] = all_staged ? bts[owner * S + j] : bt_in[n_o * S + j];
+    int len = lens[par[c]];
+    if (len < 0 || len > cap) {
+      if (tid == 0) flag_status(dev_status, GR_DEV_BAD_LENGTH);
+      len = len < 0 ? 0 : cap;
     }
+    int new_len = len;
+    if (k_new) {
+      if (len < cap) {
+        const int bdst = row_blk(owner, len / g.bs);
+        if (bdst >= 0 && bdst < g.num_blocks) {
+          if (tv * cpw <= FORK_THREADS) {
+            if (pre_new && aq == q) {
+              const int64_t dof = kv_byte_off(g, bdst, len % g.bs, nh) + nvec * 16;
+              *reinterpret_cast<u32x4_t*>(kc + dof) = knew;
+              *reinterpret_cast<u32x4_t*>(vc + dof) = vnew;
+            }
+          } else {
+            for (int e = tid; e < tv; e += FORK_THREADS) {
+              const int h = e / row_vecs, vec = e - h * row_vecs;
+              const int64_t src = (n_c * new_tok_stride + (int64_t)h * g.D) * g.esize + vec * 16;
+              const int64_t dof = kv_byte_off(g, bdst, len % g.bs, h) + vec * 16;
+              *reinterpret_cast<u32x4_t*>(kc + dof) = *reinterpret_cast<const u32x4_t*>(k_new + src);
+              *reinterpret_cast<u32x4_t*>(vc + dof) = *reinterpret_cast<const u32x4_t*>(v_new + src);
+            }
+          }
+          new_len = len + 1;
+        } else if (tid == 0) {
+          flag_status(dev_status, GR_DEV_BAD_BLOCK);
+        }
+      } else if (tid == 0) {
+        flag_status(dev_status, GR_DEV_SUFFIX_FULL);
+      }
+    }
+    if (tid == 0) len_out[n_c] = new_len;
   }
-  // ---- this workgroup's share of the request's copy-on-write tokens
+  // ---- this workgroup's share of the request's copy-on-write tokens, in
+  // rounds of FORK_TOK_CHUNK tokens: one thread per token finds its copying
+  // child and block ids, then the round's vectors move
   const int total = cpre[W];
-  const int e0 = (int)((int64_t)total * c / W), e1 = (int)((int64_t)total * (c + 1) / W);
-  const int items = (e1 - e0) * tv;
-  if (items > 0 && g.num_blocks > 0) {
+  const int e0 = (int)((int64_t)total * cg / wpr), e1 = (int)((int64_t)total * (cg + 1) / wpr);
+  if (g.num_blocks > 0) {
 #pragma unroll 1
-    for (int i0 = tid; i0 < items; i0 += FORK_THREADS * FORK_BATCH) {
-      u32x4_t kb[FORK_BATCH], vb[FORK_BATCH];
-      int64_t dof[FORK_BATCH];
-      bool ok[FORK_BATCH];
-#pragma unroll
-      for (int u = 0; u < FORK_BATCH; ++u) {
-        const int it = i0 + u * FORK_THREADS;
-        ok[u] = false;
-        dof[u] = 0;
-        if (it >= items) continue;
-        const int e = e0 + it / tv, rem = it - (it / tv) * tv;
-        const int h = rem / row_vecs, vec = rem - h * row_vecs;
+    for (int t0 = e0; t0 < e1; t0 += FORK_TOK_CHUNK) {
+      const int nt = min(FORK_TOK_CHUNK, e1 - t0);
+      __syncthreads();  // the previous round's readers of tok_src / tok_dst are done
+      if (tid < nt) {
+        const int e = t0 + tid;
         int lo = 0, hi = W - 1;  // the copying child whose range holds e (skips empty ranges)
         while (lo < hi) {
           const int mid = (lo + hi + 1) >> 1;
@@ -286,23 +315,40 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
         const int bi = pos / g.bs, off = pos - bi * g.bs;
         const int bsrc = row_blk(par[lo], bi), bdst = row_blk(owner_of[lo], bi);
         const bool valid = bsrc >= 0 && bsrc < g.num_blocks && bdst >= 0 && bdst < g.num_blocks;
-        ok[u] = valid;
         if (!valid) flag_status(dev_status, GR_DEV_BAD_BLOCK);
-        const int64_t so = kv_byte_off(g, valid ? bsrc : 0, off, h) + vec * 16;
-        dof[u] = kv_byte_off(g, valid ? bdst : 0, off, h) + vec * 16;
-        kb[u] = *reinterpret_cast<const u32x4_t*>(kc + so);
-        vb[u] = *reinterpret_cast<const u32x4_t*>(vc + so);
+        tok_src[tid] = valid ? kv_byte_off(g, bsrc, off, 0) : -1;
+        tok_dst[tid] = valid ? kv_byte_off(g, bdst, off, 0) : -1;
       }
+      __syncthreads();
+      const int items = nt * tv;
+#pragma unroll 1
+      for (int i0 = tid; i0 < items; i0 += FORK_THREADS * FORK_BATCH) {
+        u32x4_t kb[FORK_BATCH], vb[FORK_BATCH];
+        int64_t dof[FORK_BATCH];
+        bool ok[FORK_BATCH];
 #pragma unroll
-      for (int u = 0; u < FORK_BATCH; ++u) {
-        if (ok[u]) {
-          *reinterpret_cast<u32x4_t*>(kc + dof[u]) = kb[u];
-          *reinterpret_cast<u32x4_t*>(vc + dof[u]) = vb[u];
+        for (int u = 0; u < FORK_BATCH; ++u) {
+          const int it = i0 + u * FORK_THREADS;
+          const int tk = it / tv, rem = it - (it / tv) * tv;
+          const int h = rem / row_vecs, vec = rem - (rem / row_vecs) * row_vecs;
+          const int64_t so = it < items ? tok_src[tk] : -1;
+          ok[u] = so >= 0;
+          const int64_t hoff = (int64_t)h * g.head_stride * g.esize + vec * 16;
+          dof[u] = ok[u] ? tok_dst[tk] + hoff : 0;
+          const int64_t sof = ok[u] ? so + hoff : 0;
+          kb[u] = *reinterpret_cast<const u32x4_t*>(kc + sof);
+          vb[u] = *reinterpret_cast<const u32x4_t*>(vc + sof);
+        }
+#pragma unroll
+        for (int u = 0; u < FORK_BATCH; ++u) {
+          if (ok[u]) {
+            *reinterpret_cast<u32x4_t*>(kc + dof[u]) = kb[u];
+            *reinterpret_cast<u32x4_t*>(vc + dof[u]) = vb[u];
+          }
         }
       }
     }
   }
-  if (tid == 0) len_out[n_c] = new_len;
 }
 
 // One 64-lane wave per beam: append its token at suffix_len[n], then bump it.
@@ -459,8 +505,13 @@ extern "C" gr_status_t gr_beam_kv_fork(const int32_t* parent, int num_reqs, int 
     return GR_ERR_INVALID_ARG;
   if ((int64_t)num_reqs * beam_width > INT32_MAX) return GR_ERR_INVALID_ARG;
   const size_t lds = sizeof(int) * (size_t)fork_lds_ints(beam_width, bt_stride);
-  hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * beam_width)), dim3(FORK_THREADS), lds, stream, parent,
-                     num_reqs, beam_width, bt_in, len_in, bt_out, len_out, bt_stride, g,
+  // children per workgroup: two when the width allows and both appended
+  // tokens fit one 16-byte vector per thread (half the workgroups to launch,
+  // half the plans worked out)
+  const int tv = num_kv_heads * (head_dim * dtype_size(dtype) / 16);
+  const int cpw = beam_width % 2 == 0 && 2 * tv <= FORK_THREADS ? 2 : 1;
+  hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * (beam_width / cpw))), dim3(FORK_THREADS), lds, stream,
+                     parent, num_reqs, beam_width, cpw, bt_in, len_in, bt_out, len_out, bt_stride, g,
                      static_cast<const uint8_t*>(k_new), static_cast<const uint8_t*>(v_new), new_tok_stride,
                      dev_status);
   return launch_status();
