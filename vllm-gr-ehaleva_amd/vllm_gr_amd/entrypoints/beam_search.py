@@ -25,6 +25,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import ops
+from ..tracing import roctx_range
 
 
 @dataclass
@@ -70,8 +71,10 @@ def prune_step(logits: torch.Tensor, cum_logprob: torch.Tensor, beam_width: int,
     (vllm_gr/entrypoints/llm.py:203-220).  ``status``: a device status
     word (``ops.new_status``) the kernels OR table errors into."""
     eos = -1 if eos_token_id is None else int(eos_token_id)
-    out = list(ops.beam_prune_topk(logits, cum_logprob, beam_width, eos, workspace=workspace, catalog=catalog,
-                                   beam_node=beam_node, candidates=candidates, status=status))
+    with roctx_range("beam_prune_topk"):
+        out = list(ops.beam_prune_topk(logits, cum_logprob, beam_width, eos, workspace=workspace,
+                                       catalog=catalog, beam_node=beam_node, candidates=candidates,
+                                       status=status))
     ct = cl = None
     if candidates:
         ct, cl = out[-2], out[-1]
@@ -115,5 +118,6 @@ def beam_search_step(table, logits: torch.Tensor, cum_logprob: torch.Tensor, kv_
                      candidates=candidates, status=status)
     parent = torch.where(res.parent >= 0, res.parent,
                          torch.arange(W, device=res.parent.device, dtype=res.parent.dtype)[None])
-    table.fork(parent, kv_caches, status=status)
+    with roctx_range("beam_kv_fork"):
+        table.fork(parent, kv_caches, status=status)
     return res

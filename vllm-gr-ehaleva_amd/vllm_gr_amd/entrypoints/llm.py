@@ -31,6 +31,7 @@ import torch
 
 from .. import logprobs as lpm
 from .. import ops
+from ..tracing import roctx_range
 from ..v1.beam_kv import BeamKVTable
 from ..v1.sid_decoder import SID_DECODER_1P7B, DecoderConfig, SidDecoder, init_weights
 from ..v1.sid_runner import SidModelRunner
@@ -185,7 +186,8 @@ class LLM:
                     sblocks = self.runner.pool.allocate(R * W * per_beam)
                     blocks += sblocks
                     sbt = torch.tensor(sblocks, dtype=torch.int32).view(R * W, per_beam).to(dev)
-                logits, prefix_bt, prefix_len, pblocks = self.runner.prefill(toks, rids)
+                with roctx_range("LLM.beam_search prefill"):
+                    logits, prefix_bt, prefix_len, pblocks = self.runner.prefill(toks, rids)
                 blocks += [b for bl in pblocks for b in bl]
                 ev.append(torch.cuda.Event(enable_timing=True))
                 ev[-1].record(stream)
@@ -204,7 +206,8 @@ class LLM:
                 table = None if sbt is None else BeamKVTable(prefix_bt, prefix_len, W, sbt, block_size=bs)
                 for s in range(1, steps):
                     tok = res.token.clamp(min=0).view(-1).to(torch.int64)
-                    logits = self.runner.decode(table, tok, rids, lens, step=s - 1)
+                    with roctx_range(f"LLM.beam_search decode step {s}"):
+                        logits = self.runner.decode(table, tok, rids, lens, step=s - 1)
                     table.advance()
                     if self.logits_hook is not None:
                         self.logits_hook(s, logits, hist)

@@ -70,6 +70,7 @@ from enum import Enum
 import torch
 
 from vllm_gr_amd import ops
+from vllm_gr_amd.tracing import roctx_range
 
 MEGA_DATA_VAR = contextvars.ContextVar("mega_data", default=None)
 
@@ -173,6 +174,11 @@ class BeamAttentionMetadataBuilder:
 
     def build(self, common_prefix_len: int, common_attn_metadata: CommonAttentionMetadata,
               fast_build: bool = False) -> BeamAttentionMetadata:
+        # one roctx range per build, where the reference has its NVTX range (beam_attn.py:486, :526)
+        with roctx_range("BeamAttentionMetadataBuilder.build"):
+            return self._build(common_prefix_len, common_attn_metadata)
+
+    def _build(self, common_prefix_len: int, common_attn_metadata: CommonAttentionMetadata) -> BeamAttentionMetadata:
         m = common_attn_metadata
         info = MEGA_DATA_VAR.get()
         mega_data = info["mega_data"] if info else {}
@@ -468,6 +474,12 @@ class BeamAttentionImpl:
                 kv_cache: torch.Tensor, attn_metadata: BeamAttentionMetadata | None,
                 output: torch.Tensor | None = None, output_scale: torch.Tensor | None = None,
                 output_block_scale: torch.Tensor | None = None) -> torch.Tensor:
+        with roctx_range("BeamAttentionImpl.forward"):
+            return self._forward(layer, query, key, value, kv_cache, attn_metadata, output, output_scale,
+                                 output_block_scale)
+
+    def _forward(self, layer, query, key, value, kv_cache, attn_metadata, output, output_scale,
+                 output_block_scale) -> torch.Tensor:
         assert output is not None, "Output tensor must be provided."
         if output_scale is not None or output_block_scale is not None:
             raise NotImplementedError("fused output quantization is not yet supported for BeamAttentionImpl")
