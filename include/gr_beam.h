@@ -284,6 +284,27 @@ gr_status_t gr_beam_kv_fork(
     int32_t* dev_status, hipStream_t stream);
 
 /*
+ * gr_beam_kv_fork over every layer's cache in one launch (without the
+ * appended token, which the next forward writes per layer).  Replaces the
+ * same reference code as gr_beam_kv_fork (serving_engine.py:107-120,
+ * core.py:108-112, engine_core_patch.py:245-252), which touches all layers at
+ * once since the child's suffix is recomputed through the whole model.
+ * k_caches/v_caches: host arrays of num_layers base pointers, every layer
+ * with the same geometry (strides, num_blocks, heads, dims, block size,
+ * dtype); the tables are worked out once per launch and each workgroup copies
+ * its share of the copy-on-write tokens in every layer (up to 32 layers per
+ * launch; more take further launches on the same stream).
+ */
+gr_status_t gr_beam_kv_fork_layers(
+    const int32_t* parent, int num_reqs, int beam_width,
+    const int32_t* bt_in, const int32_t* len_in, int32_t* bt_out, int32_t* len_out,
+    int bt_stride, int num_layers,
+    void* const* k_caches, void* const* v_caches, int64_t num_blocks,
+    int64_t kv_block_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+    int num_kv_heads, int head_dim, int block_size, int dtype,
+    int32_t* dev_status, hipStream_t stream);
+
+/*
  * Append one K/V token per beam at position suffix_len[n] of its row and
  * increment suffix_len[n] (in place).  The reshape_and_cache_flash role
  * (beam_attn.py:727-732) in block-table form.

@@ -96,6 +96,20 @@ def test_fork_append_prune_argument_checks(built_lib):
                                None, None) == _C.GR_ERR_INVALID_ARG
     assert lib.gr_beam_kv_fork(_BAD, 0, 4, 0x20, 0x30, 0x40, 0x50, 1, *geom, None, None, 0, 8, 128, 16, 2,
                                None, None) == _C.GR_OK
+    # multi-layer fork: at least one layer, pointer arrays present, every layer's cache 16-byte aligned
+    import ctypes
+    ptrs = (ctypes.c_void_p * 2)(0x1000, 0x2000)
+    bad = (ctypes.c_void_p * 2)(0x1000, 0x2008)
+    lgeom = [10, 16 * 8 * 128, 8 * 128, 128]
+    args = (_BAD, 1, 4, 0x20, 0x30, 0x40, 0x50, 1)
+    assert lib.gr_beam_kv_fork_layers(*args, 0, ptrs, ptrs, *lgeom, 8, 128, 16, 2, None, None) == \
+        _C.GR_ERR_INVALID_ARG
+    assert lib.gr_beam_kv_fork_layers(*args, 2, None, ptrs, *lgeom, 8, 128, 16, 2, None, None) == \
+        _C.GR_ERR_INVALID_ARG
+    assert lib.gr_beam_kv_fork_layers(*args, 2, ptrs, bad, *lgeom, 8, 128, 16, 2, None, None) == \
+        _C.GR_ERR_INVALID_ARG
+    assert lib.gr_beam_kv_fork_layers(_BAD, 0, 4, 0x20, 0x30, 0x40, 0x50, 1, 2, ptrs, ptrs, *lgeom, 8, 128, 16, 2,
+                                      None, None) == _C.GR_OK
     # append: misaligned cache pointer
     assert lib.gr_beam_kv_append(0x20, 0x30, 1024, 0x11, 0x20, 10, 16 * 8 * 128, 8 * 128, 128, _BAD, 1, _BAD,
                                  4, 8, 128, 16, 2, None, None) == _C.GR_ERR_INVALID_ARG

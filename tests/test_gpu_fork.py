@@ -120,3 +120,60 @@ def test_append_full_row_flagged(device):
 def test_fork_table_sizes(device, W, S, Hkv, L):
     wl = workloads.make_fork(R=2, W=W, Hkv=Hkv, D=128, S=S, L_old=L, seed=W + S)
     _assert_same(run_fork(wl, device), run_oracle(wl))
+
+
+def _layer_caches(wl, n_layers, seed):
+    """The workload's cache plus n_layers - 1 more of the same geometry, each with its own contents."""
+    g = torch.Generator().manual_seed(seed)
+    out = [wl.kv_cache]
+    for _ in range(n_layers - 1):
+        out.append(torch.randn(wl.kv_cache.shape, generator=g, dtype=torch.float32).to(wl.kv_cache.dtype))
+    return out
+
+
+@pytest.mark.parametrize("n_layers,W,S,L", [
+    (3, 16, 1, (1, 15)),
+    (35, 8, 2, (3, 30)),  # more layers than one launch takes: two launches
+    (28, 128, 1, (1, 15)),
+    (2, 300, 1, (1, 15)),  # more children than threads per workgroup
+])
+def test_fork_layers_matches_oracle(device, n_layers, W, S, L):
+    """One multi-layer launch equals the oracle's fork of each layer's cache, bit for bit."""
+    wl = workloads.make_fork(R=2, W=W, Hkv=2, D=128, S=S, L_old=L, seed=n_layers + W)
+    host = _layer_caches(wl, n_layers, seed=W)
+    dev = [kv.to(device) for kv in host]
+    d = wl.to(device)
+    status = ops.new_status(device)
+    bt, ln = ops.beam_kv_fork_layers(d.parent, d.suffix_bt, d.suffix_len, dev, status=status)
+    torch.cuda.synchronize()
+    ops.check_status(status)
+    for layer, (kv_h, kv_d) in enumerate(zip(host, dev)):
+        want = of.fork_append(wl.parent.numpy(), wl.suffix_bt.numpy(), wl.suffix_len.numpy(), _bits(kv_h[0]),
+                              _bits(kv_h[1]), None, None, block_size=wl.block_size)
+        if layer == 0:
+            assert np.array_equal(bt.cpu().numpy(), want[0]) and np.array_equal(ln.cpu().numpy(), want[1])
+        assert np.array_equal(_bits(kv_d[0]), want[2]), f"layer {layer} K cache differs"
+        assert np.array_equal(_bits(kv_d[1]), want[3]), f"layer {layer} V cache differs"
+
+
+def test_fork_layers_bad_parent_flagged(device):
+    wl = workloads.make_fork(R=2, W=8, Hkv=2, D=64, seed=21)
+    wl.parent[0, 5] = -3
+    d = wl.to(device)
+    caches = [kv.to(device) for kv in _layer_caches(wl, 4, seed=3)]
+    status = ops.new_status(device)
+    bt, ln = ops.beam_kv_fork_layers(d.parent, d.suffix_bt, d.suffix_len, caches, status=status)
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError, match="parent index out of range"):
+        ops.check_status(status)
+    # the request with the bad parent keeps its tables; the other forks
+    assert np.array_equal(bt.cpu().numpy()[:8], wl.suffix_bt.numpy()[:8])
+
+
+def test_fork_layers_rejects_mixed_geometry(device):
+    wl = workloads.make_fork(R=1, W=4, Hkv=2, D=64, seed=22)
+    d = wl.to(device)
+    other = torch.zeros((2, wl.kv_cache.shape[1] + 1) + tuple(wl.kv_cache.shape[2:]), dtype=wl.kv_cache.dtype,
+                        device=device)
+    with pytest.raises(ValueError, match="same shape"):
+        ops.beam_kv_fork_layers(d.parent, d.suffix_bt, d.suffix_len, [d.kv_cache, other])

@@ -19,6 +19,8 @@
 //  * beam_append / reshape_and_cache: one wave per beam / token.
 #include "gr_common.h"
 
+#include <algorithm>
+
 namespace gr {
 namespace {
 
@@ -42,6 +44,14 @@ __host__ __device__ inline int fork_lds_ints(int W, int S) {
   return 4 * ng + 4 * FORK_TOK_CHUNK + 2 * (ng + 1) + 6 * W + 1 + 8 + 1 + (W * S <= FORK_STAGE_BT ? W * S : 0);
 }
 constexpr int FORK_BATCH = 2;        // 16-byte K and V vectors per thread in flight
+constexpr int FORK_MAX_LAYERS = 32;  // layers one fork launch moves (more take further launches)
+
+// Base addresses of the layers a fork launch moves (every layer has the same
+// geometry); layer 0 is also the KvGeom's cache.
+struct KvLayers {
+  uint8_t* k[FORK_MAX_LAYERS];
+  uint8_t* v[FORK_MAX_LAYERS];
+};
 
 struct KvGeom {
   void* k_cache;
@@ -92,9 +102,15 @@ __device__ inline void block_scan(const int* v, int* out, int n, int* tmp) {
 __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
     const int32_t* __restrict__ parent, int R, int W, int cpw, const int32_t* __restrict__ bt_in,
     const int32_t* __restrict__ len_in, int32_t* __restrict__ bt_out, int32_t* __restrict__ len_out,
-    int S, KvGeom g, const uint8_t* k_new, const uint8_t* v_new, int64_t new_tok_stride,
+    int S, KvGeom g, int L, KvLayers layers, const uint8_t* k_new, const uint8_t* v_new, int64_t new_tok_stride,
     int32_t* dev_status) {
   extern __shared__ __attribute__((aligned(8))) int fork_lds[];
+  __shared__ uint8_t* lay_k[FORK_MAX_LAYERS];  // the layers' bases, indexed per lane by the copy loop
+  __shared__ uint8_t* lay_v[FORK_MAX_LAYERS];
+  if (threadIdx.x < L) {
+    lay_k[threadIdx.x] = layers.k[threadIdx.x];
+    lay_v[threadIdx.x] = layers.v[threadIdx.x];
+  }
   const int ngroups = (W + 63) >> 6;
   uint64_t* cow_mask = reinterpret_cast<uint64_t*>(fork_lds);
   uint64_t* free_mask = cow_mask + ngroups;
@@ -320,30 +336,40 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
         tok_dst[tid] = valid ? kv_byte_off(g, bdst, off, 0) : -1;
       }
       __syncthreads();
+      // the round's vectors of every layer, one flat range: item it is layer
+      // it / items, vector it % items of the round
       const int items = nt * tv;
+      const int all_items = L * items;
 #pragma unroll 1
-      for (int i0 = tid; i0 < items; i0 += FORK_THREADS * FORK_BATCH) {
+      for (int i0 = tid; i0 < all_items; i0 += FORK_THREADS * FORK_BATCH) {
         u32x4_t kb[FORK_BATCH], vb[FORK_BATCH];
-        int64_t dof[FORK_BATCH];
+        uint8_t* kd[FORK_BATCH];
+        uint8_t* vd[FORK_BATCH];
         bool ok[FORK_BATCH];
 #pragma unroll
         for (int u = 0; u < FORK_BATCH; ++u) {
           const int it = i0 + u * FORK_THREADS;
-          const int tk = it / tv, rem = it - (it / tv) * tv;
+          const int l = it < all_items ? it / items : 0;
+          const int li = it - l * items;
+          const int tk = li / tv, rem = li - (li / tv) * tv;
           const int h = rem / row_vecs, vec = rem - (rem / row_vecs) * row_vecs;
-          const int64_t so = it < items ? tok_src[tk] : -1;
+          const int64_t so = it < all_items ? tok_src[tk] : -1;
           ok[u] = so >= 0;
           const int64_t hoff = (int64_t)h * g.head_stride * g.esize + vec * 16;
-          dof[u] = ok[u] ? tok_dst[tk] + hoff : 0;
+          const int64_t dof = ok[u] ? tok_dst[tk] + hoff : 0;
           const int64_t sof = ok[u] ? so + hoff : 0;
-          kb[u] = *reinterpret_cast<const u32x4_t*>(kc + sof);
-          vb[u] = *reinterpret_cast<const u32x4_t*>(vc + sof);
+          uint8_t* kl = lay_k[l];
+          uint8_t* vl = lay_v[l];
+          kd[u] = kl + dof;
+          vd[u] = vl + dof;
+          kb[u] = *reinterpret_cast<const u32x4_t*>(kl + sof);
+          vb[u] = *reinterpret_cast<const u32x4_t*>(vl + sof);
         }
 #pragma unroll
         for (int u = 0; u < FORK_BATCH; ++u) {
           if (ok[u]) {
-            *reinterpret_cast<u32x4_t*>(kc + dof[u]) = kb[u];
-            *reinterpret_cast<u32x4_t*>(vc + dof[u]) = vb[u];
+            *reinterpret_cast<u32x4_t*>(kd[u]) = kb[u];
+            *reinterpret_cast<u32x4_t*>(vd[u]) = vb[u];
           }
         }
       }
@@ -483,24 +509,33 @@ KvGeom make_geom(void* k_cache, void* v_cache, int64_t num_blocks, int64_t bstr,
 
 using namespace gr;
 
-extern "C" gr_status_t gr_beam_kv_fork(const int32_t* parent, int num_reqs, int beam_width,
-                                       const int32_t* bt_in, const int32_t* len_in, int32_t* bt_out,
-                                       int32_t* len_out, int bt_stride, void* k_cache, void* v_cache,
-                                       int64_t num_blocks, int64_t kv_block_stride, int64_t kv_tok_stride,
-                                       int64_t kv_head_stride, const void* k_new, const void* v_new,
-                                       int64_t new_tok_stride, int num_kv_heads, int head_dim,
-                                       int block_size, int dtype, int32_t* dev_status, hipStream_t stream) {
-  if (!cache_dtype_valid(dtype) || num_reqs < 0 || beam_width < 1 || bt_stride < 1) return GR_ERR_INVALID_ARG;
+namespace gr {
+namespace {
+
+// Checks shared by both fork entry points, then one launch per group of up to
+// FORK_MAX_LAYERS layers (each launch derives the same tables from the inputs).
+gr_status_t fork_launch(const int32_t* parent, int num_reqs, int beam_width, const int32_t* bt_in,
+                        const int32_t* len_in, int32_t* bt_out, int32_t* len_out, int bt_stride, int num_layers,
+                        void* const* k_caches, void* const* v_caches, int64_t num_blocks, int64_t kv_block_stride,
+                        int64_t kv_tok_stride, int64_t kv_head_stride, const void* k_new, const void* v_new,
+                        int64_t new_tok_stride, int num_kv_heads, int head_dim, int block_size, int dtype,
+                        int32_t* dev_status, hipStream_t stream) {
+  if (!cache_dtype_valid(dtype) || num_reqs < 0 || beam_width < 1 || bt_stride < 1 || num_layers < 1)
+    return GR_ERR_INVALID_ARG;
   if (beam_width > FORK_MAX_W) return GR_ERR_UNSUPPORTED;
+  if (!k_caches || !v_caches) return GR_ERR_INVALID_ARG;
   if (num_reqs == 0) return GR_OK;
   if (!parent || !bt_in || !len_in || !bt_out || !len_out) return GR_ERR_INVALID_ARG;
   if (bt_in == bt_out || len_in == len_out) return GR_ERR_INVALID_ARG;  // tables are written out of place
   if ((k_new == nullptr) != (v_new == nullptr)) return GR_ERR_INVALID_ARG;
-  KvGeom g = make_geom(k_cache, v_cache, num_blocks, kv_block_stride, kv_tok_stride, kv_head_stride,
-                       num_kv_heads, head_dim, block_size, dtype);
-  gr_status_t st = check_geom(g);
-  if (st != GR_OK) return st;
-  if (k_new && (!aligned16(k_new) || !aligned16(v_new) || (new_tok_stride * g.esize) % 16 ||
+  if (k_new && num_layers != 1) return GR_ERR_INVALID_ARG;  // the fused append is per layer
+  for (int l = 0; l < num_layers; ++l) {
+    KvGeom gl = make_geom(k_caches[l], v_caches[l], num_blocks, kv_block_stride, kv_tok_stride, kv_head_stride,
+                          num_kv_heads, head_dim, block_size, dtype);
+    const gr_status_t st = check_geom(gl);
+    if (st != GR_OK) return st;
+  }
+  if (k_new && (!aligned16(k_new) || !aligned16(v_new) || (new_tok_stride * dtype_size(dtype)) % 16 ||
                 new_tok_stride < (int64_t)num_kv_heads * head_dim))
     return GR_ERR_INVALID_ARG;
   if ((int64_t)num_reqs * beam_width > INT32_MAX) return GR_ERR_INVALID_ARG;
@@ -510,11 +545,52 @@ extern "C" gr_status_t gr_beam_kv_fork(const int32_t* parent, int num_reqs, int 
   // half the plans worked out)
   const int tv = num_kv_heads * (head_dim * dtype_size(dtype) / 16);
   const int cpw = beam_width % 2 == 0 && 2 * tv <= FORK_THREADS ? 2 : 1;
-  hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * (beam_width / cpw))), dim3(FORK_THREADS), lds, stream,
-                     parent, num_reqs, beam_width, cpw, bt_in, len_in, bt_out, len_out, bt_stride, g,
-                     static_cast<const uint8_t*>(k_new), static_cast<const uint8_t*>(v_new), new_tok_stride,
-                     dev_status);
-  return launch_status();
+  for (int l0 = 0; l0 < num_layers; l0 += FORK_MAX_LAYERS) {
+    const int L = std::min(FORK_MAX_LAYERS, num_layers - l0);
+    KvLayers layers{};
+    for (int l = 0; l < L; ++l) {
+      layers.k[l] = static_cast<uint8_t*>(k_caches[l0 + l]);
+      layers.v[l] = static_cast<uint8_t*>(v_caches[l0 + l]);
+    }
+    const KvGeom g = make_geom(k_caches[l0], v_caches[l0], num_blocks, kv_block_stride, kv_tok_stride,
+                               kv_head_stride, num_kv_heads, head_dim, block_size, dtype);
+    hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * (beam_width / cpw))), dim3(FORK_THREADS), lds, stream,
+                       parent, num_reqs, beam_width, cpw, bt_in, len_in, bt_out, len_out, bt_stride, g, L, layers,
+                       static_cast<const uint8_t*>(k_new), static_cast<const uint8_t*>(v_new), new_tok_stride,
+                       dev_status);
+    const gr_status_t st = launch_status();
+    if (st != GR_OK) return st;
+  }
+  return GR_OK;
+}
+
+}  // namespace
+}  // namespace gr
+
+extern "C" gr_status_t gr_beam_kv_fork(const int32_t* parent, int num_reqs, int beam_width,
+                                       const int32_t* bt_in, const int32_t* len_in, int32_t* bt_out,
+                                       int32_t* len_out, int bt_stride, void* k_cache, void* v_cache,
+                                       int64_t num_blocks, int64_t kv_block_stride, int64_t kv_tok_stride,
+                                       int64_t kv_head_stride, const void* k_new, const void* v_new,
+                                       int64_t new_tok_stride, int num_kv_heads, int head_dim,
+                                       int block_size, int dtype, int32_t* dev_status, hipStream_t stream) {
+  void* kc[1] = {k_cache};
+  void* vc[1] = {v_cache};
+  return fork_launch(parent, num_reqs, beam_width, bt_in, len_in, bt_out, len_out, bt_stride, 1, kc, vc, num_blocks,
+                     kv_block_stride, kv_tok_stride, kv_head_stride, k_new, v_new, new_tok_stride, num_kv_heads,
+                     head_dim, block_size, dtype, dev_status, stream);
+}
+
+extern "C" gr_status_t gr_beam_kv_fork_layers(const int32_t* parent, int num_reqs, int beam_width,
+                                              const int32_t* bt_in, const int32_t* len_in, int32_t* bt_out,
+                                              int32_t* len_out, int bt_stride, int num_layers,
+                                              void* const* k_caches, void* const* v_caches, int64_t num_blocks,
+                                              int64_t kv_block_stride, int64_t kv_tok_stride,
+                                              int64_t kv_head_stride, int num_kv_heads, int head_dim,
+                                              int block_size, int dtype, int32_t* dev_status, hipStream_t stream) {
+  return fork_launch(parent, num_reqs, beam_width, bt_in, len_in, bt_out, len_out, bt_stride, num_layers, k_caches,
+                     v_caches, num_blocks, kv_block_stride, kv_tok_stride, kv_head_stride, nullptr, nullptr, 0,
+                     num_kv_heads, head_dim, block_size, dtype, dev_status, stream);
 }
 
 extern "C" gr_status_t gr_beam_kv_append(const void* k_new, const void* v_new, int64_t new_tok_stride,

@@ -109,6 +109,11 @@ SIGNATURES = {
         _P, _P, _L, _L, _L, _L,
         _P, _P, _L, _I, _I, _I, _I, _P, _P,
     ]),
+    "gr_beam_kv_fork_layers": (_I, [
+        _P, _I, _I, _P, _P, _P, _P, _I, _I,   # parent, R, W, bt_in, len_in, bt_out, len_out, bt_stride, layers
+        _P, _P, _L, _L, _L, _L,               # k_caches, v_caches (host pointer arrays), num_blocks, strides
+        _I, _I, _I, _I, _P, _P,               # heads, head_dim, block_size, dtype, dev_status, stream
+    ]),
     "gr_beam_kv_append": (_I, [
         _P, _P, _L, _P, _P, _L, _L, _L, _L, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P,
     ]),

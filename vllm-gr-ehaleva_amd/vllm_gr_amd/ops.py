@@ -317,6 +317,87 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
     _C.check("gr_reshape_and_cache", code)
 
 
+class _LayerSet:
+    """Validated per-layer K/V base pointers of one list of caches (every
+    layer one geometry), as the host pointer arrays gr_beam_kv_fork_layers takes."""
+
+    def __init__(self, kv_caches):
+        pairs = [split_kv_cache(kv) if isinstance(kv, torch.Tensor) else tuple(kv) for kv in kv_caches]
+        k0, v0 = pairs[0]
+        self.strides = _cache_strides(k0, v0)
+        for k, v in pairs:
+            if k.shape != k0.shape or v.shape != k0.shape or k.dtype != k0.dtype or v.dtype != k0.dtype:
+                raise ValueError("every layer's cache must have the same shape and dtype")
+            if _cache_strides(k, v) != self.strides or k.device != k0.device or v.device != k0.device:
+                raise ValueError("every layer's cache must have the same strides and device")
+        self.k0 = k0
+        self.n = len(pairs)
+        self.dtype_code = _cache_dtype_code(k0)
+        self._k = (ctypes.c_void_p * self.n)(*[k.data_ptr() for k, _ in pairs])
+        self._v = (ctypes.c_void_p * self.n)(*[v.data_ptr() for _, v in pairs])
+        self.k_ptrs = ctypes.cast(self._k, ctypes.c_void_p)
+        self.v_ptrs = ctypes.cast(self._v, ctypes.c_void_p)
+        self.refs = kv_caches  # keeps the tensors (and so their addresses) alive while cached
+
+
+_LAYER_SETS: dict = {}
+
+
+def _layer_set(kv_caches) -> _LayerSet:
+    """The _LayerSet of a list of caches, built once per distinct list (keyed
+    by every cache's address, shape, strides and dtype)."""
+    def sig(kv):
+        t = kv if isinstance(kv, torch.Tensor) else kv[0]
+        return (t.data_ptr(), tuple(t.shape), t.stride(), t.dtype, isinstance(kv, torch.Tensor),
+                None if isinstance(kv, torch.Tensor) else kv[1].data_ptr())
+    key = tuple(sig(kv) for kv in kv_caches)
+    ls = _LAYER_SETS.get(key)
+    if ls is None:
+        ls = _LayerSet(list(kv_caches))
+        if len(_LAYER_SETS) >= 8:
+            _LAYER_SETS.pop(next(iter(_LAYER_SETS)))
+        _LAYER_SETS[key] = ls
+    return ls
+
+
+def beam_kv_fork_layers(parent: torch.Tensor, bt_in: torch.Tensor, len_in: torch.Tensor, kv_caches, *,
+                        bt_out: torch.Tensor | None = None, len_out: torch.Tensor | None = None,
+                        status: torch.Tensor | None = None):
+    """``beam_kv_fork`` of every layer's cache in one launch (no appended
+    token).  ``kv_caches``: a list of per-layer ``[2, NB, bs, Hkv, D]`` caches
+    (or of (k_cache, v_cache) pairs) with one geometry.  Returns (bt_out,
+    len_out)."""
+    kv_caches = list(kv_caches)
+    if not kv_caches:
+        raise ValueError("kv_caches is empty")
+    ls = _layer_set(kv_caches)
+    k0 = ls.k0
+    dev = _need_cuda(parent, bt_in, len_in, k0, bt_out, len_out, status)
+    _need_i32("parent", parent)
+    _need_i32("bt_in", bt_in)
+    _need_i32("len_in", len_in)
+    if parent.dim() != 2:
+        raise ValueError("parent must be [R, W]")
+    R, W = parent.shape
+    if bt_in.dim() != 2 or bt_in.shape[0] != R * W or len_in.numel() != R * W:
+        raise ValueError("bt_in must be [R*W, blocks] and len_in [R*W]")
+    NB, bs, Hkv, D = k0.shape
+    if bt_out is None:
+        bt_out = torch.empty_like(bt_in)
+    if len_out is None:
+        len_out = torch.empty_like(len_in)
+    _need_i32("bt_out", bt_out)
+    _need_i32("len_out", len_out)
+    if bt_out.shape != bt_in.shape or len_out.shape != len_in.shape:
+        raise ValueError("output tables must match the input tables' shapes")
+    code = _C.lib().gr_beam_kv_fork_layers(
+        parent.data_ptr(), R, W, bt_in.data_ptr(), len_in.data_ptr(), bt_out.data_ptr(), len_out.data_ptr(),
+        bt_in.shape[1], ls.n, ls.k_ptrs, ls.v_ptrs, NB, *ls.strides, Hkv, D, bs, ls.dtype_code, _ptr(status),
+        _stream(dev))
+    _C.check("gr_beam_kv_fork_layers", code)
+    return bt_out, len_out
+
+
 def beam_kv_fork(parent: torch.Tensor, bt_in: torch.Tensor, len_in: torch.Tensor,
                  k_cache: torch.Tensor, v_cache: torch.Tensor, k_new: torch.Tensor | None = None,
                  v_new: torch.Tensor | None = None, *, bt_out: torch.Tensor | None = None,

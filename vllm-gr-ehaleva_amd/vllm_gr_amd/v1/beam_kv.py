@@ -101,10 +101,9 @@ class BeamKVTable:
         caches = list(kv_caches)
         if not caches:
             raise ValueError("fork needs at least one KV cache")
-        for kv in caches:
-            k_cache, v_cache = ops.split_kv_cache(kv)
-            # every layer derives the same tables; each copies its own blocks
-            ops.beam_kv_fork(parent, self.suffix_bt, self.suffix_len, k_cache, v_cache,
-                             bt_out=self._spare_bt, len_out=self._spare_len, status=status)
+        # one launch for every layer: the tables are worked out once, each
+        # workgroup copies its share of the copy-on-write tokens in all layers
+        ops.beam_kv_fork_layers(parent, self.suffix_bt, self.suffix_len, caches,
+                                bt_out=self._spare_bt, len_out=self._spare_len, status=status)
         self.suffix_bt, self._spare_bt = self._spare_bt, self.suffix_bt
         self.suffix_len, self._spare_len = self._spare_len, self.suffix_len
