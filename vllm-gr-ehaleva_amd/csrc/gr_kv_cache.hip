@@ -99,6 +99,8 @@ __device__ inline void block_scan(const int* v, int* out, int n, int* tmp) {
 
 // 8 waves per SIMD: every workgroup of a 2048-child batch resident at once.
 // Workgroup cg of request r owns children cg*cpw .. cg*cpw + cpw-1.
+// MULTI: L layers (their bases in `layers`); otherwise the one layer of g.
+template <bool MULTI>
 __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
     const int32_t* __restrict__ parent, int R, int W, int cpw, const int32_t* __restrict__ bt_in,
     const int32_t* __restrict__ len_in, int32_t* __restrict__ bt_out, int32_t* __restrict__ len_out,
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
   extern __shared__ __attribute__((aligned(8))) int fork_lds[];
   __shared__ uint8_t* lay_k[FORK_MAX_LAYERS];  // the layers' bases, indexed per lane by the copy loop
   __shared__ uint8_t* lay_v[FORK_MAX_LAYERS];
-  if (threadIdx.x < L) {
+  if (MULTI && threadIdx.x < L) {
     lay_k[threadIdx.x] = layers.k[threadIdx.x];
     lay_v[threadIdx.x] = layers.v[threadIdx.x];
   }
@@ -339,7 +341,7 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
       // the round's vectors of every layer, one flat range: item it is layer
       // it / items, vector it % items of the round
       const int items = nt * tv;
-      const int all_items = L * items;
+      const int all_items = (MULTI ? L : 1) * items;
 #pragma unroll 1
       for (int i0 = tid; i0 < all_items; i0 += FORK_THREADS * FORK_BATCH) {
         u32x4_t kb[FORK_BATCH], vb[FORK_BATCH];
@@ -349,7 +351,7 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
 #pragma unroll
         for (int u = 0; u < FORK_BATCH; ++u) {
           const int it = i0 + u * FORK_THREADS;
-          const int l = it < all_items ? it / items : 0;
+          const int l = MULTI && it < all_items ? it / items : 0;
           const int li = it - l * items;
           const int tk = li / tv, rem = li - (li / tv) * tv;
           const int h = rem / row_vecs, vec = rem - (rem / row_vecs) * row_vecs;
@@ -358,8 +360,8 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
           const int64_t hoff = (int64_t)h * g.head_stride * g.esize + vec * 16;
           const int64_t dof = ok[u] ? tok_dst[tk] + hoff : 0;
           const int64_t sof = ok[u] ? so + hoff : 0;
-          uint8_t* kl = lay_k[l];
-          uint8_t* vl = lay_v[l];
+          uint8_t* kl = MULTI ? lay_k[l] : kc;
+          uint8_t* vl = MULTI ? lay_v[l] : vc;
           kd[u] = kl + dof;
           vd[u] = vl + dof;
           kb[u] = *reinterpret_cast<const u32x4_t*>(kl + sof);
@@ -554,10 +556,15 @@ gr_status_t fork_launch(const int32_t* parent, int num_reqs, int beam_width, con
     }
     const KvGeom g = make_geom(k_caches[l0], v_caches[l0], num_blocks, kv_block_stride, kv_tok_stride,
                                kv_head_stride, num_kv_heads, head_dim, block_size, dtype);
-    hipLaunchKernelGGL(beam_fork, dim3((unsigned)(num_reqs * (beam_width / cpw))), dim3(FORK_THREADS), lds, stream,
-                       parent, num_reqs, beam_width, cpw, bt_in, len_in, bt_out, len_out, bt_stride, g, L, layers,
-                       static_cast<const uint8_t*>(k_new), static_cast<const uint8_t*>(v_new), new_tok_stride,
-                       dev_status);
+    const dim3 grid((unsigned)(num_reqs * (beam_width / cpw)));
+    if (num_layers == 1)
+      hipLaunchKernelGGL(beam_fork<false>, grid, dim3(FORK_THREADS), lds, stream, parent, num_reqs, beam_width, cpw,
+                         bt_in, len_in, bt_out, len_out, bt_stride, g, L, layers, static_cast<const uint8_t*>(k_new),
+                         static_cast<const uint8_t*>(v_new), new_tok_stride, dev_status);
+    else
+      hipLaunchKernelGGL(beam_fork<true>, grid, dim3(FORK_THREADS), lds, stream, parent, num_reqs, beam_width, cpw,
+                         bt_in, len_in, bt_out, len_out, bt_stride, g, L, layers, static_cast<const uint8_t*>(k_new),
+                         static_cast<const uint8_t*>(v_new), new_tok_stride, dev_status);
     const gr_status_t st = launch_status();
     if (st != GR_OK) return st;
   }
