@@ -708,8 +708,42 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // Tile t+3 goes out at the top of step t, into buffer (t+3) % 4: its
   // previous tile, t-1, was last read in step t-1, before the barrier that
   // ended it.
+  // Lean loads of the loop's full tiles.  When every block id of the range sits
+  // in the first staged window (which then never moves), a block holds at
+  // least 8 keys (rows 8 wv .. 8 wv + 7 of a tile share one block) and the
+  // range has at most 64 tiles, lane t of blk_of holds the block of tile t's
+  // rows of this wave: a tile's four loads then take one lane read and scalar
+  // address arithmetic, with no LDS round trip and no window check.  They
+  // move exactly what issue_tile moves.
+  const int k_end = min(kb + n_st * ST_KEYS, P);
+  const bool lean = n_st <= 64 && a.bs >= 8 && (n_st == 0 || ((k_end - 1) >> bsh) < PBT_WIN);
+  const bool last_full = kb + n_st * ST_KEYS <= P;
+  int blk_of = -1;
+  {
+    const int key = kb + lane * ST_KEYS + 8 * wv;
+    if (lean && lane < n_st && key < P) blk_of = pbt_s[key >> bsh];
+  }
+  const S* kc_h = kc + head_off;
+  const S* vc_h = vc + head_off;
+  const int tok32 = (int)tok;
+  auto issue_tile_lean = [&](int t, int buf) {
+    const int blk = max(__builtin_amdgcn_readlane(blk_of, t), 0);
+    const int r0 = (kb + t * ST_KEYS + 8 * wv) & (a.bs - 1);
+    const int64_t el = (int64_t)((uint64_t)(uint32_t)blk * blk_stride) + (int64_t)(uint32_t)(r0 * tok32);
+    const S* kb0 = kc_h + el;
+    const S* vb0 = vc_h + el;
+    const uint32_t d = lds0 + (uint32_t)(buf * BUF * 2) + (uint32_t)(wv * 8 * KS_PITCH * 2);
+    const uint32_t dst[4] = {d, d + K_TILE * 2, d + 1024, d + K_TILE * 2 + 1024};
+    const void* const src[4] = {kb0, vb0, kb0 + 4 * tok32, vb0 + 4 * tok32};
+    const uint32_t off[4] = {vo_k, vo_v, vo_k, vo_v};
+    dma_s4(dst, src, off);
+  };
   auto fetch_ahead = [&](int t) {
-    if (t + 3 < n_st) issue_tile(t + 3, (t + 3) % NBUF);
+    const int tn = t + 3;
+    if (tn < n_st) {
+      if (lean && (tn + 1 < n_st || last_full)) issue_tile_lean(tn, tn % NBUF);
+      else issue_tile(tn, tn % NBUF);
+    }
   };
   // The end of step t: tile t+2 (read from the next step on) has landed; tile
   // t+3 may still be in flight.

@@ -83,6 +83,31 @@ __device__ inline void dma_s(uint32_t lds, const void* sbase, uint32_t voff) {
   __asm__ volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
                    : "=&s"(save) : "s"(m), "v"(voff), "s"(sb) : "memory");
 }
+// Four dma_s loads in one statement: M0 saved and restored once.  Load i
+// moves 64 x 16 bytes from sbase[i] + voff[i] to LDS byte address lds[i].
+__device__ inline void dma_s4(const uint32_t (&lds)[4], const void* const (&sbase)[4], const uint32_t (&voff)[4]) {
+  uint32_t m[4];
+  uint64_t sb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = __builtin_amdgcn_readfirstlane(lds[i]);
+    const uint64_t b = reinterpret_cast<uint64_t>(sbase[i]);
+    sb[i] = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+            (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  }
+  uint32_t save;
+  __asm__ volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %5, %9\n\t"
+      "s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %6, %10\n\t"
+      "s_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %7, %11\n\t"
+      "s_mov_b32 m0, %4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %8, %12\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "s"(m[0]), "s"(m[1]), "s"(m[2]), "s"(m[3]), "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]),
+        "s"(sb[0]), "s"(sb[1]), "s"(sb[2]), "s"(sb[3])
+      : "memory");
+}
 __device__ inline void dma_v(uint32_t lds, const void* addr) {
   const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
   uint32_t save;
