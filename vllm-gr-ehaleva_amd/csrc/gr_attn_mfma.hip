@@ -291,7 +291,9 @@ __device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH
 // alternates two register sets: no copies).  Returns true when some weight
 // could exceed 2^Rescale::THRESH or the row has no reference yet (the tile then
 // needs the exact path); otherwise adds the weight sum to the row's state.
-template <int DT, bool SOFTCAP>
+// DEFER: no wave vote -- the lane's sum is always added and the lane's own
+// flag returned (the caller votes once, after its loop, and recomputes).
+template <int DT, bool SOFTCAP, bool DEFER = false>
 __device__ inline bool phase_a1(const uint16_t* next_buf, int kbase, int lane, const u32x4_t (&qf)[8],
                                 const f32x16_t& s_in, f32x16_t& s_out, RowState& st, float c, float cap,
                                 u32x4_t (&p)[1][2]) {
@@ -318,11 +320,18 @@ __device__ inline bool phase_a1(const uint16_t* next_buf, int kbase, int lane, c
     acc0 += e0;
     acc1 += e1;
     pk[i] = M::pack2(e0, e1);
+    // keeps this segment's weights, sums and packing beside its MFMA (without
+    // it the instruction selector may gather them after the last MFMAs)
+    __asm__ volatile("" : "+v"(acc0), "+v"(acc1), "+v"(pk[i]));
     __builtin_amdgcn_sched_barrier(0);
   }
   p[0][0] = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
   p[0][1] = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
   const float acc = acc0 + acc1;
+  if constexpr (DEFER) {
+    st.lsum += acc;
+    return !(acc <= Rescale<DT>::SUM);
+  }
   if (__ballot(!(acc <= Rescale<DT>::SUM)) != 0) return true;
   st.lsum += acc;
   return false;
@@ -718,23 +727,29 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   const int k_end = min(kb + n_st * ST_KEYS, P);
   const bool lean = n_st <= 64 && a.bs >= 8 && (n_st == 0 || ((k_end - 1) >> bsh) < PBT_WIN);
   const bool last_full = kb + n_st * ST_KEYS <= P;
-  int blk_of = -1;
+  // lane t: byte offset of tile t's rows 8 wv .. from the head's K (and V) base
+  uint32_t toff_lo = 0, toff_hi = 0;
   {
     const int key = kb + lane * ST_KEYS + 8 * wv;
-    if (lean && lane < n_st && key < P) blk_of = pbt_s[key >> bsh];
+    if (lean && lane < n_st && key < P) {
+      const int blk = max(pbt_s[key >> bsh], 0);
+      const uint64_t e = (uint64_t)(uint32_t)blk * blk_stride + (uint64_t)(uint32_t)(key & (a.bs - 1)) * (uint64_t)tok;
+      toff_lo = (uint32_t)(e << 1);
+      toff_hi = (uint32_t)(e >> 31);
+    }
   }
-  const S* kc_h = kc + head_off;
-  const S* vc_h = vc + head_off;
-  const int tok32 = (int)tok;
+  const char* kc_h = reinterpret_cast<const char*>(kc + head_off);
+  const char* vc_h = reinterpret_cast<const char*>(vc + head_off);
+  const uint32_t tok4b = (uint32_t)(8 * tok);  // bytes of four token rows
+  const uint32_t dst_w = lds0 + (uint32_t)(wv * 8 * KS_PITCH * 2);
   auto issue_tile_lean = [&](int t, int buf) {
-    const int blk = max(__builtin_amdgcn_readlane(blk_of, t), 0);
-    const int r0 = (kb + t * ST_KEYS + 8 * wv) & (a.bs - 1);
-    const int64_t el = (int64_t)((uint64_t)(uint32_t)blk * blk_stride) + (int64_t)(uint32_t)(r0 * tok32);
-    const S* kb0 = kc_h + el;
-    const S* vb0 = vc_h + el;
-    const uint32_t d = lds0 + (uint32_t)(buf * BUF * 2) + (uint32_t)(wv * 8 * KS_PITCH * 2);
+    const uint64_t toff = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)toff_hi, t) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)toff_lo, t);
+    const char* kb0 = kc_h + toff;
+    const char* vb0 = vc_h + toff;
+    const uint32_t d = dst_w + (uint32_t)(buf * BUF * 2);
     const uint32_t dst[4] = {d, d + K_TILE * 2, d + 1024, d + K_TILE * 2 + 1024};
-    const void* const src[4] = {kb0, vb0, kb0 + 4 * tok32, vb0 + 4 * tok32};
+    const void* const src[4] = {kb0, vb0, kb0 + tok4b, vb0 + tok4b};
     const uint32_t off[4] = {vo_k, vo_v, vo_k, vo_v};
     dma_s4(dst, src, off);
   };
@@ -798,15 +813,29 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     it = 1;
   };
   // One fast step over tile t (not the last): consumes its S^T from s_in and
-  // leaves that of tile t+1 in s_out.
+  // leaves that of tile t+1 in s_out.  The exact-path test is deferred: each
+  // lane records its own flag and the waves vote after the loop.
   auto fast_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
     fetch_ahead(t);
-    hot_seen |= phase_a1<DT, SOFTCAP>(lds + ((t + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p);
+    hot_seen |= phase_a1<DT, SOFTCAP, true>(lds + ((t + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p);
     phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
     step_barrier(t);
   };
+  // The same step when tile t+3 exists and is full and the lean loads apply
+  // (steps t < n_lean): no run-time choices.
+  const int n_lean = lean ? (last_full ? n_st - 3 : n_st - 4) : 0;
+  auto lean_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
+    issue_tile_lean(t + 3, (t + 3) % NBUF);
+    hot_seen |= phase_a1<DT, SOFTCAP, true>(lds + ((t + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p);
+    phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
+    tile_barrier<LOADS_PER_TILE>();
+  };
   // fast steps over tiles [it, t_end): S^T alternates between s_cur and s_alt
   auto fast_steps = [&](int t_end) {
+    for (; it + 1 < min(t_end, n_lean); it += 2) {
+      lean_step(it, s_cur, s_alt);
+      lean_step(it + 1, s_alt, s_cur);
+    }
     for (; it + 1 < t_end; it += 2) {
       fast_step(it, s_cur, s_alt);
       fast_step(it + 1, s_alt, s_cur);
@@ -832,7 +861,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       s_cur = s_alt;
       it = 1;
     }
-    if (hot_seen && lane == 0) hot_flag = 1;
+    if (__ballot(hot_seen) != 0 && lane == 0) hot_flag = 1;
     for (; it < n_st; ++it) {
       fetch_ahead(it);
       uint32_t v = 0;
@@ -850,11 +879,15 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   } else {
     // the last two tiles take the general step
     if (n_st >= 3) peel();
-    for (; it + 2 < n_st; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
+    for (; it + 1 < n_lean; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
+      lean_step(it, s_cur, s_alt);
+      lean_step(it + 1, s_alt, s_cur);
+    }
+    for (; it + 2 < n_st; it += 2) {
       fast_step(it, s_cur, s_alt);
       fast_step(it + 1, s_alt, s_cur);
     }
-    if (hot_seen && lane == 0) hot_flag = 1;
+    if (__ballot(hot_seen) != 0 && lane == 0) hot_flag = 1;
     if (it + 1 < n_st) {
       prefix_step(it, s_cur, s_alt);
       last_step(it + 1, s_alt);
