@@ -720,10 +720,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // Lean loads of the loop's full tiles.  When every block id of the range sits
   // in the first staged window (which then never moves), a block holds at
   // least 8 keys (rows 8 wv .. 8 wv + 7 of a tile share one block) and the
-  // range has at most 64 tiles, lane t of blk_of holds the block of tile t's
-  // rows of this wave: a tile's four loads then take one lane read and scalar
-  // address arithmetic, with no LDS round trip and no window check.  They
-  // move exactly what issue_tile moves.
+  // range has at most 64 tiles, lane t of toff_lo / toff_hi holds the byte
+  // offset of tile t's rows of this wave: a tile's four loads then take two
+  // lane reads and scalar address arithmetic, with no LDS round trip and no
+  // window check.  They move exactly what issue_tile moves.
   const int k_end = min(kb + n_st * ST_KEYS, P);
   const bool lean = n_st <= 64 && a.bs >= 8 && (n_st == 0 || ((k_end - 1) >> bsh) < PBT_WIN);
   const bool last_full = kb + n_st * ST_KEYS <= P;
