@@ -36,12 +36,12 @@ constexpr int FORK_STAGE_BT = 2048;  // a request's whole block table is staged 
 constexpr int FORK_TOK_CHUNK = 64;
 
 // the fork kernel's LDS, sized by the request width W (ints; the 64-bit words
-// first): cow and free masks, the staged token offsets, group bases, par,
+// first): cow and free masks, the staged token offsets, par,
 // first (later the copy lengths), cnt, lens, owner_of, cpre (W + 1), the scan
 // scratch, the staged block table
 __host__ __device__ inline int fork_lds_ints(int W, int S) {
   const int ng = (W + 63) >> 6;
-  return 4 * ng + 4 * FORK_TOK_CHUNK + 2 * (ng + 1) + 6 * W + 1 + 8 + 1 + (W * S <= FORK_STAGE_BT ? W * S : 0);
+  return 4 * ng + 4 * FORK_TOK_CHUNK + 6 * W + 1 + 8 + 1 + (W * S <= FORK_STAGE_BT ? W * S : 0);
 }
 constexpr int FORK_BATCH = 2;        // 16-byte K and V vectors per thread in flight
 constexpr int FORK_MAX_LAYERS = 32;  // layers one fork launch moves (more take further launches)
@@ -67,6 +67,24 @@ __device__ inline int64_t kv_byte_off(const KvGeom& g, int64_t blk, int off, int
 
 // exclusive prefix sum of v[0 .. n) into out[0 .. n] (out[n] = total) by a
 // 256-thread workgroup, n <= FORK_MAX_W; tmp: 8 ints
+// Position of the k-th (0-based) set bit of x (k below the popcount).
+__device__ inline int select_bit(uint64_t x, int k) {
+  int pos = 0;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const uint64_t lo = x & ((1ull << w) - 1);
+    const int c = __builtin_popcountll(lo);
+    if (k >= c) {
+      k -= c;
+      x >>= w;
+      pos += w;
+    } else {
+      x = lo;
+    }
+  }
+  return pos;
+}
+
 __device__ inline void block_scan(const int* v, int* out, int n, int* tmp) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr int PER = FORK_MAX_W / FORK_THREADS;
@@ -118,9 +136,7 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
   uint64_t* free_mask = cow_mask + ngroups;
   int64_t* tok_src = reinterpret_cast<int64_t*>(free_mask + ngroups);  // byte offset of a token's head-0 row, -1: skip
   int64_t* tok_dst = tok_src + FORK_TOK_CHUNK;
-  int* cow_base = reinterpret_cast<int*>(tok_dst + FORK_TOK_CHUNK);
-  int* free_base = cow_base + ngroups + 1;
-  int* par = free_base + ngroups + 1;
+  int* par = reinterpret_cast<int*>(tok_dst + FORK_TOK_CHUNK);
   int* first = par + W;
   int* cnt = first + W;
   int* lens = cnt + W;
@@ -224,45 +240,36 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
     }
   }
   __syncthreads();
-  if (tid == 0) {  // group bases of the two rank sequences (at most 16 groups)
-    int cb = 0, fb = 0;
-    for (int gi = 0; gi < ngroups; ++gi) {
-      cow_base[gi] = cb;
-      free_base[gi] = fb;
-      cb += __builtin_popcountll(cow_mask[gi]);
-      fb += __builtin_popcountll(free_mask[gi]);
-    }
-  }
-  __syncthreads();
   // the k-th childless parent (ascending) goes to the k-th copying child
-  // (ascending): the two counts are equal; owner_of temporarily holds the
-  // list of childless parents by rank
-  for (int i = tid; i < W; i += FORK_THREADS) {
-    const uint64_t fm = free_mask[i >> 6];
-    if ((fm >> (i & 63)) & 1)
-      owner_of[free_base[i >> 6] + __builtin_popcountll(fm & ((1ull << (i & 63)) - 1))] = i;
-  }
-  __syncthreads();
+  // (ascending; the two counts are equal): a copying child takes its rank
+  // from the copy masks and selects that set bit of the childless masks
   const int cap = S * g.bs;
-  int own_i[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
     const int i = tid + u * FORK_THREADS;
-    own_i[u] = 0;
     if (i < W) {
       const uint64_t cm = cow_mask[i >> 6];
       const bool cw = (cm >> (i & 63)) & 1;
-      own_i[u] = cw ? owner_of[cow_base[i >> 6] + __builtin_popcountll(cm & ((1ull << (i & 63)) - 1))] : par[i];
+      int own = par[i];
+      if (cw) {
+        int k = __builtin_popcountll(cm & ((1ull << (i & 63)) - 1));
+        for (int gi = 0; gi < (i >> 6); ++gi) k += __builtin_popcountll(cow_mask[gi]);
+        int gw = 0;
+        uint64_t fm = free_mask[0];
+        int cnt_w = __builtin_popcountll(fm);
+        while (k >= cnt_w && gw + 1 < ngroups) {
+          k -= cnt_w;
+          fm = free_mask[++gw];
+          cnt_w = __builtin_popcountll(fm);
+        }
+        own = min(64 * gw + select_bit(fm, k), W - 1);
+      }
+      owner_of[i] = own;
       const int len = lens[par[i]];
       cplen[i] = cw ? (len < 0 ? 0 : len > cap ? cap : len) : 0;
     }
   }
   __syncthreads();
-#pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    const int i = tid + u * FORK_THREADS;
-    if (i < W) owner_of[i] = own_i[u];
-  }
   block_scan(cplen, cpre, W, scan_tmp);  // (its barriers publish owner_of too)
   auto row_blk = [&](int row, int bi) -> int {
     return all_staged ? bts[row * S + bi] : bt_in[((int64_t)r * W + row) * S + bi];
