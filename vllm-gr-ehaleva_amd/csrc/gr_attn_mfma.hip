@@ -72,6 +72,7 @@ typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
 typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
 typedef uint32_t u32x4_t __attribute__((__vector_size__(4 * sizeof(uint32_t))));
+typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 typedef uint32_t u32x2_t __attribute__((__vector_size__(2 * sizeof(uint32_t))));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -1085,13 +1086,18 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   }
 
   // ---- merge the two key halves and write O, LSE --------------------------
-  float* xo = reinterpret_cast<float*>(lds) + rg * (4 * 16 * 64);           // [rg][mb][r][lane]
-  float* xm = reinterpret_cast<float*>(lds) + 4 * (4 * 16 * 64) + rg * 128;  // [rg][m | lsum][lane]
+  // [rg][lane][64 accumulators, padded to 68]: 16-byte writes and reads, the
+  // padding spreads a row of lanes over every bank
+  constexpr int XO_PITCH = 68;
+  float* xo = reinterpret_cast<float*>(lds) + rg * (64 * XO_PITCH) + lane * XO_PITCH;
+  float* xm = reinterpret_cast<float*>(lds) + 4 * (64 * XO_PITCH) + rg * 128;  // [rg][m | lsum][lane]
   if (ks == 1) {
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr) xo[(mb * 16 + rr) * 64 + lane] = o[mb][rr];
+      for (int qd = 0; qd < 4; ++qd)
+        *reinterpret_cast<f32x4_t*>(xo + mb * 16 + qd * 4) =
+            f32x4_t{o[mb][qd * 4], o[mb][qd * 4 + 1], o[mb][qd * 4 + 2], o[mb][qd * 4 + 3]};
     xm[lane] = st.m;
     xm[64 + lane] = st.lsum;
   }
@@ -1113,10 +1119,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
           float v[4];
+          const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(xo + mb * 16 + qd * 4);
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int rr = qd * 4 + u;
-            v[u] = (o[mb][rr] * a0 + xo[(mb * 16 + rr) * 64 + lane] * a1) * inv;
+            v[u] = (o[mb][rr] * a0 + x1[u] * a1) * inv;
           }
           *reinterpret_cast<float4*>(po + mb * 32 + qd * 8) = make_float4(v[0], v[1], v[2], v[3]);
         }
@@ -1132,10 +1139,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
           float v[4];
+          const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(xo + mb * 16 + qd * 4);
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int rr = qd * 4 + u;
-            v[u] = (o[mb][rr] * a0 + xo[(mb * 16 + rr) * 64 + lane] * a1) * inv;
+            v[u] = (o[mb][rr] * a0 + x1[u] * a1) * inv;
           }
           const u32x2_t w = {Mma<DT>::pack2(v[0], v[1]), Mma<DT>::pack2(v[2], v[3])};
           *reinterpret_cast<u32x2_t*>(dst + mb * 32 + qd * 8) = w;
