@@ -364,6 +364,65 @@ __device__ inline void phase_c1(const uint16_t* cur_buf, int kbase, int lane, co
   }
 }
 
+// Phases A and C of a lean step in one body: the first two K fragment reads go
+// out before `mid` (the step's tile loads: scalar work that covers their
+// latency), and the first two V^T fragment reads of phase C during the last
+// two QK MFMAs, so neither phase starts on an LDS round trip.  Same
+// arithmetic, in the same order, as phase_a1<DEFER> followed by phase_c1.
+template <int DT, bool SOFTCAP, typename Mid>
+__device__ inline bool phase_ac(const uint16_t* next_buf, const uint16_t* cur_buf, int kbase, int lane,
+                                const u32x4_t (&qf)[8], const f32x16_t& s_in, f32x16_t& s_out, RowState& st, float c,
+                                float cap, f32x16_t (&o)[4], Mid&& mid) {
+  using M = Mma<DT>;
+  const int lhalf = lane >> 5;
+  const int krow_i = kbase + key_perm(lane & 31);
+  const uint16_t* krow = next_buf + krow_i * KS_PITCH;
+  auto kfrag = [&](int kk) { return lds_read16(krow + kchunk(krow_i, 2 * (kk & 3) + lhalf) * 8 + (kk >> 2) * 64); };
+  const int g = lane >> 4, sl = lane & 15;
+  const uint16_t* vsrc = cur_buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
+  auto vfrag = [&](int j) {
+    const uint16_t* vp = vsrc + (16 * (j >> 2)) * VS_PITCH + 32 * ((j & 3) ^ (sl >> 2));
+    const uint2 lo = lds_read_tr(vp);
+    const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
+    return u32x4_t{lo.x, lo.y, hi.x, hi.y};
+  };
+  const float mref = st.m;
+  u32x4_t kf[8];
+  kf[0] = kfrag(0);
+  kf[1] = kfrag(1);
+  __builtin_amdgcn_sched_barrier(0);
+  mid();
+  __builtin_amdgcn_sched_barrier(0);
+  s_out = f32x16_t{};
+  uint32_t pk[8];
+  u32x4_t vf[8];
+  float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i + 2 < 8) kf[i + 2] = kfrag(i + 2);
+    else vf[i - 6] = vfrag(i - 6);
+    s_out = M::mma(kf[i], qf[i], s_out);
+    const float e0 = weight1<SOFTCAP>(s_in[2 * i], c, cap, mref);
+    const float e1 = weight1<SOFTCAP>(s_in[2 * i + 1], c, cap, mref);
+    acc0 += e0;
+    acc1 += e1;
+    pk[i] = M::pack2(e0, e1);
+    __asm__ volatile("" : "+v"(acc0), "+v"(acc1), "+v"(pk[i]));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const u32x4_t p0 = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
+  const u32x4_t p1 = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
+  const float acc = acc0 + acc1;
+  st.lsum += acc;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j + 2 < 8) vf[j + 2] = vfrag(j + 2);
+    o[j & 3] = M::mma(vf[j], j < 4 ? p0 : p1, o[j & 3]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return !(acc <= Rescale<DT>::SUM);
+}
+
 // Workgroup barrier once this wave's LDS reads are done and all but its newest
 // INFLIGHT direct-to-LDS tile loads have landed (the compiler does not see
 // those loads: the count is explicit).
@@ -826,9 +885,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // (steps t < n_lean): no run-time choices.
   const int n_lean = lean ? (last_full ? n_st - 3 : n_st - 4) : 0;
   auto lean_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
-    issue_tile_lean(t + 3, (t + 3) % NBUF);
-    hot_seen |= phase_a1<DT, SOFTCAP, true>(lds + ((t + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p);
-    phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
+    hot_seen |= phase_ac<DT, SOFTCAP>(lds + ((t + 1) % NBUF) * BUF, lds + (t % NBUF) * BUF, ks * 32, lane, qf, s_in,
+                                      s_out, st, c, cap, o, [&]() { issue_tile_lean(t + 3, (t + 3) % NBUF); });
     tile_barrier<LOADS_PER_TILE>();
   };
   // fast steps over tiles [it, t_end): S^T alternates between s_cur and s_alt
