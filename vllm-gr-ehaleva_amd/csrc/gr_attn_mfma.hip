@@ -979,6 +979,17 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     }
   }
 
+  // The lane's row indices again, worked out after the prefix loop instead of
+  // being kept live through it (kept, they were spilled to scratch and the
+  // epilogue waited on three dependent scratch reloads for its output address).
+  int tid_e = tid;
+  __asm__ volatile("" : "+v"(tid_e));
+  const int rho_e = row_base + (tid_e >> 7) * 32 + (tid_e & 31);  // row group tid / 128, row tid % 32
+  const bool ok_e = rho_e < rows_r;
+  const int b_e = PREFILL ? 0 : rho_e / TG;
+  const int qi_e = PREFILL ? rho_e / G : (rho_e / G) % a.T;
+  const int g_e = rho_e % G;
+
   // ---- suffix: each row group's beams' own tokens, masked 32-key tiles ----
   // (all threads load; the two waves of a row group compute a pair of tiles
   // side by side; the group's metadata was staged in the prologue)
@@ -1088,12 +1099,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // this wave's row group against tile h of the pair
   auto suf_compute = [&](int h) {
     // register r of this lane is slot 16*(r>>3) + 8*lhalf + (r&7) of the group's 32
-    const int lim = row_ok ? my_len - a.T + my_qi : -1;
+    const int lim = ok_e ? my_len - a.T + qi_e : -1;
     uint32_t vis = 0;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
       const int info = suf_info[h][rg][16 * (rr >> 3) + 8 * lhalf + (rr & 7)];
-      const bool ok = info >= 0 && (info >> 16) == my_b && (info & 0xFFFF) <= lim;
+      const bool ok = info >= 0 && (info >> 16) == b_e && (info & 0xFFFF) <= lim;
       vis |= (ok ? 1u : 0u) << rr;
     }
     const uint16_t* sbuf = lds + (2 * h + (rg >> 1)) * BUF;
@@ -1189,9 +1200,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       if (lhalf == 0)
         a.ws_lse[slot * MF_ROWS + rg * 32 + lrow] =
             lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
-    } else if (row_ok) {
-      const int64_t tok = PREFILL ? (int64_t)(nb0 + my_qi) : (int64_t)(nb0 + my_b) * a.T + my_qi;
-      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + my_g) * HD + 4 * lhalf;
+    } else if (ok_e) {
+      const int64_t tok = PREFILL ? (int64_t)(nb0 + qi_e) : (int64_t)(nb0 + b_e) * a.T + qi_e;
+      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g_e) * HD + 4 * lhalf;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -1208,7 +1219,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         }
       }
       if (a.lse_out && lhalf == 0) {
-        a.lse_out[tok * a.Hq + hk * G + my_g] =
+        a.lse_out[tok * a.Hq + hk * G + g_e] =
             lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
       }
     }
