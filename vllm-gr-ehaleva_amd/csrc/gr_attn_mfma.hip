@@ -955,6 +955,17 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     }
   }
   __syncthreads();
+  // The lane's row indices again, worked out after the prefix loop instead of
+  // being kept live through it (kept, they were spilled to scratch and the
+  // epilogue waited on three dependent scratch reloads for its output address).
+  int tid_e = tid;
+  __asm__ volatile("" : "+v"(tid_e));
+  const int rho_e = row_base + (tid_e >> 7) * 32 + (tid_e & 31);  // row group tid / 128, row tid % 32
+  const bool ok_e = rho_e < rows_r;
+  const int b_e = PREFILL ? 0 : rho_e / TG;
+  const int qi_e = PREFILL ? rho_e / G : (rho_e / G) % a.T;
+  const int g_e = rho_e % G;
+  const int lane_e = tid_e & 63, lhalf_e = lane_e >> 5, lrow_e = lane_e & 31;
   if (hot_flag) {
     // exact recomputation of the workgroup's prefix range, one tile at a time
     // through buffer 0, every tile on the exact (masked) path
@@ -968,27 +979,16 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       uint32_t v = 0;
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
-        const int kl = ks * 32 + 16 * (rr >> 3) + 8 * lhalf + (rr & 7);  // key within the tile
+        const int kl = ks * 32 + 16 * (rr >> 3) + 8 * lhalf_e + (rr & 7);  // key within the tile
         v |= (PREFILL ? t * ST_KEYS + kl <= lim : kl < nk) ? 1u << rr : 0u;
       }
       const uint32_t vis[1] = {v};
-      const f32x16_t s1[1] = {qk_half<DT>(lds, ks * 32, lane, qf)};
+      const f32x16_t s1[1] = {qk_half<DT>(lds, ks * 32, lane_e, qf)};
       weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, p, o);
-      pv<DT, 1>(lds, ks * 32, lane, p, o);
+      pv<DT, 1>(lds, ks * 32, lane_e, p, o);
       __syncthreads();
     }
   }
-
-  // The lane's row indices again, worked out after the prefix loop instead of
-  // being kept live through it (kept, they were spilled to scratch and the
-  // epilogue waited on three dependent scratch reloads for its output address).
-  int tid_e = tid;
-  __asm__ volatile("" : "+v"(tid_e));
-  const int rho_e = row_base + (tid_e >> 7) * 32 + (tid_e & 31);  // row group tid / 128, row tid % 32
-  const bool ok_e = rho_e < rows_r;
-  const int b_e = PREFILL ? 0 : rho_e / TG;
-  const int qi_e = PREFILL ? rho_e / G : (rho_e / G) % a.T;
-  const int g_e = rho_e % G;
 
   // ---- suffix: each row group's beams' own tokens, masked 32-key tiles ----
   // (all threads load; the two waves of a row group compute a pair of tiles
@@ -1103,16 +1103,16 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     uint32_t vis = 0;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
-      const int info = suf_info[h][rg][16 * (rr >> 3) + 8 * lhalf + (rr & 7)];
+      const int info = suf_info[h][rg][16 * (rr >> 3) + 8 * lhalf_e + (rr & 7)];
       const bool ok = info >= 0 && (info >> 16) == b_e && (info & 0xFFFF) <= lim;
       vis |= (ok ? 1u : 0u) << rr;
     }
     const uint16_t* sbuf = lds + (2 * h + (rg >> 1)) * BUF;
-    const f32x16_t s1[1] = {qk_half<DT>(sbuf, (rg & 1) * 32, lane, qf)};
+    const f32x16_t s1[1] = {qk_half<DT>(sbuf, (rg & 1) * 32, lane_e, qf)};
     const uint32_t vis1[1] = {vis};
     u32x4_t pw[1][2];
     weights<DT, SOFTCAP, true, 1>(s1, vis1, st, c, cap, pw, o);
-    pv<DT, 1>(sbuf, (rg & 1) * 32, lane, pw, o);
+    pv<DT, 1>(sbuf, (rg & 1) * 32, lane_e, pw, o);
   };
   // Tiles in pairs: the key-half-0 wave of each row group takes the first
   // tile, the key-half-1 wave the second, at the same time (each adds to its
@@ -1158,7 +1158,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // [rg][lane][64 accumulators, padded to 68]: 16-byte writes and reads, the
   // padding spreads a row of lanes over every bank
   constexpr int XO_PITCH = 68;
-  float* xo = reinterpret_cast<float*>(lds) + rg * (64 * XO_PITCH) + lane * XO_PITCH;
+  float* xo = reinterpret_cast<float*>(lds) + rg * (64 * XO_PITCH) + lane_e * XO_PITCH;
   float* xm = reinterpret_cast<float*>(lds) + 4 * (64 * XO_PITCH) + rg * 128;  // [rg][m | lsum][lane]
   if (ks == 1) {
 #pragma unroll
@@ -1167,12 +1167,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       for (int qd = 0; qd < 4; ++qd)
         *reinterpret_cast<f32x4_t*>(xo + mb * 16 + qd * 4) =
             f32x4_t{o[mb][qd * 4], o[mb][qd * 4 + 1], o[mb][qd * 4 + 2], o[mb][qd * 4 + 3]};
-    xm[lane] = st.m;
-    xm[64 + lane] = st.lsum;
+    xm[lane_e] = st.m;
+    xm[64 + lane_e] = st.lsum;
   }
   __syncthreads();
   if (ks == 0) {
-    const float m1 = xm[lane], l1 = xm[64 + lane];
+    const float m1 = xm[lane_e], l1 = xm[64 + lane_e];
     const float m0 = st.m, l0 = st.lsum;
     const float m = fmaxf(m0, m1);
     const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
@@ -1182,7 +1182,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     if constexpr (SPLIT) {
       // this split's normalised partial O and LSE, every row of the tile
       const int64_t slot = (int64_t)(unit * mtiles + mt) * nsplit + split;
-      float* po = a.ws_o + (slot * MF_ROWS + rg * 32 + lrow) * HD + 4 * lhalf;
+      float* po = a.ws_o + (slot * MF_ROWS + rg * 32 + lrow_e) * HD + 4 * lhalf_e;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -1197,12 +1197,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
           *reinterpret_cast<float4*>(po + mb * 32 + qd * 8) = make_float4(v[0], v[1], v[2], v[3]);
         }
       }
-      if (lhalf == 0)
-        a.ws_lse[slot * MF_ROWS + rg * 32 + lrow] =
+      if (lhalf_e == 0)
+        a.ws_lse[slot * MF_ROWS + rg * 32 + lrow_e] =
             lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
     } else if (ok_e) {
       const int64_t tok = PREFILL ? (int64_t)(nb0 + qi_e) : (int64_t)(nb0 + b_e) * a.T + qi_e;
-      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g_e) * HD + 4 * lhalf;
+      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g_e) * HD + 4 * lhalf_e;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -1218,7 +1218,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
           *reinterpret_cast<u32x2_t*>(dst + mb * 32 + qd * 8) = w;
         }
       }
-      if (a.lse_out && lhalf == 0) {
+      if (a.lse_out && lhalf_e == 0) {
         a.lse_out[tok * a.Hq + hk * G + g_e] =
             lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
       }
