@@ -702,9 +702,50 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     for (int kk = 0; kk < 8; ++kk) qf[kk] = *reinterpret_cast<const u32x4_t*>(row_ok ? src + kk * 16 : zq);
   }
 
+  // Lean loads of the loop's full tiles.  When every block id of the range sits
+  // in the first staged window (which then never moves), a block holds at
+  // least 8 keys (rows 8 wv .. 8 wv + 7 of a tile share one block) and the
+  // range has at most 64 tiles, lane t of toff_lo / toff_hi holds the byte
+  // offset of tile t's rows of this wave: a tile's four loads then take two
+  // lane reads and scalar address arithmetic, with no LDS round trip and no
+  // window check.  They move exactly what issue_tile moves.
+  const int k_end = min(kb + n_st * ST_KEYS, P);
+  const bool lean = n_st <= 64 && a.bs >= 8 && (n_st == 0 || ((k_end - 1) >> bsh) < PBT_WIN);
+  const bool last_full = kb + n_st * ST_KEYS <= P;
+  // lane t: byte offset of tile t's rows 8 wv .. from the head's K (and V) base
+  uint32_t toff_lo = 0, toff_hi = 0;
+  {
+    const int key = kb + lane * ST_KEYS + 8 * wv;
+    if (lean && lane < n_st && key < P) {
+      const int blk = max(pbt_s[key >> bsh], 0);
+      const uint64_t e = (uint64_t)(uint32_t)blk * blk_stride + (uint64_t)(uint32_t)(key & (a.bs - 1)) * (uint64_t)tok;
+      toff_lo = (uint32_t)(e << 1);
+      toff_hi = (uint32_t)(e >> 31);
+    }
+  }
+  const char* kc_h = reinterpret_cast<const char*>(kc + head_off);
+  const char* vc_h = reinterpret_cast<const char*>(vc + head_off);
+  const uint32_t tok4b = (uint32_t)(8 * tok);  // bytes of four token rows
+  const uint32_t dst_w = lds0 + (uint32_t)(wv * 8 * KS_PITCH * 2);
+  auto issue_tile_lean = [&](int t, int buf) {
+    const uint64_t toff = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)toff_hi, t) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)toff_lo, t);
+    const char* kb0 = kc_h + toff;
+    const char* vb0 = vc_h + toff;
+    const uint32_t d = dst_w + (uint32_t)(buf * BUF * 2);
+    const uint32_t dst[4] = {d, d + K_TILE * 2, d + 1024, d + K_TILE * 2 + 1024};
+    const void* const src[4] = {kb0, vb0, kb0 + tok4b, vb0 + tok4b};
+    const uint32_t off[4] = {vo_k, vo_v, vo_k, vo_v};
+    dma_s4(dst, src, off);
+  };
+  // a prologue tile into its own buffer: lean when it can be
+  auto issue_first = [&](int t) {
+    if (lean && (t + 1 < n_st || last_full)) issue_tile_lean(t, t);
+    else issue_tile(t, t);
+  };
   // the first two tiles, into buffers 0 and 1
-  if (n_st > 0) issue_tile(0, 0);
-  if (n_st > 1) issue_tile(1, 1);
+  if (n_st > 0) issue_first(0);
+  if (n_st > 1) issue_first(1);
   int suf_len = 0, suf_incl = 0;  // this meta lane's validated suffix length, inclusive prefix sum
   if (ks == 0) {
     int len = 0;
@@ -769,7 +810,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // otherwise be a full vector-memory wait placed after the next tile load.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
-  if (n_st > 2) issue_tile(2, 2);
+  if (n_st > 2) issue_first(2);
   f32x16_t s_cur = qk_half<DT>(lds, ks * 32, lane, qf);  // (stale LDS when n_st == 0: never used)
   // One step over a fully visible tile `it` (not the last): consumes its S^T
   // from s_in, leaves that of tile it+1 in s_out.  Keys of an invalid block
@@ -777,42 +818,6 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // Tile t+3 goes out at the top of step t, into buffer (t+3) % 4: its
   // previous tile, t-1, was last read in step t-1, before the barrier that
   // ended it.
-  // Lean loads of the loop's full tiles.  When every block id of the range sits
-  // in the first staged window (which then never moves), a block holds at
-  // least 8 keys (rows 8 wv .. 8 wv + 7 of a tile share one block) and the
-  // range has at most 64 tiles, lane t of toff_lo / toff_hi holds the byte
-  // offset of tile t's rows of this wave: a tile's four loads then take two
-  // lane reads and scalar address arithmetic, with no LDS round trip and no
-  // window check.  They move exactly what issue_tile moves.
-  const int k_end = min(kb + n_st * ST_KEYS, P);
-  const bool lean = n_st <= 64 && a.bs >= 8 && (n_st == 0 || ((k_end - 1) >> bsh) < PBT_WIN);
-  const bool last_full = kb + n_st * ST_KEYS <= P;
-  // lane t: byte offset of tile t's rows 8 wv .. from the head's K (and V) base
-  uint32_t toff_lo = 0, toff_hi = 0;
-  {
-    const int key = kb + lane * ST_KEYS + 8 * wv;
-    if (lean && lane < n_st && key < P) {
-      const int blk = max(pbt_s[key >> bsh], 0);
-      const uint64_t e = (uint64_t)(uint32_t)blk * blk_stride + (uint64_t)(uint32_t)(key & (a.bs - 1)) * (uint64_t)tok;
-      toff_lo = (uint32_t)(e << 1);
-      toff_hi = (uint32_t)(e >> 31);
-    }
-  }
-  const char* kc_h = reinterpret_cast<const char*>(kc + head_off);
-  const char* vc_h = reinterpret_cast<const char*>(vc + head_off);
-  const uint32_t tok4b = (uint32_t)(8 * tok);  // bytes of four token rows
-  const uint32_t dst_w = lds0 + (uint32_t)(wv * 8 * KS_PITCH * 2);
-  auto issue_tile_lean = [&](int t, int buf) {
-    const uint64_t toff = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)toff_hi, t) << 32) |
-                         (uint32_t)__builtin_amdgcn_readlane((int)toff_lo, t);
-    const char* kb0 = kc_h + toff;
-    const char* vb0 = vc_h + toff;
-    const uint32_t d = dst_w + (uint32_t)(buf * BUF * 2);
-    const uint32_t dst[4] = {d, d + K_TILE * 2, d + 1024, d + K_TILE * 2 + 1024};
-    const void* const src[4] = {kb0, vb0, kb0 + tok4b, vb0 + tok4b};
-    const uint32_t off[4] = {vo_k, vo_v, vo_k, vo_v};
-    dma_s4(dst, src, off);
-  };
   auto fetch_ahead = [&](int t) {
     const int tn = t + 3;
     if (tn < n_st) {
