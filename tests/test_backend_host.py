@@ -27,14 +27,93 @@ def test_backend_static_contract():
     assert B.get_supported_kernel_block_sizes() == [ba.MultipleOf(16)]
     assert B.get_kv_cache_shape(10, 16, 8, 128) == (2, 10, 16, 8, 128)
     assert B.get_kv_cache_stride_order() == (0, 1, 2, 3, 4)
-    assert B.get_kv_cache_stride_order(cache_layout="HND") == (0, 1, 3, 2, 4)
     assert B.get_kv_cache_stride_order(True) == (2, 0, 1, 3, 4, 5)
-    with pytest.raises(ValueError):
-        B.get_kv_cache_stride_order(cache_layout="XYZ")
     assert B.get_impl_cls() is ba.BeamAttentionImpl
     assert B.get_builder_cls() is ba.BeamAttentionMetadataBuilder
     for hs, ok in ((8, True), (128, True), (256, True), (12, False), (264, False)):
         assert B.supports_head_size(hs) is ok
+
+
+def test_stride_order_follows_engine_layout(monkeypatch):
+    """get_kv_cache_stride_order reads the layout the engine configured
+    (beam_attn.py:787-798): the override, else $VLLM_KV_CACHE_LAYOUT."""
+    monkeypatch.delenv("VLLM_KV_CACHE_LAYOUT", raising=False)
+    assert ba.get_kv_cache_layout() == "NHD"
+    monkeypatch.setenv("VLLM_KV_CACHE_LAYOUT", "HND")
+    assert B.get_kv_cache_stride_order() == (0, 1, 3, 2, 4)
+    assert B.get_kv_cache_stride_order(True) == (2, 4, 0, 1, 3, 5)
+    try:
+        ba.set_kv_cache_layout("NHD")  # the override wins over the environment
+        assert B.get_kv_cache_stride_order() == (0, 1, 2, 3, 4)
+        ba.set_kv_cache_layout("XYZ")
+        with pytest.raises(ValueError, match="Unknown cache layout"):
+            B.get_kv_cache_stride_order()
+    finally:
+        ba.set_kv_cache_layout(None)
+    assert B.get_kv_cache_stride_order() == (0, 1, 3, 2, 4)
+
+
+def test_fp8_dtype_and_graph_support():
+    assert B.get_fp8_dtype_for_flashattn("fp8") is torch.float8_e4m3fn
+    assert B.get_fp8_dtype_for_flashattn("fp8_e4m3") is torch.float8_e4m3fn
+    with pytest.raises(ValueError, match="Unrecognized FP8 dtype"):
+        B.get_fp8_dtype_for_flashattn("fp8_e5m2")
+    assert ba.BeamAttentionMetadataBuilder._cudagraph_support is ba.AttentionCGSupport.UNIFORM_BATCH
+    assert ba.AttentionCGSupport.UNIFORM_BATCH.value == 2
+
+
+def test_plugin_members_match_reference():
+    """Every member the reference's backend, impl and builder classes define
+    (tests/golden/plugin_members.json, read from beam_attn.py's text with the
+    line of each) exists on the classes here, class members on the class and
+    __init__ members on an instance."""
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "plugin_members.json")) as f:
+        ref = json.load(f)["classes"]
+    impl = ba.BeamAttentionImpl(num_heads=32, head_size=128, scale=0.1, num_kv_heads=8, alibi_slopes=None,
+                                sliding_window=None, kv_cache_dtype="auto")
+    cfg = types.SimpleNamespace(
+        model_config=types.SimpleNamespace(get_num_attention_heads=lambda pc: 32,
+                                           get_num_kv_heads=lambda pc: 8, get_head_size=lambda: 128),
+        parallel_config=None, cache_config=None,
+        compilation_config=types.SimpleNamespace(
+            cudagraph_mode=types.SimpleNamespace(has_full_cudagraphs=lambda: True),
+            max_cudagraph_capture_size=512))
+    builder = ba.BeamAttentionMetadataBuilder(types.SimpleNamespace(block_size=16, dtype=torch.bfloat16),
+                                              ["l0"], cfg, "cpu")
+    assert (builder.num_heads_q, builder.num_heads_kv, builder.headdim) == (32, 8, 128)
+    assert builder.use_full_cuda_graph and builder.max_cudagraph_size == 512
+    assert builder.kv_cache_dtype is torch.bfloat16 and builder.max_num_splits == 0
+    here = {"BeamAttentionBackend": (B, B), "BeamAttentionImpl": (ba.BeamAttentionImpl, impl),
+            "BeamAttentionMetadataBuilder": (ba.BeamAttentionMetadataBuilder, builder)}
+    missing = []
+    for name, kinds in ref.items():
+        cls, inst = here[name]
+        missing += [f"{name}.{m} (beam_attn.py:{ln})" for m, ln in kinds["class"].items() if not hasattr(cls, m)]
+        missing += [f"{name}().{m} (beam_attn.py:{ln})" for m, ln in kinds["instance"].items()
+                    if not hasattr(inst, m)]
+    assert not missing, missing
+    assert impl.supports_quant_query_input and impl.use_cascade
+    assert callable(ba.BeamAttentionImpl.cascade_attention)
+
+
+def test_layer_set_cache_holds_no_tensor():
+    """The fork's per-cache-list pointer cache keeps addresses only: dropping
+    the caches frees them, and the dead entry is evicted on the next lookup."""
+    import gc
+    import weakref
+    from vllm_gr_amd import ops
+    caches = [torch.zeros(2, 4, 16, 2, 8, dtype=torch.bfloat16) for _ in range(3)]
+    ls = ops._layer_set(caches)
+    assert ls.n == 3 and ls.shape == (4, 16, 2, 8)
+    refs = [weakref.ref(c) for c in caches]
+    del caches, ls
+    gc.collect()
+    assert all(r() is None for r in refs)
+    other = [torch.zeros(2, 4, 16, 2, 8, dtype=torch.bfloat16)]
+    ops._layer_set(other)
+    assert all(entry.alive() for entry in ops._LAYER_SETS.values())
 
 
 def test_supports_combination_sinks_accepted():

@@ -10,6 +10,7 @@ the HIP library every call raises.
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 
@@ -107,9 +108,8 @@ def check_status(status: torch.Tensor) -> None:
 
 
 def set_decode_kernel(which: str) -> None:
-    """'auto' (the 32-row matrix-core kernel where supported), 'generic', or
-    'mfma16' (the 64-row matrix-core kernel where it applies)."""
-    code = {"auto": 0, "generic": 1, "mfma16": 2}[which]
+    """'auto' (the matrix-core kernel where supported) or 'generic'."""
+    code = {"auto": 0, "generic": 1}[which]
     _C.check("gr_set_decode_kernel", _C.lib().gr_set_decode_kernel(code))
 
 
@@ -319,7 +319,10 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
 
 class _LayerSet:
     """Validated per-layer K/V base pointers of one list of caches (every
-    layer one geometry), as the host pointer arrays gr_beam_kv_fork_layers takes."""
+    layer one geometry), as the host pointer arrays gr_beam_kv_fork_layers
+    takes.  It holds addresses and geometry only, never the tensors: a cache
+    list that is dropped is freed, and an entry whose caches died is evicted
+    on the next lookup (``alive``)."""
 
     def __init__(self, kv_caches):
         pairs = [split_kv_cache(kv) if isinstance(kv, torch.Tensor) else tuple(kv) for kv in kv_caches]
@@ -330,14 +333,19 @@ class _LayerSet:
                 raise ValueError("every layer's cache must have the same shape and dtype")
             if _cache_strides(k, v) != self.strides or k.device != k0.device or v.device != k0.device:
                 raise ValueError("every layer's cache must have the same strides and device")
-        self.k0 = k0
+        self.shape = tuple(k0.shape)
+        self.device = k0.device
         self.n = len(pairs)
         self.dtype_code = _cache_dtype_code(k0)
         self._k = (ctypes.c_void_p * self.n)(*[k.data_ptr() for k, _ in pairs])
         self._v = (ctypes.c_void_p * self.n)(*[v.data_ptr() for _, v in pairs])
         self.k_ptrs = ctypes.cast(self._k, ctypes.c_void_p)
         self.v_ptrs = ctypes.cast(self._v, ctypes.c_void_p)
-        self.refs = kv_caches  # keeps the tensors (and so their addresses) alive while cached
+        # weak references to the caller's tensors: the entry is valid while they live
+        self._refs = [weakref.ref(t) for kv in kv_caches for t in ((kv,) if isinstance(kv, torch.Tensor) else kv)]
+
+    def alive(self) -> bool:
+        return all(r() is not None for r in self._refs)
 
 
 _LAYER_SETS: dict = {}
@@ -345,11 +353,14 @@ _LAYER_SETS: dict = {}
 
 def _layer_set(kv_caches) -> _LayerSet:
     """The _LayerSet of a list of caches, built once per distinct list (keyed
-    by every cache's address, shape, strides and dtype)."""
+    by every cache's address, shape, strides and dtype).  Entries hold no
+    tensor: those whose caches were freed are dropped here."""
     def sig(kv):
         t = kv if isinstance(kv, torch.Tensor) else kv[0]
         return (t.data_ptr(), tuple(t.shape), t.stride(), t.dtype, isinstance(kv, torch.Tensor),
                 None if isinstance(kv, torch.Tensor) else kv[1].data_ptr())
+    for k in [k for k, ls in _LAYER_SETS.items() if not ls.alive()]:
+        del _LAYER_SETS[k]
     key = tuple(sig(kv) for kv in kv_caches)
     ls = _LAYER_SETS.get(key)
     if ls is None:
@@ -371,8 +382,8 @@ def beam_kv_fork_layers(parent: torch.Tensor, bt_in: torch.Tensor, len_in: torch
     if not kv_caches:
         raise ValueError("kv_caches is empty")
     ls = _layer_set(kv_caches)
-    k0 = ls.k0
-    dev = _need_cuda(parent, bt_in, len_in, k0, bt_out, len_out, status)
+    dev = _need_cuda(parent, bt_in, len_in, kv_caches[0] if isinstance(kv_caches[0], torch.Tensor)
+                     else kv_caches[0][0], bt_out, len_out, status)
     _need_i32("parent", parent)
     _need_i32("bt_in", bt_in)
     _need_i32("len_in", len_in)
@@ -381,7 +392,7 @@ def beam_kv_fork_layers(parent: torch.Tensor, bt_in: torch.Tensor, len_in: torch
     R, W = parent.shape
     if bt_in.dim() != 2 or bt_in.shape[0] != R * W or len_in.numel() != R * W:
         raise ValueError("bt_in must be [R*W, blocks] and len_in [R*W]")
-    NB, bs, Hkv, D = k0.shape
+    NB, bs, Hkv, D = ls.shape
     if bt_out is None:
         bt_out = torch.empty_like(bt_in)
     if len_out is None:

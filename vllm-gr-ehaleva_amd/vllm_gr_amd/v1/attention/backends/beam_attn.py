@@ -64,6 +64,7 @@ from __future__ import annotations
 
 import contextvars
 import copy
+import os
 from dataclasses import dataclass, field
 from enum import Enum
 
@@ -76,6 +77,54 @@ MEGA_DATA_VAR = contextvars.ContextVar("mega_data", default=None)
 
 
 FP8_KV_DTYPES = ("fp8", "fp8_e4m3")
+
+
+class AttentionCGSupport(Enum):
+    """How far a metadata builder's batches can be captured in a device
+    graph: the levels of vLLM's ``AttentionCGSupport`` (vllm==0.14,
+    ``vllm/v1/attention/backend.py``), by the same names and values."""
+    ALWAYS = 3
+    UNIFORM_BATCH = 2
+    UNIFORM_SINGLE_TOKEN_DECODE = 1
+    NEVER = 0
+
+
+_KV_CACHE_LAYOUT_OVERRIDE: str | None = None
+
+
+def set_kv_cache_layout(cache_layout: str | None) -> None:
+    """Set the engine's KV-cache layout ("NHD" / "HND"; None clears it), the
+    role of vLLM's ``set_kv_cache_layout`` (a KV connector's choice)."""
+    global _KV_CACHE_LAYOUT_OVERRIDE
+    _KV_CACHE_LAYOUT_OVERRIDE = cache_layout
+
+
+def get_kv_cache_layout() -> str:
+    """The KV-cache layout the engine configured, read as vLLM's
+    ``get_kv_cache_layout`` (``beam_attn.py:789`` calls it) reads it: the layout
+    set by :func:`set_kv_cache_layout`, else ``$VLLM_KV_CACHE_LAYOUT``, else
+    ``"NHD"``.  Inside a vLLM install the engine's own function is used, so one
+    knob drives both the engine's allocation and this backend's stride order."""
+    try:
+        from vllm.v1.attention.backends.utils import get_kv_cache_layout as engine_layout
+    except ImportError:
+        engine_layout = None
+    if engine_layout is not None:
+        return engine_layout()
+    if _KV_CACHE_LAYOUT_OVERRIDE is not None:
+        return _KV_CACHE_LAYOUT_OVERRIDE
+    return os.environ.get("VLLM_KV_CACHE_LAYOUT") or "NHD"
+
+
+def _batch_invariant() -> bool:
+    """vLLM's ``vllm_is_batch_invariant()``: ``$VLLM_BATCH_INVARIANT`` set to a
+    non-zero integer.  The kernels here are batch invariant either way (a
+    row's reduction order never depends on the batch); the flag is carried
+    for the engine's bookkeeping."""
+    try:
+        return int(os.environ.get("VLLM_BATCH_INVARIANT", "0")) != 0
+    except ValueError:
+        return False
 
 
 class AttentionType(str, Enum):
@@ -158,8 +207,19 @@ class BeamAttentionMetadata:
 
 
 class BeamAttentionMetadataBuilder:
-    """Routes each request of a batch to a decode group (beam_attn.py:163-570)."""
+    """Routes each request of a batch to a decode group (beam_attn.py:163-570).
 
+    ``_cudagraph_support`` is ``UNIFORM_BATCH`` as in the reference
+    (:164), and here it holds: a batch of resident-layout mega requests
+    routes to one decode group whose device tables the caller owns, so its
+    forward is captured once per batch shape and replayed
+    (``vllm_gr_amd.v1.sid_runner``).  The engine configuration the reference
+    reads in ``__init__`` (:167-200) is kept under the same names; the
+    ahead-of-time FlashAttention schedule (``aot_schedule``,
+    ``max_num_splits``) stays off, since the kernels here choose their own
+    split."""
+
+    _cudagraph_support = AttentionCGSupport.UNIFORM_BATCH
     supports_update_block_table: bool = True
 
     def __init__(self, kv_cache_spec, layer_names, vllm_config, device: torch.device):
@@ -168,6 +228,24 @@ class BeamAttentionMetadataBuilder:
         self.vllm_config = vllm_config
         self.device = torch.device(device)
         self.block_size = int(kv_cache_spec.block_size)
+        self.kv_cache_dtype = getattr(kv_cache_spec, "dtype", None)
+        cfg = lambda name: getattr(vllm_config, name, None)
+        self.model_config = cfg("model_config")
+        self.parallel_config = cfg("parallel_config")
+        self.cache_config = cfg("cache_config")
+        self.compilation_config = cfg("compilation_config")
+        mc, pc = self.model_config, self.parallel_config
+        self.num_heads_q = mc.get_num_attention_heads(pc) if mc is not None else None
+        self.num_heads_kv = mc.get_num_kv_heads(pc) if mc is not None else None
+        self.headdim = mc.get_head_size() if mc is not None else None
+        self.max_num_splits = 0
+        self.aot_schedule = False
+        cc = self.compilation_config
+        mode = getattr(cc, "cudagraph_mode", None)
+        self.use_full_cuda_graph = bool(mode is not None and mode.has_full_cudagraphs())
+        self.max_cudagraph_size = getattr(cc, "max_cudagraph_capture_size", None)
+        self.scheduler_metadata = None
+        self.aot_sliding_window: tuple[int, int] | None = None
         # one status word for every batch this builder routes: sticky until
         # the caller clears it (ops.check_status after a synchronisation)
         self.status = ops.new_status(self.device)
@@ -394,7 +472,13 @@ class BeamAttentionMetadataBuilder:
 
 
 class BeamAttentionImpl:
-    """``AttentionImpl`` of the backend (beam_attn.py:575-755)."""
+    """``AttentionImpl`` of the backend (beam_attn.py:575-755).
+
+    ``supports_quant_query_input`` is true as in the reference (:626): with an
+    fp8 cache vLLM then hands ``forward`` an e4m3 query, which is widened to
+    the output dtype times the layer's ``_q_scale`` before the launch (the
+    kernels take fp16/bf16 queries).  ``vllm_flash_attn_version`` is None:
+    no FlashAttention build is involved."""
 
     can_return_lse_for_decode: bool = True
 
@@ -436,6 +520,10 @@ class BeamAttentionImpl:
         self.logits_soft_cap = float(logits_soft_cap or 0.0)
         self.attn_type = attn_type
         self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
+        self.vllm_flash_attn_version = None
+        self.batch_invariant_enabled = _batch_invariant()
+        self.supports_quant_query_input = True
+        self.use_cascade = True
 
     def _kv_scales(self, layer, device):
         """The layer's (_k_scale, _v_scale) as one-element float32 device
@@ -462,9 +550,7 @@ class BeamAttentionImpl:
         copies of the sinks and slopes, made once per device)."""
         opts = self._dev_opts.get(device)
         if opts is None:
-            left, right = self.sliding_window
-            opts = dict(window=(left, right) if left >= 0 or right >= 0 else None,
-                        sinks=None if self.sinks is None else
+            opts = dict(sinks=None if self.sinks is None else
                         self.sinks.detach().to(device=device, dtype=torch.float32).contiguous(),
                         alibi_slopes=None if self.alibi_slopes is None else self.alibi_slopes.to(device))
             self._dev_opts[device] = opts
@@ -491,18 +577,55 @@ class BeamAttentionImpl:
         if self.kv_sharing_target_layer_name is None and key is not None and value is not None:
             ops.reshape_and_cache(key[:n], value[:n], k_cache, v_cache, attn_metadata.slot_mapping,
                                   status=attn_metadata.status, k_scale=k_sc, v_scale=v_sc)
+        if query.dtype == torch.float8_e4m3fn:
+            # a query vLLM quantized for the fp8 cache (supports_quant_query_input)
+            q_scale = getattr(layer, "_q_scale", None) if layer is not None else None
+            query = query.to(output.dtype)
+            if q_scale is not None:
+                query = query * (q_scale.to(device=query.device, dtype=torch.float32).to(output.dtype)
+                                 if isinstance(q_scale, torch.Tensor) else float(q_scale))
         opts = self._options(query.device)
+        BeamAttentionImpl.cascade_attention(
+            output=output, query=query, key_cache=k_cache, value_cache=v_cache, attn_metadata=attn_metadata,
+            sliding_window_size=list(self.sliding_window), scale=self.scale,
+            logits_soft_cap=self.logits_soft_cap, vllm_flash_attn_version=self.vllm_flash_attn_version,
+            s_aux=opts["sinks"], alibi_slopes=opts["alibi_slopes"], k_scale=k_sc, v_scale=v_sc)
+        return output
+
+    @staticmethod
+    def cascade_attention(output: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
+                          value_cache: torch.Tensor, attn_metadata: BeamAttentionMetadata,
+                          sliding_window_size, scale: float, logits_soft_cap: float,
+                          vllm_flash_attn_version=None, s_aux: torch.Tensor | None = None,
+                          alibi_slopes: torch.Tensor | None = None, *, k_scale: torch.Tensor | None = None,
+                          v_scale: torch.Tensor | None = None) -> None:
+        """The attention of ``forward`` after the cache write
+        (beam_attn.py:629-701, same arguments): every decode group is one
+        ``gr_beam_attn_decode`` launch (prefix, suffix and their merge in
+        one kernel) and the standard rows one ``gr_paged_attn_prefill``
+        launch, written into ``output`` in place.  ``sliding_window_size`` is
+        the impl's ``(left, right)`` window ((-1, -1) = none), applied by
+        absolute key position; ``s_aux`` are the sinks; an fp8 cache is read
+        as e4m3 times ``k_scale`` / ``v_scale`` (one-element float32 device
+        tensors).  ``vllm_flash_attn_version`` is accepted and unused."""
+        dev = query.device
+        n = attn_metadata.num_actual_tokens
+        sinks = None if s_aux is None else s_aux.detach().to(device=dev, dtype=torch.float32).contiguous()
+        slopes = None if alibi_slopes is None else alibi_slopes.to(device=dev, dtype=torch.float32).contiguous()
+        left, right = (-1, -1) if sliding_window_size is None else (int(sliding_window_size[0]),
+                                                                     int(sliding_window_size[1]))
+        window = (left, right) if left >= 0 or right >= 0 else None
         # decode attention is causal over the beam's own tokens: its window has no right bound
-        dec_window = None if opts["window"] is None else (opts["window"][0], -1)
+        dec_window = None if window is None else (window[0], -1)
         for g in attn_metadata.groups:
             q = query[:n] if g.token_index is None else query.index_select(0, g.token_index)
             out = output[:n] if g.token_index is None else None
-            res = ops.beam_attn_decode(q, k_cache, v_cache, g.prefix_bt, g.prefix_len, g.beam_start,
+            res = ops.beam_attn_decode(q, key_cache, value_cache, g.prefix_bt, g.prefix_len, g.beam_start,
                                        g.suffix_bt, g.suffix_len, g.suffix_start, q_per_beam=g.q_per_beam,
-                                       scale=self.scale, softcap=self.logits_soft_cap,
+                                       scale=scale, softcap=logits_soft_cap,
                                        max_beams_per_req=g.max_beams, out=out, max_prefix_len=g.max_prefix_len,
-                                       window=dec_window, sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"],
-                                       status=attn_metadata.status, k_scale=k_sc, v_scale=v_sc)
+                                       window=dec_window, sinks=sinks, alibi_slopes=slopes,
+                                       status=attn_metadata.status, k_scale=k_scale, v_scale=v_scale)
             if g.token_index is not None:
                 output.index_copy_(0, g.token_index, res)
         p = attn_metadata.prefill
@@ -510,17 +633,16 @@ class BeamAttentionImpl:
             q = query[:n] if p.token_index is None else query.index_select(0, p.token_index)
             out = output[:n] if p.token_index is None else None
             causal = attn_metadata.causal
-            win = opts["window"]
+            win = window
             if win is not None and causal:
                 win = (win[0], -1)
-            res = ops.paged_attn_prefill(q, k_cache, v_cache, p.block_table, p.query_start, p.seq_len,
-                                         max_query_len=p.max_query_len, scale=self.scale,
-                                         softcap=self.logits_soft_cap, out=out, causal=causal, window=win,
-                                         sinks=opts["sinks"], alibi_slopes=opts["alibi_slopes"],
-                                         status=attn_metadata.status, k_scale=k_sc, v_scale=v_sc)
+            res = ops.paged_attn_prefill(q, key_cache, value_cache, p.block_table, p.query_start, p.seq_len,
+                                         max_query_len=p.max_query_len, scale=scale,
+                                         softcap=logits_soft_cap, out=out, causal=causal, window=win,
+                                         sinks=sinks, alibi_slopes=slopes,
+                                         status=attn_metadata.status, k_scale=k_scale, v_scale=v_scale)
             if p.token_index is not None:
                 output.index_copy_(0, p.token_index, res)
-        return output
 
 
 class BeamAttentionBackend:
@@ -556,13 +678,22 @@ class BeamAttentionBackend:
         return (2, num_blocks, block_size, num_kv_heads, head_size)
 
     @staticmethod
-    def get_kv_cache_stride_order(include_num_layers_dimension: bool = False, cache_layout: str = "NHD"):
-        # the kernels take block/token/head strides, so both layouts run as is
+    def get_kv_cache_stride_order(include_num_layers_dimension: bool = False) -> tuple[int, ...]:
+        # the layout the engine configured (get_kv_cache_layout); the kernels
+        # take block/token/head strides, so both layouts run as is
+        cache_layout = get_kv_cache_layout()
         if cache_layout == "NHD":
             return (2, 0, 1, 3, 4, 5) if include_num_layers_dimension else (0, 1, 2, 3, 4)
         if cache_layout == "HND":
             return (2, 4, 0, 1, 3, 5) if include_num_layers_dimension else (0, 1, 3, 2, 4)
         raise ValueError(f"Unknown cache layout format {cache_layout}.")
+
+    @staticmethod
+    def get_fp8_dtype_for_flashattn(kv_cache_dtype: str) -> torch.dtype:
+        """The storage dtype of an fp8 cache (beam_attn.py:800-804): e4m3 only."""
+        if kv_cache_dtype in FP8_KV_DTYPES:
+            return torch.float8_e4m3fn
+        raise ValueError(f"Unrecognized FP8 dtype: {kv_cache_dtype}")
 
     @classmethod
     def supports_head_size(cls, head_size: int) -> bool:
