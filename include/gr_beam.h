@@ -55,10 +55,8 @@ const char* gr_status_string(gr_status_t status);
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
 int gr_version(void);
 /* Decode kernel selection for tests and measurement (no reference
- * counterpart): 0 = automatic (the 32-row matrix-core kernel where
- * supported, else the generic one), 1 = always the generic kernel, 2 = the
- * 64-row matrix-core kernel where it applies (head_dim 128, block size 16 ..
- * 256), else as 0.  Process-wide. */
+ * counterpart): 0 = automatic (the matrix-core kernel where supported, else
+ * the generic one), 1 = always the generic kernel.  Process-wide. */
 gr_status_t gr_set_decode_kernel(int which);
 
 /*
@@ -329,7 +327,7 @@ gr_status_t gr_beam_kv_append(
  * vocab % 4 == 0, 16-byte aligned rows), cum [num_reqs*beam_width] float32.
  * score(b, v) = (double)x + ((double)cum[b] - lse[b]), lse[b] = (double)m +
  * log(S) with m the row max and S the float32 sum of exp(x - m), each term
- * computed as exp2 of (x - m) * log2(e) by a degree-7 Taylor polynomial and
+ * computed as exp2 of (x - m) * log2(e) by a degree-5 polynomial fit and
  * summed in a fixed order (256 threads x float4 groups, then a xor
  * butterfly per 64-lane wave, then (w0 + w1) + (w2 + w3)); the log is an
  * atanh-series float64 evaluation.  All steps are single IEEE operations, so
@@ -409,7 +407,10 @@ gr_status_t gr_beam_prune_topk_noalloc(
  * offline twin vllm_gr/entrypoints/llm.py:231-245).  cum [R*W] float64 is
  * used as is (c_b = cum[b] - lse[b]); score [R, k] and eos_score [R*W]
  * receive the float64 scores themselves, not their float32 roundings, so a
- * multi-step search never rounds a beam's score.  Selection, order, ties
+ * multi-step search never rounds a beam's score.  One departure: a
+ * candidate's score is cum + (x - lse) rounded once in float64, where the
+ * reference adds the sampler's float32 logprob, cum + float64(float32(x -
+ * lse)); the two differ by at most one float32 ulp of the logprob.  Selection, order, ties
  * and workspace as in gr_beam_prune_topk.  beam_node == NULL: no catalog
  * (the trie arguments and node_out are ignored); otherwise the catalog mode
  * of gr_beam_prune_topk_catalog.

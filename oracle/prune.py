@@ -19,7 +19,10 @@ Functions and how each is pinned (tests/test_oracle_prune.py):
   ``:1229-1248``); against all-equal logits (lowest flat index wins); and,
   when ``oracle/_ref`` was built from the reference sources, against the
   reference's own ``MinHeapTuple.push_candidates_striped``
-  (``vllm_gr/csrc/minheap.cpp:75-114``) on tie-free data.
+  (``vllm_gr/csrc/minheap.cpp:75-114``) on tie-free data; and, at the full
+  64 x 128 x 8192 size, against ``topk_float64_global`` (vectorised float64
+  mathematics, checked itself against ``prune_topk_float64`` on small cases):
+  the same selections wherever the float64 128th/129th gap exceeds 1e-6.
 """
 
 from __future__ import annotations
@@ -171,6 +174,38 @@ def prune_topk_float64(logits: np.ndarray, cum: np.ndarray, k: int, eos_token_id
         out_token[r, :len(sel)] = cand_f[sel] % V
         out_score[r, :len(sel)] = cand_s[sel]
     return dict(parent=out_parent, token=out_token, score=out_score)
+
+
+def topk_float64_global(logits: np.ndarray, cum: np.ndarray, k: int):
+    """Plain float64 mathematics of the pruning at any size, vectorised:
+    ``score = cum + log_softmax(logits)`` in float64, then per request the
+    top-k of all W x V candidates by (score desc, flat index asc) -- the
+    global selection the reference's two stages compute
+    (``serving_engine.py:511,538-539,566-567``; a global top-k element is
+    within its beam's top-k).  Returns ``parent``, ``token``, ``score``
+    (float64, ``[R, k]``) and ``gap`` (``[R]``): the k-th score minus the
+    (k+1)-th, the margin by which the selected set is determined."""
+    x = np.asarray(logits, dtype=np.float32)
+    R, W, V = x.shape
+    parent = np.empty((R, k), np.int64)
+    token = np.empty((R, k), np.int64)
+    score = np.empty((R, k))
+    gap = np.empty(R)
+    cum64 = np.asarray(cum, dtype=np.float64).reshape(R, W)
+    for r in range(R):  # one request at a time: W x V float64 scores
+        x64 = x[r].astype(np.float64)
+        m = x64.max(axis=1, keepdims=True)
+        lse = m + np.log(np.exp(x64 - m).sum(axis=1, keepdims=True))
+        s = ((x64 - lse) + cum64[r][:, None]).reshape(-1)
+        n = min(k + 1, s.size)
+        part = np.argpartition(-s, n - 1)[:n]
+        o = np.lexsort((part, -s[part]))
+        part = part[o]
+        parent[r] = part[:k] // V
+        token[r] = part[:k] % V
+        score[r] = s[part[:k]]
+        gap[r] = s[part[k - 1]] - s[part[k]] if n > k else np.inf
+    return dict(parent=parent, token=token, score=score, gap=gap)
 
 
 def ref_minheap_module():

@@ -83,6 +83,7 @@ def test_decode_argument_checks(built_lib):
     assert _decode(lib, q_tok_stride=100) == _C.GR_ERR_INVALID_ARG
     assert _decode(lib, T=0) == _C.GR_ERR_INVALID_ARG
     assert lib.gr_set_decode_kernel(5) == _C.GR_ERR_INVALID_ARG
+    assert lib.gr_set_decode_kernel(2) == _C.GR_ERR_INVALID_ARG
 
 
 def test_fork_append_prune_argument_checks(built_lib):

@@ -297,3 +297,60 @@ def test_float64_cum_planted_flip():
     assert (got64["parent"][0, 0], got64["token"][0, 0]) == (1, 7)
     assert (got32["parent"][0, 0], got32["token"][0, 0]) == (0, 7)
     assert got64["score64"][0, 0] - got32["score64"][0, 0] == 2.0 ** -30
+
+
+def test_topk_float64_global_matches_two_stage():
+    """The vectorised float64 selection equals the per-beam-then-union one."""
+    for seed, (R, W, V, k) in enumerate([(3, 16, 300, 16), (2, 5, 64, 7), (1, 1, 40, 3)]):
+        x, cum = _rand(R, W, V, seed=100 + seed)
+        g = op.topk_float64_global(x, cum, k)
+        two = op.prune_topk_float64(x, cum, k)
+        np.testing.assert_array_equal(g["parent"], two["parent"])
+        np.testing.assert_array_equal(g["token"], two["token"])
+        np.testing.assert_allclose(g["score"], two["score"], rtol=0, atol=1e-12)
+
+
+def test_prune_full_size_vs_float64_mathematics():
+    """At the full 64 x 128 x 8192 pruning (logits N(0, 3^2), cum U(-20, 0)),
+    the C restatement selects what float64 mathematics selects, in the same
+    order, for every request whose 128th/129th float64 gap exceeds 1e-6 (all
+    of them at seed 0), with scores within 1e-6."""
+    from vllm_gr_amd import workloads
+    wl = workloads.prune_beam128(seed=0)
+    x, cum = wl.logits.numpy(), wl.cum.numpy()
+    ref = op.topk_float64_global(x, cum, wl.k)
+    got = op.prune_topk(x, cum, wl.k)
+    firm = ref["gap"] > 1e-6
+    print(f"requests with a 128th/129th gap <= 1e-6: {int((~firm).sum())} of {len(firm)}")
+    assert firm.sum() >= len(firm) - 2
+    for r in np.nonzero(firm)[0]:
+        np.testing.assert_array_equal(got["parent"][r], ref["parent"][r])
+        np.testing.assert_array_equal(got["token"][r], ref["token"][r])
+    np.testing.assert_allclose(got["score64"], ref["score"], rtol=0, atol=1e-6)
+
+
+def test_f64_scores_vs_float32_logprob_scores():
+    """Departure, measured: the float64 path scores a candidate as
+    ``cum + (x - lse)`` in float64 (one rounding); the reference adds vLLM's
+    float32 logprob to a Python float, ``cum + float64(float32(x - lse))``
+    (serving_engine.py:511; llm.py's ``cum_logprob + lp``).  The two differ by
+    up to one float32 ulp of the logprob.  At the full 64 x 128 x 8192 size
+    (seed 0) they select the same (parent, token) lists in the same order for
+    every request."""
+    from vllm_gr_amd import workloads
+    wl = workloads.prune_beam128(seed=0)
+    x, cum = wl.logits.numpy(), wl.cum.numpy().astype(np.float64)
+    k = wl.k
+    got = op.prune_topk(x, cum, k)
+    R, W, V = x.shape
+    differ = 0
+    for r in range(R):
+        m = x[r].max(1, keepdims=True)
+        lse32 = (m + np.log(np.exp(x[r] - m).sum(1, keepdims=True, dtype=np.float32))).astype(np.float32)
+        lp32 = (x[r] - lse32).astype(np.float32)  # the sampler's float32 logprobs
+        s = (cum[r][:, None] + lp32.astype(np.float64)).reshape(-1)
+        part = np.argpartition(-s, k)[:k]
+        part = part[np.lexsort((part, -s[part]))]
+        differ += not np.array_equal(part, got["parent"][r] * V + got["token"][r])
+    print(f"requests whose selection differs between the two score forms: {differ} of {R}")
+    assert differ == 0

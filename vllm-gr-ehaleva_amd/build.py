@@ -34,7 +34,6 @@ EXTRA = {
     "gr_prune.hip": ["-ffp-contract=off", "-Wno-pass-failed"],
     # masking uses -inf, never NaN: lets fmaxf lower to v_max3_f32 without canonicalisation
     "gr_attn_mfma.hip": ["-fno-honor-nans"],
-    "gr_attn_mfma16.hip": ["-fno-honor-nans"],
 }
 
 

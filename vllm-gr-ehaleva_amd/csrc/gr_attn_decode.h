@@ -60,14 +60,8 @@ gr_status_t launch_mfma_decode_split(const DecodeArgs& a, hipStream_t stream);
 void mfma_decode_plan(int num_reqs, int max_beams, int q_per_beam, int Hq, int Hkv, int max_prefix_len,
                       int* tiles, int* nsplit);
 
-// 64-row-per-wave MFMA decode (gr_attn_mfma16.hip): selected by
-// gr_set_decode_kernel(2) where supported (the unsplit decode mode only).
-bool d16_decode_supported(const DecodeArgs& a);
-gr_status_t launch_d16_decode(const DecodeArgs& a, hipStream_t stream);
-
-// 0 = choose automatically (the 32-row MFMA kernel where supported), 1 =
-// always the generic kernel, 2 = the 64-row MFMA kernel where supported
-// (testing and measurement hook).
+// 0 = choose automatically (the MFMA kernel where supported), 1 = always the
+// generic kernel (testing and measurement hook).
 extern int g_decode_kernel_override;
 
 }  // namespace gr

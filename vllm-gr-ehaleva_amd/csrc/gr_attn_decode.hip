@@ -393,7 +393,6 @@ extern "C" gr_status_t gr_beam_attn_decode(
   bool empty;
   const gr_status_t st = decode_args(a, empty, GR_DECODE_ARG_NAMES);
   if (st != GR_OK || empty) return st;
-  if (g_decode_kernel_override == 2 && d16_decode_supported(a)) return launch_d16_decode(a, stream);
   if (g_decode_kernel_override != 1 && mfma_decode_supported(a)) return launch_mfma_decode(a, stream);
   return launch_generic<false>(a, stream);
 }
@@ -446,10 +445,7 @@ static gr_status_t decode_ws_impl(
   int tiles, nsplit;
   mfma_decode_plan(num_reqs, max_beams_per_req, q_per_beam, num_q_heads, num_kv_heads, max_prefix_len, &tiles,
                    &nsplit);
-  if (nsplit <= 1) {
-    if (g_decode_kernel_override == 2 && d16_decode_supported(a)) return launch_d16_decode(a, stream);
-    return launch_mfma_decode(a, stream);
-  }
+  if (nsplit <= 1) return launch_mfma_decode(a, stream);
   const SplitLayout l = split_layout(tiles, nsplit);
   if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || workspace_bytes < l.total)
     return GR_ERR_WORKSPACE;
@@ -558,7 +554,7 @@ extern "C" gr_status_t gr_paged_attn_prefill_opt(
 
 
 extern "C" int gr_set_decode_kernel(int which) {
-  if (which < 0 || which > 2) return GR_ERR_INVALID_ARG;
+  if (which < 0 || which > 1) return GR_ERR_INVALID_ARG;
   g_decode_kernel_override = which;
   return GR_OK;
 }

@@ -587,6 +587,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       pbt_s[i] = blk;
     }
   };
+  int bad_blk = 0;
 #pragma unroll
   for (int i = 0; i < WIN_PER_THREAD; ++i) {
     const int bi = tid + i * MF_THREADS;
@@ -596,12 +597,15 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       if (blk < 0 || blk >= a.num_blocks) {
         flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
         blk = -1;
+        bad_blk = 1;
       }
     }
     pbt_s[tid + i * MF_THREADS] = blk;
   }
   if (tid == 0) hot_flag = 0;
-  __syncthreads();
+  // a flagged block id in the first window: its keys read the zero source,
+  // which only the general tile loads do (the lean loads below assume none)
+  const bool win_bad = __syncthreads_or(bad_blk) != 0;
 
   // keep the window over [k0, k0 + 64); switching costs two barriers and
   // happens once per PBT_WIN blocks
@@ -636,9 +640,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // Prefix tile t of this workgroup's range into buffer buf: the wave-uniform
   // addresses of its four loads (prep_tile, which may move the block-table
   // window), then the loads one at a time (issue_load n: K of rows 8 wv + 4 j,
-  // then their V, j = n >> 1).  An invalid block (flagged when the window was
-  // staged) reads block 0 in a whole tile; rows past the prefix read the zero
-  // source.
+  // then their V, j = n >> 1).  Rows of an invalid block (flagged when the
+  // window was staged) and rows past the prefix read the zero source.
   struct TileLoads {
     int64_t el[2];  // element offset of rows 8 wv + 4 j in the K and V caches
     int key[2], blk[2];
@@ -664,7 +667,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const bool isv = n & 1;
     const uint32_t d = L.dst + (isv ? K_TILE * 2 : 0) + j * 1024;
     const S* base = (isv ? vc : kc) + L.el[j];
-    if (L.key[j] + 4 <= P) {
+    if (L.key[j] + 4 <= P && L.blk[j] >= 0) {
       dma_s(d, base, isv ? vo_v : vo_k);
     } else {
       const bool ok = L.blk[j] >= 0 && L.key[j] + q4 < P;
@@ -705,12 +708,13 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // Lean loads of the loop's full tiles.  When every block id of the range sits
   // in the first staged window (which then never moves), a block holds at
   // least 8 keys (rows 8 wv .. 8 wv + 7 of a tile share one block) and the
-  // range has at most 64 tiles, lane t of toff_lo / toff_hi holds the byte
-  // offset of tile t's rows of this wave: a tile's four loads then take two
-  // lane reads and scalar address arithmetic, with no LDS round trip and no
-  // window check.  They move exactly what issue_tile moves.
+  // range has at most 64 tiles, and no block id of the window was flagged,
+  // lane t of toff_lo / toff_hi holds the byte offset of tile t's rows of this
+  // wave: a tile's four loads then take two lane reads and scalar address
+  // arithmetic, with no LDS round trip and no window check.  They move
+  // exactly what issue_tile moves.
   const int k_end = min(kb + n_st * ST_KEYS, P);
-  const bool lean = n_st <= 64 && a.bs >= 8 && (n_st == 0 || ((k_end - 1) >> bsh) < PBT_WIN);
+  const bool lean = !win_bad && n_st <= 64 && a.bs >= 8 && (n_st == 0 || ((k_end - 1) >> bsh) < PBT_WIN);
   const bool last_full = kb + n_st * ST_KEYS <= P;
   // lane t: byte offset of tile t's rows 8 wv .. from the head's K (and V) base
   uint32_t toff_lo = 0, toff_hi = 0;
@@ -1283,6 +1287,7 @@ bool mfma_decode_supported(const DecodeArgs& a) {
   if (a.D != HD || (a.dtype != GR_DTYPE_BF16 && a.dtype != GR_DTYPE_F16)) return false;
   if (has_options(a)) return false;  // windows, sinks, ALiBi, non-causal: the generic kernel
   if (a.bs_shift < 2) return false;  // power-of-two block size >= 4
+  if (a.num_blocks < 1) return false;  // an empty pool: the generic kernel reads nothing
   // the suffix tiles tag each key with its 16-bit index within the beam's suffix
   if ((int64_t)a.suffix_bt_stride * a.bs > 0xFFFF) return false;
   // 16-byte vector access: base pointers and element strides multiples of 8 elements
