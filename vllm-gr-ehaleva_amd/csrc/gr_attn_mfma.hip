@@ -16,412 +16,21 @@
 // waves of a row group (two partial states) are merged in LDS at the end.
 // One launch, no gather/merge passes over HBM (contrast beam_attn.py:656-699).
 //
-// MFMA formulation (v_mfma_f32_32x32x16_{bf16,f16}, wave64):
-//   S^T[key][row]  = K[key][:] . Q[row][:]    A = K tile, B = Q^T (registers)
-//   O^T[d][row]   += V^T[d][key] . P^T[key][row]
-// so every lane owns one query row (lane % 32) in both accumulators and the
-// online softmax needs no cross-lane traffic except the lane-pair (l, l^32)
-// max/sum.  K rows are fed to the A operand through the permutation PI that
-// swaps bits 2 and 3 of the row index; with it the S^T accumulator registers
-// of each lane hold keys in exactly the order the PV B operand needs.  V stays
-// in its natural [key][d] layout in LDS (64-byte segments XOR-swizzled per
-// row, see vchunk) and the V^T operand is assembled with
-// gfx950's transposing LDS read (ds_read_b64_tr_b16): in each 16-lane group,
-// source lane s addresses V[k0 + s/4][d0 + 4*(s%4) .. +3] and lane i receives
-// V[k0 .. k0+3][d0 + i].
+// MFMA formulation and tile layouts: gr_mfma_tile.h.
 #include <algorithm>
 
-#include "gr_attn_decode.h"
+#include "gr_mfma_tile.h"
 
 namespace gr {
 namespace {
 
 constexpr int MF_THREADS = 512;
 constexpr int MF_ROWS = 128;   // query rows per workgroup
-constexpr int ST_KEYS = 64;    // keys per super-tile (two 32-key halves)
-constexpr int HD = 128;        // head dim
-constexpr int KS_PITCH = 128;  // K tile row pitch in elements (256 B); 16-byte chunks XOR-swizzled
-constexpr int VS_PITCH = 128;  // V tile row pitch in elements (256 B); 64-byte segments XOR-swizzled
-constexpr int K_TILE = ST_KEYS * KS_PITCH;
-constexpr int V_TILE = ST_KEYS * VS_PITCH;
-constexpr int BUF = K_TILE + V_TILE;  // elements per buffer (32 KB)
-constexpr float LOG2E = 1.4426950408889634f;
-// Lazy softmax reference: a key may exceed the row's reference by up to
-// Rescale::THRESH log2 units before the exact path moves the reference; a lane
-// weight sum above 2^Rescale::THRESH forces it.  The packed P operand bounds
-// the margin: 60 for bf16 (range to 2^127), 15 for fp16 (largest finite value
-// 65504 < 2^16).
-template <int DT> struct Rescale;
-template <> struct Rescale<GR_DTYPE_BF16> {
-  static constexpr float THRESH = 60.0f;
-  static constexpr float SUM = 1.152921504606846976e18f;  // 2^60
-};
-template <> struct Rescale<GR_DTYPE_F16> {
-  static constexpr float THRESH = 15.0f;
-  static constexpr float SUM = 32768.0f;  // 2^15
-};
-static_assert(Rescale<GR_DTYPE_BF16>::SUM == (float)(1ull << 60) && Rescale<GR_DTYPE_F16>::SUM == (float)(1 << 15),
-              "Rescale::SUM is 2^THRESH");
 constexpr int PBT_WIN = 2048;  // prefix block-table entries staged in LDS
 constexpr int NBUF = 4;        // tile buffers: prefix tile t in buffer t % 4 (V of t and K of t+1 read during
                                // step t while tiles t+2 and t+3 land); a suffix tile pair takes all four
 constexpr int LOADS_PER_TILE = 4;  // direct-to-LDS loads each wave issues per prefix tile
 constexpr int SB_STAGE = 2;    // suffix block ids staged in LDS per beam (more are read from HBM)
-
-typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
-typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
-typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
-typedef uint32_t u32x4_t __attribute__((__vector_size__(4 * sizeof(uint32_t))));
-typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
-typedef uint32_t u32x2_t __attribute__((__vector_size__(2 * sizeof(uint32_t))));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-
-// Zero source for loads of keys outside the prefix or in an invalid block.
-__device__ __attribute__((aligned(16))) uint32_t g_zero16[4];
-
-template <int DT> struct Mma;
-template <> struct Mma<GR_DTYPE_BF16> {
-  using vec = bf16x8_t;
-  __device__ static inline f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(vec, a),
-                                                   __builtin_bit_cast(vec, b), c, 0, 0, 0);
-  }
-  __device__ static inline uint32_t pack2(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});  // one v_cvt_pk_bf16_f32
-  }
-};
-template <> struct Mma<GR_DTYPE_F16> {
-  using vec = f16x8_t;
-  __device__ static inline f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(vec, a),
-                                                  __builtin_bit_cast(vec, b), c, 0, 0, 0);
-  }
-  __device__ static inline uint32_t pack2(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)lo, (_Float16)hi});
-  }
-};
-
-// S^T row slot i holds tile key PI(i): bits 2 and 3 swapped.
-__device__ inline int key_perm(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
-
-// Physical 16-byte chunk of logical chunk c in K tile row `row`.  The A
-// operand reads rows PI(0..7) = {0..3, 8..11} (and +4, +16) in one 8-lane
-// group; the XOR spreads those rows over 8 distinct 16-byte bank groups.
-__device__ inline int kchunk(int row, int c) { return c ^ ((row & 3) | (((row >> 3) & 1) << 2)); }
-// Physical 16-byte chunk of logical chunk c in V tile row `row`: the 64-byte
-// segment c >> 2 (32 dims) sits at segment (c >> 2) ^ (row & 3), so the four
-// rows that one half-wave of a transposing read touches (keys k0 .. k0 + 3,
-// 64 bytes each) cover all 64 banks.
-__device__ inline int vchunk(int row, int c) { return (((c >> 2) ^ (row & 3)) << 2) | (c & 3); }
-
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-// 4 keys x 1 dim per lane via the transposing LDS read (see the header comment)
-__device__ inline uint2 lds_read_tr(const uint16_t* p) {
-  auto v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4_t*)(reinterpret_cast<uintptr_t>(p)));
-  return __builtin_bit_cast(uint2, v);
-}
-
-// Value of x held by lane l ^ 32 (the other lane of the same query row).
-// v_permlane32_swap exchanges the upper 32 lanes of its first operand with the
-// lower 32 lanes of its second: with both operands = x, lanes 0..31 find the
-// partner in the second result and lanes 32..63 in the first.  The half is
-// selected explicitly: the compiler folds fmaxf(v[0], v[1]) to v[0] when both
-// operands are the same value, which drops the partner on lanes 0..31.
-__device__ inline float lane_partner(float x) {
-  auto v = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
-                                            __builtin_bit_cast(uint32_t, x), false, false);
-  return __builtin_bit_cast(float, (threadIdx.x & 32) ? v[0] : v[1]);
-}
-// max / sum over the lane pair (l, l ^ 32); both lanes get the same result
-__device__ inline float pair_max(float x) { return fmaxf(x, lane_partner(x)); }
-__device__ inline float pair_sum(float x) { return x + lane_partner(x); }
-
-__device__ inline u32x4_t lds_read16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
-
-// Per-lane online-softmax state of the lane's query row.
-struct RowState {
-  float m;     // running max in scaled log2 units (-inf before any visible key)
-  float lsum;  // this lane's partial sum of exp2(x - m)
-};
-
-// Softmax of one 32-key x 32-row S^T tile held by this lane (16 keys of its
-// row).  vis: bit r set when register r is a visible key.  Returns the
-// rescale factor for O (1 when unchanged) and writes the packed P operand.
-// log2-domain score of one S^T entry (c = scale * log2(e), or scale / softcap
-// with the soft cap applied first)
-template <bool SOFTCAP>
-__device__ inline float score_l2(float v, float c, float cap) {
-  return SOFTCAP ? cap * tanhf(v * c) * LOG2E : v * c;
-}
-
-// A lane's 16 weights of one half-tile against the row's reference maximum
-// mref (log2 domain), with no tile maximum: the branch-free common case.
-// Weights are packed pairwise as they are produced (p0: registers 0..7, p1:
-// 8..15).  Returns the lane's weight sum.  The caller sends the tile to
-// softmax_exact when any lane's sum exceeds 2^Rescale::THRESH (some key is
-// more than Rescale::THRESH above the reference) or is not finite (the row
-// has no reference yet: mref = -inf makes every visible weight +inf).
-template <int DT, bool SOFTCAP, bool MASKED>
-__device__ inline float softmax_fast(const f32x16_t& s, uint32_t vis, float mref, float c, float cap,
-                                     u32x4_t& p0, u32x4_t& p1) {
-  using M = Mma<DT>;
-  float acc0 = 0.f, acc1 = 0.f;
-  uint32_t pk[8];
-#pragma unroll
-  for (int r = 0; r < 16; r += 2) {
-    float e0 = SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(s[r], c, cap) - mref)
-                       : __builtin_amdgcn_exp2f(fmaf(s[r], c, -mref));
-    float e1 = SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(s[r + 1], c, cap) - mref)
-                       : __builtin_amdgcn_exp2f(fmaf(s[r + 1], c, -mref));
-    if (MASKED) {
-      e0 = (vis >> r) & 1 ? e0 : 0.f;
-      e1 = (vis >> (r + 1)) & 1 ? e1 : 0.f;
-    }
-    acc0 += e0;
-    acc1 += e1;
-    pk[r >> 1] = M::pack2(e0, e1);
-  }
-  p0 = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
-  p1 = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
-  return acc0 + acc1;
-}
-
-// S^T of the wave's 32 rows against the 32-key half-tile at row kbase.
-template <int DT>
-__device__ inline f32x16_t qk_half(const uint16_t* buf, int kbase, int lane, const u32x4_t (&qf)[8]) {
-  using M = Mma<DT>;
-  const int krow_i = kbase + key_perm(lane & 31);
-  const uint16_t* krow = buf + krow_i * KS_PITCH;
-  const int lhalf = lane >> 5;
-  f32x16_t s = {};
-#pragma unroll
-  for (int kk = 0; kk < 8; ++kk)
-    s = M::mma(lds_read16(krow + kchunk(krow_i, 2 * (kk & 3) + lhalf) * 8 + (kk >> 2) * 64), qf[kk], s);
-  return s;
-}
-
-// Weight of one score against the reference mref (log2 domain).
-template <bool SOFTCAP>
-__device__ inline float weight1(float v, float c, float cap, float mref) {
-  return SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(v, c, cap) - mref)
-                 : __builtin_amdgcn_exp2f(fmaf(v, c, -mref));
-}
-
-// O += V^T . P^T over NH 32-key halves starting at row kbase.  The V^T
-// operand: lane group g = lane/16 covers dims 16*(g&1) .. +15 of the 32-dim
-// block and keys 8*(g>>1) .. +7 of the 16-key step (two 4-key transposing
-// reads).  The four dim blocks are independent accumulators, issued in turn.
-template <int DT, int NH>
-__device__ inline void pv(const uint16_t* buf, int kbase, int lane, const u32x4_t (&p)[NH][2], f32x16_t (&o)[4]) {
-  using M = Mma<DT>;
-  const int g = lane >> 4, sl = lane & 15;
-  // every row this lane reads has row & 3 == sl >> 2: dim block mb sits in segment mb ^ (sl >> 2)
-  const uint16_t* vsrc = buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
-#pragma unroll
-  for (int h = 0; h < NH; ++h) {
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const uint16_t* vp = vsrc + (32 * h + 16 * kk) * VS_PITCH + 32 * (mb ^ (sl >> 2));
-        const uint2 lo = lds_read_tr(vp);
-        const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
-        o[mb] = M::mma(u32x4_t{lo.x, lo.y, hi.x, hi.y}, p[h][kk], o[mb]);
-      }
-    }
-  }
-}
-
-// Weights of NH half-tiles of the wave's rows (one row per lane pair): the
-// branch-free fast path against the row's reference, or -- when some weight
-// could exceed 2^Rescale::THRESH or the row has no reference yet -- the exact
-// path that moves the reference to the maximum over all NH halves and scales
-// O (skipped while the row has accumulated nothing).
-template <int DT, bool SOFTCAP, bool MASKED, int NH>
-__device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH], RowState& st, float c, float cap,
-                               u32x4_t (&p)[NH][2], f32x16_t (&o)[4]) {
-  float acc = 0.f;
-  bool hot = false;
-#pragma unroll
-  for (int h = 0; h < NH; ++h) {
-    const float a_h = softmax_fast<DT, SOFTCAP, MASKED>(s[h], vis[h], st.m, c, cap, p[h][0], p[h][1]);
-    hot |= !(a_h <= Rescale<DT>::SUM);
-    acc += a_h;
-  }
-  if (__ballot(hot) == 0) {
-    st.lsum += acc;
-    return;
-  }
-  // exact path (wave-uniform; after a row's first tile it needs a score more
-  // than Rescale::THRESH log2 units above everything before it).  The empty
-  // volatile asm keeps the compiler from speculating this rare work into the
-  // common path.
-  __asm__ volatile("" ::: "memory");
-  float mx = -INFINITY;
-#pragma unroll
-  for (int h = 0; h < NH; ++h)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float v = score_l2<SOFTCAP>(s[h][r], c, cap);
-      mx = (!MASKED || ((vis[h] >> r) & 1)) ? fmaxf(mx, v) : mx;
-    }
-  mx = pair_max(mx);
-  const float new_m = fmaxf(st.m, mx);
-  const float alpha = st.m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m - new_m);
-  const float mref = new_m == -INFINITY ? 0.f : new_m;
-  const bool had_mass = st.lsum > 0.f;
-  st.m = new_m;
-  float acc2 = 0.f;
-#pragma unroll
-  for (int h = 0; h < NH; ++h) acc2 += softmax_fast<DT, SOFTCAP, MASKED>(s[h], vis[h], mref, c, cap, p[h][0], p[h][1]);
-  st.lsum = st.lsum * alpha + acc2;
-  if (__ballot(had_mass && alpha != 1.f) != 0) {
-    __asm__ volatile("" ::: "memory");
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) o[mb] *= alpha;
-  }
-}
-
-// Phase A of a pipelined step of a wave over its 32-key half of a fully
-// visible tile: in 8 fixed segments, one MFMA of the next tile's QK^T (with
-// the LDS read of the fragment two MFMAs ahead) beside the weights of two
-// scores of the current tile against the row's reference.  s_in holds S^T of
-// the current tile, s_out receives that of the next tile (the caller
-// alternates two register sets: no copies).  Returns true when some weight
-// could exceed 2^Rescale::THRESH or the row has no reference yet (the tile then
-// needs the exact path); otherwise adds the weight sum to the row's state.
-// DEFER: no wave vote -- the lane's sum is always added and the lane's own
-// flag returned (the caller votes once, after its loop, and recomputes).
-template <int DT, bool SOFTCAP, bool DEFER = false>
-__device__ inline bool phase_a1(const uint16_t* next_buf, int kbase, int lane, const u32x4_t (&qf)[8],
-                                const f32x16_t& s_in, f32x16_t& s_out, RowState& st, float c, float cap,
-                                u32x4_t (&p)[1][2]) {
-  using M = Mma<DT>;
-  const int lhalf = lane >> 5;
-  const int krow_i = kbase + key_perm(lane & 31);
-  const uint16_t* krow = next_buf + krow_i * KS_PITCH;
-  // the swizzle leaves chunk bit 3 alone: fragments kk and kk + 4 sit 64
-  // elements apart, so four lane addresses serve all eight reads
-  auto kfrag = [&](int kk) { return lds_read16(krow + kchunk(krow_i, 2 * (kk & 3) + lhalf) * 8 + (kk >> 2) * 64); };
-  const float mref = st.m;
-  u32x4_t kf[8];
-  kf[0] = kfrag(0);
-  kf[1] = kfrag(1);
-  s_out = f32x16_t{};
-  uint32_t pk[8];
-  float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if (i + 2 < 8) kf[i + 2] = kfrag(i + 2);
-    s_out = M::mma(kf[i], qf[i], s_out);
-    const float e0 = weight1<SOFTCAP>(s_in[2 * i], c, cap, mref);
-    const float e1 = weight1<SOFTCAP>(s_in[2 * i + 1], c, cap, mref);
-    acc0 += e0;
-    acc1 += e1;
-    pk[i] = M::pack2(e0, e1);
-    // keeps this segment's weights, sums and packing beside its MFMA (without
-    // it the instruction selector may gather them after the last MFMAs)
-    __asm__ volatile("" : "+v"(acc0), "+v"(acc1), "+v"(pk[i]));
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  p[0][0] = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
-  p[0][1] = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
-  const float acc = acc0 + acc1;
-  if constexpr (DEFER) {
-    st.lsum += acc;
-    return !(acc <= Rescale<DT>::SUM);
-  }
-  if (__ballot(!(acc <= Rescale<DT>::SUM)) != 0) return true;
-  st.lsum += acc;
-  return false;
-}
-
-// Phase C: the current tile's PV with its transposing reads two MFMAs ahead
-// (MFMA j: step kk = j/4, dim block mb = j%4).
-template <int DT>
-__device__ inline void phase_c1(const uint16_t* cur_buf, int kbase, int lane, const u32x4_t (&p)[1][2],
-                                f32x16_t (&o)[4]) {
-  using M = Mma<DT>;
-  const int g = lane >> 4, sl = lane & 15;
-  const uint16_t* vsrc = cur_buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
-  auto vfrag = [&](int j) {
-    const uint16_t* vp = vsrc + (16 * (j >> 2)) * VS_PITCH + 32 * ((j & 3) ^ (sl >> 2));
-    const uint2 lo = lds_read_tr(vp);
-    const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
-    return u32x4_t{lo.x, lo.y, hi.x, hi.y};
-  };
-  u32x4_t vf[8];
-  vf[0] = vfrag(0);
-  vf[1] = vfrag(1);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (j + 2 < 8) vf[j + 2] = vfrag(j + 2);
-    o[j & 3] = M::mma(vf[j], p[0][j >> 2], o[j & 3]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// Phases A and C of a lean step in one body: the first two K fragment reads go
-// out before `mid` (the step's tile loads: scalar work that covers their
-// latency), and the first two V^T fragment reads of phase C during the last
-// two QK MFMAs, so neither phase starts on an LDS round trip.  Same
-// arithmetic, in the same order, as phase_a1<DEFER> followed by phase_c1.
-template <int DT, bool SOFTCAP, typename Mid>
-__device__ inline bool phase_ac(const uint16_t* next_buf, const uint16_t* cur_buf, int kbase, int lane,
-                                const u32x4_t (&qf)[8], const f32x16_t& s_in, f32x16_t& s_out, RowState& st, float c,
-                                float cap, f32x16_t (&o)[4], Mid&& mid) {
-  using M = Mma<DT>;
-  const int lhalf = lane >> 5;
-  const int krow_i = kbase + key_perm(lane & 31);
-  const uint16_t* krow = next_buf + krow_i * KS_PITCH;
-  auto kfrag = [&](int kk) { return lds_read16(krow + kchunk(krow_i, 2 * (kk & 3) + lhalf) * 8 + (kk >> 2) * 64); };
-  const int g = lane >> 4, sl = lane & 15;
-  const uint16_t* vsrc = cur_buf + K_TILE + (kbase + 8 * (g >> 1) + (sl >> 2)) * VS_PITCH + 16 * (g & 1) + 4 * (sl & 3);
-  auto vfrag = [&](int j) {
-    const uint16_t* vp = vsrc + (16 * (j >> 2)) * VS_PITCH + 32 * ((j & 3) ^ (sl >> 2));
-    const uint2 lo = lds_read_tr(vp);
-    const uint2 hi = lds_read_tr(vp + 4 * VS_PITCH);
-    return u32x4_t{lo.x, lo.y, hi.x, hi.y};
-  };
-  const float mref = st.m;
-  u32x4_t kf[8];
-  kf[0] = kfrag(0);
-  kf[1] = kfrag(1);
-  __builtin_amdgcn_sched_barrier(0);
-  mid();
-  __builtin_amdgcn_sched_barrier(0);
-  s_out = f32x16_t{};
-  uint32_t pk[8];
-  u32x4_t vf[8];
-  float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if (i + 2 < 8) kf[i + 2] = kfrag(i + 2);
-    else vf[i - 6] = vfrag(i - 6);
-    s_out = M::mma(kf[i], qf[i], s_out);
-    const float e0 = weight1<SOFTCAP>(s_in[2 * i], c, cap, mref);
-    const float e1 = weight1<SOFTCAP>(s_in[2 * i + 1], c, cap, mref);
-    acc0 += e0;
-    acc1 += e1;
-    pk[i] = M::pack2(e0, e1);
-    __asm__ volatile("" : "+v"(acc0), "+v"(acc1), "+v"(pk[i]));
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  const u32x4_t p0 = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
-  const u32x4_t p1 = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
-  const float acc = acc0 + acc1;
-  st.lsum += acc;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (j + 2 < 8) vf[j + 2] = vfrag(j + 2);
-    o[j & 3] = M::mma(vf[j], j < 4 ? p0 : p1, o[j & 3]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  return !(acc <= Rescale<DT>::SUM);
-}
 
 // Workgroup barrier once this wave's LDS reads are done and all but its newest
 // INFLIGHT direct-to-LDS tile loads have landed (the compiler does not see
@@ -433,21 +42,6 @@ __device__ inline void tile_barrier() {
   else __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// One pipelined step with the exact path in line (phase A; the exact weights
-// when phase A reports it; phase C).
-template <int DT, bool SOFTCAP>
-__device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_buf, int kbase, int lane,
-                                 const u32x4_t (&qf)[8], const f32x16_t& s_in, f32x16_t& s_out,
-                                 f32x16_t (&o)[4], RowState& st, float c, float cap) {
-  u32x4_t p[1][2];
-  if (phase_a1<DT, SOFTCAP>(next_buf, kbase, lane, qf, s_in, s_out, st, c, cap, p)) {
-    __asm__ volatile("" ::: "memory");
-    const uint32_t vis[1] = {0xFFFFu};
-    const f32x16_t s1[1] = {s_in};
-    weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, o);
-  }
-  phase_c1<DT>(cur_buf, kbase, lane, p, o);
-}
 
 // PREFILL: the varlen causal mode (gr_paged_attn_prefill).  The argument
 // block is read as: prefix_bt = block table, prefix_len = sequence length,
@@ -816,6 +410,32 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   __syncthreads();
   if (n_st > 2) issue_first(2);
   f32x16_t s_cur = qk_half<DT>(lds, ks * 32, lane, qf);  // (stale LDS when n_st == 0: never used)
+  // Suffix prefetch.  The first suffix tile pair (64 slots per row group: the
+  // slot table's) is four pieces, piece i = 2 h + gp holding tile h of row
+  // groups 2 gp and 2 gp + 1 (their 32 slots each, rows (g & 1) * 32 ..) in
+  // buffer (n_st + i) % 4.  The last prefix steps free those buffers one by
+  // one -- step t has no tile t + 3 to fetch once t + 3 >= n_st -- so pieces
+  // 0, 1, 2 go out, as direct-to-LDS gathers of the slots' rows, at the tops
+  // of steps n_st - 3, n_st - 2, n_st - 1, and piece 3 after the loop: the
+  // gathers' latency hides behind the last prefix steps.
+  int max_tot = 0;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) max_tot = max(max_tot, suf_cum[g][32]);
+  const int n_sit = PREFILL || (SPLIT && split != nsplit - 1) ? 0 : (max_tot + 31) / 32;
+  const bool tab_ok = !(suf_tab_bad[0] | suf_tab_bad[1] | suf_tab_bad[2] | suf_tab_bad[3]);
+  const int spf_n = !PREFILL && tab_ok && n_st >= 3 ? 2 * min(n_sit, 2) : 0;  // pieces prefetched
+  const int sbase = n_st & 3;  // suffix tile h of row group g sits in buffer (sbase + 2 h + (g >> 1)) % 4
+  auto suf_piece = [&](int i) {
+    const int h = i >> 1, gp = i & 1;
+    const uint32_t d = lds0 + (uint32_t)(((sbase + i) & 3) * BUF * 2) + (uint32_t)(wv * 8 * KS_PITCH * 2);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = 8 * wv + 4 * j + q4;  // row of the piece: group 2 gp + (row >> 5), slot row & 31
+      const int64_t off = suf_off[2 * gp + (row >> 5)][h * 32 + (row & 31)];
+      dma_v(d + j * 1024, off < 0 ? zsrc : kc + off + ck * 8);
+      dma_v(d + K_TILE * 2 + j * 1024, off < 0 ? zsrc : vc + off + cv * 8);
+    }
+  };
   // One step over a fully visible tile `it` (not the last): consumes its S^T
   // from s_in, leaves that of tile it+1 in s_out.  Keys of an invalid block
   // read as zero rows (the block was flagged when the window was staged).
@@ -827,12 +447,14 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     if (tn < n_st) {
       if (lean && (tn + 1 < n_st || last_full)) issue_tile_lean(tn, tn % NBUF);
       else issue_tile(tn, tn % NBUF);
+    } else if (tn - n_st < min(spf_n, 3)) {
+      suf_piece(tn - n_st);
     }
   };
   // The end of step t: tile t+2 (read from the next step on) has landed; tile
-  // t+3 may still be in flight.
+  // t+3, or the suffix piece issued in its place, may still be in flight.
   auto step_barrier = [&](int t) {
-    if (t + 3 < n_st) tile_barrier<LOADS_PER_TILE>();
+    if (t + 3 < n_st || t + 3 - n_st < min(spf_n, 3)) tile_barrier<LOADS_PER_TILE>();
     else tile_barrier<0>();
   };
   auto prefix_step = [&](int it, const f32x16_t& s_in, f32x16_t& s_out) {
@@ -844,6 +466,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // The last tile: no next tile; masked when only p_last of its keys exist.
   const int p_last = min(ST_KEYS, P - kb - (n_st - 1) * ST_KEYS);  // keys in the last tile (1 .. 64)
   auto last_step = [&](int it, const f32x16_t& s_in) {
+    fetch_ahead(it);  // (a suffix piece, if any)
     // register r of lane half lhalf holds tile key ks*32 + 16*(r>>3) + 8*lhalf + (r&7)
     uint32_t v = 0;
 #pragma unroll
@@ -975,9 +598,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   const int qi_e = PREFILL ? rho_e / G : (rho_e / G) % a.T;
   const int g_e = rho_e % G;
   const int lane_e = tid_e & 63, lhalf_e = lane_e >> 5, lrow_e = lane_e & 31;
-  if (hot_flag) {
+  const bool hot = hot_flag != 0;
+  if (hot) {
     // exact recomputation of the workgroup's prefix range, one tile at a time
-    // through buffer 0, every tile on the exact (masked) path
+    // through buffer 0, every tile on the exact (masked) path (after every
+    // suffix piece has landed: their data is gathered again below)
+    tile_barrier<0>();
     st = RowState{-INFINITY, 0.f};
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
@@ -1002,10 +628,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // ---- suffix: each row group's beams' own tokens, masked 32-key tiles ----
   // (all threads load; the two waves of a row group compute a pair of tiles
   // side by side; the group's metadata was staged in the prologue)
-  int max_tot = 0;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) max_tot = max(max_tot, suf_cum[g][32]);
-  const int n_sit = !SPLIT || split == nsplit - 1 ? (max_tot + 31) / 32 : 0;
+  const bool spf_ok = spf_n > 0 && !hot;  // the prefetched pieces are in place
   // loader: 4 row groups x 32 slots x 16 chunks per tile; row group g's slots
   // live in buffer g >> 1, rows / columns (g & 1) * 32 .. + 31; all loads of a
   // tile are issued before its first LDS store.
@@ -1071,7 +694,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       const int grp = e >> 9;
       const int slot = (e >> 4) & 31;
       const int ch = e & 15;
-      uint16_t* buf = lds + (2 * h + (grp >> 1)) * BUF;
+      uint16_t* buf = lds + ((sbase + 2 * h + (grp >> 1)) & 3) * BUF;
       const int key = (grp & 1) * 32 + slot;
       *reinterpret_cast<u32x4_t*>(buf + key * KS_PITCH + kchunk(key, ch) * 8) = skv[i];
       *reinterpret_cast<u32x4_t*>(buf + K_TILE + key * VS_PITCH + vchunk(key, ch) * 8) = svv[i];
@@ -1116,7 +739,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       const bool ok = info >= 0 && (info >> 16) == b_e && (info & 0xFFFF) <= lim;
       vis |= (ok ? 1u : 0u) << rr;
     }
-    const uint16_t* sbuf = lds + (2 * h + (rg >> 1)) * BUF;
+    const uint16_t* sbuf = lds + ((sbase + 2 * h + (rg >> 1)) & 3) * BUF;
     const f32x16_t s1[1] = {qk_half<DT>(sbuf, (rg & 1) * 32, lane_e, qf)};
     const uint32_t vis1[1] = {vis};
     u32x4_t pw[1][2];
@@ -1126,7 +749,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // Tiles in pairs: the key-half-0 wave of each row group takes the first
   // tile, the key-half-1 wave the second, at the same time (each adds to its
   // own partial state; the halves merge below).
-  const bool tab_ok = !(suf_tab_bad[0] | suf_tab_bad[1] | suf_tab_bad[2] | suf_tab_bad[3]);
+  if (spf_ok && spf_n > 3) suf_piece(3);  // its buffer held the last prefix tile
   for (int it = 0; it < n_sit; it += 2) {
     // a fresh copy of the thread index each trip: the slot addresses derived
     // from it are recomputed in registers rather than hoisted out of the loop
@@ -1134,7 +757,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     int t = tid;
     __asm__ volatile("" : "+v"(t));
     const bool two = it + 1 < n_sit;
-    if (it == 0 && tab_ok) {
+    if (it == 0 && spf_ok) {
+      // the pair is in LDS (prefetched pieces, tags from the slot table)
+    } else if (it == 0 && tab_ok) {
       // both tiles' loads in flight at once (a missing second tile's slots are
       // empty and read the zero source)
       u32x4_t skv0[SUF_PER_THREAD], svv0[SUF_PER_THREAD], skv1[SUF_PER_THREAD], svv1[SUF_PER_THREAD];
@@ -1158,16 +783,27 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         suf_tag(t, 1, sinfo1);
       }
     }
-    __syncthreads();
+    if (it == 0 && spf_ok) tile_barrier<0>();  // every piece has landed
+    else __syncthreads();
     if (ks == 0 || two) suf_compute(ks);
     __syncthreads();
   }
 
   // ---- merge the two key halves and write O, LSE --------------------------
+  // (the row indices once more, from a fresh copy of the thread index, so
+  // none of them lives through the suffix phase)
+  int tid_f = tid;
+  __asm__ volatile("" : "+v"(tid_f));
+  const int rho_f = row_base + (tid_f >> 7) * 32 + (tid_f & 31);
+  const bool ok_f = rho_f < rows_r;
+  const int b_f = PREFILL ? 0 : rho_f / TG;
+  const int qi_f = PREFILL ? rho_f / G : (rho_f / G) % a.T;
+  const int g_f = rho_f % G;
+  const int lane_f = tid_f & 63, lhalf_f = lane_f >> 5, lrow_f = lane_f & 31;
   // [rg][lane][64 accumulators, padded to 68]: 16-byte writes and reads, the
   // padding spreads a row of lanes over every bank
   constexpr int XO_PITCH = 68;
-  float* xo = reinterpret_cast<float*>(lds) + rg * (64 * XO_PITCH) + lane_e * XO_PITCH;
+  float* xo = reinterpret_cast<float*>(lds) + rg * (64 * XO_PITCH) + lane_f * XO_PITCH;
   float* xm = reinterpret_cast<float*>(lds) + 4 * (64 * XO_PITCH) + rg * 128;  // [rg][m | lsum][lane]
   if (ks == 1) {
 #pragma unroll
@@ -1176,12 +812,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       for (int qd = 0; qd < 4; ++qd)
         *reinterpret_cast<f32x4_t*>(xo + mb * 16 + qd * 4) =
             f32x4_t{o[mb][qd * 4], o[mb][qd * 4 + 1], o[mb][qd * 4 + 2], o[mb][qd * 4 + 3]};
-    xm[lane_e] = st.m;
-    xm[64 + lane_e] = st.lsum;
+    xm[lane_f] = st.m;
+    xm[64 + lane_f] = st.lsum;
   }
   __syncthreads();
   if (ks == 0) {
-    const float m1 = xm[lane_e], l1 = xm[64 + lane_e];
+    const float m1 = xm[lane_f], l1 = xm[64 + lane_f];
     const float m0 = st.m, l0 = st.lsum;
     const float m = fmaxf(m0, m1);
     const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
@@ -1191,7 +827,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     if constexpr (SPLIT) {
       // this split's normalised partial O and LSE, every row of the tile
       const int64_t slot = (int64_t)(unit * mtiles + mt) * nsplit + split;
-      float* po = a.ws_o + (slot * MF_ROWS + rg * 32 + lrow_e) * HD + 4 * lhalf_e;
+      float* po = a.ws_o + (slot * MF_ROWS + rg * 32 + lrow_f) * HD + 4 * lhalf_f;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -1206,12 +842,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
           *reinterpret_cast<float4*>(po + mb * 32 + qd * 8) = make_float4(v[0], v[1], v[2], v[3]);
         }
       }
-      if (lhalf_e == 0)
-        a.ws_lse[slot * MF_ROWS + rg * 32 + lrow_e] =
+      if (lhalf_f == 0)
+        a.ws_lse[slot * MF_ROWS + rg * 32 + lrow_f] =
             lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
-    } else if (ok_e) {
-      const int64_t tok = PREFILL ? (int64_t)(nb0 + qi_e) : (int64_t)(nb0 + b_e) * a.T + qi_e;
-      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g_e) * HD + 4 * lhalf_e;
+    } else if (ok_f) {
+      const int64_t tok = PREFILL ? (int64_t)(nb0 + qi_f) : (int64_t)(nb0 + b_f) * a.T + qi_f;
+      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g_f) * HD + 4 * lhalf_f;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -1227,8 +863,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
           *reinterpret_cast<u32x2_t*>(dst + mb * 32 + qd * 8) = w;
         }
       }
-      if (a.lse_out && lhalf_e == 0) {
-        a.lse_out[tok * a.Hq + hk * G + g_e] =
+      if (a.lse_out && lhalf_f == 0) {
+        a.lse_out[tok * a.Hq + hk * G + g_f] =
             lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
       }
     }
