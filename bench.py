@@ -351,6 +351,10 @@ def main() -> int:
     ap.add_argument("--no-warm", action="store_true",
                     help="skip the warm (one relaunched copy) timing; the cold rotation is the headline")
     ap.add_argument("--kernel", choices=["auto", "generic"], default="auto")
+    ap.add_argument("--option", choices=["none", "window", "sinks", "alibi", "fp8"], default="none",
+                    help="decode with one optional attention feature of the reference's impl "
+                         "(beam_attn.py:597-625): a 1024-token sliding window, per-head sinks, ALiBi "
+                         "slopes, or an fp8 e4m3 KV cache (scales 1)")
     ap.add_argument("--workload", choices=["decode", "fork", "prune", "e2e"], default="decode",
                     help="decode (the headline line), the fork+append / pruning kernels, or e2e "
                          "(whole semantic-ID beam decode through a 28-layer decoder; a step is one batch)")
@@ -388,23 +392,42 @@ def main() -> int:
     wl = host_wl.to(dev)
     ops.set_decode_kernel(args.kernel)
 
+    Hq = wl.q.shape[1]
+    opt_kw = {}
+    if args.option == "window":
+        opt_kw["window"] = (1023, -1)
+    elif args.option == "sinks":
+        opt_kw["sinks"] = torch.linspace(-1.0, 1.0, Hq, device=dev)
+    elif args.option == "alibi":
+        opt_kw["alibi_slopes"] = torch.tensor([2.0 ** (-8.0 * (h + 1) / Hq) for h in range(Hq)], device=dev)
+    elif args.option == "fp8":
+        one = torch.ones(1, dtype=torch.float32, device=dev)
+        opt_kw.update(k_scale=one, v_scale=one)
+        wl.kv_cache = wl.kv_cache.to(torch.float8_e4m3fn)
+
     def make_step(kv, q):
         out = torch.empty_like(q)
 
         def step():
             ops.beam_attn_decode(q, kv[0], kv[1], wl.prefix_bt, wl.prefix_len, wl.beam_start,
                                  wl.suffix_bt, wl.suffix_len, scale=wl.scale, max_beams_per_req=wl.max_beams,
-                                 out=out)
+                                 out=out, **opt_kw)
         return step
 
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
     warm = make_step(wl.kv_cache, wl.q)
+    nbytes = host_wl.algorithmic_bytes()
+    if args.option == "fp8":  # one byte per cached element
+        nbytes -= (int(host_wl.prefix_len.sum()) + int(host_wl.suffix_len.sum())) * 2 * 8 * 128
+    if args.option == "window":  # prefix keys no row of a request can see are not read
+        hidden = sum(max(0, int(p) - 1 - opt_kw["window"][0]) for p in host_wl.prefix_len.tolist())
+        nbytes -= hidden * 2 * 8 * 128 * 2
+    copies = max(COLD_COPIES, -(-MALL_BYTES // nbytes) + 2)
     # each copy: its own cache pool and queries (the same tables: tiny), drawn on the device
     cold = [warm] + [make_step(_device_copy(wl.kv_cache, gen), _device_copy(wl.q, gen))
-                     for _ in range(COLD_COPIES - 1)]
-    nbytes = host_wl.algorithmic_bytes()
-    assert (COLD_COPIES - 1) * nbytes > MALL_BYTES
+                     for _ in range(copies - 1)]
+    assert (copies - 1) * nbytes > MALL_BYTES
     us_step = _time_launches(cold, args.steps, args.warmup, "cold")
     us_warm = None if args.no_warm else _time_launches(warm, args.steps, args.warmup, "warm")
     gbps = nbytes / (us_step * 1e-6) / 1e9
@@ -434,7 +457,7 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1)/sqrt(128) Q/K/V, random block tables)",
         "config": {"workload": "beam decode: 8 requests x 128 beams, shared prefix 2048, suffix U[1,8], "
                                "32 q / 8 kv heads, head_dim 128, block 16",
-                   "requests": 8, "beams": 128, "prefix": 2048, "kernel": args.kernel,
+                   "requests": 8, "beams": 128, "prefix": 2048, "kernel": args.kernel, "option": args.option,
                    "algorithmic_bytes_per_step": nbytes, "flops_per_step": host_wl.flops(),
                    "inputs": f"{len(cold)} copies rotated per launch (cold: no reuse through the 256 MB "
                              f"Infinity Cache)"},

@@ -6,7 +6,9 @@ flash_attn_varlen_func call of its cascade and standard path
 (vllm_gr/v1/attention/backends/beam_attn.py:597-625, :643-695); the oracle
 (oracle.attention.beam_attention_dense) states them per key position and is
 pinned in tests/test_oracle_options.py.  Decode runs gr_beam_attn_decode_opt,
-prefill gr_paged_attn_prefill_opt (both on the generic kernel).
+prefill gr_paged_attn_prefill_opt (windows and sinks of bf16/fp16 head-dim-128
+decodes, and sinks of such prefills, on the matrix-core kernel; the rest on
+the generic kernel).
 Tolerances: float32 1e-5, bf16/fp16 2e-2 on N(0,1) inputs.
 """
 
@@ -82,6 +84,35 @@ def test_decode_options(device, feature, dtype, D, T):
     gpu_kw, orc_kw = _split(kw, device)
     _close(_decode_gpu(wl, device, **gpu_kw), _decode_oracle(wl, **orc_kw),
            1e-5 if dtype == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("kw", [dict(window=(300, -1)), dict(window=(999, -1)), dict(window=(3, -1)),
+                                dict(window=(70, -1)), dict(sinks=True), dict(window=(250, -1), sinks=True)])
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_options_long_prefix(device, kw, split, dtype):
+    """Windows and sinks on the matrix-core decode at a long prefix (many
+    pipelined tiles, the window's edge tiles masked, the rest on the fast
+    loop; split and unsplit): suffix lengths differ between requests, so the
+    window edge falls at different keys per row."""
+    print(f"[options] long decode {kw} split={split} {dtype}", flush=True)
+    wl = workloads.make_decode(R=3, W=24, P=1000, L=(1, 8), Hq=16, Hkv=4, D=128, dtype=dtype,
+                               input_scale=1.0, seed=77)
+    kw = dict(kw)
+    if kw.get("sinks"):
+        kw["sinks"] = torch.randn(16, generator=torch.Generator().manual_seed(5)) * 3
+    gpu_kw, orc_kw = _split(kw, device)
+    d = wl.to(device)
+    out = torch.empty_like(d.q)
+    lse = torch.empty(d.q.shape[:2], dtype=torch.float32, device=device)
+    st = ops.new_status(device)
+    ops.beam_attn_decode(d.q, d.k_cache, d.v_cache, d.prefix_bt, d.prefix_len, d.beam_start, d.suffix_bt,
+                         d.suffix_len, scale=d.scale, out=out, lse=lse, status=st, split=split,
+                         max_prefix_len=1000 if split else None, **gpu_kw)
+    torch.cuda.synchronize()
+    ops.check_status(st)
+    got = (out.cpu().to(torch.float64).numpy(), lse.cpu().to(torch.float64).numpy())
+    _close(got, _decode_oracle(wl, **orc_kw), 2e-2)
 
 
 def test_decode_window_with_softcap(device):

@@ -520,7 +520,7 @@ static gr_status_t prefill_impl(
   a.causal = 1;
   const gr_status_t st = apply_options(a, opt, true);
   if (st != GR_OK) return st;
-  if (g_decode_kernel_override != 1 && mfma_decode_supported(a)) return launch_mfma_prefill(a, stream);
+  if (g_decode_kernel_override != 1 && mfma_prefill_supported(a)) return launch_mfma_prefill(a, stream);
   return launch_generic<true>(a, stream);
 }
 

@@ -52,7 +52,13 @@ __device__ inline void tile_barrier() {
 // SPLIT: a.nsplit workgroups per row tile, each over a contiguous share of
 // the prefix's 64-key tiles (the last one also takes the suffix), writing its
 // normalised partial O and LSE to the workspace; split_merge combines them.
-template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false>
+// WIN (decode only): a left window a.win_left >= 0 -- row r sees key k iff k >=
+// qpos_r - win_left, qpos_r its query token's index in [prefix ; suffix].
+// The prefix range starts at the first tile any row can see; its first tiles
+// (up to the WG's highest lower bound) take masked steps, the rest the fast
+// loop.  Sinks (a.sinks, any mode) join each row's softmax in the epilogue
+// (in split_merge for the split mode).
+template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false, bool WIN = false>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
   __shared__ __attribute__((aligned(1024))) uint16_t lds[NBUF * BUF];
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
@@ -63,6 +69,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   __shared__ int suf_tab_bad[4];         // per row group: its slot table is not built (unstaged block ids)
   __shared__ int pbt_s[PBT_WIN];         // staged prefix block ids (-1 = invalid)
   __shared__ int hot_flag;               // a tile of the fast loop needed the exact path
+  __shared__ int win_hi[8];              // per wave: the highest window lower bound of its rows
 
   // ---- XCD-aware tile placement: all m-tiles of a (request, KV head) land on
   // the same XCD (round-robin dispatch puts workgroup i on XCD i % 8)
@@ -157,8 +164,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     P = P < 0 ? 0 : pre_cap;
   }
   const int n_all = (P + ST_KEYS - 1) / ST_KEYS;
-  const int ts0 = SPLIT ? (int)((int64_t)split * n_all / nsplit) : 0;  // first tile of this workgroup
-  const int n_st = SPLIT ? (int)((int64_t)(split + 1) * n_all / nsplit) - ts0 : n_all;
+  // window: no row sees keys below P - T - win_left (its query sits at P - T or later)
+  const int tw0 = WIN ? max(0, P - a.T - a.win_left) / ST_KEYS : 0;
+  const int n_rng = n_all - tw0;
+  const int ts0 = tw0 + (SPLIT ? (int)((int64_t)split * n_rng / nsplit) : 0);  // first tile of this workgroup
+  const int n_st = SPLIT ? tw0 + (int)((int64_t)(split + 1) * n_rng / nsplit) - ts0 : n_rng;
   const int kb = ts0 * ST_KEYS;  // first key of this workgroup's prefix range
   const int bsh = a.bs_shift;
 
@@ -407,7 +417,24 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // the compiler sees: its own wait before the first read of qf would
   // otherwise be a full vector-memory wait placed after the next tile load.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  // window: this lane's row sees keys from lo_row on; the workgroup's highest
+  // bound says how many of its first tiles need masks
+  int lo_row = 0;
+  if constexpr (WIN) {
+    lo_row = P + my_len - a.T + my_qi - a.win_left;
+    int hi = row_ok ? lo_row : INT_MIN;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) hi = max(hi, __shfl_xor(hi, off, 64));
+    if (lane == 0) win_hi[wave] = hi;
+  }
   __syncthreads();
+  int n_edge = 0;  // tiles [0, n_edge) of the range: some row's window starts inside or after them
+  if constexpr (WIN) {
+    int hi = win_hi[0];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) hi = max(hi, win_hi[w]);
+    n_edge = hi > kb ? min(n_st, (int)(((int64_t)hi - kb + ST_KEYS - 1) / ST_KEYS)) : 0;
+  }
   if (n_st > 2) issue_first(2);
   f32x16_t s_cur = qk_half<DT>(lds, ks * 32, lane, qf);  // (stale LDS when n_st == 0: never used)
   // Suffix prefetch.  The first suffix tile pair (64 slots per row group: the
@@ -568,8 +595,30 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       step_barrier(it);
     }
   } else {
+    if constexpr (WIN) {
+      // the window's edge tiles, one at a time with each row's mask (the
+      // prefill's causal-edge step with a lower bound instead of an upper)
+      for (; it < n_edge; ++it) {
+        fetch_ahead(it);
+        const int nk = it == n_st - 1 ? p_last : ST_KEYS;
+        uint32_t v = 0;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) {
+          const int kl = ks * 32 + 16 * (rr >> 3) + 8 * lhalf + (rr & 7);
+          v |= (kl < nk && kb + it * ST_KEYS + kl >= lo_row ? 1u : 0u) << rr;
+        }
+        const uint32_t vis[1] = {v};
+        const f32x16_t s1[1] = {s_cur};
+        u32x4_t pw[1][2];
+        weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o);
+        pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
+        if (it + 1 < n_st) s_cur = qk_half<DT>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf);
+        if (it + 1 < n_st) step_barrier(it);
+        else __syncthreads();
+      }
+    }
     // the last two tiles take the general step
-    if (n_st >= 3) peel();
+    if (it == 0 && n_st >= 3) peel();
     for (; it + 1 < n_lean; it += 2) {  // two steps per trip: S^T alternates between s_cur and s_alt
       lean_step(it, s_cur, s_alt);
       lean_step(it + 1, s_alt, s_cur);
@@ -604,6 +653,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     // through buffer 0, every tile on the exact (masked) path (after every
     // suffix piece has landed: their data is gathered again below)
     tile_barrier<0>();
+    const int lo_e = WIN ? P + my_len - a.T + qi_e - a.win_left : 0;  // the row's window bound
     st = RowState{-INFINITY, 0.f};
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
@@ -615,7 +665,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
         const int kl = ks * 32 + 16 * (rr >> 3) + 8 * lhalf_e + (rr & 7);  // key within the tile
-        v |= (PREFILL ? t * ST_KEYS + kl <= lim : kl < nk) ? 1u << rr : 0u;
+        v |= (PREFILL ? t * ST_KEYS + kl <= lim : kl < nk && (!WIN || kb + t * ST_KEYS + kl >= lo_e)) ? 1u << rr : 0u;
       }
       const uint32_t vis[1] = {v};
       const f32x16_t s1[1] = {qk_half<DT>(lds, ks * 32, lane_e, qf)};
@@ -629,6 +679,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // (all threads load; the two waves of a row group compute a pair of tiles
   // side by side; the group's metadata was staged in the prologue)
   const bool spf_ok = spf_n > 0 && !hot;  // the prefetched pieces are in place
+  // this lane's row's sink (log2 units), read now so its latency hides behind
+  // the suffix (the split mode adds it in split_merge)
+  const float sink_l2 = !SPLIT && a.sinks && ok_e ? a.sinks[hk * G + g_e] * LOG2E : -INFINITY;
   // loader: 4 row groups x 32 slots x 16 chunks per tile; row group g's slots
   // live in buffer g >> 1, rows / columns (g & 1) * 32 .. + 31; all loads of a
   // tile are issued before its first LDS store.
@@ -732,11 +785,13 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   auto suf_compute = [&](int h) {
     // register r of this lane is slot 16*(r>>3) + 8*lhalf + (r&7) of the group's 32
     const int lim = ok_e ? my_len - a.T + qi_e : -1;
+    // window: suffix token j sits at key P + j
+    const int jlo = WIN ? my_len - a.T + qi_e - a.win_left : 0;
     uint32_t vis = 0;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
       const int info = suf_info[h][rg][16 * (rr >> 3) + 8 * lhalf_e + (rr & 7)];
-      const bool ok = info >= 0 && (info >> 16) == b_e && (info & 0xFFFF) <= lim;
+      const bool ok = info >= 0 && (info >> 16) == b_e && (info & 0xFFFF) <= lim && (info & 0xFFFF) >= jlo;
       vis |= (ok ? 1u : 0u) << rr;
     }
     const uint16_t* sbuf = lds + ((sbase + 2 * h + (rg >> 1)) & 3) * BUF;
@@ -819,10 +874,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   if (ks == 0) {
     const float m1 = xm[lane_f], l1 = xm[64 + lane_f];
     const float m0 = st.m, l0 = st.lsum;
-    const float m = fmaxf(m0, m1);
+    // a sink joins the row's softmax: in the maximum and, once, in the sum
+    const float m = fmaxf(fmaxf(m0, m1), sink_l2);
     const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
     const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
-    const float lrow_sum = pair_sum(l0 * a0 + l1 * a1);
+    const float lrow_sum =
+        pair_sum(l0 * a0 + l1 * a1) + (sink_l2 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sink_l2 - m));
     const float inv = lrow_sum > 0.f ? 1.f / lrow_sum : 0.f;
     if constexpr (SPLIT) {
       // this split's normalised partial O and LSE, every row of the tile
@@ -893,10 +950,11 @@ __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
   const int nsplit = a.nsplit;
   const float* lse = a.ws_lse + (int64_t)tile * nsplit * MF_ROWS + row;
   const float* po = a.ws_o + ((int64_t)tile * nsplit * MF_ROWS + row) * HD + d4;
-  float mx = -INFINITY;
+  const float sk = a.sinks ? a.sinks[hk * G + rho % G] : -INFINITY;  // joins the merged softmax once
+  float mx = sk;
 #pragma unroll 4
   for (int s2 = 0; s2 < nsplit; ++s2) mx = fmaxf(mx, lse[s2 * MF_ROWS]);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f}, sum = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f}, sum = sk == -INFINITY ? 0.f : __expf(sk - mx);
   if (mx != -INFINITY) {
 #pragma unroll 4
     for (int s2 = 0; s2 < nsplit; ++s2) {
@@ -921,7 +979,9 @@ __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
 
 bool mfma_decode_supported(const DecodeArgs& a) {
   if (a.D != HD || (a.dtype != GR_DTYPE_BF16 && a.dtype != GR_DTYPE_F16)) return false;
-  if (has_options(a)) return false;  // windows, sinks, ALiBi, non-causal: the generic kernel
+  // options here: sinks and a decode's left window; ALiBi, fp8 caches, right
+  // windows and non-causal batches take the generic kernel
+  if (a.alibi || a.kv8 || !a.causal || a.win_right >= 0) return false;
   if (a.bs_shift < 2) return false;  // power-of-two block size >= 4
   if (a.num_blocks < 1) return false;  // an empty pool: the generic kernel reads nothing
   // the suffix tiles tag each key with its 16-bit index within the beam's suffix
@@ -937,6 +997,20 @@ bool mfma_decode_supported(const DecodeArgs& a) {
   return true;
 }
 
+bool mfma_prefill_supported(const DecodeArgs& a) { return mfma_decode_supported(a) && a.win_left < 0; }
+
+template <bool PREFILL, bool SPLIT, bool WIN>
+static void launch_mfma_kernel(const DecodeArgs& a, dim3 grid, int units, int mtiles, hipStream_t stream) {
+  const bool cap = a.softcap > 0.f;
+  if (a.dtype == GR_DTYPE_BF16) {
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL, SPLIT, WIN>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL, SPLIT, WIN>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+  } else {
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL, SPLIT, WIN>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL, SPLIT, WIN>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+  }
+}
+
 template <bool PREFILL, bool SPLIT>
 static gr_status_t launch_mfma(const DecodeArgs& a, hipStream_t stream) {
   const int G = a.Hq / a.Hkv;
@@ -948,14 +1022,8 @@ static gr_status_t launch_mfma(const DecodeArgs& a, hipStream_t stream) {
   if (nwg > 0x7fffffff) return GR_ERR_INVALID_ARG;
   const int mtiles = (int)mt64;
   dim3 grid((unsigned)nwg);
-  const bool cap = a.softcap > 0.f;
-  if (a.dtype == GR_DTYPE_BF16) {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL, SPLIT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL, SPLIT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-  } else {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL, SPLIT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL, SPLIT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-  }
+  if (!PREFILL && a.win_left >= 0) launch_mfma_kernel<PREFILL, SPLIT, !PREFILL>(a, grid, units, mtiles, stream);
+  else launch_mfma_kernel<PREFILL, SPLIT, false>(a, grid, units, mtiles, stream);
   return launch_status();
 }
 

@@ -176,12 +176,17 @@ def beam_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
             float(scale), float(softcap or 0.0), _ptr(lse), _ptr(status))
     hint = int(max_prefix_len or 0)
     opt = _attn_options(dev, Hq, window, True, sinks, alibi_slopes, kv8, k_scale, v_scale)
-    if opt is not None:
-        code = _C.lib().gr_beam_attn_decode_opt(*args, hint, None, 0, ctypes.byref(opt), _stream(dev))
-        _C.check("gr_beam_attn_decode_opt", code)
-        return out
     ws_bytes = (_C.lib().gr_beam_attn_decode_workspace_size(R, max_beams_per_req, q_per_beam, Hq, Hkv, D, hint)
                 if split and R else 0)
+    if opt is not None:
+        # windows and sinks run on the matrix-core kernel, split like a plain
+        # decode; without split, a prefix hint below one split's minimum (256
+        # keys) plans none
+        ws = _split_workspace(dev, ws_bytes) if ws_bytes else None
+        code = _C.lib().gr_beam_attn_decode_opt(*args, hint if split else 1, _ptr(ws), ws_bytes,
+                                                ctypes.byref(opt), _stream(dev))
+        _C.check("gr_beam_attn_decode_opt", code)
+        return out
     if ws_bytes:
         ws = _split_workspace(dev, ws_bytes)
         code = _C.lib().gr_beam_attn_decode_ws(*args, hint, ws.data_ptr(), ws_bytes, _stream(dev))
