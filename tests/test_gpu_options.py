@@ -87,11 +87,12 @@ def test_decode_options(device, feature, dtype, D, T):
 
 
 @pytest.mark.parametrize("kw", [dict(window=(300, -1)), dict(window=(999, -1)), dict(window=(3, -1)),
-                                dict(window=(70, -1)), dict(sinks=True), dict(window=(250, -1), sinks=True)])
+                                dict(window=(70, -1)), dict(sinks=True), dict(window=(250, -1), sinks=True),
+                                dict(alibi=True), dict(window=(400, -1), alibi=True, sinks=True)])
 @pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_decode_options_long_prefix(device, kw, split, dtype):
-    """Windows and sinks on the matrix-core decode at a long prefix (many
+    """Windows, sinks and ALiBi on the matrix-core decode at a long prefix (many
     pipelined tiles, the window's edge tiles masked, the rest on the fast
     loop; split and unsplit): suffix lengths differ between requests, so the
     window edge falls at different keys per row."""
@@ -101,6 +102,8 @@ def test_decode_options_long_prefix(device, kw, split, dtype):
     kw = dict(kw)
     if kw.get("sinks"):
         kw["sinks"] = torch.randn(16, generator=torch.Generator().manual_seed(5)) * 3
+    if kw.pop("alibi", False):  # the usual geometric slopes 2^(-8 h / H), h = 1 .. 16
+        kw["alibi_slopes"] = torch.tensor([2.0 ** (-8.0 * (h + 1) / 16) for h in range(16)])
     gpu_kw, orc_kw = _split(kw, device)
     d = wl.to(device)
     out = torch.empty_like(d.q)

@@ -49,7 +49,7 @@ inline bool has_options(const DecodeArgs& a) {
 }
 
 // MFMA path (gr_attn_mfma.hip): bf16/fp16, head_dim 128, 16-byte aligned rows.
-// (decode: sinks and a left window run here too; prefill: sinks, no window)
+// (decode: sinks, a left window and ALiBi run here too; prefill: sinks)
 bool mfma_decode_supported(const DecodeArgs& a);
 bool mfma_prefill_supported(const DecodeArgs& a);
 gr_status_t launch_mfma_decode(const DecodeArgs& a, hipStream_t stream);

@@ -52,13 +52,16 @@ __device__ inline void tile_barrier() {
 // SPLIT: a.nsplit workgroups per row tile, each over a contiguous share of
 // the prefix's 64-key tiles (the last one also takes the suffix), writing its
 // normalised partial O and LSE to the workspace; split_merge combines them.
-// WIN (decode only): a left window a.win_left >= 0 -- row r sees key k iff k >=
-// qpos_r - win_left, qpos_r its query token's index in [prefix ; suffix].
-// The prefix range starts at the first tile any row can see; its first tiles
-// (up to the WG's highest lower bound) take masked steps, the rest the fast
-// loop.  Sinks (a.sinks, any mode) join each row's softmax in the epilogue
+// OPT (decode only): a left window and/or ALiBi.  Window a.win_left >= 0:
+// row r sees key k iff k >= qpos_r - win_left, qpos_r its query token's index
+// in [prefix ; suffix]; the prefix range starts at the first tile any row can
+// see, its first tiles (up to the WG's highest lower bound) take masked
+// steps, the rest the fast loop.  ALiBi (a.alibi): each weight's exponent
+// gains slope * (k - qpos_r) (log2 units: times log2 e), a linear function
+// of the key in each tile (LinBias); the softmax reference follows the raw
+// scores.  Sinks (a.sinks, any mode) join each row's softmax in the epilogue
 // (in split_merge for the split mode).
-template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false, bool WIN = false>
+template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false, bool OPT = false>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
   __shared__ __attribute__((aligned(1024))) uint16_t lds[NBUF * BUF];
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
@@ -165,7 +168,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   }
   const int n_all = (P + ST_KEYS - 1) / ST_KEYS;
   // window: no row sees keys below P - T - win_left (its query sits at P - T or later)
-  const int tw0 = WIN ? max(0, P - a.T - a.win_left) / ST_KEYS : 0;
+  const int wl = OPT ? a.win_left : -1;
+  const int tw0 = wl >= 0 ? max(0, P - a.T - wl) / ST_KEYS : 0;
   const int n_rng = n_all - tw0;
   const int ts0 = tw0 + (SPLIT ? (int)((int64_t)split * n_rng / nsplit) : 0);  // first tile of this workgroup
   const int n_st = SPLIT ? tw0 + (int)((int64_t)(split + 1) * n_rng / nsplit) - ts0 : n_rng;
@@ -308,6 +312,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) qf[kk] = *reinterpret_cast<const u32x4_t*>(row_ok ? src + kk * 16 : zq);
   }
+  // ALiBi: this lane's row's slope (log2 units), read with Q
+  const float alpha = OPT && a.alibi ? *(row_ok ? a.alibi + hk * G + my_g : reinterpret_cast<const float*>(zint)) * LOG2E
+                                     : 0.f;
 
   // Lean loads of the loop's full tiles.  When every block id of the range sits
   // in the first staged window (which then never moves), a block holds at
@@ -420,8 +427,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // window: this lane's row sees keys from lo_row on; the workgroup's highest
   // bound says how many of its first tiles need masks
   int lo_row = 0;
-  if constexpr (WIN) {
-    lo_row = P + my_len - a.T + my_qi - a.win_left;
+  // ALiBi: the bias of this lane's first key of a tile at key k0 is
+  // alpha * (k0 + al_off) -- its keys sit at k0 + ks * 32 + 8 * lhalf + r'
+  const int al_off = OPT ? ks * 32 + 8 * lhalf - (P + my_len - a.T + my_qi) : 0;
+  if constexpr (OPT) {
+    lo_row = wl >= 0 ? P + my_len - a.T + my_qi - wl : INT_MIN;
     int hi = row_ok ? lo_row : INT_MIN;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) hi = max(hi, __shfl_xor(hi, off, 64));
@@ -429,7 +439,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   }
   __syncthreads();
   int n_edge = 0;  // tiles [0, n_edge) of the range: some row's window starts inside or after them
-  if constexpr (WIN) {
+  if constexpr (OPT) {
     int hi = win_hi[0];
 #pragma unroll
     for (int w = 1; w < 8; ++w) hi = max(hi, win_hi[w]);
@@ -437,6 +447,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   }
   if (n_st > 2) issue_first(2);
   f32x16_t s_cur = qk_half<DT>(lds, ks * 32, lane, qf);  // (stale LDS when n_st == 0: never used)
+  // the exponent terms of prefix tile t's weights: ALiBi's linear bias, or none
+  auto tb = [&](int t) {
+    if constexpr (OPT) return LinBias{alpha, alpha * (float)(kb + t * ST_KEYS + al_off)};
+    else return NoBias{};
+  };
   // Suffix prefetch.  The first suffix tile pair (64 slots per row group: the
   // slot table's) is four pieces, piece i = 2 h + gp holding tile h of row
   // groups 2 gp and 2 gp + 1 (their 32 slots each, rows (g & 1) * 32 ..) in
@@ -487,7 +502,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   auto prefix_step = [&](int it, const f32x16_t& s_in, f32x16_t& s_out) {
     fetch_ahead(it);
     pipe_step<DT, SOFTCAP>(lds + (it % NBUF) * BUF, lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out,
-                           o, st, c, cap);
+                           o, st, c, cap, tb(it));
     step_barrier(it);
   };
   // The last tile: no next tile; masked when only p_last of its keys exist.
@@ -501,7 +516,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const uint32_t vis[1] = {v};
     const f32x16_t s1[1] = {s_in};
     u32x4_t pw[1][2];
-    weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o);
+    weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o, tb(it));
     pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
     __syncthreads();
   };
@@ -522,11 +537,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // tile 0 (and S^T of tile 1): exact weights, O still zero
   auto peel = [&]() {
     fetch_ahead(0);
-    phase_a1<DT, SOFTCAP>(lds + BUF, ks * 32, lane, qf, s_cur, s_alt, st, c, cap, p);
+    phase_a1<DT, SOFTCAP>(lds + BUF, ks * 32, lane, qf, s_cur, s_alt, st, c, cap, p, tb(0));
     f32x16_t zo[4] = {};
     const uint32_t vis[1] = {0xFFFFu};
     const f32x16_t s1[1] = {s_cur};
-    weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, zo);
+    weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, zo, tb(0));
     finish_step(0);
     s_cur = s_alt;
     it = 1;
@@ -536,7 +551,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // lane records its own flag and the waves vote after the loop.
   auto fast_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
     fetch_ahead(t);
-    hot_seen |= phase_a1<DT, SOFTCAP, true>(lds + ((t + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p);
+    hot_seen |= phase_a1<DT, SOFTCAP, true>(lds + ((t + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p, tb(t));
     phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
     step_barrier(t);
   };
@@ -545,7 +560,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   const int n_lean = lean ? (last_full ? n_st - 3 : n_st - 4) : 0;
   auto lean_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
     hot_seen |= phase_ac<DT, SOFTCAP>(lds + ((t + 1) % NBUF) * BUF, lds + (t % NBUF) * BUF, ks * 32, lane, qf, s_in,
-                                      s_out, st, c, cap, o, [&]() { issue_tile_lean(t + 3, (t + 3) % NBUF); });
+                                      s_out, st, c, cap, o, [&]() { issue_tile_lean(t + 3, (t + 3) % NBUF); }, tb(t));
     tile_barrier<LOADS_PER_TILE>();
   };
   // fast steps over tiles [it, t_end): S^T alternates between s_cur and s_alt
@@ -589,13 +604,13 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       const uint32_t vis[1] = {v};
       const f32x16_t s1[1] = {s_cur};
       u32x4_t pw[1][2];
-      weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o);
+      weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o, tb(it));
       pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
       if (it + 1 < n_st) s_cur = qk_half<DT>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf);
       step_barrier(it);
     }
   } else {
-    if constexpr (WIN) {
+    if constexpr (OPT) {
       // the window's edge tiles, one at a time with each row's mask (the
       // prefill's causal-edge step with a lower bound instead of an upper)
       for (; it < n_edge; ++it) {
@@ -610,7 +625,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         const uint32_t vis[1] = {v};
         const f32x16_t s1[1] = {s_cur};
         u32x4_t pw[1][2];
-        weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o);
+        weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o, tb(it));
         pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
         if (it + 1 < n_st) s_cur = qk_half<DT>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf);
         if (it + 1 < n_st) step_barrier(it);
@@ -653,7 +668,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     // through buffer 0, every tile on the exact (masked) path (after every
     // suffix piece has landed: their data is gathered again below)
     tile_barrier<0>();
-    const int lo_e = WIN ? P + my_len - a.T + qi_e - a.win_left : 0;  // the row's window bound
+    const int lo_e = wl >= 0 ? P + my_len - a.T + qi_e - wl : INT_MIN;  // the row's window bound
     st = RowState{-INFINITY, 0.f};
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
@@ -665,11 +680,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
         const int kl = ks * 32 + 16 * (rr >> 3) + 8 * lhalf_e + (rr & 7);  // key within the tile
-        v |= (PREFILL ? t * ST_KEYS + kl <= lim : kl < nk && (!WIN || kb + t * ST_KEYS + kl >= lo_e)) ? 1u << rr : 0u;
+        v |= (PREFILL ? t * ST_KEYS + kl <= lim : kl < nk && kb + t * ST_KEYS + kl >= lo_e) ? 1u << rr : 0u;
       }
       const uint32_t vis[1] = {v};
       const f32x16_t s1[1] = {qk_half<DT>(lds, ks * 32, lane_e, qf)};
-      weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, p, o);
+      weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, p, o, tb(t));
       pv<DT, 1>(lds, ks * 32, lane_e, p, o);
       __syncthreads();
     }
@@ -786,7 +801,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     // register r of this lane is slot 16*(r>>3) + 8*lhalf + (r&7) of the group's 32
     const int lim = ok_e ? my_len - a.T + qi_e : -1;
     // window: suffix token j sits at key P + j
-    const int jlo = WIN ? my_len - a.T + qi_e - a.win_left : 0;
+    const int jlo = wl >= 0 ? my_len - a.T + qi_e - wl : 0;
     uint32_t vis = 0;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
@@ -798,7 +813,18 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const f32x16_t s1[1] = {qk_half<DT>(sbuf, (rg & 1) * 32, lane_e, qf)};
     const uint32_t vis1[1] = {vis};
     u32x4_t pw[1][2];
-    weights<DT, SOFTCAP, true, 1>(s1, vis1, st, c, cap, pw, o);
+    if constexpr (OPT) {
+      // ALiBi of suffix token j (key P + j): alpha * (j - (len - T + qi))
+      float bb[16];
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int info = suf_info[h][rg][16 * (rr >> 3) + 8 * lhalf_e + (rr & 7)];
+        bb[rr] = alpha * (float)((info & 0xFFFF) - (my_len - a.T + qi_e));
+      }
+      weights<DT, SOFTCAP, true, 1>(s1, vis1, st, c, cap, pw, o, ArrBias{bb});
+    } else {
+      weights<DT, SOFTCAP, true, 1>(s1, vis1, st, c, cap, pw, o);
+    }
     pv<DT, 1>(sbuf, (rg & 1) * 32, lane_e, pw, o);
   };
   // Tiles in pairs: the key-half-0 wave of each row group takes the first
@@ -979,9 +1005,9 @@ __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
 
 bool mfma_decode_supported(const DecodeArgs& a) {
   if (a.D != HD || (a.dtype != GR_DTYPE_BF16 && a.dtype != GR_DTYPE_F16)) return false;
-  // options here: sinks and a decode's left window; ALiBi, fp8 caches, right
-  // windows and non-causal batches take the generic kernel
-  if (a.alibi || a.kv8 || !a.causal || a.win_right >= 0) return false;
+  // options here: sinks, and a decode's left window and ALiBi; fp8 caches,
+  // right windows and non-causal batches take the generic kernel
+  if (a.kv8 || !a.causal || a.win_right >= 0) return false;
   if (a.bs_shift < 2) return false;  // power-of-two block size >= 4
   if (a.num_blocks < 1) return false;  // an empty pool: the generic kernel reads nothing
   // the suffix tiles tag each key with its 16-bit index within the beam's suffix
@@ -997,17 +1023,17 @@ bool mfma_decode_supported(const DecodeArgs& a) {
   return true;
 }
 
-bool mfma_prefill_supported(const DecodeArgs& a) { return mfma_decode_supported(a) && a.win_left < 0; }
+bool mfma_prefill_supported(const DecodeArgs& a) { return mfma_decode_supported(a) && a.win_left < 0 && !a.alibi; }
 
-template <bool PREFILL, bool SPLIT, bool WIN>
+template <bool PREFILL, bool SPLIT, bool OPT>
 static void launch_mfma_kernel(const DecodeArgs& a, dim3 grid, int units, int mtiles, hipStream_t stream) {
   const bool cap = a.softcap > 0.f;
   if (a.dtype == GR_DTYPE_BF16) {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL, SPLIT, WIN>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL, SPLIT, WIN>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL, SPLIT, OPT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL, SPLIT, OPT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
   } else {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL, SPLIT, WIN>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL, SPLIT, WIN>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL, SPLIT, OPT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL, SPLIT, OPT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
   }
 }
 
@@ -1022,7 +1048,8 @@ static gr_status_t launch_mfma(const DecodeArgs& a, hipStream_t stream) {
   if (nwg > 0x7fffffff) return GR_ERR_INVALID_ARG;
   const int mtiles = (int)mt64;
   dim3 grid((unsigned)nwg);
-  if (!PREFILL && a.win_left >= 0) launch_mfma_kernel<PREFILL, SPLIT, !PREFILL>(a, grid, units, mtiles, stream);
+  if (!PREFILL && (a.win_left >= 0 || a.alibi))
+    launch_mfma_kernel<PREFILL, SPLIT, !PREFILL>(a, grid, units, mtiles, stream);
   else launch_mfma_kernel<PREFILL, SPLIT, false>(a, grid, units, mtiles, stream);
   return launch_status();
 }

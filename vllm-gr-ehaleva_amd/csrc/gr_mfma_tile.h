@@ -133,6 +133,28 @@ __device__ inline float score_l2(float v, float c, float cap) {
   return SOFTCAP ? cap * tanhf(v * c) * LOG2E : v * c;
 }
 
+// The additive term of a weight's exponent (log2 units) for register r of a
+// lane's 16: the negated reference mref plus the key's own bias.  NoBias: none.
+// LinBias: ALiBi's alpha * (key - qpos) over a tile's keys, b0 = the bias of
+// the lane's first key (register r holds the key 16 (r >> 3) + (r & 7) past
+// it).  ArrBias: one bias per register (gathered suffix keys).  The reference
+// itself follows the scores without bias: an ALiBi bias is never positive for
+// a key at or before the query, so it cannot push a weight past the bound the
+// fast path checks.
+struct NoBias {
+  __device__ float operator()(int, float mref) const { return -mref; }
+};
+struct LinBias {
+  float alpha, b0;
+  __device__ float operator()(int r, float mref) const {
+    return fmaf(alpha, (float)(16 * (r >> 3) + (r & 7)), b0 - mref);
+  }
+};
+struct ArrBias {
+  const float* b;
+  __device__ float operator()(int r, float mref) const { return b[r] - mref; }
+};
+
 // A lane's 16 weights of one half-tile against the row's reference maximum
 // mref (log2 domain), with no tile maximum: the branch-free common case.
 // Weights are packed pairwise as they are produced (p0: registers 0..7, p1:
@@ -140,18 +162,18 @@ __device__ inline float score_l2(float v, float c, float cap) {
 // softmax_exact when any lane's sum exceeds 2^Rescale::THRESH (some key is
 // more than Rescale::THRESH above the reference) or is not finite (the row
 // has no reference yet: mref = -inf makes every visible weight +inf).
-template <int DT, bool SOFTCAP, bool MASKED>
+template <int DT, bool SOFTCAP, bool MASKED, typename B = NoBias>
 __device__ inline float softmax_fast(const f32x16_t& s, uint32_t vis, float mref, float c, float cap,
-                                     u32x4_t& p0, u32x4_t& p1) {
+                                     u32x4_t& p0, u32x4_t& p1, const B& bias = B{}) {
   using M = Mma<DT>;
   float acc0 = 0.f, acc1 = 0.f;
   uint32_t pk[8];
 #pragma unroll
   for (int r = 0; r < 16; r += 2) {
-    float e0 = SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(s[r], c, cap) - mref)
-                       : __builtin_amdgcn_exp2f(fmaf(s[r], c, -mref));
-    float e1 = SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(s[r + 1], c, cap) - mref)
-                       : __builtin_amdgcn_exp2f(fmaf(s[r + 1], c, -mref));
+    float e0 = SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(s[r], c, cap) + bias(r, mref))
+                       : __builtin_amdgcn_exp2f(fmaf(s[r], c, bias(r, mref)));
+    float e1 = SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(s[r + 1], c, cap) + bias(r + 1, mref))
+                       : __builtin_amdgcn_exp2f(fmaf(s[r + 1], c, bias(r + 1, mref)));
     if (MASKED) {
       e0 = (vis >> r) & 1 ? e0 : 0.f;
       e1 = (vis >> (r + 1)) & 1 ? e1 : 0.f;
@@ -179,11 +201,12 @@ __device__ inline f32x16_t qk_half(const uint16_t* buf, int kbase, int lane, con
   return s;
 }
 
-// Weight of one score against the reference mref (log2 domain).
+// Weight of one score given its exponent term negoff (the negated reference
+// plus the key's bias, log2 domain).
 template <bool SOFTCAP>
-__device__ inline float weight1(float v, float c, float cap, float mref) {
-  return SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(v, c, cap) - mref)
-                 : __builtin_amdgcn_exp2f(fmaf(v, c, -mref));
+__device__ inline float weight1(float v, float c, float cap, float negoff) {
+  return SOFTCAP ? __builtin_amdgcn_exp2f(score_l2<true>(v, c, cap) + negoff)
+                 : __builtin_amdgcn_exp2f(fmaf(v, c, negoff));
 }
 
 // O += V^T . P^T over NH 32-key halves starting at row kbase.  The V^T
@@ -216,14 +239,15 @@ __device__ inline void pv(const uint16_t* buf, int kbase, int lane, const u32x4_
 // could exceed 2^Rescale::THRESH or the row has no reference yet -- the exact
 // path that moves the reference to the maximum over all NH halves and scales
 // O (skipped while the row has accumulated nothing).
-template <int DT, bool SOFTCAP, bool MASKED, int NH>
+template <int DT, bool SOFTCAP, bool MASKED, int NH, typename B = NoBias>
 __device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH], RowState& st, float c, float cap,
-                               u32x4_t (&p)[NH][2], f32x16_t (&o)[4]) {
+                               u32x4_t (&p)[NH][2], f32x16_t (&o)[4], const B& bias = B{}) {
+  static_assert(NH == 1 || sizeof(B) == sizeof(NoBias), "a bias covers one half-tile");
   float acc = 0.f;
   bool hot = false;
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
-    const float a_h = softmax_fast<DT, SOFTCAP, MASKED>(s[h], vis[h], st.m, c, cap, p[h][0], p[h][1]);
+    const float a_h = softmax_fast<DT, SOFTCAP, MASKED>(s[h], vis[h], st.m, c, cap, p[h][0], p[h][1], bias);
     hot |= !(a_h <= Rescale<DT>::SUM);
     acc += a_h;
   }
@@ -252,7 +276,8 @@ __device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH
   st.m = new_m;
   float acc2 = 0.f;
 #pragma unroll
-  for (int h = 0; h < NH; ++h) acc2 += softmax_fast<DT, SOFTCAP, MASKED>(s[h], vis[h], mref, c, cap, p[h][0], p[h][1]);
+  for (int h = 0; h < NH; ++h)
+    acc2 += softmax_fast<DT, SOFTCAP, MASKED>(s[h], vis[h], mref, c, cap, p[h][0], p[h][1], bias);
   st.lsum = st.lsum * alpha + acc2;
   if (__ballot(had_mass && alpha != 1.f) != 0) {
     __asm__ volatile("" ::: "memory");
@@ -271,10 +296,10 @@ __device__ inline void weights(const f32x16_t (&s)[NH], const uint32_t (&vis)[NH
 // needs the exact path); otherwise adds the weight sum to the row's state.
 // DEFER: no wave vote -- the lane's sum is always added and the lane's own
 // flag returned (the caller votes once, after its loop, and recomputes).
-template <int DT, bool SOFTCAP, bool DEFER = false>
+template <int DT, bool SOFTCAP, bool DEFER = false, typename B = NoBias>
 __device__ inline bool phase_a1(const uint16_t* next_buf, int kbase, int lane, const u32x4_t (&qf)[8],
                                 const f32x16_t& s_in, f32x16_t& s_out, RowState& st, float c, float cap,
-                                u32x4_t (&p)[1][2]) {
+                                u32x4_t (&p)[1][2], const B& bias = B{}) {
   using M = Mma<DT>;
   const int lhalf = lane >> 5;
   const int krow_i = kbase + key_perm(lane & 31);
@@ -293,8 +318,8 @@ __device__ inline bool phase_a1(const uint16_t* next_buf, int kbase, int lane, c
   for (int i = 0; i < 8; ++i) {
     if (i + 2 < 8) kf[i + 2] = kfrag(i + 2);
     s_out = M::mma(kf[i], qf[i], s_out);
-    const float e0 = weight1<SOFTCAP>(s_in[2 * i], c, cap, mref);
-    const float e1 = weight1<SOFTCAP>(s_in[2 * i + 1], c, cap, mref);
+    const float e0 = weight1<SOFTCAP>(s_in[2 * i], c, cap, bias(2 * i, mref));
+    const float e1 = weight1<SOFTCAP>(s_in[2 * i + 1], c, cap, bias(2 * i + 1, mref));
     acc0 += e0;
     acc1 += e1;
     pk[i] = M::pack2(e0, e1);
@@ -346,10 +371,10 @@ __device__ inline void phase_c1(const uint16_t* cur_buf, int kbase, int lane, co
 // latency), and the first two V^T fragment reads of phase C during the last
 // two QK MFMAs, so neither phase starts on an LDS round trip.  Same
 // arithmetic, in the same order, as phase_a1<DEFER> followed by phase_c1.
-template <int DT, bool SOFTCAP, typename Mid>
+template <int DT, bool SOFTCAP, typename Mid, typename B = NoBias>
 __device__ inline bool phase_ac(const uint16_t* next_buf, const uint16_t* cur_buf, int kbase, int lane,
                                 const u32x4_t (&qf)[8], const f32x16_t& s_in, f32x16_t& s_out, RowState& st, float c,
-                                float cap, f32x16_t (&o)[4], Mid&& mid) {
+                                float cap, f32x16_t (&o)[4], Mid&& mid, const B& bias = B{}) {
   using M = Mma<DT>;
   const int lhalf = lane >> 5;
   const int krow_i = kbase + key_perm(lane & 31);
@@ -379,8 +404,8 @@ __device__ inline bool phase_ac(const uint16_t* next_buf, const uint16_t* cur_bu
     if (i + 2 < 8) kf[i + 2] = kfrag(i + 2);
     else vf[i - 6] = vfrag(i - 6);
     s_out = M::mma(kf[i], qf[i], s_out);
-    const float e0 = weight1<SOFTCAP>(s_in[2 * i], c, cap, mref);
-    const float e1 = weight1<SOFTCAP>(s_in[2 * i + 1], c, cap, mref);
+    const float e0 = weight1<SOFTCAP>(s_in[2 * i], c, cap, bias(2 * i, mref));
+    const float e1 = weight1<SOFTCAP>(s_in[2 * i + 1], c, cap, bias(2 * i + 1, mref));
     acc0 += e0;
     acc1 += e1;
     pk[i] = M::pack2(e0, e1);
@@ -402,16 +427,16 @@ __device__ inline bool phase_ac(const uint16_t* next_buf, const uint16_t* cur_bu
 
 // One pipelined step with the exact path in line (phase A; the exact weights
 // when phase A reports it; phase C).
-template <int DT, bool SOFTCAP>
+template <int DT, bool SOFTCAP, typename B = NoBias>
 __device__ inline void pipe_step(const uint16_t* cur_buf, const uint16_t* next_buf, int kbase, int lane,
                                  const u32x4_t (&qf)[8], const f32x16_t& s_in, f32x16_t& s_out,
-                                 f32x16_t (&o)[4], RowState& st, float c, float cap) {
+                                 f32x16_t (&o)[4], RowState& st, float c, float cap, const B& bias = B{}) {
   u32x4_t p[1][2];
-  if (phase_a1<DT, SOFTCAP>(next_buf, kbase, lane, qf, s_in, s_out, st, c, cap, p)) {
+  if (phase_a1<DT, SOFTCAP, false, B>(next_buf, kbase, lane, qf, s_in, s_out, st, c, cap, p, bias)) {
     __asm__ volatile("" ::: "memory");
     const uint32_t vis[1] = {0xFFFFu};
     const f32x16_t s1[1] = {s_in};
-    weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, o);
+    weights<DT, SOFTCAP, false, 1>(s1, vis, st, c, cap, p, o, bias);
   }
   phase_c1<DT>(cur_buf, kbase, lane, p, o);
 }
