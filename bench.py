@@ -467,7 +467,9 @@ def main() -> int:
         "host_us_per_enqueue": dict(HOST_US),
         "timing": TIMING_NOTE,
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": _traffic_from_profile("decode")},
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     # the committed counter profile covers the default decode only
+                     "traffic": _traffic_from_profile("decode") if args.option == "none" else None},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -4,9 +4,13 @@ reference, vllm_gr/v1/attention/backends/beam_attn.py:617-618, :727-737).
 * the quantising cache write (gr_reshape_and_cache_fp8) equals the oracle's
   e4m3(clamp(x / scale, -448, 448)) byte for byte (oracle/fp8.py, pinned
   against torch's float8_e4m3fn);
-* decode and prefill over fp8 caches (the generic kernel) equal the float64
-  oracle over the dequantised caches (e4m3 * scale) within the bf16/fp16
-  output tolerance 2e-2;
+* decode and prefill over fp8 caches equal the float64 oracle over the
+  dequantised caches (e4m3 * scale) within the bf16/fp16 output tolerance
+  2e-2: the matrix-core kernel (bytes staged in LDS and widened to bf16 /
+  fp16 tiles, K scale folded into the softmax constant, V scale into the
+  output) at short and long prefixes, split and unsplit, with the decode
+  options, through lean and row-by-row tile loads and the exact
+  recomputation; the generic kernel on the short case;
 * the fork moves fp8 bytes exactly as oracle.fork does;
 * BeamAttentionImpl.forward with an fp8 cache and the layer's scales.
 """
@@ -74,8 +78,9 @@ def test_reshape_and_cache_fp8_bit_exact(device, src_dtype, scales, view):
 
 @pytest.mark.parametrize("dtype,T", [(torch.bfloat16, 1), (torch.float16, 2), (torch.bfloat16, 3)])
 @pytest.mark.parametrize("scales", [(1.0, 1.0), (0.05, 0.02)])
-def test_decode_fp8_cache(device, dtype, T, scales):
-    print(f"[fp8] decode {dtype} T={T} scales={scales}", flush=True)
+@pytest.mark.parametrize("kernel", ["auto", "generic"])
+def test_decode_fp8_cache(device, dtype, T, scales, kernel):
+    print(f"[fp8] decode {dtype} T={T} scales={scales} kernel={kernel}", flush=True)
     wl = workloads.make_decode(R=3, W=5, P=140, L=(T, T + 9), Hq=8, Hkv=2, D=128, dtype=dtype,
                                input_scale=1.0, seed=11 + T, q_per_beam=T)
     g = torch.Generator().manual_seed(5 + T)
@@ -86,10 +91,14 @@ def test_decode_fp8_cache(device, dtype, T, scales):
     out = torch.empty_like(d.q)
     lse = torch.empty(d.q.shape[:2], dtype=torch.float32, device=device)
     st = ops.new_status(device)
-    ops.beam_attn_decode(d.q, kc.to(device), vc.to(device), d.prefix_bt, d.prefix_len, d.beam_start, d.suffix_bt,
-                         d.suffix_len, q_per_beam=T, scale=d.scale, out=out, lse=lse, status=st,
-                         k_scale=torch.tensor([sk], device=device), v_scale=torch.tensor([sv], device=device))
-    torch.cuda.synchronize()
+    ops.set_decode_kernel(kernel)
+    try:
+        ops.beam_attn_decode(d.q, kc.to(device), vc.to(device), d.prefix_bt, d.prefix_len, d.beam_start,
+                             d.suffix_bt, d.suffix_len, q_per_beam=T, scale=d.scale, out=out, lse=lse, status=st,
+                             k_scale=torch.tensor([sk], device=device), v_scale=torch.tensor([sv], device=device))
+        torch.cuda.synchronize()
+    finally:
+        ops.set_decode_kernel("auto")
     ops.check_status(st)
     ro, rl = oa.beam_attention_dense(wl.q.to(torch.float64).numpy(), _deq(kc, sk), _deq(vc, sv),
                                      wl.prefix_bt.numpy(), wl.prefix_len.numpy(), wl.beam_start.numpy(),
@@ -97,6 +106,76 @@ def test_decode_fp8_cache(device, dtype, T, scales):
                                      block_size=wl.block_size)
     assert np.abs(out.cpu().double().numpy() - ro).max() <= 2e-2
     assert np.abs(lse.cpu().double().numpy() - rl).max() <= 2e-2
+
+
+def _long_fp8_case(dtype, bs, seed, sk=0.05, sv=0.02):
+    wl = workloads.make_decode(R=3, W=24, P=1000, L=(1, 8), Hq=16, Hkv=4, D=128, block_size=bs, dtype=dtype,
+                               input_scale=1.0, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    return wl, _codes(wl.kv_cache.shape[1:], sk, g), _codes(wl.kv_cache.shape[1:], sv, g)
+
+
+def _run_fp8_decode(wl, kc, vc, sk, sv, device, split, **kw):
+    d = wl.to(device)
+    out = torch.empty_like(d.q)
+    lse = torch.empty(d.q.shape[:2], dtype=torch.float32, device=device)
+    st = ops.new_status(device)
+    kw = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
+    ops.beam_attn_decode(d.q, kc.to(device).view(torch.float8_e4m3fn), vc.to(device).view(torch.float8_e4m3fn),
+                         d.prefix_bt, d.prefix_len, d.beam_start, d.suffix_bt, d.suffix_len, scale=d.scale, out=out,
+                         lse=lse, status=st, split=split, max_prefix_len=int(wl.prefix_len.max()) if split else None,
+                         k_scale=torch.tensor([sk], device=device), v_scale=torch.tensor([sv], device=device), **kw)
+    torch.cuda.synchronize()
+    ops.check_status(st)
+    return out.cpu().double().numpy(), lse.cpu().double().numpy()
+
+
+def _fp8_oracle(wl, kc, vc, sk, sv, **kw):
+    kw = {k: (v.numpy() if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
+    return oa.beam_attention_dense(wl.q.to(torch.float64).numpy(), _deq(kc, sk), _deq(vc, sv),
+                                   wl.prefix_bt.numpy(), wl.prefix_len.numpy(), wl.beam_start.numpy(),
+                                   wl.suffix_bt.numpy(), wl.suffix_len.numpy(), scale=wl.scale,
+                                   block_size=wl.block_size, **kw)
+
+
+@pytest.mark.parametrize("opts", [False, True])
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("dtype,bs", [(torch.bfloat16, 16), (torch.float16, 16), (torch.bfloat16, 4)])
+def test_decode_fp8_long_prefix(device, dtype, bs, split, opts):
+    """Sixteen 64-key prefix tiles per request on the matrix-core decode: the
+    fp8 staging ring through the pipelined loop, with lean tile loads (block
+    size 16) and row-by-row loads through the staged block table (block size
+    4); with a left window, sinks and ALiBi (the option variant) or none."""
+    print(f"[fp8] long decode {dtype} bs={bs} split={split} opts={opts}", flush=True)
+    sk, sv = 0.05, 0.02
+    wl, kc, vc = _long_fp8_case(dtype, bs, seed=61 + bs)
+    kw = {}
+    if opts:
+        kw = dict(window=(400, -1), sinks=torch.randn(16, generator=torch.Generator().manual_seed(2)) * 3,
+                  alibi_slopes=torch.tensor([2.0 ** (-8.0 * (h + 1) / 16) for h in range(16)]))
+    out, lse = _run_fp8_decode(wl, kc, vc, sk, sv, device, split, **kw)
+    ro, rl = _fp8_oracle(wl, kc, vc, sk, sv, **kw)
+    assert np.abs(out - ro).max() <= 2e-2
+    assert np.abs(lse - rl).max() <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,pos", [(torch.bfloat16, 200), (torch.float16, 930)])
+def test_decode_fp8_dominant_key(device, dtype, pos):
+    """A K row planted (in fp8) to dominate one query row far beyond the lazy
+    softmax margin: the workgroup's exact recomputation stages and widens the
+    fp8 tiles one at a time."""
+    sk, sv = 0.05, 0.02
+    wl, kc, vc = _long_fp8_case(dtype, 16, seed=71)
+    n, h = int(wl.beam_start[1]) + 3, 2  # request 1's beam 3, query head 2 (KV head 0)
+    q = wl.q[n, h].double()
+    blk = int(wl.prefix_bt[1, pos // wl.block_size])
+    kc[blk, pos % wl.block_size, 0] = torch.from_numpy(fp8.quantize((q / q.norm() * 60.0).float().numpy(), sk))
+    print(f"[fp8] dominant key {dtype} pos={pos}", flush=True)
+    out, lse = _run_fp8_decode(wl, kc, vc, sk, sv, device, False)
+    ro, rl = _fp8_oracle(wl, kc, vc, sk, sv)
+    assert rl[n, h] > 50.0
+    assert np.abs(out - ro).max() <= 2e-2
+    assert np.abs(lse - rl).max() <= 2e-2
 
 
 @pytest.mark.parametrize("causal", [True, False])

@@ -37,8 +37,9 @@ constexpr int SB_STAGE = 2;    // suffix block ids staged in LDS per beam (more 
 // those loads: the count is explicit).
 template <int INFLIGHT>
 __device__ inline void tile_barrier() {
-  static_assert(INFLIGHT == 0 || INFLIGHT == LOADS_PER_TILE, "one tile in flight at most");
+  static_assert(INFLIGHT == 0 || INFLIGHT == 2 || INFLIGHT == LOADS_PER_TILE, "one tile in flight at most");
   if constexpr (INFLIGHT == LOADS_PER_TILE) __asm__ volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (INFLIGHT == 2) __asm__ volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   else __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
@@ -61,9 +62,16 @@ __device__ inline void tile_barrier() {
 // of the key in each tile (LinBias); the softmax reference follows the raw
 // scores.  Sinks (a.sinks, any mode) join each row's softmax in the epilogue
 // (in split_merge for the split mode).
-template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false, bool OPT = false>
+// KV8: the caches hold OCP e4m3 bytes (read as e4m3 * k_scale / v_scale).
+// Tiles land as bytes in a three-slot staging ring after three tile buffers;
+// each wave converts the rows it loaded into a tile buffer one step ahead of
+// their use, so the matrix-core steps read bf16 / fp16 tiles as usual.  The K
+// scale folds into the softmax constant, the V scale into the output.
+template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false, bool OPT = false, bool KV8 = false>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[NBUF * BUF];
+  constexpr int NB = KV8 ? 3 : NBUF;       // tile buffers
+  constexpr int STG = 16384;               // bytes per fp8 staging slot: 64 rows x 128 B of K, then of V
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[KV8 ? 3 * BUF + 3 * STG / 2 : NBUF * BUF];
   __shared__ int suf_cum[4][34];         // per row group: cumulative suffix lengths of its beams
   __shared__ int suf_info[2][4][32];     // per suffix tile and row group slot: (beam << 16) | j, or -1
   __shared__ int suf_s0[4][32];          // per row group beam: first suffix position
@@ -151,7 +159,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   const int my_qi = PREFILL ? my_rho / G : (my_rho / G) % a.T, my_g = my_rho % G;
   const int64_t my_tok = PREFILL ? (int64_t)(nb0 + my_qi) : (int64_t)((nb0 + my_b) * a.T + my_qi);
   u32x4_t qf[8];
-  const float c = SOFTCAP ? a.scale / a.softcap : a.scale * LOG2E;
+  // an fp8 cache's K scale multiplies every score: it folds into c
+  const float ksc = KV8 && a.k_scale ? a.k_scale[0] : 1.f;
+  const float vsc = KV8 && a.v_scale ? a.v_scale[0] : 1.f;
+  const float c = (SOFTCAP ? a.scale / a.softcap : a.scale * LOG2E) * ksc;
   const float cap = a.softcap;
 
   f32x16_t o[4];
@@ -334,8 +345,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     if (lean && lane < n_st && key < P) {
       const int blk = max(pbt_s[key >> bsh], 0);
       const uint64_t e = (uint64_t)(uint32_t)blk * blk_stride + (uint64_t)(uint32_t)(key & (a.bs - 1)) * (uint64_t)tok;
-      toff_lo = (uint32_t)(e << 1);
-      toff_hi = (uint32_t)(e >> 31);
+      const uint64_t eb = KV8 ? e : e << 1;  // bytes
+      toff_lo = (uint32_t)eb;
+      toff_hi = (uint32_t)(eb >> 32);
     }
   }
   const char* kc_h = reinterpret_cast<const char*>(kc + head_off);
@@ -358,9 +370,57 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     if (lean && (t + 1 < n_st || last_full)) issue_tile_lean(t, t);
     else issue_tile(t, t);
   };
-  // the first two tiles, into buffers 0 and 1
-  if (n_st > 0) issue_first(0);
-  if (n_st > 1) issue_first(1);
+  // fp8: tile t's bytes into staging slot `slot`, this wave's rows 8 wv .. 8 wv
+  // + 7 of K and of V (lane i: row 8 wv + (i >> 3), 16-byte chunk i & 7), one
+  // 1 KB load each; lean tiles from the lane offsets, others row by row
+  // through the staged window (rows past the prefix or in an invalid block
+  // read the zero source)
+  const uint8_t* kc8 = static_cast<const uint8_t*>(a.k_cache);
+  const uint8_t* vc8 = static_cast<const uint8_t*>(a.v_cache);
+  const int r8 = lane >> 3, c8 = lane & 7;
+  const uint32_t vo8 = (uint32_t)(r8 * tok + c8 * 16);
+  const uint32_t stg_w = lds0 + (uint32_t)(3 * BUF * 2) + (uint32_t)(wv * 1024);
+  auto dma8 = [&](int t, int slot) {
+    const uint32_t d = stg_w + (uint32_t)(slot * STG);
+    if (lean && (t + 1 < n_st || last_full)) {
+      const uint64_t toff = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)toff_hi, t) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)toff_lo, t);
+      dma_s(d, kc8 + head_off + toff, vo8);
+      dma_s(d + 8192, vc8 + head_off + toff, vo8);
+    } else {
+      const int k0 = kb + t * ST_KEYS;
+      ensure_window(k0);
+      const int key = k0 + 8 * wv + r8;
+      const int blk = key < P ? pbt_s[(key >> bsh) - win0] : -1;
+      const int64_t off = (int64_t)((uint64_t)(uint32_t)max(blk, 0) * blk_stride) + (int64_t)(key & (a.bs - 1)) * tok +
+                          head_off + c8 * 16;
+      const bool ok = key < P && blk >= 0;
+      dma_v(d, ok ? (const void*)(kc8 + off) : (const void*)zsrc);
+      dma_v(d + 8192, ok ? (const void*)(vc8 + off) : (const void*)zsrc);
+    }
+  };
+  // fp8: this wave's rows of staging slot `slot` as bf16 / fp16 into tile
+  // buffer `buf`, in the swizzled layouts the fragment reads expect
+  auto convert8 = [&](int slot, int buf) {
+    const uint8_t* st8 = reinterpret_cast<const uint8_t*>(lds) + 3 * BUF * 2 + slot * STG;
+    const int row = 8 * wv + r8;
+    const u32x4_t rk = *reinterpret_cast<const u32x4_t*>(st8 + row * 128 + c8 * 16);
+    const u32x4_t rv = *reinterpret_cast<const u32x4_t*>(st8 + 8192 + row * 128 + c8 * 16);
+    uint16_t* bk = lds + buf * BUF + row * KS_PITCH;
+    uint16_t* bvv = lds + buf * BUF + K_TILE + row * VS_PITCH;
+    *reinterpret_cast<u32x4_t*>(bk + kchunk(row, 2 * c8) * 8) = Fp8Cvt<DT>::x8(rk[0], rk[1]);
+    *reinterpret_cast<u32x4_t*>(bk + kchunk(row, 2 * c8 + 1) * 8) = Fp8Cvt<DT>::x8(rk[2], rk[3]);
+    *reinterpret_cast<u32x4_t*>(bvv + vchunk(row, 2 * c8) * 8) = Fp8Cvt<DT>::x8(rv[0], rv[1]);
+    *reinterpret_cast<u32x4_t*>(bvv + vchunk(row, 2 * c8 + 1) * 8) = Fp8Cvt<DT>::x8(rv[2], rv[3]);
+  };
+  // the first tiles: bf16 / fp16 tiles 0 and 1 into buffers 0 and 1; fp8
+  // tiles 0, 1, 2 into staging slots 0, 1, 2 (0 and 1 converted below)
+  if constexpr (KV8) {
+    for (int t = 0; t < min(n_st, 3); ++t) dma8(t, t);
+  } else {
+    if (n_st > 0) issue_first(0);
+    if (n_st > 1) issue_first(1);
+  }
   int suf_len = 0, suf_incl = 0;  // this meta lane's validated suffix length, inclusive prefix sum
   if (ks == 0) {
     int len = 0;
@@ -437,6 +497,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     for (int off = 32; off >= 1; off >>= 1) hi = max(hi, __shfl_xor(hi, off, 64));
     if (lane == 0) win_hi[wave] = hi;
   }
+  if constexpr (KV8) {
+    if (n_st > 0) convert8(0, 0);
+    if (n_st > 1) convert8(1, 1);
+  }
   __syncthreads();
   int n_edge = 0;  // tiles [0, n_edge) of the range: some row's window starts inside or after them
   if constexpr (OPT) {
@@ -445,7 +509,11 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     for (int w = 1; w < 8; ++w) hi = max(hi, win_hi[w]);
     n_edge = hi > kb ? min(n_st, (int)(((int64_t)hi - kb + ST_KEYS - 1) / ST_KEYS)) : 0;
   }
-  if (n_st > 2) issue_first(2);
+  if constexpr (KV8) {
+    if (n_st > 3) dma8(3, 0);  // into tile 0's slot, converted above
+  } else {
+    if (n_st > 2) issue_first(2);
+  }
   f32x16_t s_cur = qk_half<DT>(lds, ks * 32, lane, qf);  // (stale LDS when n_st == 0: never used)
   // the exponent terms of prefix tile t's weights: ALiBi's linear bias, or none
   auto tb = [&](int t) {
@@ -465,7 +533,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   for (int g = 0; g < 4; ++g) max_tot = max(max_tot, suf_cum[g][32]);
   const int n_sit = PREFILL || (SPLIT && split != nsplit - 1) ? 0 : (max_tot + 31) / 32;
   const bool tab_ok = !(suf_tab_bad[0] | suf_tab_bad[1] | suf_tab_bad[2] | suf_tab_bad[3]);
-  const int spf_n = !PREFILL && tab_ok && n_st >= 3 ? 2 * min(n_sit, 2) : 0;  // pieces prefetched
+  const int spf_n = !PREFILL && !KV8 && tab_ok && n_st >= 3 ? 2 * min(n_sit, 2) : 0;  // pieces prefetched
   const int sbase = n_st & 3;  // suffix tile h of row group g sits in buffer (sbase + 2 h + (g >> 1)) % 4
   auto suf_piece = [&](int i) {
     const int h = i >> 1, gp = i & 1;
@@ -484,11 +552,19 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // Tile t+3 goes out at the top of step t, into buffer (t+3) % 4: its
   // previous tile, t-1, was last read in step t-1, before the barrier that
   // ended it.
+  // fp8: the top of step t converts tile t + 2 (staged since step t - 2) into
+  // its buffer (tile t - 1's, read up to step t - 1) and loads tile t + 4 into
+  // staging (tile t + 1's slot, converted in step t - 1).
   auto fetch_ahead = [&](int t) {
+    if constexpr (KV8) {
+      if (t + 2 < n_st) convert8((t + 2) % 3, (t + 2) % 3);
+      if (t + 4 < n_st) dma8(t + 4, (t + 4) % 3);
+      return;
+    }
     const int tn = t + 3;
     if (tn < n_st) {
-      if (lean && (tn + 1 < n_st || last_full)) issue_tile_lean(tn, tn % NBUF);
-      else issue_tile(tn, tn % NBUF);
+      if (lean && (tn + 1 < n_st || last_full)) issue_tile_lean(tn, tn % NB);
+      else issue_tile(tn, tn % NB);
     } else if (tn - n_st < min(spf_n, 3)) {
       suf_piece(tn - n_st);
     }
@@ -496,12 +572,17 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // The end of step t: tile t+2 (read from the next step on) has landed; tile
   // t+3, or the suffix piece issued in its place, may still be in flight.
   auto step_barrier = [&](int t) {
-    if (t + 3 < n_st || t + 3 - n_st < min(spf_n, 3)) tile_barrier<LOADS_PER_TILE>();
-    else tile_barrier<0>();
+    if constexpr (KV8) {  // tile t + 3's bytes (converted next step) have landed; t + 4's may not
+      if (t + 4 < n_st) tile_barrier<2>();
+      else tile_barrier<0>();
+    } else {
+      if (t + 3 < n_st || t + 3 - n_st < min(spf_n, 3)) tile_barrier<LOADS_PER_TILE>();
+      else tile_barrier<0>();
+    }
   };
   auto prefix_step = [&](int it, const f32x16_t& s_in, f32x16_t& s_out) {
     fetch_ahead(it);
-    pipe_step<DT, SOFTCAP>(lds + (it % NBUF) * BUF, lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out,
+    pipe_step<DT, SOFTCAP>(lds + (it % NB) * BUF, lds + ((it + 1) % NB) * BUF, ks * 32, lane, qf, s_in, s_out,
                            o, st, c, cap, tb(it));
     step_barrier(it);
   };
@@ -517,7 +598,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const f32x16_t s1[1] = {s_in};
     u32x4_t pw[1][2];
     weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o, tb(it));
-    pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
+    pv<DT, 1>(lds + (it % NB) * BUF, ks * 32, lane, pw, o);
     __syncthreads();
   };
   f32x16_t s_alt;
@@ -531,7 +612,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   bool hot_seen = false;
   u32x4_t p[1][2];
   auto finish_step = [&](int t) {
-    phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
+    phase_c1<DT>(lds + (t % NB) * BUF, ks * 32, lane, p, o);
     step_barrier(t);
   };
   // tile 0 (and S^T of tile 1): exact weights, O still zero
@@ -551,17 +632,24 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // lane records its own flag and the waves vote after the loop.
   auto fast_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
     fetch_ahead(t);
-    hot_seen |= phase_a1<DT, SOFTCAP, true>(lds + ((t + 1) % NBUF) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p, tb(t));
-    phase_c1<DT>(lds + (t % NBUF) * BUF, ks * 32, lane, p, o);
+    hot_seen |= phase_a1<DT, SOFTCAP, true>(lds + ((t + 1) % NB) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p, tb(t));
+    phase_c1<DT>(lds + (t % NB) * BUF, ks * 32, lane, p, o);
     step_barrier(t);
   };
   // The same step when tile t+3 exists and is full and the lean loads apply
   // (steps t < n_lean): no run-time choices.
-  const int n_lean = lean ? (last_full ? n_st - 3 : n_st - 4) : 0;
+  const int n_lean = !lean ? 0 : KV8 ? (last_full ? n_st - 4 : n_st - 5) : (last_full ? n_st - 3 : n_st - 4);
   auto lean_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
-    hot_seen |= phase_ac<DT, SOFTCAP>(lds + ((t + 1) % NBUF) * BUF, lds + (t % NBUF) * BUF, ks * 32, lane, qf, s_in,
-                                      s_out, st, c, cap, o, [&]() { issue_tile_lean(t + 3, (t + 3) % NBUF); }, tb(t));
-    tile_barrier<LOADS_PER_TILE>();
+    hot_seen |= phase_ac<DT, SOFTCAP>(lds + ((t + 1) % NB) * BUF, lds + (t % NB) * BUF, ks * 32, lane, qf, s_in,
+                                      s_out, st, c, cap, o, [&]() {
+                                        if constexpr (KV8) {
+                                          convert8((t + 2) % 3, (t + 2) % 3);
+                                          dma8(t + 4, (t + 4) % 3);
+                                        } else {
+                                          issue_tile_lean(t + 3, (t + 3) % NB);
+                                        }
+                                      }, tb(t));
+    tile_barrier<KV8 ? 2 : LOADS_PER_TILE>();
   };
   // fast steps over tiles [it, t_end): S^T alternates between s_cur and s_alt
   auto fast_steps = [&](int t_end) {
@@ -605,8 +693,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       const f32x16_t s1[1] = {s_cur};
       u32x4_t pw[1][2];
       weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o, tb(it));
-      pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
-      if (it + 1 < n_st) s_cur = qk_half<DT>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf);
+      pv<DT, 1>(lds + (it % NB) * BUF, ks * 32, lane, pw, o);
+      if (it + 1 < n_st) s_cur = qk_half<DT>(lds + ((it + 1) % NB) * BUF, ks * 32, lane, qf);
       step_barrier(it);
     }
   } else {
@@ -626,8 +714,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         const f32x16_t s1[1] = {s_cur};
         u32x4_t pw[1][2];
         weights<DT, SOFTCAP, true, 1>(s1, vis, st, c, cap, pw, o, tb(it));
-        pv<DT, 1>(lds + (it % NBUF) * BUF, ks * 32, lane, pw, o);
-        if (it + 1 < n_st) s_cur = qk_half<DT>(lds + ((it + 1) % NBUF) * BUF, ks * 32, lane, qf);
+        pv<DT, 1>(lds + (it % NB) * BUF, ks * 32, lane, pw, o);
+        if (it + 1 < n_st) s_cur = qk_half<DT>(lds + ((it + 1) % NB) * BUF, ks * 32, lane, qf);
         if (it + 1 < n_st) step_barrier(it);
         else __syncthreads();
       }
@@ -673,8 +761,15 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
     for (int t = 0; t < n_st; ++t) {
-      issue_tile(t, 0);
-      tile_barrier<0>();
+      if constexpr (KV8) {
+        dma8(t, 0);
+        tile_barrier<0>();
+        convert8(0, 0);
+        __syncthreads();
+      } else {
+        issue_tile(t, 0);
+        tile_barrier<0>();
+      }
       const int nk = t == n_st - 1 ? p_last : ST_KEYS;
       uint32_t v = 0;
 #pragma unroll
@@ -702,6 +797,20 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // tile are issued before its first LDS store.
   constexpr int SUF_PER_THREAD = 4 * 32 * 16 / MF_THREADS;
   static_assert(4 * 32 * 16 % MF_THREADS == 0, "suffix loader split");
+  // element el of the K / V cache (a byte of an fp8 cache), and one 16-byte
+  // chunk of a bf16 / fp16 row loaded from there: eight fp8 bytes converted
+  using gvec = const __attribute__((address_space(1))) u32x4_t*;  // global loads, not flat
+  using gvec2 = const __attribute__((address_space(1))) u32x2_t*;
+  auto kel = [&](int64_t el) { return KV8 ? reinterpret_cast<const S*>(kc8 + el) : kc + el; };
+  auto vel = [&](int64_t el) { return KV8 ? reinterpret_cast<const S*>(vc8 + el) : vc + el; };
+  auto ldchunk = [&](const S* p) -> u32x4_t {
+    if constexpr (KV8) {
+      const u32x2_t w = *(gvec2)(p);
+      return Fp8Cvt<DT>::x8(w[0], w[1]);
+    } else {
+      return *(gvec)(p);
+    }
+  };
   auto suf_gather = [&](int it, int t, u32x4_t (&skv)[SUF_PER_THREAD], u32x4_t (&svv)[SUF_PER_THREAD],
                         int (&sinfo)[SUF_PER_THREAD]) {
     // Two passes: every address first, then all the loads back to back.  Any
@@ -737,8 +846,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
         if (blk >= 0 && blk < a.num_blocks) {
           const int64_t base = (int64_t)blk * a.kv_block_stride + (int64_t)(pos & (a.bs - 1)) * a.kv_tok_stride +
                                head_off + ch * 8;
-          ksrc[i] = kc + base;
-          vsrc[i] = vc + base;
+          ksrc[i] = kel(base);
+          vsrc[i] = vel(base);
           sinfo[i] = (b << 16) | j;
         } else {
           flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
@@ -746,11 +855,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    using gvec = const __attribute__((address_space(1))) u32x4_t*;  // global loads, not flat
 #pragma unroll
     for (int i = 0; i < SUF_PER_THREAD; ++i) {
-      skv[i] = *(gvec)(ksrc[i]);
-      svv[i] = *(gvec)(vsrc[i]);
+      skv[i] = ldchunk(ksrc[i]);
+      svv[i] = ldchunk(vsrc[i]);
     }
   };
   // tile h (0 or 1) of a pair: row group g's slots in buffer 2h + (g >> 1),
@@ -785,15 +893,14 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       const int e = t + i * MF_THREADS;
       const int64_t off = suf_off[e >> 9][h * 32 + ((e >> 4) & 31)];
       const int ch = e & 15;
-      ksrc[i] = off < 0 ? zsrc : kc + off + ch * 8;
-      vsrc[i] = off < 0 ? zsrc : vc + off + ch * 8;
+      ksrc[i] = off < 0 ? zsrc : kel(off + ch * 8);
+      vsrc[i] = off < 0 ? zsrc : vel(off + ch * 8);
     }
     __builtin_amdgcn_sched_barrier(0);
-    using gvec = const __attribute__((address_space(1))) u32x4_t*;  // global loads, not flat
 #pragma unroll
     for (int i = 0; i < SUF_PER_THREAD; ++i) {
-      skv[i] = *(gvec)(ksrc[i]);
-      svv[i] = *(gvec)(vsrc[i]);
+      skv[i] = ldchunk(ksrc[i]);
+      svv[i] = ldchunk(vsrc[i]);
     }
   };
   // this wave's row group against tile h of the pair
@@ -906,7 +1013,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
     const float lrow_sum =
         pair_sum(l0 * a0 + l1 * a1) + (sink_l2 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sink_l2 - m));
-    const float inv = lrow_sum > 0.f ? 1.f / lrow_sum : 0.f;
+    // (an fp8 cache's V scale multiplies the normalised output)
+    const float inv = lrow_sum > 0.f ? vsc / lrow_sum : 0.f;
     if constexpr (SPLIT) {
       // this split's normalised partial O and LSE, every row of the tile
       const int64_t slot = (int64_t)(unit * mtiles + mt) * nsplit + split;
@@ -1005,9 +1113,9 @@ __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
 
 bool mfma_decode_supported(const DecodeArgs& a) {
   if (a.D != HD || (a.dtype != GR_DTYPE_BF16 && a.dtype != GR_DTYPE_F16)) return false;
-  // options here: sinks, and a decode's left window and ALiBi; fp8 caches,
+  // options here: sinks, fp8 caches, and a decode's left window and ALiBi;
   // right windows and non-causal batches take the generic kernel
-  if (a.kv8 || !a.causal || a.win_right >= 0) return false;
+  if (!a.causal || a.win_right >= 0) return false;
   if (a.bs_shift < 2) return false;  // power-of-two block size >= 4
   if (a.num_blocks < 1) return false;  // an empty pool: the generic kernel reads nothing
   // the suffix tiles tag each key with its 16-bit index within the beam's suffix
@@ -1015,8 +1123,10 @@ bool mfma_decode_supported(const DecodeArgs& a) {
   // 16-byte vector access: base pointers and element strides multiples of 8 elements
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!al(a.q) || !al(a.out) || !al(a.k_cache) || !al(a.v_cache)) return false;
-  if (a.q_tok_stride % 8 || a.out_tok_stride % 8 || a.kv_block_stride % 8 || a.kv_tok_stride % 8 ||
-      a.kv_head_stride % 8)
+  // (an fp8 cache's rows move in 16-byte chunks of 16 elements)
+  const int kv_al = a.kv8 ? 16 : 8;
+  if (a.q_tok_stride % 8 || a.out_tok_stride % 8 || a.kv_block_stride % kv_al || a.kv_tok_stride % kv_al ||
+      a.kv_head_stride % kv_al)
     return false;
   // tile loads multiply block ids by the block stride in 32 bits
   if (a.kv_block_stride <= 0 || a.kv_block_stride > 0xFFFFFFFFll) return false;
@@ -1025,16 +1135,25 @@ bool mfma_decode_supported(const DecodeArgs& a) {
 
 bool mfma_prefill_supported(const DecodeArgs& a) { return mfma_decode_supported(a) && a.win_left < 0 && !a.alibi; }
 
-template <bool PREFILL, bool SPLIT, bool OPT>
+template <bool PREFILL, bool SPLIT, bool OPT, bool KV8>
 static void launch_mfma_kernel(const DecodeArgs& a, dim3 grid, int units, int mtiles, hipStream_t stream) {
   const bool cap = a.softcap > 0.f;
+  const dim3 blk(MF_THREADS);
   if (a.dtype == GR_DTYPE_BF16) {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL, SPLIT, OPT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL, SPLIT, OPT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL, SPLIT, OPT, KV8>), grid, blk, 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL, SPLIT, OPT, KV8>), grid, blk, 0, stream, a, units, mtiles);
   } else {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL, SPLIT, OPT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL, SPLIT, OPT>), grid, dim3(MF_THREADS), 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL, SPLIT, OPT, KV8>), grid, blk, 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL, SPLIT, OPT, KV8>), grid, blk, 0, stream, a, units, mtiles);
   }
+}
+
+// the option variant (a decode's window or ALiBi) and the fp8-cache variant
+template <bool PREFILL, bool SPLIT, bool KV8>
+static void launch_mfma_opt(const DecodeArgs& a, dim3 grid, int units, int mtiles, hipStream_t stream) {
+  if (!PREFILL && (a.win_left >= 0 || a.alibi))
+    launch_mfma_kernel<PREFILL, SPLIT, !PREFILL, KV8>(a, grid, units, mtiles, stream);
+  else launch_mfma_kernel<PREFILL, SPLIT, false, KV8>(a, grid, units, mtiles, stream);
 }
 
 template <bool PREFILL, bool SPLIT>
@@ -1048,9 +1167,8 @@ static gr_status_t launch_mfma(const DecodeArgs& a, hipStream_t stream) {
   if (nwg > 0x7fffffff) return GR_ERR_INVALID_ARG;
   const int mtiles = (int)mt64;
   dim3 grid((unsigned)nwg);
-  if (!PREFILL && (a.win_left >= 0 || a.alibi))
-    launch_mfma_kernel<PREFILL, SPLIT, !PREFILL>(a, grid, units, mtiles, stream);
-  else launch_mfma_kernel<PREFILL, SPLIT, false>(a, grid, units, mtiles, stream);
+  if (a.kv8) launch_mfma_opt<PREFILL, SPLIT, true>(a, grid, units, mtiles, stream);
+  else launch_mfma_opt<PREFILL, SPLIT, false>(a, grid, units, mtiles, stream);
   return launch_status();
 }
 

@@ -79,6 +79,26 @@ template <> struct Mma<GR_DTYPE_F16> {
   }
 };
 
+// Eight OCP e4m3 bytes (two dwords, element 0 in the low byte) as eight
+// bf16 / fp16 values (exact: e4m3 fits both).
+template <int DT> struct Fp8Cvt;
+template <> struct Fp8Cvt<GR_DTYPE_BF16> {
+  __device__ static inline u32x4_t x8(uint32_t w0, uint32_t w1) {
+    return u32x4_t{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+  }
+};
+template <> struct Fp8Cvt<GR_DTYPE_F16> {
+  __device__ static inline u32x4_t x8(uint32_t w0, uint32_t w1) {
+    return u32x4_t{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
+  }
+};
+
 // S^T row slot i holds tile key PI(i): bits 2 and 3 swapped.
 __device__ inline int key_perm(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
