@@ -33,8 +33,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "vllm-gr-ehaleva_amd")]
 
 METRIC = "BeamAttention decode µs/step + HBM GB/s (% peak) at 128 beams, 2K prefix"
+METRIC_SID = ("BeamAttention decode (split prefix) µs/step + HBM GB/s (% peak) at the semantic-ID decode "
+              "step's shape: 4 requests x 128 beams, 2K prefix")
 HBM_PEAK_GBPS = 8000.0
 PMC_SUMMARY = {w: os.path.join(ROOT, "profiles", f"{w}_beam128_hbm_traffic.txt") for w in ("decode", "fork", "prune")}
+PMC_SUMMARY["decode_sid"] = os.path.join(ROOT, "profiles", "decode_sid_step_hbm_traffic.txt")
 
 
 def _log(*a):
@@ -355,6 +358,10 @@ def main() -> int:
                     help="decode with one optional attention feature of the reference's impl "
                          "(beam_attn.py:597-625): a 1024-token sliding window, per-head sinks, ALiBi "
                          "slopes, or an fp8 e4m3 KV cache (scales 1)")
+    ap.add_argument("--shape", choices=["c2", "sid"], default="c2",
+                    help="decode shape: c2 (8 requests x 128 beams, 32/8 heads; the headline) or sid (one "
+                         "layer of the semantic-ID decode step: 4 x 128 beams, 16/8 heads, suffix 1-3, "
+                         "the split prefix with the longest-prefix hint, as the backend runs it)")
     ap.add_argument("--workload", choices=["decode", "fork", "prune", "e2e"], default="decode",
                     help="decode (the headline line), the fork+append / pruning kernels, or e2e "
                          "(whole semantic-ID beam decode through a 28-layer decoder; a step is one batch)")
@@ -387,8 +394,10 @@ def main() -> int:
         return bench_other(args)
 
     dev = torch.device("cuda:0")
-    _log("bench: building decode_beam128 inputs (seed 0)")
-    host_wl = workloads.decode_beam128(seed=0)
+    sid = args.shape == "sid"
+    _log(f"bench: building {'decode_sid_step' if sid else 'decode_beam128'} inputs (seed 0)")
+    host_wl = workloads.decode_sid_step(seed=0) if sid else workloads.decode_beam128(seed=0)
+    hint = int(host_wl.prefix_len.max()) if sid else None
     wl = host_wl.to(dev)
     ops.set_decode_kernel(args.kernel)
 
@@ -411,7 +420,7 @@ def main() -> int:
         def step():
             ops.beam_attn_decode(q, kv[0], kv[1], wl.prefix_bt, wl.prefix_len, wl.beam_start,
                                  wl.suffix_bt, wl.suffix_len, scale=wl.scale, max_beams_per_req=wl.max_beams,
-                                 out=out, **opt_kw)
+                                 out=out, max_prefix_len=hint, **opt_kw)
         return step
 
     gen = torch.Generator(device=dev)
@@ -440,8 +449,11 @@ def main() -> int:
         cpu = cpu_baseline(host_wl)
         _log(f"bench: cpu {cpu}")
 
+    R, W = host_wl.prefix_len.numel(), host_wl.max_beams
+    Hq_, Hkv_ = host_wl.q.shape[1], host_wl.kv_cache.shape[3]
+    lmin, lmax = int(host_wl.suffix_len.min()), int(host_wl.suffix_len.max())
     line = {
-        "metric": METRIC,
+        "metric": METRIC_SID if sid else METRIC,
         "value": round(gbps, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -455,9 +467,10 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)/sqrt(128) Q/K/V, random block tables)",
-        "config": {"workload": "beam decode: 8 requests x 128 beams, shared prefix 2048, suffix U[1,8], "
-                               "32 q / 8 kv heads, head_dim 128, block 16",
-                   "requests": 8, "beams": 128, "prefix": 2048, "kernel": args.kernel, "option": args.option,
+        "config": {"workload": f"beam decode: {R} requests x {W} beams, shared prefix 2048, suffix "
+                               f"{'U[1,3]' if sid else 'U[1,8]'} (drawn {lmin}-{lmax}), {Hq_} q / {Hkv_} kv "
+                               f"heads, head_dim 128, block 16" + (", split prefix" if sid else ""),
+                   "requests": R, "beams": W, "prefix": 2048, "kernel": args.kernel, "option": args.option,
                    "algorithmic_bytes_per_step": nbytes, "flops_per_step": host_wl.flops(),
                    "inputs": f"{len(cold)} copies rotated per launch (cold: no reuse through the 256 MB "
                              f"Infinity Cache)"},
@@ -468,8 +481,9 @@ def main() -> int:
         "timing": TIMING_NOTE,
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                     # the committed counter profile covers the default decode only
-                     "traffic": _traffic_from_profile("decode") if args.option == "none" else None},
+                     # the committed counter profiles cover the option-free decodes
+                     "traffic": (_traffic_from_profile("decode_sid" if sid else "decode")
+                                 if args.option == "none" else None)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

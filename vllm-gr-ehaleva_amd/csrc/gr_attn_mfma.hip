@@ -742,21 +742,26 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // The lane's row indices again, worked out after the prefix loop instead of
   // being kept live through it (kept, they were spilled to scratch and the
   // epilogue waited on three dependent scratch reloads for its output address).
-  int tid_e = tid;
-  __asm__ volatile("" : "+v"(tid_e));
+  // (the divisors too: the compiler would otherwise keep the prologue's
+  // integer-division reciprocals live through the loop)
+  int tid_e = tid, G_e = G, TG_e = TG, T_e = a.T;
+  __asm__ volatile("" : "+v"(tid_e), "+v"(G_e), "+v"(TG_e), "+v"(T_e));
   const int rho_e = row_base + (tid_e >> 7) * 32 + (tid_e & 31);  // row group tid / 128, row tid % 32
   const bool ok_e = rho_e < rows_r;
-  const int b_e = PREFILL ? 0 : rho_e / TG;
-  const int qi_e = PREFILL ? rho_e / G : (rho_e / G) % a.T;
-  const int g_e = rho_e % G;
+  const int b_e = PREFILL ? 0 : rho_e / TG_e;
+  const int qi_e = PREFILL ? rho_e / G_e : (rho_e / G_e) % T_e;
+  const int g_e = rho_e % G_e;
   const int lane_e = tid_e & 63, lhalf_e = lane_e >> 5, lrow_e = lane_e & 31;
+  // the row's beam's suffix length read again (an L2 hit) rather than kept
+  // live through the loop
+  const int len_e = *(!PREFILL && ok_e ? a.suffix_len + nb0 + b_e : zint);
   const bool hot = hot_flag != 0;
   if (hot) {
     // exact recomputation of the workgroup's prefix range, one tile at a time
     // through buffer 0, every tile on the exact (masked) path (after every
     // suffix piece has landed: their data is gathered again below)
     tile_barrier<0>();
-    const int lo_e = wl >= 0 ? P + my_len - a.T + qi_e - wl : INT_MIN;  // the row's window bound
+    const int lo_e = wl >= 0 ? P + len_e - a.T + qi_e - wl : INT_MIN;  // the row's window bound
     st = RowState{-INFINITY, 0.f};
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) o[mb] = f32x16_t{};
@@ -906,9 +911,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // this wave's row group against tile h of the pair
   auto suf_compute = [&](int h) {
     // register r of this lane is slot 16*(r>>3) + 8*lhalf + (r&7) of the group's 32
-    const int lim = ok_e ? my_len - a.T + qi_e : -1;
+    const int lim = ok_e ? len_e - a.T + qi_e : -1;
     // window: suffix token j sits at key P + j
-    const int jlo = wl >= 0 ? my_len - a.T + qi_e - wl : 0;
+    const int jlo = wl >= 0 ? len_e - a.T + qi_e - wl : 0;
     uint32_t vis = 0;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
@@ -926,7 +931,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
         const int info = suf_info[h][rg][16 * (rr >> 3) + 8 * lhalf_e + (rr & 7)];
-        bb[rr] = alpha * (float)((info & 0xFFFF) - (my_len - a.T + qi_e));
+        bb[rr] = alpha * (float)((info & 0xFFFF) - (len_e - a.T + qi_e));
       }
       weights<DT, SOFTCAP, true, 1>(s1, vis1, st, c, cap, pw, o, ArrBias{bb});
     } else {
@@ -980,13 +985,13 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // ---- merge the two key halves and write O, LSE --------------------------
   // (the row indices once more, from a fresh copy of the thread index, so
   // none of them lives through the suffix phase)
-  int tid_f = tid;
-  __asm__ volatile("" : "+v"(tid_f));
+  int tid_f = tid, G_f = G, TG_f = TG, T_f = a.T;
+  __asm__ volatile("" : "+v"(tid_f), "+v"(G_f), "+v"(TG_f), "+v"(T_f));
   const int rho_f = row_base + (tid_f >> 7) * 32 + (tid_f & 31);
   const bool ok_f = rho_f < rows_r;
-  const int b_f = PREFILL ? 0 : rho_f / TG;
-  const int qi_f = PREFILL ? rho_f / G : (rho_f / G) % a.T;
-  const int g_f = rho_f % G;
+  const int b_f = PREFILL ? 0 : rho_f / TG_f;
+  const int qi_f = PREFILL ? rho_f / G_f : (rho_f / G_f) % T_f;
+  const int g_f = rho_f % G_f;
   const int lane_f = tid_f & 63, lhalf_f = lane_f >> 5, lrow_f = lane_f & 31;
   // [rg][lane][64 accumulators, padded to 68]: 16-byte writes and reads, the
   // padding spreads a row of lanes over every bank

@@ -134,6 +134,14 @@ def decode_beam128(seed: int = 0) -> DecodeWorkload:
                        input_scale=1.0 / math.sqrt(128), seed=seed)
 
 
+def decode_sid_step(seed: int = 0) -> DecodeWorkload:
+    """One layer's attention in a decode step of the semantic-ID beam search:
+    4 requests x 128 beams over 2048-token prompts, 16 q / 8 kv heads, each
+    beam's 1-3 generated tokens as its suffix."""
+    return make_decode(R=4, W=128, P=2048, L=(1, 3), Hq=16, Hkv=8, D=128, dtype=torch.bfloat16,
+                       input_scale=1.0 / math.sqrt(128), seed=seed)
+
+
 @dataclass
 class ForkWorkload:
     parent: torch.Tensor      # [R, W] int32
