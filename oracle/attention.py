@@ -31,7 +31,12 @@ Functions and how each is pinned (tests/test_oracle_attention.py):
 * ``beam_attention_cascade`` -- prefix pass (non-causal, LSE) + suffix pass
   (causal, LSE) + LSE merge, restating ``cascade_attention``
   (``beam_attn.py:629-701``) and ``merge_attn_states``.  Pinned against
-  ``beam_attention_dense`` (must agree to 1e-12).
+  ``beam_attention_dense`` (must agree to 1e-12; with sinks too, and with a
+  window covering every key).  Its window / ALiBi / sinks arguments restate
+  the reference's per-pass semantics (flash-attention's bottom-right
+  alignment in each pass), pinned by a scalar loop written from the
+  documented formulas; ``tests/test_oracle_options.py`` measures how far
+  they depart from this build's absolute-position semantics.
 * ``gather_tokens`` -- paged gather, restating the index arithmetic of
   ``paged_kv_to_contig_suffix_kernel`` (``beam_attn.py:62-92``).  Pinned by
   a block-permutation test.
@@ -179,6 +184,21 @@ def beam_attention_dense(q, k_cache, v_cache, prefix_bt, prefix_len, beam_start,
     return out, lse
 
 
+def _fa_window(Lq: int, Lk: int, window, causal: bool):
+    """One flash-attention pass's visibility ``[Lq, Lk]`` and ALiBi distances
+    under its bottom-right alignment: query row i sits at ``i + Lk - Lq``."""
+    qpos = np.arange(Lq) + Lk - Lq
+    kpos = np.arange(Lk)
+    vis = np.ones((Lq, Lk), bool)
+    if causal:
+        vis &= kpos[None, :] <= qpos[:, None]
+    if window[0] >= 0:
+        vis &= kpos[None, :] >= (qpos - window[0])[:, None]
+    if window[1] >= 0:
+        vis &= kpos[None, :] <= (qpos + window[1])[:, None]
+    return vis, np.abs(qpos[:, None] - kpos[None, :]).astype(np.float64)
+
+
 def merge_states(out_a, lse_a, out_b, lse_b):
     """LSE merge of two partial attention states (the role of vLLM's
     ``merge_attn_states`` at ``beam_attn.py:697-699``): both inputs are
@@ -201,7 +221,8 @@ def merge_states(out_a, lse_a, out_b, lse_b):
 
 def beam_attention_cascade(q, k_cache, v_cache, prefix_bt, prefix_len, beam_start,
                            suffix_bt, suffix_len, suffix_start=None, *, q_per_beam=1,
-                           scale, softcap=0.0, block_size):
+                           scale, softcap=0.0, block_size, window=(-1, -1), sinks=None,
+                           alibi_slopes=None):
     """Cascade form of the same step in float64 (``beam_attn.py:629-701``).
 
     (i) all query rows of a request attend the shared prefix non-causally, as
@@ -209,6 +230,19 @@ def beam_attention_cascade(q, k_cache, v_cache, prefix_bt, prefix_len, beam_star
     one prefix group, ``:381-384``); (ii) each beam's rows attend the beam's
     suffix causally, bottom-right aligned (``:686-695``); (iii) the two
     states are merged by LSE (``:697-699``).
+
+    The options follow the reference's per-pass arguments literally, with
+    flash-attention's documented conventions for a pass of ``Lq`` query rows
+    against ``Lk`` keys: query row i sits at ``i + Lk - Lq``; the window keeps
+    keys ``j`` in ``[i + Lk - Lq - left, i + Lk - Lq + right]`` (a negative
+    bound is unbounded); ALiBi adds ``-slope * |i + Lk - Lq - j|``.  In the
+    prefix pass the request's W * T stacked rows are one sequence (row i =
+    beam-major token index), with ``s_aux`` (the sinks, ``:676``) joining its
+    softmax; in the suffix pass each beam's T rows face its L keys, with no
+    sinks.  These are the reference's semantics, which this build departs
+    from for windows and ALiBi (it places every query at its own token's
+    absolute position, as ``beam_attention_dense`` does); with no window and
+    no ALiBi the two agree.
     """
     q = np.asarray(q, dtype=np.float64)
     T = int(q_per_beam)
@@ -227,10 +261,17 @@ def beam_attention_cascade(q, k_cache, v_cache, prefix_bt, prefix_len, beam_star
         kp = gather_tokens(k_cache, prefix_bt[r], np.arange(P), block_size).astype(np.float64)
         vp = gather_tokens(v_cache, prefix_bt[r], np.arange(P), block_size).astype(np.float64)
         rows = slice(n0 * T, n1 * T)
+        Lq = (n1 - n0) * T
+        vis_p, dist_p = _fa_window(Lq, P, window, causal=False)
         for hk in range(Hkv):
-            qg = q[rows, hk * G:(hk + 1) * G].reshape(-1, D)
-            o, l = _attend_group(qg, kp[:, hk], vp[:, hk], np.ones((qg.shape[0], P), bool),
-                                 scale, softcap)
+            qg = q[rows, hk * G:(hk + 1) * G].reshape(-1, D)  # row (i, g): stacked row i, head hk*G + g
+            heads = np.tile(np.arange(hk * G, (hk + 1) * G), Lq)
+            bias = None
+            if alibi_slopes is not None:
+                bias = -np.asarray(alibi_slopes, np.float64)[heads][:, None] * np.repeat(dist_p, G, axis=0)
+            sink = None if sinks is None else np.asarray(sinks, np.float64)[heads]
+            o, l = _attend_group(qg, kp[:, hk], vp[:, hk], np.repeat(vis_p, G, axis=0),
+                                 scale, softcap, bias, sink)
             o_pre[rows, hk * G:(hk + 1) * G] = o.reshape(-1, G, D)
             l_pre[rows, hk * G:(hk + 1) * G] = l.reshape(-1, G)
         for n in range(n0, n1):
@@ -238,11 +279,15 @@ def beam_attention_cascade(q, k_cache, v_cache, prefix_bt, prefix_len, beam_star
             s0 = 0 if suffix_start is None else int(suffix_start[n])
             ks = gather_tokens(k_cache, suffix_bt[n], s0 + np.arange(L), block_size).astype(np.float64)
             vs = gather_tokens(v_cache, suffix_bt[n], s0 + np.arange(L), block_size).astype(np.float64)
-            vis_t = np.arange(L)[None, :] <= (L - T + np.arange(T))[:, None]
+            vis_t, dist_s = _fa_window(T, L, window, causal=True)
             for hk in range(Hkv):
                 qg = q[n * T:(n + 1) * T, hk * G:(hk + 1) * G].reshape(T * G, D)
+                heads = np.tile(np.arange(hk * G, (hk + 1) * G), T)
+                bias = None
+                if alibi_slopes is not None:
+                    bias = -np.asarray(alibi_slopes, np.float64)[heads][:, None] * np.repeat(dist_s, G, axis=0)
                 o, l = _attend_group(qg, ks[:, hk], vs[:, hk], np.repeat(vis_t, G, axis=0),
-                                     scale, softcap)
+                                     scale, softcap, bias)
                 o_suf[n * T:(n + 1) * T, hk * G:(hk + 1) * G] = o.reshape(T, G, D)
                 l_suf[n * T:(n + 1) * T, hk * G:(hk + 1) * G] = l.reshape(T, G)
     return merge_states(o_pre, l_pre, o_suf, l_suf)

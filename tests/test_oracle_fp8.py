@@ -45,3 +45,29 @@ def test_quantize_with_scale_and_nan():
         y = xs / np.float32(s)                          # the same float32 division as the kernel
         assert np.array_equal(fp8.quantize(xs, s), _torch_q(y))
     assert fp8.quantize(np.float32(np.nan)) == 0x7F and fp8.quantize(np.float32(-np.nan)) == 0x7F
+
+
+def test_unscaled_read_departure_measured():
+    """Departure, measured: the reference writes an fp8 cache with the
+    layer's scales but its flash-attention calls pass no descale
+    (beam_attn.py:646-695), so it attends over e4m3 codes = x / scale; this
+    build reads e4m3 * scale.  At scale 1.0 the two are the same attention;
+    at K / V scales 0.05 / 0.02 the reference's reading is far from the
+    attention over the cached values."""
+    from oracle import attention as oa
+    rng = np.random.default_rng(7)
+    NB, BS, Hkv, D, P, W = 12, 16, 2, 32, 100, 4
+    x_k = rng.standard_normal((NB, BS, Hkv, D))
+    x_v = rng.standard_normal((NB, BS, Hkv, D))
+    q = rng.standard_normal((W, 4, D))
+    pbt = rng.permutation(NB)[None, :7]
+    sbt = np.array([[7], [8], [9], [10]])
+    args = dict(prefix_bt=pbt, prefix_len=np.array([P]), beam_start=np.array([0, W]), suffix_bt=sbt,
+                suffix_len=np.array([1, 2, 3, 1]), scale=D ** -0.5, block_size=BS)
+    for sk, sv, same in ((1.0, 1.0, True), (0.05, 0.02, False)):
+        ck, cv = fp8.decode(fp8.quantize(x_k, sk)), fp8.decode(fp8.quantize(x_v, sv))
+        ours = oa.beam_attention_dense(q, ck * sk, cv * sv, **args)[0]
+        ref = oa.beam_attention_dense(q, ck, cv, **args)[0]
+        diff = np.abs(ours - ref).max()
+        print(f"scales {sk}/{sv}: max |out difference| {diff:.3g}")
+        assert (diff == 0.0) if same else diff > 1.0

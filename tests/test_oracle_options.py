@@ -166,3 +166,118 @@ def test_reductions():
     # an unbounded window is no window
     w = _oracle(q, kc, vc, pbt, sbt, P, Ls, T, 0.3, window=(P + 20, -1))
     np.testing.assert_allclose(w[0], base[0], atol=1e-12)
+
+
+# ---- the reference's per-pass option semantics, and the departure from them ----
+
+def _brute_reference_cascade(q, kc, vc, pbt, sbt, P, Ls, T, scale, window, sinks, alibi):
+    """The reference's cascade with options, written from flash-attention's
+    documented conventions as scalar loops: a pass of Lq rows against Lk keys
+    puts row i at i + Lk - Lq; the prefix pass stacks the request's beams'
+    rows (beam-major) non-causally with the sinks; each beam's suffix pass is
+    causal; the two states merge by LSE (beam_attn.py:656-699)."""
+    N = len(Ls)
+    Hq, D = q.shape[1], q.shape[2]
+    Hkv = kc.shape[2]
+    G = Hq // Hkv
+    out = np.zeros(q.shape)
+    lse = np.full(q.shape[:2], -math.inf)
+
+    def attend(qv, keys, qpos, causal, hk, h, sink):
+        sc, vals = [], []
+        for kpos, (b, off) in enumerate(keys):
+            if causal and kpos > qpos:
+                continue
+            if window[0] >= 0 and kpos < qpos - window[0]:
+                continue
+            if window[1] >= 0 and kpos > qpos + window[1]:
+                continue
+            x = scale * sum(qv[d] * kc[b, off, hk, d] for d in range(D))
+            if alibi is not None:
+                x -= alibi[h] * abs(qpos - kpos)
+            sc.append(x)
+            vals.append(vc[b, off, hk])
+        if sink is not None:
+            sc.append(sink)
+            vals.append(np.zeros(D))
+        if not sc:
+            return np.zeros(D), -math.inf
+        m = max(sc)
+        w = [math.exp(x - m) for x in sc]
+        return sum(wi * v for wi, v in zip(w, vals)) / sum(w), m + math.log(sum(w))
+
+    pkeys = [(pbt[0][j // BS], j % BS) for j in range(P)]
+    Lq = N * T
+    for n in range(N):
+        skeys = [(sbt[n][j // BS], j % BS) for j in range(Ls[n])]
+        for i in range(T):
+            row = n * T + i
+            for h in range(Hq):
+                hk = h // G
+                o1, l1 = attend(q[row, h], pkeys, row + P - Lq, False, hk, h, None if sinks is None else sinks[h])
+                o2, l2 = attend(q[row, h], skeys, i + Ls[n] - T, True, hk, h, None)
+                m = max(l1, l2)
+                if m == -math.inf:
+                    continue
+                w1, w2 = math.exp(l1 - m), math.exp(l2 - m)
+                out[row, h] = (w1 * o1 + w2 * o2) / (w1 + w2)
+                lse[row, h] = m + math.log(w1 + w2)
+    return out, lse
+
+
+def _cascade(q, kc, vc, pbt, sbt, P, Ls, T, scale, **kw):
+    N = len(Ls)
+    return oa.beam_attention_cascade(q, kc, vc, pbt, np.array([P]), np.array([0, N]), sbt, np.array(Ls),
+                                     q_per_beam=T, scale=scale, block_size=BS, **kw)
+
+
+@pytest.mark.parametrize("window", [(-1, -1), (3, -1), (5, 0), (2, 2)])
+@pytest.mark.parametrize("extras", [False, True])
+def test_reference_cascade_options_vs_scalar_loop(window, extras):
+    """The oracle's restatement of the reference's per-pass options equals the
+    scalar loop written from flash-attention's documented formulas."""
+    P, Ls, T, Hq, Hkv, D = 7, [3, 5, 2], 2, 4, 2, 3
+    kc, vc, pbt, sbt, rng = _layout(P, Ls, T, Hkv, D, seed=11 + window[0])
+    q = rng.standard_normal((len(Ls) * T, Hq, D))
+    sinks = rng.standard_normal(Hq) if extras else None
+    alibi = rng.uniform(0.05, 0.5, Hq) if extras else None
+    got = _cascade(q, kc, vc, pbt, sbt, P, Ls, T, 0.5, window=window, sinks=sinks, alibi_slopes=alibi)
+    want = _brute_reference_cascade(q, kc, vc, pbt, sbt, P, Ls, T, 0.5, window, sinks, alibi)
+    np.testing.assert_allclose(got[0], want[0], atol=1e-12)
+    np.testing.assert_allclose(got[1], want[1], atol=1e-12)
+
+
+def test_reference_cascade_agrees_without_window_or_alibi():
+    """Sinks alone, or a window that covers every key: the reference's
+    per-pass semantics and this build's absolute positions give the same
+    attention (the sink joins the prefix pass once, as it joins the whole
+    softmax once)."""
+    P, Ls, T, Hq, Hkv, D = 9, [4, 2, 6], 2, 4, 2, 3
+    kc, vc, pbt, sbt, rng = _layout(P, Ls, T, Hkv, D, seed=5)
+    q = rng.standard_normal((len(Ls) * T, Hq, D))
+    sinks = rng.standard_normal(Hq)
+    for kw in (dict(sinks=sinks), dict(window=(P + 10, -1)), dict(window=(P + 10, P + 10), sinks=sinks)):
+        ref = _cascade(q, kc, vc, pbt, sbt, P, Ls, T, 0.5, **kw)
+        ours = _oracle(q, kc, vc, pbt, sbt, P, Ls, T, 0.5, **kw)
+        np.testing.assert_allclose(ref[0], ours[0], atol=1e-12)
+        np.testing.assert_allclose(ref[1], ours[1], atol=1e-12)
+
+
+def test_reference_cascade_window_alibi_departure_measured():
+    """Departure, measured: with a sliding window or ALiBi the reference's
+    prefix pass places a request's stacked beam rows at P - W*T + i, not at
+    each query's own position P + L - T + t, so its attention differs from
+    this build's.  On a W = 8, T = 1, P = 64 request with suffixes of 1-4
+    tokens, a left window of 16 changes every row, and ALiBi (slopes
+    2^(-8h/H)) changes them by a measurable amount; the printed maxima are
+    the size of the departure."""
+    P, Ls, T, Hq, Hkv, D = 64, [1, 2, 3, 4, 1, 2, 3, 4], 1, 4, 2, 8
+    kc, vc, pbt, sbt, rng = _layout(P, Ls, T, Hkv, D, seed=23)
+    q = rng.standard_normal((len(Ls) * T, Hq, D))
+    slopes = np.array([2.0 ** (-8.0 * (h + 1) / Hq) for h in range(Hq)])
+    for name, kw in (("window 16", dict(window=(16, -1))), ("alibi", dict(alibi_slopes=slopes))):
+        ref_o, ref_l = _cascade(q, kc, vc, pbt, sbt, P, Ls, T, D ** -0.5, **kw)
+        our_o, our_l = _oracle(q, kc, vc, pbt, sbt, P, Ls, T, D ** -0.5, **kw)
+        d_o, d_l = np.abs(ref_o - our_o).max(), np.abs(ref_l - our_l).max()
+        print(f"{name}: max |out difference| {d_o:.3g}, max |lse difference| {d_l:.3g}")
+        assert d_o > 1e-3 and d_l > 1e-3
