@@ -244,6 +244,85 @@ def bench_other(args) -> int:
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+PMC_SUMMARY["prefill"] = os.path.join(ROOT, "profiles", "prefill_sid_prompt_hbm_traffic.txt")
+
+
+def bench_prefill(args) -> int:
+    """One layer's prompt attention of the semantic-ID workload: 4 requests x
+    2048-token prompts, 16 q / 8 kv heads, head_dim 128, bf16, causal over the
+    paged cache (the standard path's flash_attn_varlen_func call,
+    beam_attn.py:643-654).  The kernel is MFMA-bound: the line's roofline is
+    TFLOP/s against the dense bf16 peak."""
+    import torch
+    from vllm_gr_amd import ops
+
+    dev = torch.device("cuda:0")
+    R, S, Hq, Hkv, D, bs = 4, 2048, 16, 8, 128, 16
+    nb = R * S // bs
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    bt = torch.randperm(nb, generator=gen, device=dev).to(torch.int32).view(R, S // bs)
+    qs = torch.arange(0, R * S + 1, S, device=dev, dtype=torch.int32)
+    sl = torch.full((R,), S, device=dev, dtype=torch.int32)
+    flops = R * Hq * 4 * D * (S * (S + 1) // 2)  # QK^T and PV over the causal triangle
+    nbytes = 2 * R * S * Hq * D * 2 + 2 * R * S * Hkv * D * 2  # Q, O; K, V once
+
+    def make_step():
+        kv = torch.randn((2, nb, bs, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+        q = torch.randn((R * S, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+        out = torch.empty_like(q)
+
+        def step():
+            ops.paged_attn_prefill(q, kv[0], kv[1], bt, qs, sl, max_query_len=S, scale=D ** -0.5, out=out)
+        return step
+    copies = -(-MALL_BYTES // nbytes) + 2
+    cold = [make_step() for _ in range(copies)]
+    us = _time_launches(cold, args.steps, args.warmup, "cold")
+    us_warm = None if args.no_warm else _time_launches(cold[0], args.steps, args.warmup, "warm")
+    tflops = flops / (us * 1e-6) / 1e12
+    gbps = nbytes / (us * 1e-6) / 1e9
+    _log(f"bench: prefill: cold {us:.2f} us/step, {tflops:.1f} TFLOP/s, {gbps:.1f} GB/s; warm {us_warm}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        n_cpu = len(os.sched_getaffinity(0))
+        torch.set_num_threads(n_cpu)
+        g = torch.Generator().manual_seed(0)
+        qh = torch.randn((1, 2, S, D), generator=g)  # one request, one KV head's two query heads
+        kh = torch.randn((1, 1, S, D), generator=g).expand(1, 2, S, D)
+        vh = torch.randn((1, 1, S, D), generator=g).expand(1, 2, S, D)
+        run = lambda: torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True)
+        run()
+        times = []
+        t_end = time.perf_counter() + 10.0
+        while len(times) < 3 or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        us_cpu = times[len(times) // 2] * 1e6 * R * Hkv
+        cpu = {"value": round(flops / (us_cpu * 1e-6) / 1e12, 4), "unit": "TFLOP/s", "cores": n_cpu,
+               "kind": "port", "us_per_step": round(us_cpu, 1),
+               "sample": f"one request's one KV head (2 query heads, 2048 causal tokens) in torch float32 "
+                         f"SDPA, median of {len(times)} runs, scaled x{R * Hkv} to the layer"}
+    line = {"metric": "paged causal prefill us/layer + TFLOP/s (% bf16 MFMA peak) at 4 x 2048-token prompts",
+            "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 5), "us_per_step": round(us, 3),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) Q/K/V, random block table)",
+            "config": {"workload": "prefill: 4 requests x 2048-token prompts, causal, 16 q / 8 kv heads, "
+                                   "head_dim 128, block 16 (one layer)", "flops_per_step": flops,
+                       "algorithmic_bytes_per_step": nbytes, "gbps": round(gbps, 2),
+                       "inputs": f"{len(cold)} copies rotated per launch"},
+            "warm": None if us_warm is None else {"us_per_step": round(us_warm, 3),
+                                                  "tflops": round(flops / (us_warm * 1e-6) / 1e12, 2)},
+            "host_us_per_enqueue": dict(HOST_US),
+            "timing": TIMING_NOTE,
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                         "traffic": _traffic_from_profile("prefill")},
+            "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
 
 
 def e2e_cpu_baseline(cfg, prompt, n_req: int, budget_s: float = 15.0):
@@ -362,9 +441,10 @@ def main() -> int:
                     help="decode shape: c2 (8 requests x 128 beams, 32/8 heads; the headline) or sid (one "
                          "layer of the semantic-ID decode step: 4 x 128 beams, 16/8 heads, suffix 1-3, "
                          "the split prefix with the longest-prefix hint, as the backend runs it)")
-    ap.add_argument("--workload", choices=["decode", "fork", "prune", "e2e"], default="decode",
-                    help="decode (the headline line), the fork+append / pruning kernels, or e2e "
-                         "(whole semantic-ID beam decode through a 28-layer decoder; a step is one batch)")
+    ap.add_argument("--workload", choices=["decode", "fork", "prune", "prefill", "e2e"], default="decode",
+                    help="decode (the headline line), the fork+append / pruning kernels, prefill (one "
+                         "layer's prompt attention of the semantic-ID workload), or e2e (whole semantic-ID "
+                         "beam decode through a 28-layer decoder; a step is one batch)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 256 MiB device-to-device copy (5 launches), the reference point "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -390,6 +470,8 @@ def main() -> int:
 
     if args.workload == "e2e":
         return bench_e2e(args)
+    if args.workload == "prefill":
+        return bench_prefill(args)
     if args.workload != "decode":
         return bench_other(args)
 

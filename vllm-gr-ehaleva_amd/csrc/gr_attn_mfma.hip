@@ -182,8 +182,14 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   const int wl = OPT ? a.win_left : -1;
   const int tw0 = wl >= 0 ? max(0, P - a.T - wl) / ST_KEYS : 0;
   const int n_rng = n_all - tw0;
-  const int ts0 = tw0 + (SPLIT ? (int)((int64_t)split * n_rng / nsplit) : 0);  // first tile of this workgroup
-  const int n_st = SPLIT ? tw0 + (int)((int64_t)(split + 1) * n_rng / nsplit) - ts0 : n_rng;
+  // split: the last split also runs the suffix phase (about three prefix
+  // steps), so the others share up to three of its tiles
+  const int sb = SPLIT ? min(3, n_rng / (2 * nsplit)) : 0;
+  auto split_bound = [&](int s) {
+    return s >= nsplit ? n_rng : min(n_rng, (int)((int64_t)s * (n_rng + sb) / nsplit));
+  };
+  const int ts0 = tw0 + (SPLIT ? split_bound(split) : 0);  // first tile of this workgroup
+  const int n_st = SPLIT ? tw0 + split_bound(split + 1) - ts0 : n_rng;
   const int kb = ts0 * ST_KEYS;  // first key of this workgroup's prefix range
   const int bsh = a.bs_shift;
 
