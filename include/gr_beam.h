@@ -190,8 +190,10 @@ typedef struct gr_attn_options {
   const float* v_scale;       /* [1] device float, or NULL for 1.0 */
 } gr_attn_options;
 
-/* gr_beam_attn_decode_ws with options (the optional features run on the
- * generic kernel). */
+/* gr_beam_attn_decode_ws with options.  bf16/fp16 head-dim-128 decodes with a
+ * left window, sinks, ALiBi and / or an fp8 cache run on the matrix-core
+ * kernel (split like a plain decode when a workspace is given); a right
+ * window, fp32 or another head size takes the generic kernel. */
 gr_status_t gr_beam_attn_decode_opt(
     void* out, int64_t out_tok_stride,
     const void* q, int64_t q_tok_stride,
@@ -207,7 +209,10 @@ gr_status_t gr_beam_attn_decode_opt(
     int max_prefix_len, void* workspace, size_t workspace_bytes,
     const gr_attn_options* options, hipStream_t stream);
 
-/* gr_paged_attn_prefill with options. */
+/* gr_paged_attn_prefill with options.  Causal bf16/fp16 head-dim-128 prefills
+ * with sinks and / or an fp8 cache run on the matrix-core kernel; windows,
+ * ALiBi, non-causal batches, fp32 and other head sizes take the generic
+ * kernel. */
 gr_status_t gr_paged_attn_prefill_opt(
     void* out, int64_t out_tok_stride,
     const void* q, int64_t q_tok_stride,

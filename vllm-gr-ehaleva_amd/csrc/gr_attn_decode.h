@@ -43,10 +43,6 @@ struct DecodeArgs {
   const float* v_scale;      // [1] or null (1.0)
 };
 
-// any of the optional features set (only the generic kernel implements them)
-inline bool has_options(const DecodeArgs& a) {
-  return a.win_left >= 0 || a.win_right >= 0 || !a.causal || a.sinks || a.alibi || a.kv8;
-}
 
 // MFMA path (gr_attn_mfma.hip): bf16/fp16, head_dim 128, 16-byte aligned rows.
 // (decode: sinks, a left window and ALiBi run here too; prefill: sinks)

@@ -705,7 +705,7 @@ class BeamAttentionBackend:
 
     @classmethod
     def supports_sink(cls) -> bool:
-        return True  # the sinks run on the generic kernels (gr_attn_options)
+        return True  # sinks join every row's softmax (gr_attn_options)
 
     @classmethod
     def supports_compute_capability(cls, capability) -> bool:
