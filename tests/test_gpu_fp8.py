@@ -178,11 +178,14 @@ def test_decode_fp8_dominant_key(device, dtype, pos):
     assert np.abs(lse - rl).max() <= 2e-2
 
 
-@pytest.mark.parametrize("causal", [True, False])
-def test_prefill_fp8_cache(device, causal):
-    print(f"[fp8] prefill causal={causal}", flush=True)
-    g = torch.Generator().manual_seed(8)
-    qlens, ctxs, Hq, Hkv, D = [1, 30, 70], [0, 20, 50], 8, 4, 128
+@pytest.mark.parametrize("causal,qlens,ctxs,dtype", [
+    (True, [1, 30, 70], [0, 20, 50], torch.bfloat16), (False, [1, 30, 70], [0, 20, 50], torch.bfloat16),
+    # long causal prompts: the matrix-core prefill's pipelined fp8 loop, cached context included
+    (True, [500, 260, 3], [0, 300, 900], torch.bfloat16), (True, [500, 260, 3], [0, 300, 900], torch.float16)])
+def test_prefill_fp8_cache(device, causal, qlens, ctxs, dtype):
+    print(f"[fp8] prefill causal={causal} qlens={qlens} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(8 + qlens[0])
+    Hq, Hkv, D = 8, 4, 128
     seqs = [c + q for c, q in zip(ctxs, qlens)]
     nbs = [-(-s // BS) for s in seqs]
     NB = sum(nbs) + 3
@@ -193,7 +196,7 @@ def test_prefill_fp8_cache(device, causal):
         bt[r, :n] = perm[o:o + n]
         o += n
     kc, vc = _codes((NB, BS, Hkv, D), 0.1, g), _codes((NB, BS, Hkv, D), 0.08, g)
-    q = torch.randn((sum(qlens), Hq, D), generator=g).to(torch.bfloat16)
+    q = torch.randn((sum(qlens), Hq, D), generator=g).to(dtype)
     qs = torch.tensor([0] + qlens).cumsum(0).to(torch.int32)
     sq = torch.tensor(seqs, dtype=torch.int32)
     out = torch.empty_like(q, device=device)

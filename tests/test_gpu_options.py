@@ -178,13 +178,17 @@ def _prefill_oracle(q, kv, bt, qs, seqs, scale, **kw):
 
 @pytest.mark.parametrize("causal,window", [(True, (50, -1)), (False, (-1, -1)), (False, (30, 30)),
                                            (False, (20, 0)), (True, (-1, -1))])
-@pytest.mark.parametrize("extras", [False, True])
+@pytest.mark.parametrize("extras", [False, True, "sinks"])
 def test_prefill_options(device, causal, window, extras):
+    """extras: sinks and ALiBi, or sinks alone (a causal prefill with sinks
+    alone runs on the matrix-core kernel)."""
     print(f"[options] prefill causal={causal} window={window} extras={extras}", flush=True)
     q, kv, bt, qs, seqs, g = _prefill_case([1, 37, 120], [0, 25, 64], 8, 4, 128, torch.bfloat16,
-                                           seed=int(causal) + window[0] + 3 * extras)
+                                           seed=int(causal) + window[0] + 3 * bool(extras))
     kw = dict(window=window)
-    if extras:
+    if extras == "sinks":
+        kw.update(sinks=torch.randn(8, generator=g) * 2)
+    elif extras:
         kw.update(sinks=torch.randn(8, generator=g), alibi_slopes=torch.rand(8, generator=g) * 0.05)
     gpu_kw, orc_kw = _split(kw, device)
     kv_d = kv.to(device)
