@@ -566,6 +566,9 @@ def main() -> int:
                      # the committed counter profiles cover the option-free decodes
                      "traffic": (_traffic_from_profile("decode_sid" if sid else "decode")
                                  if args.option == "none" else None)},
+        # the kernel sits near the ridge: its matrix-core use beside the HBM roofline
+        "mfma": {"achieved": round(host_wl.flops() / (us_step * 1e-6) / 1e12, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                 "unit": "TFLOP/s", "frac": round(host_wl.flops() / (us_step * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
