@@ -30,7 +30,7 @@ struct DecodeArgs {
   // split prefix (MFMA decode only): nsplit workgroups share each row tile's
   // prefix; each writes its normalised partial O / LSE, a second kernel merges
   int nsplit;
-  float* ws_o;    // [tiles * nsplit][128 rows][128] float32
+  uint16_t* ws_o;  // [tiles * nsplit][128 rows][128] in the query dtype
   float* ws_lse;  // [tiles * nsplit][128 rows] float32 (natural log)
   // optional features (gr_attn_options); positions are indices into the
   // row's [prefix ; suffix] sequence, a query row sitting at its own token's

@@ -407,7 +407,7 @@ static SplitLayout split_layout(int tiles, int nsplit) {
   const size_t slots = (size_t)tiles * nsplit;
   l.lse_off = 0;
   l.o_off = (sizeof(float) * slots * 128 + 255) & ~(size_t)255;
-  l.total = l.o_off + sizeof(float) * slots * 128 * 128;
+  l.total = l.o_off + sizeof(uint16_t) * slots * 128 * 128;
   return l;
 }
 
@@ -452,7 +452,7 @@ static gr_status_t decode_ws_impl(
   char* ws = static_cast<char*>(workspace);
   a.nsplit = nsplit;
   a.ws_lse = reinterpret_cast<float*>(ws + l.lse_off);
-  a.ws_o = reinterpret_cast<float*>(ws + l.o_off);
+  a.ws_o = reinterpret_cast<uint16_t*>(ws + l.o_off);
   return launch_mfma_decode_split(a, stream);
 }
 

@@ -52,7 +52,9 @@ __device__ inline void tile_barrier() {
 // (fully visible tiles pipelined, the causal edge masked per row), no suffix.
 // SPLIT: a.nsplit workgroups per row tile, each over a contiguous share of
 // the prefix's 64-key tiles (the last one also takes the suffix), writing its
-// normalised partial O and LSE to the workspace; split_merge combines them.
+// normalised partial O (in the query dtype, as the two passes of a cascade
+// hand over their outputs) and fp32 LSE to the workspace; split_merge
+// combines them in fp32.
 // OPT (decode only): a left window and/or ALiBi.  Window a.win_left >= 0:
 // row r sees key k iff k >= qpos_r - win_left, qpos_r its query token's index
 // in [prefix ; suffix]; the prefix range starts at the first tile any row can
@@ -82,6 +84,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   __shared__ int hot_flag;               // a tile of the fast loop needed the exact path
   __shared__ int win_hi[8];              // per wave: the highest window lower bound of its rows
 
+  // the arguments' five scalar-cache lines at once (DecodeArgs, units, mtiles)
+  kernarg_lines<kernarg_line_count<DecodeArgs>(8)>();
   // ---- XCD-aware tile placement: all m-tiles of a (request, KV head) land on
   // the same XCD (round-robin dispatch puts workgroup i on XCD i % 8)
   const int bid = blockIdx.x;
@@ -186,7 +190,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // steps), so the others share up to three of its tiles
   const int sb = SPLIT ? min(3, n_rng / (2 * nsplit)) : 0;
   auto split_bound = [&](int s) {
-    return s >= nsplit ? n_rng : min(n_rng, (int)((int64_t)s * (n_rng + sb) / nsplit));
+    return s >= nsplit ? n_rng : min(n_rng, s * (n_rng + sb) / nsplit);  // < 2^30: n_rng < 2^25, s <= 16
   };
   const int ts0 = tw0 + (SPLIT ? split_bound(split) : 0);  // first tile of this workgroup
   const int n_st = SPLIT ? tw0 + split_bound(split + 1) - ts0 : n_rng;
@@ -196,7 +200,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // The request's prefix block-table row is staged in LDS (a window of
   // PBT_WIN entries), validated once; invalid ids become -1 and read as zeros.
   // Tile loads then need no dependent global reads and no atomics.
-  const int nblk = (P + a.bs - 1) / a.bs;
+  const int nblk = (P + a.bs - 1) >> bsh;
   int win0 = 0;
   auto load_window = [&](int w0) {
     for (int i = tid; i < PBT_WIN; i += MF_THREADS) {
@@ -1029,7 +1033,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     if constexpr (SPLIT) {
       // this split's normalised partial O and LSE, every row of the tile
       const int64_t slot = (int64_t)(unit * mtiles + mt) * nsplit + split;
-      float* po = a.ws_o + (slot * MF_ROWS + rg * 32 + lrow_f) * HD + 4 * lhalf_f;
+      uint16_t* po = a.ws_o + (slot * MF_ROWS + rg * 32 + lrow_f) * HD + 4 * lhalf_f;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -1041,7 +1045,8 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
             const int rr = qd * 4 + u;
             v[u] = (o[mb][rr] * a0 + x1[u] * a1) * inv;
           }
-          *reinterpret_cast<float4*>(po + mb * 32 + qd * 8) = make_float4(v[0], v[1], v[2], v[3]);
+          const u32x2_t w = {Mma<DT>::pack2(v[0], v[1]), Mma<DT>::pack2(v[2], v[3])};
+          *reinterpret_cast<u32x2_t*>(po + mb * 32 + qd * 8) = w;
         }
       }
       if (lhalf_f == 0)
@@ -1080,6 +1085,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 constexpr int MG_ROWS = 8;
 template <int DT>
 __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
+  kernarg_lines<kernarg_line_count<DecodeArgs>(4)>();
   using S = uint16_t;
   constexpr int PER_TILE = MF_ROWS / MG_ROWS;
   const int tile = blockIdx.x / PER_TILE;
@@ -1094,7 +1100,7 @@ __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
   if (rho >= rows_r) return;
   const int nsplit = a.nsplit;
   const float* lse = a.ws_lse + (int64_t)tile * nsplit * MF_ROWS + row;
-  const float* po = a.ws_o + ((int64_t)tile * nsplit * MF_ROWS + row) * HD + d4;
+  const uint16_t* po = a.ws_o + ((int64_t)tile * nsplit * MF_ROWS + row) * HD + d4;
   const float sk = a.sinks ? a.sinks[hk * G + rho % G] : -INFINITY;  // joins the merged softmax once
   float mx = sk;
 #pragma unroll 4
@@ -1104,12 +1110,12 @@ __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
 #pragma unroll 4
     for (int s2 = 0; s2 < nsplit; ++s2) {
       const float w = __expf(lse[s2 * MF_ROWS] - mx);
-      const float4 pv = *reinterpret_cast<const float4*>(po + (int64_t)s2 * MF_ROWS * HD);
+      const u32x2_t pv = *reinterpret_cast<const u32x2_t*>(po + (int64_t)s2 * MF_ROWS * HD);
       sum += w;
-      acc[0] += w * pv.x;
-      acc[1] += w * pv.y;
-      acc[2] += w * pv.z;
-      acc[3] += w * pv.w;
+      acc[0] += w * Mma<DT>::lo(pv[0]);
+      acc[1] += w * Mma<DT>::hi(pv[0]);
+      acc[2] += w * Mma<DT>::lo(pv[1]);
+      acc[3] += w * Mma<DT>::hi(pv[1]);
     }
   }
   const float inv = sum > 0.f ? 1.f / sum : 0.f;

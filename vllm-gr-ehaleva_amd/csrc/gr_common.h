@@ -10,6 +10,41 @@
 
 namespace gr {
 
+// ---- kernel arguments ------------------------------------------------------
+// A kernel reads its arguments through the scalar cache where the code first
+// uses them, and the compiler waits for each read before work that needs it,
+// so arguments that span several 64-byte lines can cost one cache miss per
+// line, in turn, on the kernel's critical path.  kernarg_lines<N>() reads one
+// dword of each of the first N lines (N * 64 <= the explicit arguments'
+// size, rounded up) in one statement that then waits once, so the misses
+// overlap; call it first in the kernel.  Loads only: nothing is written.
+template <int N>
+__device__ __forceinline__ void kernarg_lines() {
+  static_assert(N >= 1 && N <= 12, "one to twelve lines");
+  int d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10, d11;
+  __asm__ volatile(
+      "s_load_dword %0, %12, 0x0\n\t"
+      ".if %13 > 1\n\ts_load_dword %1, %12, 0x40\n\t.endif\n\t"
+      ".if %13 > 2\n\ts_load_dword %2, %12, 0x80\n\t.endif\n\t"
+      ".if %13 > 3\n\ts_load_dword %3, %12, 0xc0\n\t.endif\n\t"
+      ".if %13 > 4\n\ts_load_dword %4, %12, 0x100\n\t.endif\n\t"
+      ".if %13 > 5\n\ts_load_dword %5, %12, 0x140\n\t.endif\n\t"
+      ".if %13 > 6\n\ts_load_dword %6, %12, 0x180\n\t.endif\n\t"
+      ".if %13 > 7\n\ts_load_dword %7, %12, 0x1c0\n\t.endif\n\t"
+      ".if %13 > 8\n\ts_load_dword %8, %12, 0x200\n\t.endif\n\t"
+      ".if %13 > 9\n\ts_load_dword %9, %12, 0x240\n\t.endif\n\t"
+      ".if %13 > 10\n\ts_load_dword %10, %12, 0x280\n\t.endif\n\t"
+      ".if %13 > 11\n\ts_load_dword %11, %12, 0x2c0\n\t.endif\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=s"(d0), "=s"(d1), "=s"(d2), "=s"(d3), "=s"(d4), "=s"(d5), "=s"(d6), "=s"(d7), "=s"(d8), "=s"(d9),
+        "=s"(d10), "=s"(d11)
+      : "s"(__builtin_amdgcn_kernarg_segment_ptr()), "n"(N));
+  __builtin_amdgcn_sched_barrier(0);  // no argument read moves above it
+}
+template <typename T> constexpr int kernarg_line_count(int extra_bytes = 0) {
+  return (int)((sizeof(T) + extra_bytes + 63) / 64);
+}
+
 // ---- element conversion ---------------------------------------------------
 // bf16 and fp16 are handled as raw 16-bit patterns; conversion to float is
 // exact, conversion from float rounds to nearest even.

@@ -115,6 +115,22 @@ __device__ inline void block_scan(const int* v, int* out, int n, int* tmp) {
   __syncthreads();
 }
 
+// beam_fork's argument list as one struct (same types in the same order, so
+// the same layout): its size is the span of argument lines the kernel touches.
+struct ForkKernargs {
+  const int32_t* parent;
+  int R, W, cpw;
+  const int32_t *bt_in, *len_in;
+  int32_t *bt_out, *len_out;
+  int S;
+  KvGeom g;
+  int L;
+  KvLayers layers;
+  const uint8_t *k_new, *v_new;
+  int64_t new_tok_stride;
+  int32_t* dev_status;
+};
+
 // 8 waves per SIMD: every workgroup of a 2048-child batch resident at once.
 // Workgroup cg of request r owns children cg*cpw .. cg*cpw + cpw-1.
 // MULTI: L layers (their bases in `layers`); otherwise the one layer of g.
@@ -124,6 +140,7 @@ __global__ __launch_bounds__(FORK_THREADS, 8) void beam_fork(
     const int32_t* __restrict__ len_in, int32_t* __restrict__ bt_out, int32_t* __restrict__ len_out,
     int S, KvGeom g, int L, KvLayers layers, const uint8_t* k_new, const uint8_t* v_new, int64_t new_tok_stride,
     int32_t* dev_status) {
+  kernarg_lines<kernarg_line_count<ForkKernargs>()>();
   extern __shared__ __attribute__((aligned(8))) int fork_lds[];
   __shared__ uint8_t* lay_k[FORK_MAX_LAYERS];  // the layers' bases, indexed per lane by the copy loop
   __shared__ uint8_t* lay_v[FORK_MAX_LAYERS];

@@ -67,6 +67,8 @@ template <> struct Mma<GR_DTYPE_BF16> {
   __device__ static inline uint32_t pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});  // one v_cvt_pk_bf16_f32
   }
+  __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 };
 template <> struct Mma<GR_DTYPE_F16> {
   using vec = f16x8_t;
@@ -77,6 +79,8 @@ template <> struct Mma<GR_DTYPE_F16> {
   __device__ static inline uint32_t pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)lo, (_Float16)hi});
   }
+  __device__ static inline float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[0]; }
+  __device__ static inline float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[1]; }
 };
 
 // Eight OCP e4m3 bytes (two dwords, element 0 in the low byte) as eight

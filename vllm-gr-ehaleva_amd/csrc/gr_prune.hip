@@ -377,6 +377,7 @@ __device__ __noinline__ void row_topk_radix(const float* xg, int V, int k1, uint
 // top-K, serving_engine.py:504-506, 526-528).
 template <int MAXC, bool CATALOG = false>
 __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
+  kernarg_lines<kernarg_line_count<PruneArgs>()>();
   __shared__ uint64_t sk[PR_MAXK];  // candidates as row_key
   __shared__ float ox[PR_MAXK];
   __shared__ int ov[PR_MAXK];
@@ -667,6 +668,7 @@ constexpr int MG_REG = 16;  // candidates per thread held in registers (W * k1 <
 
 template <int MPT>  // > 0: thread t holds candidates [MPT t, MPT t + MPT) in registers; 0: re-read per pass
 __global__ __launch_bounds__(MG_THREADS) void prune_merge(PruneArgs a) {
+  kernarg_lines<kernarg_line_count<PruneArgs>()>();
   __shared__ double cs[PR_MAXW];
   // the radix histogram during the selection, then the selected keys / flats
   __shared__ __attribute__((aligned(16))) uint8_t work[PR_MAXK * 16];
@@ -973,6 +975,7 @@ constexpr int MG_MAX_ROWS = 128;  // rows a group may hold on the bounded path
 constexpr int MG_MAX_EXTRA = 64;  // other rows' entries at or above the bound, merged one by one
 
 __global__ __launch_bounds__(MG_THREADS) void prune_merge_part(PruneArgs a) {
+  kernarg_lines<kernarg_line_count<PruneArgs>()>();
   __shared__ uint64_t mk[2][MG_GROUP_CAND];        // [0]: the group's keys by position; then merge lists
   __shared__ unsigned short mi[2][MG_GROUP_CAND];  // position in the group of each merge-list entry
   __shared__ int mtok[MG_GROUP_CAND];              // token of the group's candidate i
@@ -1246,6 +1249,7 @@ __global__ __launch_bounds__(MG_THREADS) void prune_merge_part(PruneArgs a) {
 
 template <int NT, int MPT>  // threads, candidates per thread: ng * k <= MPT * NT
 __global__ __launch_bounds__(NT) void prune_merge_final(PruneArgs a) {
+  kernarg_lines<kernarg_line_count<PruneArgs>()>();
   __shared__ int hist[PR_BINS];
   __shared__ uint64_t fkeys[PR_MAXK];
   __shared__ int64_t ffl[PR_MAXK];
@@ -1310,6 +1314,7 @@ constexpr int MG_LIST_MAX = 4096;  // ng * k staged in LDS
 constexpr int MG_LIST_THREADS = 512;
 constexpr int MG_LIST_MAXG = 16;   // lists searched side by side
 __global__ __launch_bounds__(MG_LIST_THREADS) void prune_merge_lists(PruneArgs a) {
+  kernarg_lines<kernarg_line_count<PruneArgs>()>();
   __shared__ uint64_t lk[MG_LIST_MAX];
   __shared__ int64_t lf[MG_LIST_MAX];
   __shared__ int cnt_s;
