@@ -377,7 +377,6 @@ __device__ __noinline__ void row_topk_radix(const float* xg, int V, int k1, uint
 // top-K, serving_engine.py:504-506, 526-528).
 template <int MAXC, bool CATALOG = false>
 __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
-  kernarg_lines<kernarg_line_count<PruneArgs>()>();
   __shared__ uint64_t sk[PR_MAXK];  // candidates as row_key
   __shared__ float ox[PR_MAXK];
   __shared__ int ov[PR_MAXK];
@@ -975,7 +974,6 @@ constexpr int MG_MAX_ROWS = 128;  // rows a group may hold on the bounded path
 constexpr int MG_MAX_EXTRA = 64;  // other rows' entries at or above the bound, merged one by one
 
 __global__ __launch_bounds__(MG_THREADS) void prune_merge_part(PruneArgs a) {
-  kernarg_lines<kernarg_line_count<PruneArgs>()>();
   __shared__ uint64_t mk[2][MG_GROUP_CAND];        // [0]: the group's keys by position; then merge lists
   __shared__ unsigned short mi[2][MG_GROUP_CAND];  // position in the group of each merge-list entry
   __shared__ int mtok[MG_GROUP_CAND];              // token of the group's candidate i
