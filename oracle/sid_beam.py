@@ -1,6 +1,6 @@
 """CPU oracle of the end-to-end semantic-ID beam decode.  TEST INFRASTRUCTURE ONLY.
 
-Two pieces, both float64 on the CPU:
+Three pieces, all float64:
 
 * ``decoder_logits(weights, cfg, tokens)`` -- the Qwen-style decoder's full
   forward over one token sequence at positions 0..n-1 (causal attention,
@@ -9,6 +9,13 @@ Two pieces, both float64 on the CPU:
   (vllm_gr/entrypoints/llm.py:183-199: each beam's whole token list becomes a
   new one-token request).  Pinned against transformers' ``Qwen3ForCausalLM``
   loaded with the same weights (tests/test_oracle_sid.py).
+* ``decoder_prompt`` / ``decoder_suffix_logits`` -- the same forward split
+  at the prompt: the prompt's per-layer keys and values computed once, then
+  the logits after every token of many suffixes that share it (teacher
+  forcing of whole beams).  Same arithmetic, float64, on whatever device the
+  weights sit (the full-size model's checks run it on the GPU, as a checker).
+  Pinned against ``decoder_logits`` over each whole list
+  (tests/test_oracle_sid.py).
 * ``beam_search(next_logprobs, prompts, ...)`` -- the reference's offline
   beam-search loop (llm.py:118-292) over a callable that returns a token
   list's next-token log-probabilities: the begin token appended to each
@@ -87,6 +94,106 @@ def decoder_logits(w: dict, cfg, tokens) -> torch.Tensor:
         x = x + (torch.nn.functional.silu(g) * u) @ w[p + "down"].T
     x = _rms(x, w["final_norm"], cfg.rms_eps)
     return x @ w["lm_head"].T
+
+
+def _rope_table(cfg, n: int, device, dtype):
+    D = cfg.head_dim
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(D // 2, dtype=torch.float64, device=device) * 2.0 / D))
+    ang = torch.arange(n, dtype=torch.float64, device=device)[:, None] * inv[None]
+    return ang.cos().to(dtype), ang.sin().to(dtype)
+
+
+def _attend(q, k, v, mask):
+    """q [.., Hq, t, D], k / v [.., Hq, s, D] (contiguous), mask [t, s] or
+    [.., 1, t, s] (True = hidden): softmax(q k^T / sqrt D) v."""
+    s = torch.matmul(q, k.transpose(-1, -2).contiguous()) / math.sqrt(q.shape[-1])
+    s = s.masked_fill(mask, float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), v)
+
+
+@dataclass
+class PromptCache:
+    """decoder_prompt's output: each layer's rotated keys and values of the
+    prompt (float64, [Hkv, P, D]) and the prompt's last-position logits."""
+    keys: list
+    values: list
+    last_logits: torch.Tensor
+    length: int
+
+
+def decoder_prompt(w: dict, cfg, prompt) -> PromptCache:
+    """The forward of ``decoder_logits`` over ``prompt`` alone, keeping every
+    layer's keys and values for ``decoder_suffix_logits``.  Runs on the
+    weights' device (a GPU makes the 28-layer, 2048-token forward take
+    seconds instead of minutes); the arithmetic is decoder_logits' step for
+    step (matmul in place of einsum)."""
+    dev, dt = w["embed"].device, w["embed"].dtype
+    n, D, Hq, Hkv = len(prompt), cfg.head_dim, cfg.num_heads, cfg.num_kv_heads
+    G = Hq // Hkv
+    x = w["embed"][torch.as_tensor(list(prompt), dtype=torch.int64, device=dev)]
+    cos, sin = _rope_table(cfg, n, dev, dt)
+    mask = torch.triu(torch.ones(n, n, dtype=torch.bool, device=dev), diagonal=1)
+    keys, values = [], []
+    for i in range(cfg.num_layers):
+        p = f"layers.{i}."
+        qkv = _rms(x, w[p + "input_norm"], cfg.rms_eps) @ w[p + "qkv"].T
+        q = qkv[:, :Hq * D].reshape(n, Hq, D)
+        k = qkv[:, Hq * D:(Hq + Hkv) * D].reshape(n, Hkv, D)
+        v = qkv[:, (Hq + Hkv) * D:].reshape(n, Hkv, D)
+        q = _rope(_rms(q, w[p + "q_norm"], cfg.rms_eps), cos, sin)
+        k = _rope(_rms(k, w[p + "k_norm"], cfg.rms_eps), cos, sin)
+        kh, vh = k.transpose(0, 1).contiguous(), v.transpose(0, 1).contiguous()  # [Hkv, n, D]
+        keys.append(kh)
+        values.append(vh)
+        o = _attend(q.transpose(0, 1).contiguous(), kh.repeat_interleave(G, dim=0),
+                    vh.repeat_interleave(G, dim=0), mask)  # [Hq, n, D]
+        x = x + o.transpose(0, 1).reshape(n, Hq * D) @ w[p + "o"].T
+        gu = _rms(x, w[p + "post_norm"], cfg.rms_eps) @ w[p + "gate_up"].T
+        x = x + (torch.nn.functional.silu(gu[:, :cfg.ffn]) * gu[:, cfg.ffn:]) @ w[p + "down"].T
+    last = _rms(x[-1:], w["final_norm"], cfg.rms_eps) @ w["lm_head"].T
+    return PromptCache(keys, values, last[0], n)
+
+
+def decoder_suffix_logits(w: dict, cfg, cache: PromptCache, suffixes) -> torch.Tensor:
+    """Logits after each token of ``suffixes`` ([B, S] token lists, equal S)
+    appended to the cached prompt: row [b, j] equals
+    ``decoder_logits(prompt + suffixes[b])[P + j]``.  Suffix token j sits at
+    position P + j and attends to every prompt key and to its own suffix's
+    tokens 0..j -- the causal attention decoder_logits computes over the
+    whole list.  Returns float64 [B, S, V] on the weights' device."""
+    dev, dt = w["embed"].device, w["embed"].dtype
+    B, S = len(suffixes), len(suffixes[0])
+    P, D, Hq, Hkv = cache.length, cfg.head_dim, cfg.num_heads, cfg.num_kv_heads
+    G = Hq // Hkv
+    x = w["embed"][torch.as_tensor(suffixes, dtype=torch.int64, device=dev).reshape(B, S)]  # [B, S, H]
+    cos, sin = _rope_table(cfg, P + S, dev, dt)
+    cos, sin = cos[P:], sin[P:]
+    # suffix query j sees the P prompt keys and suffix keys 0..j
+    mask = torch.zeros(S, P + S, dtype=torch.bool, device=dev)
+    mask[:, P:] = torch.triu(torch.ones(S, S, dtype=torch.bool, device=dev), diagonal=1)
+    for i in range(cfg.num_layers):
+        p = f"layers.{i}."
+        qkv = _rms(x, w[p + "input_norm"], cfg.rms_eps) @ w[p + "qkv"].T  # [B, S, .]
+        q = qkv[..., :Hq * D].reshape(B, S, Hq, D)
+        k = qkv[..., Hq * D:(Hq + Hkv) * D].reshape(B, S, Hkv, D)
+        v = qkv[..., (Hq + Hkv) * D:].reshape(B, S, Hkv, D)
+        q = _rope(_rms(q, w[p + "q_norm"], cfg.rms_eps), cos, sin)
+        k = _rope(_rms(k, w[p + "k_norm"], cfg.rms_eps), cos, sin)
+        # scores against the shared prompt keys (broadcast over the suffixes)
+        # and against the suffix's own keys, one softmax over both
+        kp = cache.keys[i].repeat_interleave(G, dim=0)  # [Hq, P, D]
+        vp = cache.values[i].repeat_interleave(G, dim=0)
+        qh = q.transpose(1, 2).contiguous()  # [B, Hq, S, D]
+        ks = k.transpose(1, 2).repeat_interleave(G, dim=1).contiguous()
+        vs = v.transpose(1, 2).repeat_interleave(G, dim=1).contiguous()
+        sc = torch.cat((torch.matmul(qh, kp.transpose(-1, -2).contiguous()),
+                        torch.matmul(qh, ks.transpose(-1, -2).contiguous())), dim=-1) / math.sqrt(D)
+        a = torch.softmax(sc.masked_fill(mask, float("-inf")), dim=-1)  # [B, Hq, S, P + S]
+        o = torch.matmul(a[..., :P].contiguous(), vp) + torch.matmul(a[..., P:].contiguous(), vs)
+        x = x + o.transpose(1, 2).reshape(B, S, Hq * D) @ w[p + "o"].T
+        gu = _rms(x, w[p + "post_norm"], cfg.rms_eps) @ w[p + "gate_up"].T
+        x = x + (torch.nn.functional.silu(gu[..., :cfg.ffn]) * gu[..., cfg.ffn:]) @ w[p + "down"].T
+    return _rms(x, w["final_norm"], cfg.rms_eps) @ w["lm_head"].T
 
 
 def decoder_next_logprobs(w: dict, cfg):

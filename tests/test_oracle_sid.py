@@ -262,3 +262,39 @@ def test_builder_batch_table_count_mismatch():
                 builder.build(0, _common(R, W, pbt))
         finally:
             ba.MEGA_DATA_VAR.reset(tok)
+
+
+@pytest.mark.parametrize("cfg_seed", [0, 1])
+def test_prompt_cache_suffix_logits_match_full_forward(cfg_seed):
+    """decoder_prompt + decoder_suffix_logits equal decoder_logits over each
+    whole token list (the prompt's last row and every suffix row)."""
+    cfg = DecoderConfig(num_layers=3, hidden=48, num_heads=6, num_kv_heads=2, head_dim=8, ffn=64, vocab=80,
+                        init_std=0.3, dtype=torch.float32)
+    w = so.weights_f64(_random_norms(init_weights(cfg, cfg_seed), cfg_seed))
+    g = torch.Generator().manual_seed(cfg_seed)
+    prompt = torch.randint(0, cfg.vocab, (23,), generator=g).tolist()
+    sufs = torch.randint(0, cfg.vocab, (5, 3), generator=g).tolist()
+    cache = so.decoder_prompt(w, cfg, prompt)
+    got = so.decoder_suffix_logits(w, cfg, cache, sufs)
+    assert got.shape == (5, 3, cfg.vocab)
+    for b, suf in enumerate(sufs):
+        full = so.decoder_logits(w, cfg, prompt + suf)
+        assert torch.allclose(cache.last_logits, full[len(prompt) - 1], rtol=0, atol=1e-10)
+        assert torch.allclose(got[b], full[len(prompt):], rtol=0, atol=1e-10)
+
+
+def test_prompt_cache_suffix_reads_the_cached_prompt():
+    """The suffix rows depend on the cached prompt's keys and values: a cache
+    built from a prompt that differs in its first token moves them, by far
+    more than the 1e-10 agreement above."""
+    cfg = DecoderConfig(num_layers=2, hidden=48, num_heads=6, num_kv_heads=2, head_dim=8, ffn=64, vocab=80,
+                        init_std=0.3, dtype=torch.float32)
+    w = so.weights_f64(_random_norms(init_weights(cfg, 3), 3))
+    prompt = list(range(10, 27))
+    other = [11] + prompt[1:]
+    sufs = [[5, 6]]
+    full = so.decoder_logits(w, cfg, prompt + sufs[0])[len(prompt):]
+    good = so.decoder_suffix_logits(w, cfg, so.decoder_prompt(w, cfg, prompt), sufs)[0]
+    bad = so.decoder_suffix_logits(w, cfg, so.decoder_prompt(w, cfg, other), sufs)[0]
+    assert torch.allclose(good, full, rtol=0, atol=1e-10)
+    assert (bad - full).abs().max() > 1e-3
