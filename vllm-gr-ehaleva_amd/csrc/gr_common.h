@@ -36,8 +36,11 @@ __device__ __forceinline__ void kernarg_lines() {
       ".if %13 > 10\n\ts_load_dword %10, %12, 0x280\n\t.endif\n\t"
       ".if %13 > 11\n\ts_load_dword %11, %12, 0x2c0\n\t.endif\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=s"(d0), "=s"(d1), "=s"(d2), "=s"(d3), "=s"(d4), "=s"(d5), "=s"(d6), "=s"(d7), "=s"(d8), "=s"(d9),
-        "=s"(d10), "=s"(d11)
+      // early-clobber outputs: a destination must never share a register
+      // with the base address, which later loads of the statement still read
+      // while earlier ones are pending (a load may return between the two)
+      : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7), "=&s"(d8),
+        "=&s"(d9), "=&s"(d10), "=&s"(d11)
       : "s"(__builtin_amdgcn_kernarg_segment_ptr()), "n"(N));
   __builtin_amdgcn_sched_barrier(0);  // no argument read moves above it
 }
