@@ -28,19 +28,41 @@ OBJDUMP = "/opt/rocm/llvm/bin/llvm-objdump"
 LOAD = re.compile(r"^\s+s_load_dword\s+s(\d+),\s*s\[(\d+):(\d+)\],\s*(0x[0-9a-f]+|0)\s")
 
 
-def _disassembly():
+READELF = "/opt/rocm/llvm/bin/llvm-readelf"
+
+
+def _code_objects(tool_args):
+    """Run an LLVM tool over every gfx950 code object in the library."""
     if not os.path.exists(LIB):
         pytest.skip("library not built")
-    if not os.path.exists(OBJDUMP):
-        pytest.skip("llvm-objdump not available")
+    if not (os.path.exists(OBJDUMP) and os.path.exists(READELF)):
+        pytest.skip("LLVM tools not available")
     with tempfile.TemporaryDirectory() as d:
         lib = os.path.join(d, "lib.so")
         shutil.copy(LIB, lib)
         subprocess.run([OBJDUMP, "--offloading", lib], cwd=d, check=True, capture_output=True)
         objs = sorted(os.path.join(d, f) for f in os.listdir(d) if "amdgcn" in f)
         assert objs, "no gfx950 code object in the library"
-        return "\n".join(subprocess.run([OBJDUMP, "-d", o], check=True, capture_output=True,
+        return "\n".join(subprocess.run(tool_args + [o], check=True, capture_output=True,
                                         text=True).stdout for o in objs)
+
+
+def _disassembly():
+    return _code_objects([OBJDUMP, "-d"])
+
+
+def _scratch_sizes():
+    """Kernel name -> private segment (scratch) bytes per lane, from the code
+    objects' metadata notes."""
+    out, name = {}, None
+    for line in _code_objects([READELF, "--notes"]).split("\n"):
+        m = re.match(r"^\s+\.name:\s+(\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.match(r"^\s+\.private_segment_fixed_size:\s+(\d+)", line)
+        if m and name:
+            out[name] = int(m.group(1))
+    return out
 
 
 def _touch_sequences(text):
@@ -90,3 +112,22 @@ def test_touch_check_flags_an_overlap():
     seqs = _touch_sequences(text)
     assert seqs == [("kern", (0, 1), [0, 3, 4])]
     assert any(seqs[0][1][0] <= x <= seqs[0][1][1] for x in seqs[0][2])
+
+
+def test_attention_kernels_keep_no_stack():
+    """The decode / prefill kernel keeps its row state in registers: no step
+    lambda is left out of line (one that is takes what it captures by
+    reference -- O, Q, the row state -- through a per-lane stack in scratch:
+    1.7 KB per lane in the soft-capped prefill, 11x slower), the plain
+    kernels (no soft cap, window, ALiBi or fp8) use no scratch at all and
+    the soft-capped ones at most a few spilled registers."""
+    text = _disassembly()
+    out_of_line = sorted(set(re.findall(r"<(_ZZN2gr\S*decode_mfma\S*)>:", text)))
+    assert not out_of_line, out_of_line[:4]
+    sizes = _scratch_sizes()
+    # decode_mfma<DT, SOFTCAP, PREFILL, SPLIT, OPT, KV8>: OPT = KV8 = false
+    plain = {k: v for k, v in sizes.items() if re.search(r"decode_mfmaILi[12]ELb[01]ELb[01]ELb[01]ELb0ELb0E", k)}
+    assert len(plain) >= 12, sorted(plain)
+    assert all(v <= 64 for v in plain.values()), {k: v for k, v in plain.items() if v > 64}
+    nocap = {k: v for k, v in plain.items() if re.search(r"decode_mfmaILi[12]ELb0E", k)}
+    assert all(v == 0 for v in nocap.values()), {k: v for k, v in nocap.items() if v}

@@ -590,7 +590,10 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
       else tile_barrier<0>();
     }
   };
-  auto prefix_step = [&](int it, const f32x16_t& s_in, f32x16_t& s_out) {
+  // (the step lambdas are forced inline: one left out of line -- the compiler
+  // did that in the soft-capped prefill -- takes everything it captures by
+  // reference, O and Q included, through a 1.7 KB per-lane stack in scratch)
+  auto prefix_step = [&](int it, const f32x16_t& s_in, f32x16_t& s_out) __attribute__((always_inline)) {
     fetch_ahead(it);
     pipe_step<DT, SOFTCAP>(lds + (it % NB) * BUF, lds + ((it + 1) % NB) * BUF, ks * 32, lane, qf, s_in, s_out,
                            o, st, c, cap, tb(it));
@@ -598,7 +601,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   };
   // The last tile: no next tile; masked when only p_last of its keys exist.
   const int p_last = min(ST_KEYS, P - kb - (n_st - 1) * ST_KEYS);  // keys in the last tile (1 .. 64)
-  auto last_step = [&](int it, const f32x16_t& s_in) {
+  auto last_step = [&](int it, const f32x16_t& s_in) __attribute__((always_inline)) {
     fetch_ahead(it);  // (a suffix piece, if any)
     // register r of lane half lhalf holds tile key ks*32 + 16*(r>>3) + 8*lhalf + (r&7)
     uint32_t v = 0;
@@ -621,12 +624,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // recomputes its prefix range exactly (after the masked tiles).
   bool hot_seen = false;
   u32x4_t p[1][2];
-  auto finish_step = [&](int t) {
+  auto finish_step = [&](int t) __attribute__((always_inline)) {
     phase_c1<DT>(lds + (t % NB) * BUF, ks * 32, lane, p, o);
     step_barrier(t);
   };
   // tile 0 (and S^T of tile 1): exact weights, O still zero
-  auto peel = [&]() {
+  auto peel = [&]() __attribute__((always_inline)) {
     fetch_ahead(0);
     phase_a1<DT, SOFTCAP>(lds + BUF, ks * 32, lane, qf, s_cur, s_alt, st, c, cap, p, tb(0));
     f32x16_t zo[4] = {};
@@ -640,7 +643,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // One fast step over tile t (not the last): consumes its S^T from s_in and
   // leaves that of tile t+1 in s_out.  The exact-path test is deferred: each
   // lane records its own flag and the waves vote after the loop.
-  auto fast_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
+  auto fast_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) __attribute__((always_inline)) {
     fetch_ahead(t);
     hot_seen |= phase_a1<DT, SOFTCAP, true>(lds + ((t + 1) % NB) * BUF, ks * 32, lane, qf, s_in, s_out, st, c, cap, p, tb(t));
     phase_c1<DT>(lds + (t % NB) * BUF, ks * 32, lane, p, o);
@@ -649,7 +652,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   // The same step when tile t+3 exists and is full and the lean loads apply
   // (steps t < n_lean): no run-time choices.
   const int n_lean = !lean ? 0 : KV8 ? (last_full ? n_st - 4 : n_st - 5) : (last_full ? n_st - 3 : n_st - 4);
-  auto lean_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) {
+  auto lean_step = [&](int t, const f32x16_t& s_in, f32x16_t& s_out) __attribute__((always_inline)) {
     hot_seen |= phase_ac<DT, SOFTCAP>(lds + ((t + 1) % NB) * BUF, lds + (t % NB) * BUF, ks * 32, lane, qf, s_in,
                                       s_out, st, c, cap, o, [&]() {
                                         if constexpr (KV8) {
