@@ -433,10 +433,10 @@ def main() -> int:
     ap.add_argument("--no-warm", action="store_true",
                     help="skip the warm (one relaunched copy) timing; the cold rotation is the headline")
     ap.add_argument("--kernel", choices=["auto", "generic"], default="auto")
-    ap.add_argument("--option", choices=["none", "window", "sinks", "alibi", "fp8"], default="none",
+    ap.add_argument("--option", choices=["none", "window", "sinks", "alibi", "fp8", "softcap"], default="none",
                     help="decode with one optional attention feature of the reference's impl "
                          "(beam_attn.py:597-625): a 1024-token sliding window, per-head sinks, ALiBi "
-                         "slopes, or an fp8 e4m3 KV cache (scales 1)")
+                         "slopes, an fp8 e4m3 KV cache (scales 1), or a logit soft cap of 50")
     ap.add_argument("--shape", choices=["c2", "sid"], default="c2",
                     help="decode shape: c2 (8 requests x 128 beams, 32/8 heads; the headline) or sid (one "
                          "layer of the semantic-ID decode step: 4 x 128 beams, 16/8 heads, suffix 1-3, "
@@ -491,6 +491,8 @@ def main() -> int:
         opt_kw["sinks"] = torch.linspace(-1.0, 1.0, Hq, device=dev)
     elif args.option == "alibi":
         opt_kw["alibi_slopes"] = torch.tensor([2.0 ** (-8.0 * (h + 1) / Hq) for h in range(Hq)], device=dev)
+    elif args.option == "softcap":
+        opt_kw["softcap"] = 50.0
     elif args.option == "fp8":
         one = torch.ones(1, dtype=torch.float32, device=dev)
         opt_kw.update(k_scale=one, v_scale=one)
