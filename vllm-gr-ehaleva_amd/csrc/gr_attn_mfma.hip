@@ -1081,19 +1081,19 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   }
 }
 
-// Merge of the split decode's partials: one thread per (row, 4 dims), 8 rows
+// Merge of the split decode's partials: one thread per (row, 8 dims), 16 rows
 // of one row tile per workgroup.  LSE* = log sum_s exp(LSE_s), O = sum_s
 // exp(LSE_s - LSE*) O_s (the merge_attn_states rule), written as the final
 // output and LSE.
-constexpr int MG_ROWS = 8;
+constexpr int MG_ROWS = 16;
 template <int DT>
 __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
   kernarg_lines<kernarg_line_count<DecodeArgs>(4)>();
   using S = uint16_t;
   constexpr int PER_TILE = MF_ROWS / MG_ROWS;
   const int tile = blockIdx.x / PER_TILE;
-  const int row = (blockIdx.x % PER_TILE) * MG_ROWS + threadIdx.x / (HD / 4);
-  const int d4 = (threadIdx.x % (HD / 4)) * 4;
+  const int row = (blockIdx.x % PER_TILE) * MG_ROWS + threadIdx.x / (HD / 8);
+  const int d8 = (threadIdx.x % (HD / 8)) * 8;  // 8 dims: one 16-byte vector per partial
   const int unit = tile / mtiles, mt = tile % mtiles;
   const int r = unit / a.Hkv, hk = unit % a.Hkv;
   const int nb0 = a.beam_start[r], W = a.beam_start[r + 1] - nb0;
@@ -1103,30 +1103,33 @@ __global__ __launch_bounds__(256) void split_merge(DecodeArgs a, int mtiles) {
   if (rho >= rows_r) return;
   const int nsplit = a.nsplit;
   const float* lse = a.ws_lse + (int64_t)tile * nsplit * MF_ROWS + row;
-  const uint16_t* po = a.ws_o + ((int64_t)tile * nsplit * MF_ROWS + row) * HD + d4;
+  const uint16_t* po = a.ws_o + ((int64_t)tile * nsplit * MF_ROWS + row) * HD + d8;
   const float sk = a.sinks ? a.sinks[hk * G + rho % G] : -INFINITY;  // joins the merged softmax once
   float mx = sk;
 #pragma unroll 4
   for (int s2 = 0; s2 < nsplit; ++s2) mx = fmaxf(mx, lse[s2 * MF_ROWS]);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f}, sum = sk == -INFINITY ? 0.f : __expf(sk - mx);
+  float acc[8] = {}, sum = sk == -INFINITY ? 0.f : __expf(sk - mx);
   if (mx != -INFINITY) {
 #pragma unroll 4
     for (int s2 = 0; s2 < nsplit; ++s2) {
       const float w = __expf(lse[s2 * MF_ROWS] - mx);
-      const u32x2_t pv = *reinterpret_cast<const u32x2_t*>(po + (int64_t)s2 * MF_ROWS * HD);
+      const u32x4_t pv = *reinterpret_cast<const u32x4_t*>(po + (int64_t)s2 * MF_ROWS * HD);
       sum += w;
-      acc[0] += w * Mma<DT>::lo(pv[0]);
-      acc[1] += w * Mma<DT>::hi(pv[0]);
-      acc[2] += w * Mma<DT>::lo(pv[1]);
-      acc[3] += w * Mma<DT>::hi(pv[1]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += w * Mma<DT>::lo(pv[e]);
+        acc[2 * e + 1] += w * Mma<DT>::hi(pv[e]);
+      }
     }
   }
   const float inv = sum > 0.f ? 1.f / sum : 0.f;
   const int b = rho / TG, qi = (rho / G) % a.T, g = rho % G;
   const int64_t tok = (int64_t)(nb0 + b) * a.T + qi;
-  const u32x2_t wv = {Mma<DT>::pack2(acc[0] * inv, acc[1] * inv), Mma<DT>::pack2(acc[2] * inv, acc[3] * inv)};
-  *reinterpret_cast<u32x2_t*>(static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g) * HD + d4) = wv;
-  if (a.lse_out && d4 == 0) a.lse_out[tok * a.Hq + hk * G + g] = mx == -INFINITY ? -INFINITY : mx + __logf(sum);
+  u32x4_t wv;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) wv[e] = Mma<DT>::pack2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+  *reinterpret_cast<u32x4_t*>(static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g) * HD + d8) = wv;
+  if (a.lse_out && d8 == 0) a.lse_out[tok * a.Hq + hk * G + g] = mx == -INFINITY ? -INFINITY : mx + __logf(sum);
 }
 
 }  // namespace
