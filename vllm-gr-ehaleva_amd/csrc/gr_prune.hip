@@ -171,10 +171,33 @@ __device__ inline void catalog_range(const PruneArgs& a, int b, int& c0, int& c1
   c1 = s1;
 }
 
+// v of lane (lane ^ M), M < 32: ds_swizzle's bit-mask mode (and 0x1F, xor M)
+// reads across the 32-lane half without the address arithmetic of a
+// general shuffle
+template <int M>
+__device__ inline float lane_xor(float v) {
+  static_assert(M > 0 && M < 32, "within a 32-lane half");
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), (M << 10) | 0x1F));
+}
+
 __device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  v = fmaxf(v, lane_xor<16>(v));
+  v = fmaxf(v, lane_xor<8>(v));
+  v = fmaxf(v, lane_xor<4>(v));
+  v = fmaxf(v, lane_xor<2>(v));
+  return fmaxf(v, lane_xor<1>(v));
+}
+
+// xor butterfly sum over the wave, masks 32, 16, .., 1 in turn (every lane
+// ends with the same float: each step adds the same two values)
+__device__ inline float wave_sum_butterfly(float v) {
+  v = v + __shfl_xor(v, 32, 64);
+  v = v + lane_xor<16>(v);
+  v = v + lane_xor<8>(v);
+  v = v + lane_xor<4>(v);
+  v = v + lane_xor<2>(v);
+  return v + lane_xor<1>(v);
 }
 
 // block-wide exclusive scan of one int per thread (NT threads); returns the total
@@ -375,8 +398,12 @@ __device__ __noinline__ void row_topk_radix(const float* xg, int V, int k1, uint
 // CATALOG: the beam's top-k candidates outside its trie node's children are
 // dropped (the reference masks them to -inf after the sampler's per-beam
 // top-K, serving_engine.py:504-506, 526-528).
-template <int MAXC, bool CATALOG = false>
+// FULL: the row is exactly MAXC chunks (V = MAXC * PR_CHUNK), so every chunk
+// and element is live: no padding, no per-chunk bounds tests (the same
+// arithmetic, in the same order, as the general form).
+template <int MAXC, bool CATALOG = false, bool FULL = false>
 __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
+  static_assert(!FULL || MAXC > 0, "a full row is held in registers");
   __shared__ uint64_t sk[PR_MAXK];  // candidates as row_key
   __shared__ float ox[PR_MAXK];
   __shared__ int ov[PR_MAXK];
@@ -384,27 +411,31 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   __shared__ int hist_part[PR_BINS > PR_SURV * (PR_THREADS / 64) ? PR_BINS : PR_SURV * (PR_THREADS / 64)];
   int* hist = hist_part;
   int* part = hist_part;
-  __shared__ int scnt;
   __shared__ float wred[PR_THREADS / 64];
   __shared__ int itmp[PR_THREADS / 64];
   __shared__ int sel[3];
   __shared__ uint32_t wkey[PR_THREADS / 64];
   __shared__ int eos_pos;
+  __shared__ double lse_sh;  // the row's LSE, for the logprob lists
 
   const int row = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* xg = a.logits + (int64_t)row * a.row_stride;
   const int V = a.V, k1 = a.k1;
   const int nch = (V + PR_CHUNK - 1) / PR_CHUNK;
-  if (tid == 0) scnt = 0;  // ordered before its use by the barriers below
 
   float xr[MAXC > 0 ? MAXC : 1][PR_VEC];
   if constexpr (MAXC > 0) {
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
       const int idx = c * PR_CHUNK + PR_VEC * tid;
-      f32x4_t v = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-      if (c < nch && idx < V) v = *reinterpret_cast<const f32x4_t*>(xg + idx);
+      f32x4_t v;
+      if constexpr (FULL) {
+        v = *reinterpret_cast<const f32x4_t*>(xg + idx);
+      } else {
+        v = f32x4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        if (c < nch && idx < V) v = *reinterpret_cast<const f32x4_t*>(xg + idx);
+      }
 #pragma unroll
       for (int j = 0; j < PR_VEC; ++j) xr[c][j] = v[j];  // (-0 stays: only survivor keys are made canonical)
     }
@@ -420,7 +451,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     else return xg[c * PR_CHUNK + PR_VEC * tid + j] + 0.0f;
   };
 #define PR_FOR_CHUNKS(c) \
-  _Pragma("unroll") for (int c = 0; c < (MAXC > 0 ? MAXC : nch); ++c) if (c < nch)
+  _Pragma("unroll") for (int c = 0; c < (MAXC > 0 ? MAXC : nch); ++c) if (FULL || c < nch)
 
   // ---- row max; also the thread's second-largest chunk maximum (an element
   // other than the thread maximum: it tightens the selection bound below) ----
@@ -455,14 +486,17 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
         }
       }
     }
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) acc = acc + __shfl_xor(acc, msk, 64);
+    acc = wave_sum_butterfly(acc);
     if (lane == 0) wred[wave] = acc;
     __syncthreads();
-    const float S = (wred[0] + wred[1]) + (wred[2] + wred[3]);
-    const double lse = (double)m + log_f64((double)S);
-    c_row = (a.cum64 ? a.cum64[row] : (double)a.cum[row]) - lse;
-    lse_row = lse;
+    // one wave works out the LSE (float64): only thread 0 and the logprob
+    // lists, which read it from LDS, need it
+    if (__builtin_amdgcn_readfirstlane(wave) == 0) {
+      const float S = (wred[0] + wred[1]) + (wred[2] + wred[3]);
+      const double lse = (double)m + log_f64((double)S);
+      c_row = (a.cum64 ? a.cum64[row] : (double)a.cum[row]) - lse;
+      lse_row = lse;
+    }
   }
 
   // ---- stage 1: row top-k1 by (logit desc, token asc) ----
@@ -514,17 +548,18 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     }
   }
   int pos;
-  const int n_surv = block_scan(ns, pos, itmp);
-  if (tid == 0) scnt = n_surv;
-  if (ns > 0) {
+  // (the total is the same in every thread: held in a scalar register)
+  const int n_surv = __builtin_amdgcn_readfirstlane(block_scan(ns, pos, itmp));
+  // more than PR_SURV survivors: the radix path below selects from the row
+  // itself, so nothing is written (and no write needs a bound check)
+  if (n_surv <= PR_SURV && ns > 0) {
     PR_FOR_CHUNKS(c) {
       if (live(c)) {
 #pragma unroll
         for (int j = 0; j < PR_VEC; ++j) {
           const float y = get(c, j);
           if (y >= t0f) {  // (logit bits, token); made a row key once, below
-            if (pos < PR_SURV)
-              sk[pos] = ((uint64_t)__builtin_bit_cast(uint32_t, y) << 32) | (uint32_t)(c * PR_CHUNK + PR_VEC * tid + j);
+            sk[pos] = ((uint64_t)__builtin_bit_cast(uint32_t, y) << 32) | (uint32_t)(c * PR_CHUNK + PR_VEC * tid + j);
             ++pos;
           }
         }
@@ -532,7 +567,7 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     }
   }
   __syncthreads();
-  const int S = scnt;
+  const int S = n_surv;
   if (S <= PR_SURV && k1 <= PR_THREADS) {
     // the survivors as row keys (all distinct: the token is part of the key)
     auto to_key = [](uint64_t raw) {  // (+ 0.0f: -0 orders as +0)
@@ -548,7 +583,8 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     // rank < k1 are the row's top-k1, in order.  Wave w counts over the
     // survivors [w*Q, (w+1)*Q) for every target; lane l holds the targets l,
     // l + 64, ...; the four partial counts are summed in LDS.
-    const int Q = (S + 3) >> 2, q0 = wave * Q, q1 = min(S, q0 + Q);
+    // (wave-uniform bounds in scalar registers: the count loop is a scalar loop)
+    const int Q = (S + 3) >> 2, q0 = __builtin_amdgcn_readfirstlane(wave) * Q, q1 = min(S, q0 + Q);
     auto partial = [&](auto tg_c) {
       constexpr int TG = decltype(tg_c)::value;
       uint64_t kt[TG];
@@ -594,14 +630,18 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     row_topk_radix(xg, V, k1, t0, fkey(m), sk, ox, ov, hist, itmp, sel);
   }
 #undef PR_FOR_CHUNKS
-  if (tid == 0) eos_pos = -1;
+  if (tid == 0) {
+    eos_pos = -1;
+    lse_sh = lse_row;
+  }
   __syncthreads();
   if (a.cand_token) {
     // the row's whole top-k1 list with its logprobs (the sampler's per-beam
     // logprobs, before EOS or the catalog take anything out)
+    const double lse = lse_sh;
     for (int i = tid; i < k1; i += PR_THREADS) {
       a.cand_token[(int64_t)row * k1 + i] = ov[i];
-      a.cand_logprob[(int64_t)row * k1 + i] = (float)((double)ox[i] - lse_row);
+      a.cand_logprob[(int64_t)row * k1 + i] = (float)((double)ox[i] - lse);
     }
   }
   float* cx = a.cand_x + (int64_t)row * k1;
@@ -1480,7 +1520,10 @@ static gr_status_t prune_launch(PruneArgs& a, const float* logits, int64_t logit
   a.part_key = reinterpret_cast<uint64_t*>(part_base);
   a.part_flat = reinterpret_cast<int64_t*>(part_base + align256(parts * sizeof(uint64_t)));
   const bool cat = a.beam_node != nullptr;
-  if (vocab <= PR_CHUNK * PR_REG_CHUNKS) {
+  if (vocab == PR_CHUNK * PR_REG_CHUNKS) {
+    if (cat) hipLaunchKernelGGL((prune_rows<PR_REG_CHUNKS, true, true>), dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
+    else hipLaunchKernelGGL((prune_rows<PR_REG_CHUNKS, false, true>), dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
+  } else if (vocab <= PR_CHUNK * PR_REG_CHUNKS) {
     if (cat) hipLaunchKernelGGL((prune_rows<PR_REG_CHUNKS, true>), dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
     else hipLaunchKernelGGL((prune_rows<PR_REG_CHUNKS, false>), dim3((unsigned)rows), dim3(PR_THREADS), 0, stream, a);
   } else {
