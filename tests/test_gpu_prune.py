@@ -55,6 +55,25 @@ def test_prune_shapes(device, R, W, V, k):
     _assert_exact(run_gpu(wl, device), op.prune_topk(wl.logits.numpy(), wl.cum.numpy(), k))
 
 
+@pytest.mark.parametrize("V", [8192, 12288])
+def test_prune_one_wave_holds_most_survivors(device, V):
+    """200 large logits per row among the elements one wave of the row's
+    workgroup reads (token % 1024 in [0, 256) or [768, 1024)): that wave has
+    ~235 of the row's ~350 keys above the selection bound, so the direct rank
+    runs with eight targets per lane and one wave's survivors filling most of
+    the list.  Bit-exact."""
+    wl = workloads.make_prune(R=2, W=16, V=V, k=128, seed=5)
+    g = np.random.default_rng(5)
+    lg = wl.logits.numpy()
+    tok = np.arange(V) % 1024
+    for r in range(2):
+        for b in range(16):
+            base = 0 if b % 2 == 0 else 768
+            pick = g.choice(np.nonzero((tok >= base) & (tok < base + 256))[0], 200, replace=False)
+            lg[r, b, pick] = 10 + g.random(200).astype(np.float32)
+    _assert_exact(run_gpu(wl, device), op.prune_topk(lg, wl.cum.numpy(), 128))
+
+
 def test_prune_all_equal_logits(device):
     """Every score ties: the lowest flat indices (beam 0, tokens 0..k-1) win."""
     wl = workloads.make_prune(R=2, W=8, V=1024, k=8, seed=1)
