@@ -441,12 +441,7 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
 #pragma unroll
       for (int j = 0; j < SB_STAGE; ++j) suf_blk[rg][lane][j] = j < a.suffix_bt_stride ? sBlk[j] : -1;
     }
-    int incl = len;  // inclusive scan over the first 32 lanes
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) {
-      const int y = __shfl_up(incl, off, 64);
-      if ((lane & 31) >= off) incl += y;
-    }
+    const int incl = wave_incl_scan<32>(len);  // inclusive scan over the first 32 lanes (and the last 32)
     if (lane < 32) suf_cum[rg][lane + 1] = incl;
     suf_len = len;
     suf_incl = incl;

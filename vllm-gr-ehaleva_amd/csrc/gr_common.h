@@ -48,6 +48,29 @@ template <typename T> constexpr int kernarg_line_count(int extra_bytes = 0) {
   return (int)((sizeof(T) + extra_bytes + 63) / 64);
 }
 
+// ---- wave prefix sums --------------------------------------------------------
+// Inclusive prefix sum of one int per lane over the wave's 64 lanes (L = 64)
+// or over each 32-lane half (L = 32), by DPP moves: within each row of 16
+// lanes, shifts by 1, 2 and 3 of the inputs, then by 4 (banks 1-3) and 8
+// (banks 2-3) of the partial sums; across rows, row 0's and row 2's last
+// lanes broadcast into rows 1 and 3 (row_bcast:15), then lane 31 into rows 2
+// and 3 (row_bcast:31).  A lane whose source lies outside its row, or whose
+// row or bank is masked off, adds 0.  No LDS round trip and no lane-address
+// arithmetic, against six of each for a shuffle-based scan.
+template <int L = 64>
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  static_assert(L == 32 || L == 64, "a wave or each half");
+  int s = v;
+  s += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
+  s += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
+  s += __builtin_amdgcn_update_dpp(0, v, 0x113, 0xf, 0xf, true);  // row_shr:3
+  s += __builtin_amdgcn_update_dpp(0, s, 0x114, 0xf, 0xe, true);  // row_shr:4, banks 1-3
+  s += __builtin_amdgcn_update_dpp(0, s, 0x118, 0xf, 0xc, true);  // row_shr:8, banks 2-3
+  s += __builtin_amdgcn_update_dpp(0, s, 0x142, 0xa, 0xf, true);  // row_bcast:15 into rows 1, 3
+  if constexpr (L == 64) s += __builtin_amdgcn_update_dpp(0, s, 0x143, 0xc, 0xf, true);  // row_bcast:31 into rows 2, 3
+  return s;
+}
+
 // ---- element conversion ---------------------------------------------------
 // bf16 and fp16 are handled as raw 16-bit patterns; conversion to float is
 // exact, conversion from float rounds to nearest even.

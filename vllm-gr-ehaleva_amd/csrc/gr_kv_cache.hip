@@ -95,12 +95,7 @@ __device__ inline void block_scan(const int* v, int* out, int n, int* tmp) {
     x[u] = i < n ? v[i] : 0;
     s += x[u];
   }
-  int incl = s;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += y;
-  }
+  const int incl = wave_incl_scan(s);
   if (lane == 63) tmp[wave] = incl;
   __syncthreads();
   int base = incl - s;

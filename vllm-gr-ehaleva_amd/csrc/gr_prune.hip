@@ -204,12 +204,7 @@ __device__ inline float wave_sum_butterfly(float v) {
 template <int NT = PR_THREADS>
 __device__ int block_scan(int v, int& excl, int* tmp) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int incl = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    int y = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += y;
-  }
+  const int incl = wave_incl_scan(v);
   if (lane == 63) tmp[wave] = incl;
   __syncthreads();
   int base = 0, total = 0;
