@@ -40,7 +40,9 @@ def _ulp32(x):
 
 def test_exp2_neg_accuracy():
     ts = np.concatenate([np.linspace(-126, 0, 20001), -np.random.default_rng(0).random(5000) * 126,
-                         [0.0, -0.5, -1.0, -1e-7, -124.999, -125.5, -126.0]]).astype(np.float32)
+                         [0.0, -0.5, -1.0, -1e-7, -124.999, -125.5, -126.0],
+                         # arguments just below an integer (the row maximum's own term is one)
+                         [-2.0 ** -25, -2.0 ** -30, -1e-20, -3.0 - 2.0 ** -23]]).astype(np.float32)
     worst = 0.0
     for t in ts:
         got = op.exp2_neg(float(t))
