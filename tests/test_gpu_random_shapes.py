@@ -2,7 +2,8 @@
 the C ABI: shapes the hand-picked tests do not reach (odd GQA ratios, block
 size 32, empty prefixes and suffixes, two query tokens per beam, the split
 decode on and off, ragged prefill batches, fork tables of several blocks,
-wide prune rows).  Tolerances as elsewhere: bf16 attention <= 2e-2 on N(0,1)
+wide prune rows), and decodes over random dtypes, fp8 caches and attention
+options.  Tolerances as elsewhere: bf16 attention <= 2e-2 on N(0,1)
 inputs, fork and prune bit for bit."""
 
 import numpy as np
@@ -11,6 +12,7 @@ import torch
 
 from oracle import attention as oa
 from oracle import fork as of
+from oracle import fp8
 from oracle import prune as op
 from vllm_gr_amd import ops, workloads
 
@@ -57,6 +59,71 @@ def test_random_decode(device, seed):
     fin = np.isfinite(ref_lse)
     assert (np.isfinite(lse.cpu().numpy()) == fin).all()
     assert np.abs(lse.cpu().numpy()[fin] - ref_lse[fin]).max(initial=0.0) <= 2e-2
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_decode_variants(device, seed):
+    """Random decodes over the space the shape sweep above keeps fixed: bf16
+    and fp16, fp8 e4m3 caches with random scales, a left window, sinks and
+    ALiBi in any combination, soft cap, split or not -- against the dense
+    float64 oracle with the same options (within 2e-2, LSE finiteness equal)."""
+    rng = np.random.default_rng(7000 + seed)
+    Hkv = _pick(rng, [1, 2, 4, 8])
+    G = _pick(rng, [1, 2, 4, 8])
+    Hq = Hkv * G
+    R = int(rng.integers(1, 4))
+    W = int(rng.integers(1, 33))
+    P = int(_pick(rng, [0, 33, 64, 300, 1000]))
+    T = _pick(rng, [1, 1, 2])
+    L = (T, T + int(rng.integers(0, 12)))
+    bs = _pick(rng, [16, 32])
+    dtype = _pick(rng, [torch.bfloat16, torch.float16])
+    kv8 = bool(rng.integers(0, 3) == 0)
+    cap = float(_pick(rng, [0.0, 0.0, 0.0, 30.0]))
+    split = bool(rng.integers(0, 2))
+    g = torch.Generator().manual_seed(seed)
+    kw = {}
+    if rng.integers(0, 2):
+        kw["window"] = (int(_pick(rng, [2, 40, 70, 300, 999])), -1)
+    if rng.integers(0, 2):
+        kw["sinks"] = torch.randn(Hq, generator=g) * 2
+    if rng.integers(0, 2):
+        kw["alibi_slopes"] = torch.rand(Hq, generator=g) * 0.05
+    print(f"[random] decode variant R={R} W={W} P={P} T={T} L={L} Hkv={Hkv} G={G} bs={bs} {dtype} kv8={kv8} "
+          f"cap={cap} split={split} options={sorted(kw)} window={kw.get('window')}", flush=True)
+    wl = workloads.make_decode(R=R, W=W, P=P, L=L, Hq=Hq, Hkv=Hkv, D=128, block_size=bs, dtype=dtype,
+                               input_scale=1.0, seed=seed, q_per_beam=T, softcap=cap)
+    d = wl.to(device)
+    if kv8:
+        sk, sv = 0.05 * (1 + rng.random()), 0.02 * (1 + rng.random())
+        codes = [torch.from_numpy(fp8.quantize(torch.randn(wl.kv_cache.shape[1:], generator=g).numpy()
+                                               .astype(np.float32), s_)) for s_ in (sk, sv)]
+        kd, vd = (c.to(device).view(torch.float8_e4m3fn) for c in codes)
+        extra = dict(k_scale=torch.tensor([sk], device=device), v_scale=torch.tensor([sv], device=device))
+        k64, v64 = fp8.decode(codes[0].numpy()) * sk, fp8.decode(codes[1].numpy()) * sv
+    else:
+        kd, vd, extra = d.k_cache, d.v_cache, {}
+        kv = wl.kv_cache.to(torch.float64).numpy()
+        k64, v64 = kv[0], kv[1]
+    out = torch.empty_like(d.q)
+    lse = torch.empty(d.q.shape[:2], dtype=torch.float32, device=device)
+    status = ops.new_status(device)
+    gkw = {k_: (v_.to(device) if isinstance(v_, torch.Tensor) else v_) for k_, v_ in kw.items()}
+    ops.beam_attn_decode(d.q, kd, vd, d.prefix_bt, d.prefix_len, d.beam_start, d.suffix_bt, d.suffix_len,
+                         q_per_beam=T, scale=d.scale, softcap=cap, max_beams_per_req=d.max_beams, out=out, lse=lse,
+                         status=status, split=split, max_prefix_len=P if split else None, **gkw, **extra)
+    torch.cuda.synchronize()
+    ops.check_status(status)
+    okw = {k_: (v_.numpy() if isinstance(v_, torch.Tensor) else v_) for k_, v_ in kw.items()}
+    ref, ref_lse = oa.beam_attention_dense(wl.q.to(torch.float64).numpy(), k64, v64, wl.prefix_bt.numpy(),
+                                           wl.prefix_len.numpy(), wl.beam_start.numpy(), wl.suffix_bt.numpy(),
+                                           wl.suffix_len.numpy(), q_per_beam=T, scale=wl.scale, softcap=cap,
+                                           block_size=bs, **okw)
+    got, got_lse = out.cpu().double().numpy(), lse.cpu().double().numpy()
+    assert np.abs(got - ref).max() <= 2e-2
+    fin = np.isfinite(ref_lse)
+    assert (np.isfinite(got_lse) == fin).all()
+    assert np.abs(got_lse[fin] - ref_lse[fin]).max(initial=0.0) <= 2e-2
 
 
 @pytest.mark.parametrize("seed", range(8))
