@@ -7,7 +7,8 @@
 //
 // Two kernels sit behind gr_beam_attn_decode:
 //  * decode_generic: any dtype (fp32/fp16/bf16), head_dim % 8 == 0 <= 256.
-//    One workgroup per (beam, KV head, 32-row chunk); fp32 VALU math.
+//    One workgroup per (request, KV head, 32-row chunk of the request's beam
+//    rows): the chunk's beams share each prefix tile; fp32 VALU math.
 //  * the MFMA kernel in gr_attn_mfma.hip for bf16/fp16 at head_dim 128,
 //    which stages each request's prefix tile once in LDS for all its beams.
 #include "gr_common.h"
@@ -19,16 +20,6 @@ constexpr int GEN_ROWS = 32;     // query rows per workgroup
 constexpr int GEN_TK = 32;       // keys per tile
 constexpr int GEN_THREADS = 256;
 constexpr int GEN_ACC = GEN_ROWS * 256 / GEN_THREADS;  // acc slots per thread at D=256
-
-__device__ inline int find_request(const int32_t* beam_start, int num_reqs, int n) {
-  // largest r with beam_start[r] <= n  (beam_start is non-decreasing)
-  int lo = 0, hi = num_reqs - 1;
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (beam_start[mid] <= n) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
 
 // PREFILL: the varlen mode (gr_paged_attn_prefill): blockIdx.x / chunks is
 // the request, prefix_bt / prefix_len its block table and sequence length,
@@ -43,11 +34,22 @@ __device__ inline int find_request(const int32_t* beam_start, int num_reqs, int 
 // window_size / alibi_slopes / s_aux).
 // KV8: the caches hold fp8 e4m3 elements, dequantised on load by the
 // per-tensor scales (value = e4m3 * scale).
+// Decode: the chunk's rows belong to consecutive beams b_lo .. of request r
+// (row rho of the request: beam rho / (T G), query (rho / G) % T, head
+// rho % G).  Its keys are the prefix, then the chunk's beams' suffixes one
+// after another (slot j of the concatenation: the beam whose cumulative
+// lengths cover it); a suffix key is visible to the rows of its own beam only.
 template <int DT, bool PREFILL = false, bool KV8 = false>
 __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   using E = Elem<DT>;
   using S = typename E::storage;
   extern __shared__ float smem[];
+  __shared__ int c_len[GEN_ROWS];       // decode: the chunk's beams' validated suffix lengths
+  __shared__ int c_s0[GEN_ROWS];        // ... their first suffix positions
+  __shared__ int c_cum[GEN_ROWS + 1];   // ... cumulative lengths (slot of each beam's first key)
+  __shared__ int64_t k_off[GEN_TK];     // per tile key: element offset of its head-0 row (valid keys)
+  __shared__ int k_beam[GEN_TK];        // ... chunk beam of a suffix key, -1 for a prefix key
+  __shared__ int k_pos[GEN_TK];         // ... position in [prefix ; own suffix]
   const int D = a.D;
   float* q_s = smem;                              // [ROWS][D]
   float* k_s = q_s + GEN_ROWS * D;                // [TK][D+1]
@@ -59,19 +61,18 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   int* kv_ok = reinterpret_cast<int*>(a_s + GEN_ROWS);  // [TK]
 
   const int G = a.Hq / a.Hkv;
-  const int rows_total = G * a.T;
-  const int chunks = (rows_total + GEN_ROWS - 1) / GEN_ROWS;
-  const int n = blockIdx.x / chunks;
+  const int TG = a.T * G;  // decode: rows per beam
+  const int chunks = PREFILL ? (TG + GEN_ROWS - 1) / GEN_ROWS : (a.max_beams * TG + GEN_ROWS - 1) / GEN_ROWS;
+  const int r = blockIdx.x / chunks;
   const int chunk = blockIdx.x % chunks;
   const int hk = blockIdx.y;
   const int t = threadIdx.x;
-  if (n >= (PREFILL ? a.num_reqs : a.num_beams)) return;
+  if (r >= a.num_reqs) return;
   const int row0 = chunk * GEN_ROWS;
   const int pre_cap = a.prefix_bt_stride * a.bs;
-  int r, P, L, s0, nrows, Pc, Lc, ctx = 0;
-  int64_t tok0;  // token row of query 0 of this beam / request
+  int P, nrows, Pc, Lsum = 0, ctx = 0, nb0 = 0, b_lo = 0;
+  int64_t tok0 = 0;  // prefill: token row of the request's first query
   if constexpr (PREFILL) {
-    r = n;
     const int q0 = a.beam_start[r], ql = a.beam_start[r + 1] - q0, seq = a.prefix_len[r];
     if (q0 < 0 || ql < 0 || q0 + ql > a.num_beams || ql > a.T || seq < ql || seq > pre_cap) {
       if (t == 0 && chunk == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
@@ -82,20 +83,51 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
     ctx = seq - ql;
     // keys up to the chunk's last query token (all of them when non-causal)
     P = Pc = a.causal ? ctx + (row0 + nrows - 1) / G + 1 : seq;
-    L = Lc = s0 = 0;
     tok0 = q0;
   } else {
-    r = find_request(a.beam_start, a.num_reqs, n);
+    nb0 = a.beam_start[r];
+    const int W = a.beam_start[r + 1] - nb0;
+    // beam_start is device data: never trust it (a request past max_beams
+    // would leave rows no workgroup computes)
+    if (nb0 < 0 || W < 0 || nb0 + W > a.num_beams || W > a.max_beams) {
+      if (t == 0 && chunk == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+      return;
+    }
+    if (row0 >= W * TG) return;
+    nrows = min(GEN_ROWS, W * TG - row0);
     P = a.prefix_len[r];
-    L = a.suffix_len[n];
-    s0 = a.suffix_start ? a.suffix_start[n] : 0;
-    nrows = min(GEN_ROWS, rows_total - row0);
-    const int suf_cap = a.suffix_bt_stride * a.bs;
     Pc = min(max(P, 0), pre_cap);
-    Lc = (L < 0 || s0 < 0 || s0 + L > suf_cap) ? 0 : L;
-    if (t == 0 && (Pc != P || Lc != L)) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
-    tok0 = (int64_t)n * a.T;
+    if (t == 0 && chunk == 0 && Pc != P) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+    b_lo = row0 / TG;
+    const int nbm = (row0 + nrows - 1) / TG - b_lo + 1;  // beams in the chunk (<= GEN_ROWS)
+    if (t < nbm) {
+      const int n = nb0 + b_lo + t;
+      const int L = a.suffix_len[n], s0 = a.suffix_start ? a.suffix_start[n] : 0;
+      const int suf_cap = a.suffix_bt_stride * a.bs;
+      const int Lc = (L < 0 || s0 < 0 || s0 + L > suf_cap) ? 0 : L;
+      if (Lc != L) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
+      c_len[t] = Lc;
+      c_s0[t] = s0;
+    }
+    __syncthreads();
+    if (t == 0) {
+      int c = 0;
+      for (int j = 0; j < nbm; ++j) {
+        c_cum[j] = c;
+        c += c_len[j];
+      }
+      c_cum[nbm] = c;
+    }
+    __syncthreads();
+    Lsum = c_cum[nbm];
   }
+  // the chunk beam of a row, and its query index within the beam
+  auto row_beam = [&](int row) { return (row0 + row) / TG - b_lo; };
+  auto row_qi = [&](int row) { return PREFILL ? (row0 + row) / G : ((row0 + row) / G) % a.T; };
+  // token row (of q / out) of a chunk row
+  auto row_tok = [&](int row) -> int64_t {
+    return PREFILL ? tok0 + row_qi(row) : (int64_t)(nb0 + b_lo + row_beam(row)) * a.T + row_qi(row);
+  };
 
   const S* q = static_cast<const S*>(a.q);
   const S* kc = static_cast<const S*>(a.k_cache);
@@ -108,9 +140,8 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
     int row = e / D, d = e % D;
     float v = 0.f;
     if (row < nrows) {
-      int rho = row0 + row;
-      int qi = rho / G, g = rho % G;
-      v = E::to_float(q[(tok0 + qi) * a.q_tok_stride + (int64_t)(hk * G + g) * D + d]);
+      const int g = (row0 + row) % G;
+      v = E::to_float(q[row_tok(row) * a.q_tok_stride + (int64_t)(hk * G + g) * D + d]);
     }
     q_s[e] = v;
   }
@@ -122,41 +153,55 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
 #pragma unroll
   for (int i = 0; i < GEN_ACC; ++i) acc[i] = 0.f;
 
-  const int total = Pc + Lc;
-  // position of the query token of chunk row `row`
-  auto qpos_of = [&](int row) { return PREFILL ? ctx + (row0 + row) / G : Pc + Lc - a.T + (row0 + row) / G; };
-  // a left window: the tiles before the chunk's first row's window hold no visible key
-  const int k_start = a.win_left >= 0 ? max(0, qpos_of(0) - a.win_left) / GEN_TK * GEN_TK : 0;
+  // keys of the workgroup: the prefix (prefill: up to the chunk's last query),
+  // then (decode) the chunk's beams' suffixes
+  const int total = Pc + Lsum;
+  // position of the query token of chunk row `row` in its [prefix ; suffix]
+  auto qpos_of = [&](int row) {
+    return PREFILL ? ctx + row_qi(row) : Pc + c_len[row_beam(row)] - a.T + row_qi(row);
+  };
+  // a left window: the prefix tiles before every row's window hold no visible key
+  int k_start = 0;
+  if (a.win_left >= 0) {
+    int lo = INT_MAX;
+    for (int row = 0; row < nrows; ++row) lo = min(lo, qpos_of(row) - a.win_left);
+    k_start = min(max(0, lo), Pc) / GEN_TK * GEN_TK;
+  }
   for (int k0 = k_start; k0 < total; k0 += GEN_TK) {
     __syncthreads();
     if (t < GEN_TK) {
-      int kk = k0 + t;
-      int ok = 0;
+      const int kk = k0 + t;
+      int ok = 0, kb = -1, kp = kk;
+      int64_t off = 0;
       if (kk < total) {
-        int blk = kk < Pc ? a.prefix_bt[(int64_t)r * a.prefix_bt_stride + kk / a.bs]
-                          : a.suffix_bt[(int64_t)n * a.suffix_bt_stride + (s0 + kk - Pc) / a.bs];
+        int blk, o;
+        if (kk < Pc) {
+          blk = a.prefix_bt[(int64_t)r * a.prefix_bt_stride + kk / a.bs];
+          o = kk % a.bs;
+        } else {  // suffix slot j: beam kb holds slots c_cum[kb] .. c_cum[kb + 1] - 1
+          const int j = kk - Pc;
+          kb = 0;
+          while (c_cum[kb + 1] <= j) ++kb;
+          const int p = j - c_cum[kb], pos = c_s0[kb] + p;
+          kp = Pc + p;
+          blk = a.suffix_bt[(int64_t)(nb0 + b_lo + kb) * a.suffix_bt_stride + pos / a.bs];
+          o = pos % a.bs;
+        }
         ok = (blk >= 0 && blk < a.num_blocks);
         if (!ok) flag_status(a.dev_status, GR_DEV_BAD_BLOCK);
+        off = ok ? (int64_t)blk * a.kv_block_stride + (int64_t)o * a.kv_tok_stride : 0;
       }
       kv_ok[t] = ok;
+      k_off[t] = off;
+      k_beam[t] = kb;
+      k_pos[t] = kp;
     }
     __syncthreads();
     for (int e = t; e < GEN_TK * D; e += GEN_THREADS) {
       int key = e / D, d = e % D;
-      int kk = k0 + key;
       float kv = 0.f, vv = 0.f;
       if (kv_ok[key]) {
-        int blk, off;
-        if (kk < Pc) {
-          blk = a.prefix_bt[(int64_t)r * a.prefix_bt_stride + kk / a.bs];
-          off = kk % a.bs;
-        } else {
-          int pos = s0 + kk - Pc;
-          blk = a.suffix_bt[(int64_t)n * a.suffix_bt_stride + pos / a.bs];
-          off = pos % a.bs;
-        }
-        int64_t o = (int64_t)blk * a.kv_block_stride + (int64_t)off * a.kv_tok_stride +
-                    (int64_t)hk * a.kv_head_stride + d;
+        const int64_t o = k_off[key] + (int64_t)hk * a.kv_head_stride + d;
         if constexpr (KV8) {
           kv = fp8e4m3_to_float(kc8[o]) * k_sc;
           vv = fp8e4m3_to_float(vc8[o]) * v_sc;
@@ -172,21 +217,20 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
     {
       const int key = t % GEN_TK;
       const int kk = k0 + key;
+      const int kpos = k_pos[key], kbeam = k_beam[key];
       for (int row = t / GEN_TK; row < GEN_ROWS; row += GEN_THREADS / GEN_TK) {
         float s = 0.f;
         for (int d = 0; d < D; ++d) s += q_s[row * D + d] * k_s[key * (D + 1) + d];
         s *= a.scale;
         if (a.softcap > 0.f) s = a.softcap * tanhf(s / a.softcap);
-        const int qpos = qpos_of(row);
-        if (a.alibi) s -= a.alibi[hk * G + (row0 + row) % G] * (float)abs(qpos - kk);
         bool vis = row < nrows && kk < total && kv_ok[key];
-        if (PREFILL && a.causal) vis = vis && kk <= qpos;
-        if (!PREFILL && vis && kk >= Pc) {
-          int qi = (row0 + row) / G;
-          vis = (kk - Pc) <= Lc - a.T + qi;
-        }
-        if (a.win_left >= 0) vis = vis && kk >= qpos - a.win_left;
-        if (a.win_right >= 0) vis = vis && kk <= qpos + a.win_right;
+        const int qpos = vis ? qpos_of(row) : 0;
+        if (a.alibi) s -= a.alibi[hk * G + (row0 + row) % G] * (float)abs(qpos - kpos);
+        if (PREFILL && a.causal) vis = vis && kpos <= qpos;
+        // a suffix key: its own beam's rows only, up to the row's query (bottom-right causal)
+        if (!PREFILL && vis && kbeam >= 0) vis = kbeam == row_beam(row) && kpos <= qpos;
+        if (a.win_left >= 0) vis = vis && kpos >= qpos - a.win_left;
+        if (a.win_right >= 0) vis = vis && kpos <= qpos + a.win_right;
         p_s[row * (GEN_TK + 1) + key] = vis ? s : -INFINITY;
       }
     }
@@ -243,19 +287,17 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
     if (e < GEN_ROWS * D) {
       int row = e / D, d = e % D;
       if (row < nrows) {
-        int rho = row0 + row;
-        int qi = rho / G, g = rho % G;
+        const int g = (row0 + row) % G;
         float l = l_s[row];
         float o = l > 0.f ? (a.sinks ? acc[i] * a_s[row] : acc[i]) / l : 0.f;
-        out[(tok0 + qi) * a.out_tok_stride + (int64_t)(hk * G + g) * D + d] = E::from_float(o);
+        out[row_tok(row) * a.out_tok_stride + (int64_t)(hk * G + g) * D + d] = E::from_float(o);
       }
     }
   }
   if (a.lse_out && t < nrows) {
-    int rho = row0 + t;
-    int qi = rho / G, g = rho % G;
+    const int g = (row0 + t) % G;
     float l = l_s[t];
-    a.lse_out[(tok0 + qi) * a.Hq + hk * G + g] = l > 0.f ? m_s[t] + logf(l) : -INFINITY;
+    a.lse_out[row_tok(t) * a.Hq + hk * G + g] = l > 0.f ? m_s[t] + logf(l) : -INFINITY;
   }
 }
 
@@ -293,8 +335,8 @@ static gr_status_t launch_generic_kv(const DecodeArgs& a, dim3 grid, size_t smem
 template <bool PREFILL>
 static gr_status_t launch_generic(const DecodeArgs& a, hipStream_t stream) {
   const int G = a.Hq / a.Hkv;
-  const int64_t chunks = ((int64_t)G * a.T + GEN_ROWS - 1) / GEN_ROWS;
-  const int64_t gx = (int64_t)(PREFILL ? a.num_reqs : a.num_beams) * chunks;
+  const int64_t chunks = ((int64_t)(PREFILL ? 1 : a.max_beams) * G * a.T + GEN_ROWS - 1) / GEN_ROWS;
+  const int64_t gx = (int64_t)a.num_reqs * chunks;
   if (gx == 0) return GR_OK;
   if (gx > 0x7fffffff || a.Hkv > 65535) return GR_ERR_INVALID_ARG;
   dim3 grid((unsigned)gx, (unsigned)a.Hkv);
