@@ -213,6 +213,26 @@ def test_decode_bad_block_flagged(device, kernel, P):
         assert err <= 2e-2, f"max abs err {err:.3e}"
 
 
+@pytest.mark.parametrize("kernel", ["auto", "generic"])
+def test_decode_understated_max_beams_flagged(device, kernel):
+    """A request with more beams than max_beams_per_req says would leave rows
+    that no workgroup computes: the request is reported instead."""
+    wl = workloads.make_decode(R=2, W=6, P=100, L=2, Hq=8, Hkv=2, D=128, dtype=torch.bfloat16, seed=4,
+                               input_scale=1.0)
+    d = wl.to(device)
+    out = torch.zeros_like(d.q)
+    status = ops.new_status(device)
+    ops.set_decode_kernel(kernel)
+    try:
+        ops.beam_attn_decode(d.q, d.k_cache, d.v_cache, d.prefix_bt, d.prefix_len, d.beam_start, d.suffix_bt,
+                             d.suffix_len, scale=d.scale, max_beams_per_req=d.max_beams - 1, out=out,
+                             status=status, split=False)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_decode_kernel("auto")
+    assert int(status.item()) & ops._C.GR_DEV_BAD_LENGTH
+
+
 def test_decode_late_dominant_key(device):
     """A key far above every earlier score of its row, late in the prefix (its
     weight relative to the running reference exceeds 2^60), must move the

@@ -139,7 +139,9 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     W = a.beam_start[r + 1] - nb0;
     TG = a.T * G;
     rows_r = W * TG;
-    if (nb0 < 0 || W < 0 || nb0 + W > a.num_beams) {  // beam_start is device data: never trust it
+    // beam_start is device data: never trust it (a request past max_beams
+    // would leave rows no workgroup computes)
+    if (nb0 < 0 || W < 0 || nb0 + W > a.num_beams || W > a.max_beams) {
       if (threadIdx.x == 0 && mt == 0) flag_status(a.dev_status, GR_DEV_BAD_LENGTH);
       return;
     }
