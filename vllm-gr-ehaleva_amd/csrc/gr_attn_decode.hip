@@ -20,6 +20,7 @@ constexpr int GEN_ROWS = 32;     // query rows per workgroup
 constexpr int GEN_TK = 32;       // keys per tile
 constexpr int GEN_THREADS = 256;
 constexpr int GEN_ACC = GEN_ROWS * 256 / GEN_THREADS;  // acc slots per thread at D=256
+constexpr int GEN_KPAD = 4;      // floats past each staged K row: 16-byte rows, keys spread over banks
 
 // PREFILL: the varlen mode (gr_paged_attn_prefill): blockIdx.x / chunks is
 // the request, prefix_bt / prefix_len its block table and sequence length,
@@ -52,8 +53,9 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   __shared__ int k_pos[GEN_TK];         // ... position in [prefix ; own suffix]
   const int D = a.D;
   float* q_s = smem;                              // [ROWS][D]
-  float* k_s = q_s + GEN_ROWS * D;                // [TK][D+1]
-  float* v_s = k_s + GEN_TK * (D + 1);            // [TK][D]
+  const int KP = D + GEN_KPAD;
+  float* k_s = q_s + GEN_ROWS * D;                // [TK][D+KPAD]
+  float* v_s = k_s + GEN_TK * KP;                 // [TK][D]
   float* p_s = v_s + GEN_TK * D;                  // [ROWS][TK+1]
   float* m_s = p_s + GEN_ROWS * (GEN_TK + 1);     // [ROWS]
   float* l_s = m_s + GEN_ROWS;                    // [ROWS]
@@ -135,6 +137,12 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   const uint8_t* kc8 = static_cast<const uint8_t*>(a.k_cache);
   const uint8_t* vc8 = static_cast<const uint8_t*>(a.v_cache);
   const float k_sc = KV8 && a.k_scale ? a.k_scale[0] : 1.f, v_sc = KV8 && a.v_scale ? a.v_scale[0] : 1.f;
+  // every key row's eight-element chunks start on a vector boundary: bases
+  // and strides in whole vectors (16 bytes; 8 for fp8)
+  const int vbytes = KV8 ? 8 : 16, esz = KV8 ? 1 : (int)sizeof(S);
+  const bool vec = (reinterpret_cast<uintptr_t>(a.k_cache) % vbytes) == 0 &&
+                   (reinterpret_cast<uintptr_t>(a.v_cache) % vbytes) == 0 && (a.kv_block_stride * esz) % vbytes == 0 &&
+                   (a.kv_tok_stride * esz) % vbytes == 0 && (a.kv_head_stride * esz) % vbytes == 0;
 
   for (int e = t; e < GEN_ROWS * D; e += GEN_THREADS) {
     int row = e / D, d = e % D;
@@ -197,31 +205,86 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
       k_pos[t] = kp;
     }
     __syncthreads();
-    for (int e = t; e < GEN_TK * D; e += GEN_THREADS) {
-      int key = e / D, d = e % D;
-      float kv = 0.f, vv = 0.f;
+    // eight elements of one key row per step: one 16-byte load each for K
+    // and V (two for fp32, 8 bytes for fp8) when the cache is aligned for it
+    for (int e = t; e < GEN_TK * (D / 8); e += GEN_THREADS) {
+      const int key = e / (D / 8), d = (e - key * (D / 8)) * 8;
+      float kv[8], vv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kv[j] = vv[j] = 0.f;
       if (kv_ok[key]) {
         const int64_t o = k_off[key] + (int64_t)hk * a.kv_head_stride + d;
         if constexpr (KV8) {
-          kv = fp8e4m3_to_float(kc8[o]) * k_sc;
-          vv = fp8e4m3_to_float(vc8[o]) * v_sc;
+          if (vec) {
+            const uint2 kb = *reinterpret_cast<const uint2*>(kc8 + o), vb = *reinterpret_cast<const uint2*>(vc8 + o);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              kv[j] = fp8e4m3_to_float(((j < 4 ? kb.x : kb.y) >> (8 * (j & 3))) & 0xFFu) * k_sc;
+              vv[j] = fp8e4m3_to_float(((j < 4 ? vb.x : vb.y) >> (8 * (j & 3))) & 0xFFu) * v_sc;
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              kv[j] = fp8e4m3_to_float(kc8[o + j]) * k_sc;
+              vv[j] = fp8e4m3_to_float(vc8[o + j]) * v_sc;
+            }
+          }
         } else {
-          kv = E::to_float(kc[o]);
-          vv = E::to_float(vc[o]);
+          if (vec) {
+            struct alignas(16) V16 { S e[16 / sizeof(S)]; };
+            constexpr int PER = 16 / sizeof(S);  // elements per 16-byte load
+#pragma unroll
+            for (int h = 0; h < 8 / PER; ++h) {
+              const V16 kq = *reinterpret_cast<const V16*>(kc + o + h * PER);
+              const V16 vq = *reinterpret_cast<const V16*>(vc + o + h * PER);
+#pragma unroll
+              for (int j = 0; j < PER; ++j) {
+                kv[h * PER + j] = E::to_float(kq.e[j]);
+                vv[h * PER + j] = E::to_float(vq.e[j]);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              kv[j] = E::to_float(kc[o + j]);
+              vv[j] = E::to_float(vc[o + j]);
+            }
+          }
         }
       }
-      k_s[key * (D + 1) + d] = kv;
-      v_s[key * D + d] = vv;
+      *reinterpret_cast<float4*>(k_s + key * KP + d) = float4{kv[0], kv[1], kv[2], kv[3]};
+      *reinterpret_cast<float4*>(k_s + key * KP + d + 4) = float4{kv[4], kv[5], kv[6], kv[7]};
+      *reinterpret_cast<float4*>(v_s + key * D + d) = float4{vv[0], vv[1], vv[2], vv[3]};
+      *reinterpret_cast<float4*>(v_s + key * D + d + 4) = float4{vv[4], vv[5], vv[6], vv[7]};
     }
     __syncthreads();
     {
+      // key t % TK against rows t / TK + 8 j: each K chunk read once for the
+      // four rows, four dims per LDS read; every dot product sums over d in order
       const int key = t % GEN_TK;
       const int kk = k0 + key;
       const int kpos = k_pos[key], kbeam = k_beam[key];
-      for (int row = t / GEN_TK; row < GEN_ROWS; row += GEN_THREADS / GEN_TK) {
-        float s = 0.f;
-        for (int d = 0; d < D; ++d) s += q_s[row * D + d] * k_s[key * (D + 1) + d];
-        s *= a.scale;
+      constexpr int RPT = GEN_ROWS / (GEN_THREADS / GEN_TK);  // rows per thread
+      float sr[RPT];
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) sr[j] = 0.f;
+      for (int d = 0; d < D; d += 4) {
+        const float4 k4 = *reinterpret_cast<const float4*>(k_s + key * KP + d);
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+          const float4 q4 = *reinterpret_cast<const float4*>(q_s + (t / GEN_TK + j * (GEN_THREADS / GEN_TK)) * D + d);
+          float s_ = sr[j];
+          s_ += q4.x * k4.x;
+          s_ += q4.y * k4.y;
+          s_ += q4.z * k4.z;
+          s_ += q4.w * k4.w;
+          sr[j] = s_;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const int row = t / GEN_TK + j * (GEN_THREADS / GEN_TK);
+        float s = sr[j] * a.scale;
         if (a.softcap > 0.f) s = a.softcap * tanhf(s / a.softcap);
         bool vis = row < nrows && kk < total && kv_ok[key];
         const int qpos = vis ? qpos_of(row) : 0;
@@ -257,14 +320,26 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
       a_s[t] = alpha;
     }
     __syncthreads();
+    // slot i of a thread: four consecutive dims (one LDS read of V each key)
 #pragma unroll
-    for (int i = 0; i < GEN_ACC; ++i) {
-      int e = t + i * GEN_THREADS;
+    for (int i = 0; i < GEN_ACC / 4; ++i) {
+      const int e = (t + i * GEN_THREADS) * 4;
       if (e < GEN_ROWS * D) {
-        int row = e / D, d = e % D;
-        float o = acc[i] * a_s[row];
-        for (int key = 0; key < GEN_TK; ++key) o += p_s[row * (GEN_TK + 1) + key] * v_s[key * D + d];
-        acc[i] = o;
+        const int row = e / D, d = e % D;
+        const float al = a_s[row];
+        float o0 = acc[4 * i] * al, o1 = acc[4 * i + 1] * al, o2 = acc[4 * i + 2] * al, o3 = acc[4 * i + 3] * al;
+        for (int key = 0; key < GEN_TK; ++key) {
+          const float p = p_s[row * (GEN_TK + 1) + key];
+          const float4 v4 = *reinterpret_cast<const float4*>(v_s + key * D + d);
+          o0 += p * v4.x;
+          o1 += p * v4.y;
+          o2 += p * v4.z;
+          o3 += p * v4.w;
+        }
+        acc[4 * i] = o0;
+        acc[4 * i + 1] = o1;
+        acc[4 * i + 2] = o2;
+        acc[4 * i + 3] = o3;
       }
     }
   }
@@ -283,7 +358,7 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
   S* out = static_cast<S*>(a.out);
 #pragma unroll
   for (int i = 0; i < GEN_ACC; ++i) {
-    int e = t + i * GEN_THREADS;
+    const int e = (t + (i / 4) * GEN_THREADS) * 4 + (i & 3);
     if (e < GEN_ROWS * D) {
       int row = e / D, d = e % D;
       if (row < nrows) {
@@ -302,7 +377,7 @@ __global__ __launch_bounds__(GEN_THREADS) void decode_generic(DecodeArgs a) {
 }
 
 static size_t generic_smem_bytes(int D) {
-  return sizeof(float) * ((size_t)GEN_ROWS * D + GEN_TK * (D + 1) + GEN_TK * D +
+  return sizeof(float) * ((size_t)GEN_ROWS * D + GEN_TK * (D + GEN_KPAD) + GEN_TK * D +
                           GEN_ROWS * (GEN_TK + 1) + 3 * GEN_ROWS) + sizeof(int) * GEN_TK;
 }
 
