@@ -210,9 +210,10 @@ gr_status_t gr_beam_attn_decode_opt(
     const gr_attn_options* options, hipStream_t stream);
 
 /* gr_paged_attn_prefill with options.  Causal bf16/fp16 head-dim-128 prefills
- * with sinks and / or an fp8 cache run on the matrix-core kernel; windows,
- * ALiBi, non-causal batches, fp32 and other head sizes take the generic
- * kernel. */
+ * with sinks and / or an fp8 cache run on the matrix-core kernel (head dim 64
+ * too, with an even KV head count: adjacent KV heads read as one 128-dim
+ * head); windows, ALiBi, non-causal batches, fp32 and other head sizes take
+ * the generic kernel. */
 gr_status_t gr_paged_attn_prefill_opt(
     void* out, int64_t out_tok_stride,
     const void* q, int64_t q_tok_stride,

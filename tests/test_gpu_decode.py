@@ -213,6 +213,52 @@ def test_decode_bad_block_flagged(device, kernel, P):
         assert err <= 2e-2, f"max abs err {err:.3e}"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Hq,Hkv,T,split", [(32, 8, 1, False), (8, 2, 2, True), (4, 4, 1, True), (16, 2, 1, False),
+                                            (6, 3, 1, False)])
+def test_decode_head_dim_64(device, dtype, Hq, Hkv, T, split):
+    """head_dim 64: an even KV head count runs on the matrix-core kernel as
+    pairs of adjacent KV heads read as 128-dim heads (each query row's Q fills
+    its own head's half, only that half of its output is written; never
+    split); an odd count (6/3) takes the generic kernel.  Against the float64
+    oracle, and the generic kernel's output."""
+    wl = workloads.make_decode(R=2, W=16, P=300, L=(T, T + 5), Hq=Hq, Hkv=Hkv, D=64, dtype=dtype, input_scale=1.0,
+                               seed=Hq + Hkv + T, q_per_beam=T)
+    out, lse = run_gpu(wl, device, split=split, max_prefix_len=300 if split else None)
+    ref, ref_lse = run_oracle(wl)
+    _check(out, lse, ref, ref_lse, 2e-2)
+    gen, _ = run_gpu(wl, device, kernel="generic")
+    assert np.abs(out - gen).max() <= 2e-2
+
+
+@pytest.mark.parametrize("opt", ["window", "sinks_alibi"])
+def test_decode_head_dim_64_options(device, opt):
+    """head_dim 64 head pairs with the option variant: a left window, or
+    sinks and ALiBi (indexed by the real query head)."""
+    wl = workloads.make_decode(R=2, W=8, P=400, L=(1, 6), Hq=16, Hkv=4, D=64, dtype=torch.bfloat16,
+                               input_scale=1.0, seed=5)
+    g = torch.Generator().manual_seed(7)
+    kw = dict(window=(90, -1)) if opt == "window" else dict(sinks=torch.randn(16, generator=g),
+                                                              alibi_slopes=torch.rand(16, generator=g) * 0.05)
+    d = wl.to(device)
+    out = torch.empty_like(d.q)
+    lse = torch.empty(d.q.shape[:2], dtype=torch.float32, device=device)
+    status = ops.new_status(device)
+    ops.beam_attn_decode(d.q, d.k_cache, d.v_cache, d.prefix_bt, d.prefix_len, d.beam_start, d.suffix_bt,
+                         d.suffix_len, scale=d.scale, max_beams_per_req=d.max_beams, out=out, lse=lse,
+                         status=status, **{k_: (v_.to(device) if isinstance(v_, torch.Tensor) else v_)
+                                           for k_, v_ in kw.items()})
+    torch.cuda.synchronize()
+    ops.check_status(status)
+    kv = wl.kv_cache.to(torch.float64).numpy()
+    ref, ref_lse = oa.beam_attention_dense(_host(wl.q), kv[0], kv[1], wl.prefix_bt.numpy(), wl.prefix_len.numpy(),
+                                           wl.beam_start.numpy(), wl.suffix_bt.numpy(), wl.suffix_len.numpy(),
+                                           scale=wl.scale, block_size=wl.block_size,
+                                           **{k_: (v_.numpy() if isinstance(v_, torch.Tensor) else v_)
+                                              for k_, v_ in kw.items()})
+    _check(_host(out), lse.cpu().numpy().astype(np.float64), ref, ref_lse, 2e-2)
+
+
 @pytest.mark.parametrize("kernel", ["auto", "generic"])
 def test_decode_understated_max_beams_flagged(device, kernel):
     """A request with more beams than max_beams_per_req says would leave rows

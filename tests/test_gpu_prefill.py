@@ -93,6 +93,26 @@ def test_prefill_mfma_bf16(device, heads):
     assert np.abs(lse - ref_lse).max() <= 2e-2
 
 
+@pytest.mark.parametrize("heads,dtype", [((16, 8), torch.bfloat16), ((8, 2), torch.float16), ((6, 6), torch.bfloat16),
+                                         ((9, 3), torch.bfloat16)])
+def test_prefill_head_dim_64(device, heads, dtype):
+    """head_dim 64: an even KV head count runs on the matrix-core kernel as
+    pairs of adjacent KV heads read as 128-dim heads (each query row's half
+    of Q zero in the other half, only its own half written); an odd count
+    takes the generic kernel.  Against the float64 oracle, and the generic
+    kernel's output."""
+    Hq, Hkv = heads
+    q, kv, bt, qs, seqs = _case(QLENS, CTXS, Hq, Hkv, 64, dtype, seed=Hq * 3 + Hkv)
+    out, lse, st = _run(device, q, kv, bt, qs, seqs, 64 ** -0.5)
+    ops.check_status(st)
+    ref, ref_lse = _oracle(q, kv, bt, qs, seqs, 64 ** -0.5)
+    assert np.abs(out - ref).max() <= 2e-2
+    assert np.abs(lse - ref_lse).max() <= 2e-2
+    gen, _, st = _run(device, q, kv, bt, qs, seqs, 64 ** -0.5, kernel="generic")
+    ops.check_status(st)
+    assert np.abs(out - gen).max() <= 2e-2
+
+
 def test_prefill_long_prompt_one_request(device):
     """The 2048-token prompt of the end-to-end decode (16 query / 8 KV heads)."""
     q, kv, bt, qs, seqs = _case([2048], [0], 16, 8, 128, torch.bfloat16, seed=11)

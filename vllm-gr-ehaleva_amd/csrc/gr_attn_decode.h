@@ -41,6 +41,10 @@ struct DecodeArgs {
   int kv8;                   // the caches hold fp8 e4m3 elements (dequantised by k_scale / v_scale)
   const float* k_scale;      // [1] or null (1.0)
   const float* v_scale;      // [1] or null (1.0)
+  // head pairs (matrix-core kernel, head_dim 64): KV heads 2j and 2j + 1
+  // read as one 128-dim head j; each query row fills and writes only its own
+  // head's half of the 128 dims (mfma_pair_args)
+  int pair;
 };
 
 
@@ -48,6 +52,10 @@ struct DecodeArgs {
 // (decode: sinks, a left window and ALiBi run here too; prefill: sinks)
 bool mfma_decode_supported(const DecodeArgs& a);
 bool mfma_prefill_supported(const DecodeArgs& a);
+// head_dim 64 on the matrix-core kernel: p = a with adjacent KV head pairs as
+// 128-dim heads, when the cache allows it (an even KV head count, heads 64
+// elements apart) and the kernel takes p.
+bool mfma_pair_args(const DecodeArgs& a, DecodeArgs& p);
 gr_status_t launch_mfma_decode(const DecodeArgs& a, hipStream_t stream);
 // Varlen causal mode of the same kernel (see gr_paged_attn_prefill).
 gr_status_t launch_mfma_prefill(const DecodeArgs& a, hipStream_t stream);

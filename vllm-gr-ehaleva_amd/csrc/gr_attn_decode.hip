@@ -510,7 +510,11 @@ extern "C" gr_status_t gr_beam_attn_decode(
   bool empty;
   const gr_status_t st = decode_args(a, empty, GR_DECODE_ARG_NAMES);
   if (st != GR_OK || empty) return st;
-  if (g_decode_kernel_override != 1 && mfma_decode_supported(a)) return launch_mfma_decode(a, stream);
+  if (g_decode_kernel_override != 1) {
+    if (mfma_decode_supported(a)) return launch_mfma_decode(a, stream);
+    DecodeArgs p;
+    if (mfma_pair_args(a, p)) return launch_mfma_decode(p, stream);
+  }
   return launch_generic<false>(a, stream);
 }
 
@@ -558,6 +562,10 @@ static gr_status_t decode_ws_impl(
   st = apply_options(a, opt, false);
   if (st != GR_OK || empty) return st;
   if (max_prefix_len < 0) return GR_ERR_INVALID_ARG;
+  if (g_decode_kernel_override != 1 && !mfma_decode_supported(a)) {
+    DecodeArgs p;  // head_dim 64 as head pairs, never split (the workspace is for head_dim 128)
+    if (mfma_pair_args(a, p)) return launch_mfma_decode(p, stream);
+  }
   if (g_decode_kernel_override == 1 || !mfma_decode_supported(a)) return launch_generic<false>(a, stream);
   int tiles, nsplit;
   mfma_decode_plan(num_reqs, max_beams_per_req, q_per_beam, num_q_heads, num_kv_heads, max_prefix_len, &tiles,
@@ -637,7 +645,11 @@ static gr_status_t prefill_impl(
   a.causal = 1;
   const gr_status_t st = apply_options(a, opt, true);
   if (st != GR_OK) return st;
-  if (g_decode_kernel_override != 1 && mfma_prefill_supported(a)) return launch_mfma_prefill(a, stream);
+  if (g_decode_kernel_override != 1) {
+    if (mfma_prefill_supported(a)) return launch_mfma_prefill(a, stream);
+    DecodeArgs p;
+    if (mfma_pair_args(a, p) && mfma_prefill_supported(p)) return launch_mfma_prefill(p, stream);
+  }
   return launch_generic<true>(a, stream);
 }
 

@@ -330,10 +330,15 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   const int my_len = *(!PREFILL && row_ok ? a.suffix_len + nb0 + my_b : zint);  // this lane's beam (causal limit)
   __builtin_amdgcn_sched_barrier(0);  // the metadata loads stay first: the slot table waits only for them
   {
-    const S* src = qp + my_tok * a.q_tok_stride + (int64_t)(hk * G + my_g) * HD + lhalf * 8;
+    // head pairs: query head hq's 64 dims fill dims [64 half, 64 half + 64),
+    // half = which KV head of the pair it reads; the other half stays zero
+    const int hq = hk * G + my_g, half = a.pair ? my_g / (G >> 1) : 0;
+    const S* src = qp + my_tok * a.q_tok_stride + (int64_t)hq * (a.pair ? HD / 2 : HD) + lhalf * 8 -
+                   (a.pair ? half * (HD / 2) : 0);
     const S* zq = reinterpret_cast<const S*>(g_zero16);
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qf[kk] = *reinterpret_cast<const u32x4_t*>(row_ok ? src + kk * 16 : zq);
+    for (int kk = 0; kk < 8; ++kk)
+      qf[kk] = *reinterpret_cast<const u32x4_t*>(row_ok && (!a.pair || (kk >> 2) == half) ? src + kk * 16 : zq);
   }
   // ALiBi: this lane's row's slope (log2 units), read with Q
   const float alpha = OPT && a.alibi ? *(row_ok ? a.alibi + hk * G + my_g : reinterpret_cast<const float*>(zint)) * LOG2E
@@ -1054,9 +1059,13 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
             lrow_sum > 0.f ? (m + __builtin_amdgcn_logf(lrow_sum)) * 0.6931471805599453f : -INFINITY;
     } else if (ok_f) {
       const int64_t tok = PREFILL ? (int64_t)(nb0 + qi_f) : (int64_t)(nb0 + b_f) * a.T + qi_f;
-      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g_f) * HD + 4 * lhalf_f;
+      // (head pairs: only the row's own half of the 128 dims, dim blocks 2 half, 2 half + 1)
+      const int half_f = a.pair ? g_f / (G >> 1) : 0;
+      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g_f) * (a.pair ? HD / 2 : HD) +
+               4 * lhalf_f - (a.pair ? half_f * (HD / 2) : 0);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
+        if (a.pair && (mb >> 1) != half_f) continue;
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
           float v[4];
@@ -1154,6 +1163,22 @@ bool mfma_decode_supported(const DecodeArgs& a) {
 }
 
 bool mfma_prefill_supported(const DecodeArgs& a) { return mfma_decode_supported(a) && a.win_left < 0 && !a.alibi; }
+
+// head_dim 64: KV heads 2j and 2j + 1 sit side by side in a cache row (head
+// stride 64), so they read as one 128-dim head j serving both heads' query
+// heads (2 G of them).  A query row's Q fills its own head's half of the 128
+// dims and zeros the other, so its scores are its own head's; the PV product
+// gives both halves and only the row's own half is written.  Twice the
+// matrix-core work of the 64-dim problem, at the 128-dim kernel's speed.
+bool mfma_pair_args(const DecodeArgs& a, DecodeArgs& p) {
+  if (a.D != HD / 2 || a.Hkv % 2 != 0 || a.kv_head_stride != HD / 2) return false;
+  p = a;
+  p.D = HD;
+  p.Hkv = a.Hkv / 2;
+  p.kv_head_stride = HD;
+  p.pair = 1;
+  return mfma_decode_supported(p);
+}
 
 template <bool PREFILL, bool SPLIT, bool OPT, bool KV8>
 static void launch_mfma_kernel(const DecodeArgs& a, dim3 grid, int units, int mtiles, hipStream_t stream) {
