@@ -119,15 +119,17 @@ def test_attention_kernels_keep_no_stack():
     lambda is left out of line (one that is takes what it captures by
     reference -- O, Q, the row state -- through a per-lane stack in scratch:
     1.7 KB per lane in the soft-capped prefill, 11x slower), the plain
-    kernels (no soft cap, window, ALiBi or fp8) use no scratch at all and
-    the soft-capped ones at most a few spilled registers."""
+    128-dim kernels (no soft cap, window, ALiBi or fp8) use no scratch at
+    all and the soft-capped and head-pair (head_dim 64) ones at most a few
+    spilled registers."""
     text = _disassembly()
     out_of_line = sorted(set(re.findall(r"<(_ZZN2gr\S*decode_mfma\S*)>:", text)))
     assert not out_of_line, out_of_line[:4]
     sizes = _scratch_sizes()
-    # decode_mfma<DT, SOFTCAP, PREFILL, SPLIT, OPT, KV8>: OPT = KV8 = false
+    # decode_mfma<DT, SOFTCAP, PREFILL, SPLIT, OPT, KV8, PAIR>: OPT = KV8 = false
     plain = {k: v for k, v in sizes.items() if re.search(r"decode_mfmaILi[12]ELb[01]ELb[01]ELb[01]ELb0ELb0E", k)}
     assert len(plain) >= 12, sorted(plain)
     assert all(v <= 64 for v in plain.values()), {k: v for k, v in plain.items() if v > 64}
-    nocap = {k: v for k, v in plain.items() if re.search(r"decode_mfmaILi[12]ELb0E", k)}
+    nocap = {k: v for k, v in plain.items() if re.search(r"decode_mfmaILi[12]ELb0ELb[01]ELb[01]ELb0ELb0ELb0E", k)}
+    assert len(nocap) >= 6, sorted(nocap)
     assert all(v == 0 for v in nocap.values()), {k: v for k, v in nocap.items() if v}

@@ -39,12 +39,13 @@ struct DecodeArgs {
   const float* sinks;        // [Hq] sink logits (natural log units) or null
   const float* alibi;        // [Hq] ALiBi slopes or null
   int kv8;                   // the caches hold fp8 e4m3 elements (dequantised by k_scale / v_scale)
-  const float* k_scale;      // [1] or null (1.0)
-  const float* v_scale;      // [1] or null (1.0)
   // head pairs (matrix-core kernel, head_dim 64): KV heads 2j and 2j + 1
   // read as one 128-dim head j; each query row fills and writes only its own
-  // head's half of the 128 dims (mfma_pair_args)
+  // head's half of the 128 dims (mfma_pair_args).  (In kv8's padding: the
+  // block's size and layout stay as they were.)
   int pair;
+  const float* k_scale;      // [1] or null (1.0)
+  const float* v_scale;      // [1] or null (1.0)
 };
 
 

@@ -69,8 +69,11 @@ __device__ inline void tile_barrier() {
 // each wave converts the rows it loaded into a tile buffer one step ahead of
 // their use, so the matrix-core steps read bf16 / fp16 tiles as usual.  The K
 // scale folds into the softmax constant, the V scale into the output.
-template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false, bool OPT = false, bool KV8 = false>
+// PAIR: head_dim 64 as pairs of adjacent KV heads (a.pair; see mfma_pair_args).
+template <int DT, bool SOFTCAP, bool PREFILL = false, bool SPLIT = false, bool OPT = false, bool KV8 = false,
+          bool PAIR = false>
 __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int units, int mtiles) {
+  static_assert(!(PAIR && SPLIT), "head pairs are never split");
   constexpr int NB = KV8 ? 3 : NBUF;       // tile buffers
   constexpr int STG = 16384;               // bytes per fp8 staging slot: 64 rows x 128 B of K, then of V
   __shared__ __attribute__((aligned(1024))) uint16_t lds[KV8 ? 3 * BUF + 3 * STG / 2 : NBUF * BUF];
@@ -332,13 +335,13 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
   {
     // head pairs: query head hq's 64 dims fill dims [64 half, 64 half + 64),
     // half = which KV head of the pair it reads; the other half stays zero
-    const int hq = hk * G + my_g, half = a.pair ? my_g / (G >> 1) : 0;
-    const S* src = qp + my_tok * a.q_tok_stride + (int64_t)hq * (a.pair ? HD / 2 : HD) + lhalf * 8 -
-                   (a.pair ? half * (HD / 2) : 0);
+    const int hq = hk * G + my_g, half = PAIR ? my_g / (G >> 1) : 0;
+    const S* src = qp + my_tok * a.q_tok_stride + (int64_t)hq * (PAIR ? HD / 2 : HD) + lhalf * 8 -
+                   (PAIR ? half * (HD / 2) : 0);
     const S* zq = reinterpret_cast<const S*>(g_zero16);
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
-      qf[kk] = *reinterpret_cast<const u32x4_t*>(row_ok && (!a.pair || (kk >> 2) == half) ? src + kk * 16 : zq);
+      qf[kk] = *reinterpret_cast<const u32x4_t*>(row_ok && (!PAIR || (kk >> 2) == half) ? src + kk * 16 : zq);
   }
   // ALiBi: this lane's row's slope (log2 units), read with Q
   const float alpha = OPT && a.alibi ? *(row_ok ? a.alibi + hk * G + my_g : reinterpret_cast<const float*>(zint)) * LOG2E
@@ -1060,12 +1063,12 @@ __global__ __launch_bounds__(MF_THREADS, 1) void decode_mfma(DecodeArgs a, int u
     } else if (ok_f) {
       const int64_t tok = PREFILL ? (int64_t)(nb0 + qi_f) : (int64_t)(nb0 + b_f) * a.T + qi_f;
       // (head pairs: only the row's own half of the 128 dims, dim blocks 2 half, 2 half + 1)
-      const int half_f = a.pair ? g_f / (G >> 1) : 0;
-      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g_f) * (a.pair ? HD / 2 : HD) +
-               4 * lhalf_f - (a.pair ? half_f * (HD / 2) : 0);
+      const int half_f = PAIR ? g_f / (G >> 1) : 0;
+      S* dst = static_cast<S*>(a.out) + tok * a.out_tok_stride + (int64_t)(hk * G + g_f) * (PAIR ? HD / 2 : HD) +
+               4 * lhalf_f - (PAIR ? half_f * (HD / 2) : 0);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        if (a.pair && (mb >> 1) != half_f) continue;
+        if (PAIR && (mb >> 1) != half_f) continue;
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
           float v[4];
@@ -1180,17 +1183,30 @@ bool mfma_pair_args(const DecodeArgs& a, DecodeArgs& p) {
   return mfma_decode_supported(p);
 }
 
-template <bool PREFILL, bool SPLIT, bool OPT, bool KV8>
-static void launch_mfma_kernel(const DecodeArgs& a, dim3 grid, int units, int mtiles, hipStream_t stream) {
+template <bool PREFILL, bool SPLIT, bool OPT, bool KV8, bool PAIR>
+static void launch_mfma_kernel_p(const DecodeArgs& a, dim3 grid, int units, int mtiles, hipStream_t stream) {
   const bool cap = a.softcap > 0.f;
   const dim3 blk(MF_THREADS);
   if (a.dtype == GR_DTYPE_BF16) {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL, SPLIT, OPT, KV8>), grid, blk, 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL, SPLIT, OPT, KV8>), grid, blk, 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, true, PREFILL, SPLIT, OPT, KV8, PAIR>), grid, blk, 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_BF16, false, PREFILL, SPLIT, OPT, KV8, PAIR>), grid, blk, 0, stream, a, units, mtiles);
   } else {
-    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL, SPLIT, OPT, KV8>), grid, blk, 0, stream, a, units, mtiles);
-    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL, SPLIT, OPT, KV8>), grid, blk, 0, stream, a, units, mtiles);
+    if (cap) hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, true, PREFILL, SPLIT, OPT, KV8, PAIR>), grid, blk, 0, stream, a, units, mtiles);
+    else hipLaunchKernelGGL((decode_mfma<GR_DTYPE_F16, false, PREFILL, SPLIT, OPT, KV8, PAIR>), grid, blk, 0, stream, a, units, mtiles);
   }
+}
+
+// head pairs have their own instantiations (never split), so the 128-dim
+// kernels carry none of their arithmetic
+template <bool PREFILL, bool SPLIT, bool OPT, bool KV8>
+static void launch_mfma_kernel(const DecodeArgs& a, dim3 grid, int units, int mtiles, hipStream_t stream) {
+  if constexpr (!SPLIT) {
+    if (a.pair) {
+      launch_mfma_kernel_p<PREFILL, SPLIT, OPT, KV8, true>(a, grid, units, mtiles, stream);
+      return;
+    }
+  }
+  launch_mfma_kernel_p<PREFILL, SPLIT, OPT, KV8, false>(a, grid, units, mtiles, stream);
 }
 
 // the option variant (a decode's window or ALiBi) and the fp8-cache variant
