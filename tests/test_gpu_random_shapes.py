@@ -61,12 +61,14 @@ def test_random_decode(device, seed):
     assert np.abs(lse.cpu().numpy()[fin] - ref_lse[fin]).max(initial=0.0) <= 2e-2
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(24))
 def test_random_decode_variants(device, seed):
     """Random decodes over the space the shape sweep above keeps fixed: bf16
-    and fp16, fp8 e4m3 caches with random scales, a left window, sinks and
-    ALiBi in any combination, soft cap, split or not -- against the dense
-    float64 oracle with the same options (within 2e-2, LSE finiteness equal)."""
+    and fp16, head dim 128 or 64 (head pairs on the matrix-core kernel for an
+    even KV head count, the generic kernel for an odd one), fp8 e4m3 caches
+    with random scales, a left window, sinks and ALiBi in any combination,
+    soft cap, split or not -- against the dense float64 oracle with the same
+    options (within 2e-2, LSE finiteness equal)."""
     rng = np.random.default_rng(7000 + seed)
     Hkv = _pick(rng, [1, 2, 4, 8])
     G = _pick(rng, [1, 2, 4, 8])
@@ -81,6 +83,7 @@ def test_random_decode_variants(device, seed):
     kv8 = bool(rng.integers(0, 3) == 0)
     cap = float(_pick(rng, [0.0, 0.0, 0.0, 30.0]))
     split = bool(rng.integers(0, 2))
+    D = int(_pick(rng, [128, 128, 64]))
     g = torch.Generator().manual_seed(seed)
     kw = {}
     if rng.integers(0, 2):
@@ -89,9 +92,9 @@ def test_random_decode_variants(device, seed):
         kw["sinks"] = torch.randn(Hq, generator=g) * 2
     if rng.integers(0, 2):
         kw["alibi_slopes"] = torch.rand(Hq, generator=g) * 0.05
-    print(f"[random] decode variant R={R} W={W} P={P} T={T} L={L} Hkv={Hkv} G={G} bs={bs} {dtype} kv8={kv8} "
+    print(f"[random] decode variant R={R} W={W} P={P} T={T} L={L} Hkv={Hkv} G={G} D={D} bs={bs} {dtype} kv8={kv8} "
           f"cap={cap} split={split} options={sorted(kw)} window={kw.get('window')}", flush=True)
-    wl = workloads.make_decode(R=R, W=W, P=P, L=L, Hq=Hq, Hkv=Hkv, D=128, block_size=bs, dtype=dtype,
+    wl = workloads.make_decode(R=R, W=W, P=P, L=L, Hq=Hq, Hkv=Hkv, D=D, block_size=bs, dtype=dtype,
                                input_scale=1.0, seed=seed, q_per_beam=T, softcap=cap)
     d = wl.to(device)
     if kv8:
