@@ -133,3 +133,17 @@ def test_attention_kernels_keep_no_stack():
     nocap = {k: v for k, v in plain.items() if re.search(r"decode_mfmaILi[12]ELb0ELb[01]ELb[01]ELb0ELb0ELb0E", k)}
     assert len(nocap) >= 6, sorted(nocap)
     assert all(v == 0 for v in nocap.values()), {k: v for k, v in nocap.items() if v}
+
+
+def test_path_kernels_outside_attention_keep_no_stack():
+    """The pruning, fork and split-merge kernels of the decode step hold
+    their state in registers and LDS: none of them touches scratch (the
+    very wide requests' one-pass merge, which keeps 16 candidates per thread,
+    is the exception and is not checked)."""
+    sizes = _scratch_sizes()
+    names = ("prune_rows", "prune_merge_part", "prune_merge_lists", "beam_fork", "beam_append",
+             "split_merge", "catalog_advance")
+    found = {k: v for k, v in sizes.items() if any(n in k for n in names)}
+    for n in names:
+        assert any(n in k for k in found), n
+    assert all(v == 0 for v in found.values()), {k: v for k, v in found.items() if v}
