@@ -400,12 +400,17 @@ template <int MAXC, bool CATALOG = false, bool FULL = false>
 __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
   static_assert(!FULL || MAXC > 0, "a full row is held in registers");
   __shared__ uint64_t sk[PR_MAXK];  // candidates as row_key
-  __shared__ float ox[PR_MAXK];
-  __shared__ int ov[PR_MAXK];
-  // radix histogram (fallback path) or the survivors' partial ranks
-  __shared__ int hist_part[PR_BINS > PR_SURV * (PR_THREADS / 64) ? PR_BINS : PR_SURV * (PR_THREADS / 64)];
+  // radix histogram (fallback path) or the survivors' partial ranks; then
+  // the row's top-k1 logits and tokens (ox, ov), written once the histogram
+  // or the partial ranks are dead (the LDS saved lets a seventh workgroup
+  // share a CU)
+  constexpr int HP_INTS = PR_BINS > PR_SURV * (PR_THREADS / 64) ? PR_BINS : PR_SURV * (PR_THREADS / 64);
+  static_assert(HP_INTS >= 2 * PR_MAXK, "ox and ov fit the histogram's space");
+  __shared__ int hist_part[HP_INTS];
   int* hist = hist_part;
   int* part = hist_part;
+  float* ox = reinterpret_cast<float*>(hist_part);
+  int* ov = hist_part + PR_MAXK;
   __shared__ float wred[PR_THREADS / 64];
   __shared__ int itmp[PR_THREADS / 64];
   __shared__ int sel[3];
@@ -607,18 +612,26 @@ __global__ __launch_bounds__(PR_THREADS) void prune_rows(PruneArgs a) {
     else if (S <= 256) partial(std::integral_constant<int, 4>{});
     else partial(std::integral_constant<int, 8>{});
     __syncthreads();
+    int rk_h[PR_SURV / PR_THREADS];
 #pragma unroll
     for (int h = 0; h < PR_SURV / PR_THREADS; ++h) {
       const int i = tid + h * PR_THREADS;
+      int rank = k1;
       if (i < S) {
-        int rank = 0;
+        rank = 0;
 #pragma unroll
         for (int w = 0; w < PR_THREADS / 64; ++w) rank += part[w * PR_SURV + i];
-        if (rank < k1) {
-          const uint64_t ki = sk[i];
-          ox[rank] = fval((uint32_t)(ki >> 32));
-          ov[rank] = (int)~(uint32_t)ki;
-        }
+      }
+      rk_h[h] = rank;
+    }
+    __syncthreads();  // ox and ov take the partial ranks' space
+#pragma unroll
+    for (int h = 0; h < PR_SURV / PR_THREADS; ++h) {
+      const int i = tid + h * PR_THREADS;
+      if (rk_h[h] < k1) {
+        const uint64_t ki = sk[i];
+        ox[rk_h[h]] = fval((uint32_t)(ki >> 32));
+        ov[rk_h[h]] = (int)~(uint32_t)ki;
       }
     }
   } else {
